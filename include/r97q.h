@@ -1,0 +1,182 @@
+/* r97q.h -- C ABI of the MI355X (gfx950) IQR-quantized linear + LoRA path.
+ *
+ * Plain C: every argument is a pointer, a size or a flag; no C++ or torch type crosses it.
+ * All device pointers are HIP device memory on the current device. Every launch is asynchronous
+ * on the caller's stream (a hipStream_t passed as `R97IqrStream`, NULL = the null stream); the
+ * caller synchronises. Every entry returns 0 on success or one of the R97Q_E* codes below, and
+ * `r97q_last_error()` gives a one-line message for the calling thread's last failure.
+ *
+ * The path:  Y  = X.W^T + s.(X.A^T).B^T            (forward, t = X.A^T kept for the backward)
+ *            dX = dY.W + s.(dY.B).A,  dA = s.(dY.B)^T.X,  dB = s.dY^T.t   (backward)
+ * with W a frozen IQR weight [N, K] (tail-biting trellis codes down each column plus a block
+ * scale), A [r, K] and B [N, r] the LoRA factors, s = alpha / r.
+ */
+#ifndef R97Q_H
+#define R97Q_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ status codes */
+#define R97Q_OK 0
+#define R97Q_EINVAL 1       /* a description or size outside the rules (the reference's "1") */
+#define R97Q_EUNSUPPORTED 2 /* a valid form this entry point has no kernel for */
+#define R97Q_ELAUNCH 3      /* the HIP runtime refused a launch or a query */
+#define R97Q_EWORKSPACE 4   /* the workspace passed is smaller than the entry point needs */
+
+/* The last failure's message on the calling thread ("" when none). */
+const char* r97q_last_error(void);
+
+/* ------------------------------------------------------------------ the stored IQR form
+ *
+ * Scale element types. Same numbering as the reference's R97IqrScaleType
+ * (src/iqr_decode.h:43-48), because the description below is laid out like its
+ * R97IqrDecodeDesc and a caller may fill either. */
+enum R97IqrScaleType {
+    R97_IQR_F32 = 0,
+    R97_IQR_BF16 = 1,
+    R97_IQR_F8E4M3 = 2,
+    R97_IQR_F16 = 3,
+};
+
+/* One stored IQR weight and one range of its output rows: field for field the reference's
+ * R97IqrDecodeDesc (src/iqr_decode.h:59-114), so the struct a reference caller fills is accepted
+ * unchanged. Plane pointers are DEVICE pointers for the device entry points below. `codes`,
+ * `scale` (and `zero`) start at row `row0`; `lut` and `scale2` are whole planes. `out_codes` is
+ * [rows, cols] int8 and `out_scale` [rows, cols/128] bf16 bits. */
+typedef struct R97IqrDecodeDesc {
+    int64_t rows_all;
+    int64_t cols;
+    int64_t row0;
+    int64_t rows;
+
+    int32_t bits;
+    int32_t state_bits;
+    int32_t run_rows;
+    int32_t rb;
+
+    int32_t mad;
+    int32_t round_mad;
+    uint32_t mad_a;
+    uint32_t mad_b;
+    const int8_t* lut;
+
+    const uint8_t* codes;
+    int64_t codes_row_bytes;
+
+    const uint8_t* scale;
+    int32_t scale_dtype;
+    int64_t scale_block_cols;
+    int64_t scale_row_bytes;
+
+    int32_t affine;
+    const uint8_t* zero;
+    int32_t zero_bits;
+    int64_t zero_row_bytes;
+
+    const uint8_t* scale2;
+    int32_t scale2_dtype;
+    int64_t scale2_row_bytes;
+    int64_t scale2_block_rows;
+    int64_t scale2_block_cols;
+
+    int8_t* out_codes;
+    uint16_t* out_scale;
+} R97IqrDecodeDesc;
+
+/* The stream a launch runs on: a hipStream_t. */
+typedef void* R97IqrStream;
+
+/* 0 when `desc` is inside the decode's rules, 1 when not. Host-side check of the description
+ * only (it reads no plane). Same rules as the reference's r97_iqr_validate
+ * (src/iqr_decode.h:321-349). */
+int r97q_iqr_validate(const R97IqrDecodeDesc* desc);
+
+/* Decode rows [row0, row0+rows) of a stored IQR weight to the int8 grid and its bf16 scale, on
+ * the card. Replaces the reference's device entry `r97_iqr_decode` (src/iqr_decode.h:386,
+ * src/adjoint/device/iqr_decode.hip:47-56), same name, signature and contract: asynchronous on
+ * `stream`, returns 0, or 1 when the description is outside the rules or the launch failed. */
+int r97_iqr_decode(const R97IqrDecodeDesc* desc, R97IqrStream stream);
+
+/* ------------------------------------------------------------------ the prepared weight
+ *
+ * The fused kernels read a weight in a GPU layout made once per weight (the weight is frozen):
+ *   stream  : for every trellis run and every column, the column's codes in
+ *             descending row order, packed LSB first, so that the trellis state of row n is the
+ *             `state_bits`-wide bit window that starts at row n's code. Grouped in 32-row
+ *             segments of `bits` dwords; dword d of a segment is stored for 4 consecutive columns
+ *             together (one 128-bit load), see the layout in csrc/iqr_layout.h. Same size as
+ *             the canonical codes plane: no halo is stored.
+ *   scale_t : the effective bf16 scale of every (row, 128-column block), transposed to
+ *             [cols/128][rows]: the block scale with scale.1 settled (src/iqr_decode.h:223-235) and
+ *             the optional scale.col factor folded in with one rounding (src/iqr_form.h:203-216).
+ * The fused path serves trellis forms with rb = 1 (computed `mad` or stored `lut` codebook, any
+ * scale dtype, optional scale.1 / scale.col), cols % 128 == 0, rows % 32 == 0 and run_rows % 32 == 0. */
+typedef struct R97qWeight {
+    int64_t rows;          /* N */
+    int64_t cols;          /* K */
+    int32_t bits;
+    int32_t state_bits;
+    int32_t run_rows;
+    int32_t mad;
+    uint32_t mad_a;
+    uint32_t mad_b;
+    const int8_t* lut;     /* device, 2^state_bits int8 values when !mad */
+    const uint32_t* stream;   /* device, r97q_weight_stream_bytes() bytes */
+    const uint16_t* scale_t;  /* device, (cols/128) * rows bf16 */
+} R97qWeight;
+
+/* Bytes of the stream plane for the whole weight `desc` describes (row0 = 0, rows = rows_all);
+ * -1 when the form is not one the fused path serves (r97q_last_error says why). */
+int64_t r97q_weight_stream_bytes(const R97IqrDecodeDesc* desc);
+
+/* Build the prepared weight from the canonical device planes `desc` points at (whole weight:
+ * row0 = 0, rows = rows_all; the out_* fields are unused). `scale_col` is the optional
+ * scale.col plane (cols/128 f32 on the device, NULL when the form has none). Writes `stream_out`
+ * (r97q_weight_stream_bytes bytes) and `scale_t_out` ((cols/128)*rows bf16) and fills `w`. */
+int r97q_weight_prepare(const R97IqrDecodeDesc* desc, const float* scale_col, uint32_t* stream_out,
+                        uint16_t* scale_t_out, R97qWeight* w, R97IqrStream stream);
+
+/* ------------------------------------------------------------------ fused forward / backward
+ *
+ * dtype codes for the activations the entry points write. */
+#define R97Q_BF16 1
+#define R97Q_F32 0
+
+/* Workspace the forward / backward need at this shape (bytes, 256-aligned pieces inside). */
+int64_t r97q_fwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank);
+int64_t r97q_bwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank);
+
+/* Forward: Y[T,N] = X[T,K].W^T + scale.t.B^T with t[T,r] = X.A^T.
+ *   X bf16 [T,K]; A bf16 [r,K]; B bf16 [N,r]; rank 0 = no adapter (A, B, t_out unused).
+ *   Y is written (not added to) in `y_dtype` (R97Q_BF16 or R97Q_F32).
+ *   t_out f32 [T,r] receives t (the unscaled shrink), which the backward reads.
+ * The base product is the reference's gemm_nt twin (src/adjoint/host/linear.cpp:193-219), the
+ * adapter its lora_shrink and lora_expand twins (src/adjoint/host/lora.cpp:226-244,416-441). */
+int r97q_qlinear_lora_fwd(const R97qWeight* w, const uint16_t* X, int64_t T, const uint16_t* A,
+                          const uint16_t* B, int32_t rank, float scale, void* Y, int32_t y_dtype,
+                          float* t_out, void* workspace, int64_t workspace_bytes,
+                          R97IqrStream stream);
+
+/* Backward of the forward above, given dY bf16 [T,N] and the forward's X and t:
+ *   dX[T,K]  = dY.W + scale.(dY.B).A       written, or added to when dx_accumulate != 0,
+ *                                           in `dx_dtype`;
+ *   dA[r,K] += scale.(dY.B)^T.X            f32, always added to (a gradient leaf);
+ *   dB[N,r] += scale.dY^T.t                f32, always added to.
+ * dA and dB may be NULL to skip them. The reference's rows are gemm_nt_adjoint
+ * (src/adjoint/host/linear.cpp:221-243), lora_expand_host_adjoint (lora.cpp:451-521) and the
+ * float lora_shrink_host_adjoint (lora.cpp:260-328). */
+int r97q_qlinear_lora_bwd(const R97qWeight* w, const uint16_t* X, const uint16_t* dY, int64_t T,
+                          const uint16_t* A, const uint16_t* B, int32_t rank, float scale,
+                          const float* t, void* dX, int32_t dx_dtype, int32_t dx_accumulate,
+                          float* dA, float* dB, void* workspace, int64_t workspace_bytes,
+                          R97IqrStream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* R97Q_H */

@@ -1,0 +1,553 @@
+/* oracle/oracle.c -- CPU restatement of the reference host path (see oracle.h).
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP path and the reported CPU baseline. The
+ * product never links it.
+ *
+ * What pins each function (tests/test_oracle.py):
+ *   bf16 / f16 / e4m3 converters   exhaustive over all 2^16 / 2^8 inputs against numpy's IEEE
+ *                                  conversions and the OCP E4M3 table; and the golden vectors.
+ *   orc_state_value                all 2^16 states against an independent numpy evaluation of the
+ *                                  closed form, and the reference's own decode (golden vectors).
+ *   orc_iqr_validate / _decode     golden vectors written by the reference's own r97_iqr_decode_host
+ *                                  (oracle/_ref) over the case list of tests/host/iqr_decode.cpp;
+ *                                  invariants: chunk decode == whole decode at run boundaries, a
+ *                                  short last run, brute-force state walk on tiny weights.
+ *   orc_fold_scale_col             one-rounding definition against numpy; golden vectors.
+ *   orc_gemm_nt_twin / _adjoint    golden vectors from the reference rows (oracle/_ref);
+ *                                  brute-force numpy f64 matmul; <dy, twin(x)> == <adj(dy), x>.
+ *   orc_lora_*                     golden vectors from the reference rows; numpy f64 closed forms;
+ *                                  central finite differences of the twins; B = 0 => dA = 0, dt = 0.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+/* ------------------------------------------------------------------ parallel for
+ * src/parallel.h:39-90: partition by output, fixed chunks, worker t takes chunks t, t+T, ...;
+ * fewer than one chunk of work or one worker runs inline. */
+static int g_forced_threads = 0;
+
+void orc_set_threads(int n) { g_forced_threads = n > 0 ? n : 0; }
+
+int orc_thread_count(void) {
+    if (g_forced_threads > 0) return g_forced_threads;
+    const char* e = getenv("R97_THREADS");
+    if (e && *e) {
+        char* end = NULL;
+        long v = strtol(e, &end, 10);
+        if (end != e && *end == '\0' && v >= 1) return (int)v;
+    }
+    long hw = sysconf(_SC_NPROCESSORS_ONLN);
+    if (hw <= 0) return 1;
+    return hw < 8 ? (int)hw : 8;
+}
+
+typedef void (*body_fn)(void* ctx, int64_t i);
+
+typedef struct {
+    body_fn body;
+    void* ctx;
+    int64_t n, chunk, nchunks;
+    int t, T;
+} worker_arg;
+
+static void* worker_main(void* p) {
+    worker_arg* a = (worker_arg*)p;
+    for (int64_t c = a->t; c < a->nchunks; c += a->T) {
+        const int64_t lo = c * a->chunk;
+        int64_t hi = lo + a->chunk;
+        if (hi > a->n) hi = a->n;
+        for (int64_t i = lo; i < hi; ++i) a->body(a->ctx, i);
+    }
+    return NULL;
+}
+
+static void parallel_for(int64_t n, int64_t chunk, body_fn body, void* ctx) {
+    if (n <= 0) return;
+    if (chunk < 1) chunk = 1;
+    const int T = orc_thread_count();
+    if (T < 2 || n < chunk) {
+        for (int64_t i = 0; i < n; ++i) body(ctx, i);
+        return;
+    }
+    const int64_t nchunks = (n + chunk - 1) / chunk;
+    pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)T);
+    worker_arg* args = (worker_arg*)malloc(sizeof(worker_arg) * (size_t)T);
+    int started = 0;
+    for (int t = 0; t < T; ++t) {
+        args[t].body = body;
+        args[t].ctx = ctx;
+        args[t].n = n;
+        args[t].chunk = chunk;
+        args[t].nchunks = nchunks;
+        args[t].t = t;
+        args[t].T = T;
+        if (pthread_create(&th[t], NULL, worker_main, &args[t]) != 0) break;
+        ++started;
+    }
+    /* a worker that would not start: run its chunks here, so every unit still runs once */
+    for (int t = started; t < T; ++t) worker_main(&args[t]);
+    for (int t = 0; t < started; ++t) pthread_join(th[t], NULL);
+    free(th);
+    free(args);
+}
+
+/* ------------------------------------------------------------------ scalar formats
+ * src/iqr_decode.h:118-188 */
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    const uint32_t round = 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)((u + round) >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, u;
+    if (e == 0) {
+        if (m == 0) {
+            u = sign;
+        } else {
+            /* subnormal: normalise the significand */
+            int32_t ex = 127 - 15 + 1;
+            while ((m & 0x400u) == 0) {
+                m <<= 1;
+                --ex;
+            }
+            m &= 0x3FFu;
+            u = sign | ((uint32_t)ex << 23) | (m << 13);
+        }
+    } else if (e == 31) {
+        u = sign | 0x7F800000u | (m << 13);
+    } else {
+        u = sign | ((e + 127 - 15) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+float orc_e4m3_to_f32(uint8_t b) {
+    const uint32_t s = (uint32_t)(b >> 7) << 31;
+    uint32_t e = (uint32_t)(b >> 3) & 0xFu;
+    uint32_t m = (uint32_t)b & 0x7u;
+    uint32_t u;
+    if (e == 0u) {
+        if (m == 0u) {
+            u = s;
+        } else {
+            int sh = 0;
+            while (!(m & 0x8u)) {
+                m <<= 1;
+                ++sh;
+            }
+            m &= 0x7u;
+            u = s | ((uint32_t)(127 - 6 - sh) << 23) | (m << 20);
+        }
+    } else if (e == 0xFu && m == 0x7u) {
+        u = s | 0x7FC00000u;
+    } else {
+        u = s | ((e - 7u + 127u) << 23) | (m << 20);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static float load_scalar(const uint8_t* base, int32_t dtype, int64_t i) {
+    switch (dtype) {
+        case R97_IQR_F32: {
+            float f;
+            memcpy(&f, base + 4 * i, 4);
+            return f;
+        }
+        case R97_IQR_BF16: {
+            uint16_t h;
+            memcpy(&h, base + 2 * i, 2);
+            return orc_bf16_to_f32(h);
+        }
+        case R97_IQR_F8E4M3: return orc_e4m3_to_f32(base[i]);
+        case R97_IQR_F16: {
+            uint16_t h;
+            memcpy(&h, base + 2 * i, 2);
+            return orc_f16_to_f32(h);
+        }
+        default: return 0.0f;
+    }
+}
+
+/* element i of a packed row, LSB first (src/iqr_decode.h:191-200) */
+static uint32_t load_bits(const uint8_t* row, int32_t bits, int64_t i) {
+    const int64_t o = i * (int64_t)bits;
+    const int64_t byte = o >> 3;
+    const int sh = (int)(o & 7);
+    uint32_t w = row[byte];
+    if (sh + bits > 8) w |= (uint32_t)row[byte + 1] << 8;
+    if (sh + bits > 16) w |= (uint32_t)row[byte + 2] << 16;
+    if (sh + bits > 24) w |= (uint32_t)row[byte + 3] << 24;
+    return (w >> sh) & ((1u << bits) - 1u);
+}
+
+/* ------------------------------------------------------------------ one value */
+int32_t orc_state_value(const R97IqrDecodeDesc* d, uint32_t st) {
+    if (d->mad) {
+        const uint32_t h = ((st & 0xFFFFFFu) * (d->mad_a & 0xFFFFFFu) + d->mad_b) & 0x3F3F3F3Fu;
+        const uint32_t v = (h & 0xFFu) + ((h >> 8) & 0xFFu) + ((h >> 16) & 0xFFu) + ((h >> 24) & 0xFFu);
+        return (int32_t)v - 126;
+    }
+    return (int32_t)d->lut[st];
+}
+
+/* src/iqr_decode.h:216-219 */
+static int64_t scale_group(const R97IqrDecodeDesc* d, int64_t kb) {
+    const int64_t bc = d->scale_block_cols > 0 ? d->scale_block_cols : d->cols;
+    return bc == d->cols ? 0 : (kb * 128) / bc;
+}
+
+/* src/iqr_decode.h:223-235 */
+static float block_scale(const R97IqrDecodeDesc* d, int64_t r, int64_t kb) {
+    const int64_t bc = d->scale_block_cols > 0 ? d->scale_block_cols : d->cols;
+    const int64_t gb = scale_group(d, kb);
+    const uint8_t* row = d->scale + (r - d->row0) * d->scale_row_bytes;
+    float v = load_scalar(row, d->scale_dtype, gb);
+    if (d->scale2) {
+        const int64_t i2 = d->scale2_block_rows > 0 ? (r / d->scale2_block_rows) : 0;
+        const int64_t j2 = d->scale2_block_cols > 0 ? (gb * bc) / d->scale2_block_cols : 0;
+        const float s2 = load_scalar(d->scale2 + i2 * d->scale2_row_bytes, d->scale2_dtype, j2);
+        v = orc_bf16_to_f32(orc_f32_to_bf16(v * s2));
+    }
+    return v;
+}
+
+/* src/iqr_decode.h:239-250 */
+static float block_max(const R97IqrDecodeDesc* d, int64_t r, int64_t kb) {
+    const int64_t rb = d->rb;
+    const int64_t r0 = (r / rb) * rb;
+    int64_t r1 = r0 + rb;
+    if (r1 > d->rows_all) r1 = d->rows_all;
+    float m = 0.0f;
+    for (int64_t q = r0; q < r1; ++q) {
+        const float v = block_scale(d, q, kb);
+        m = v > m ? v : m;
+    }
+    return m;
+}
+
+/* src/iqr_decode.h:253-256 */
+static int32_t rb_round(int32_t v, float ratio, int32_t mad) {
+    if (mad) return (int32_t)(fmaf((float)v, ratio, 12582912.0f) - 12582912.0f);
+    return (int32_t)rintf((float)v * ratio);
+}
+
+/* src/iqr_decode.h:260-272 */
+static int32_t value_at(const R97IqrDecodeDesc* d, uint32_t st, int64_t r, int64_t kb, float* cur,
+                        float* scale) {
+    const int32_t v = orc_state_value(d, st);
+    if (d->rb > 1) {
+        if (r % d->rb == 0) *cur = block_max(d, r, kb);
+        const float sr = block_scale(d, r, kb);
+        *scale = *cur;
+        if (*cur <= 0.0f) return 0;
+        return rb_round(v, sr / *cur, d->round_mad);
+    }
+    *scale = block_scale(d, r, kb);
+    return v;
+}
+
+/* src/iqr_decode.h:278-287 */
+static void decode_affine(const R97IqrDecodeDesc* d, int64_t r, int64_t j) {
+    const int64_t kb = j >> 7;
+    const uint32_t code = load_bits(d->codes + (r - d->row0) * d->codes_row_bytes, d->bits, j);
+    const uint32_t zero =
+        load_bits(d->zero + (r - d->row0) * d->zero_row_bytes, d->zero_bits, scale_group(d, kb));
+    d->out_codes[(r - d->row0) * d->cols + j] = (int8_t)((int32_t)code - (int32_t)zero);
+    if ((j & 127) == 0)
+        d->out_scale[(r - d->row0) * (d->cols >> 7) + kb] = orc_f32_to_bf16(block_scale(d, r, kb));
+}
+
+/* src/iqr_decode.h:291-315 */
+static void decode_column(const R97IqrDecodeDesc* d, int64_t run_start, int64_t run_end, int64_t j) {
+    if (d->affine) {
+        for (int64_t r = run_start; r < run_end; ++r) decode_affine(d, r, j);
+        return;
+    }
+    const int32_t c = (d->state_bits + d->bits - 1) / d->bits;
+    const uint32_t mask = (d->state_bits >= 32) ? 0xFFFFFFFFu : ((1u << d->state_bits) - 1u);
+    uint32_t st = 0;
+    for (int32_t q = 0; q < c; ++q) {
+        const int64_t t = run_end - c + q;
+        st = ((st << d->bits) | load_bits(d->codes + (t - d->row0) * d->codes_row_bytes, d->bits, j)) & mask;
+    }
+    const int64_t kb = j >> 7;
+    const int64_t nkb = d->cols >> 7;
+    float cur = 0.0f;
+    for (int64_t r = run_start; r < run_end; ++r) {
+        st = ((st << d->bits) | load_bits(d->codes + (r - d->row0) * d->codes_row_bytes, d->bits, j)) & mask;
+        float sc;
+        const int32_t v = value_at(d, st, r, kb, &cur, &sc);
+        d->out_codes[(r - d->row0) * d->cols + j] = (int8_t)v;
+        if ((j & 127) == 0) d->out_scale[(r - d->row0) * nkb + kb] = orc_f32_to_bf16(sc);
+    }
+}
+
+/* src/iqr_decode.h:321-349 */
+int32_t orc_iqr_validate(const R97IqrDecodeDesc* d) {
+    if (!d->codes || !d->out_codes || !d->out_scale) return 1;
+    if (d->rows <= 0 || d->row0 < 0 || d->rows_all <= 0 || d->rows > d->rows_all - d->row0) return 1;
+    if (d->cols <= 0 || (d->cols & 127) != 0) return 1;
+    if (d->run_rows <= 0 || d->rb <= 0 || d->run_rows % d->rb != 0) return 1;
+    if (d->row0 % d->run_rows != 0) return 1;
+    if (d->rows % d->run_rows != 0 && d->row0 + d->rows != d->rows_all) return 1;
+    const int64_t bc = d->scale_block_cols > 0 ? d->scale_block_cols : d->cols;
+    if (bc != 128 && bc != d->cols) return 1;
+    if (d->affine) {
+        if (!d->zero || d->bits < 1 || d->bits > 7 || d->zero_bits < 1 || d->zero_bits > 8) return 1;
+        if (d->run_rows != 1 || d->rb != 1 || d->scale2) return 1;
+        return 0;
+    }
+    if (d->bits < 1 || d->bits > 16 || d->state_bits < 1 || d->state_bits > 24) return 1;
+    if (!d->mad && !d->lut) return 1;
+    if (d->scale2 && (d->scale2_block_rows < 0 || d->scale2_block_cols < 0)) return 1;
+    if (d->scale2 && d->scale2_block_cols > 0 && d->scale2_block_cols % 128 != 0) return 1;
+    const int32_t c = (d->state_bits + d->bits - 1) / d->bits;
+    for (int64_t r0 = d->row0; r0 < d->row0 + d->rows; r0 += d->run_rows) {
+        int64_t r1 = r0 + d->run_rows;
+        if (r1 > d->rows_all) r1 = d->rows_all;
+        if (r1 - r0 < c) return 1;
+    }
+    return 0;
+}
+
+typedef struct {
+    const R97IqrDecodeDesc* d;
+} decode_ctx;
+
+static void decode_unit(void* p, int64_t u) {
+    const R97IqrDecodeDesc* d = ((decode_ctx*)p)->d;
+    const int64_t r0 = d->row0 + (u / d->cols) * d->run_rows;
+    int64_t r1 = r0 + d->run_rows;
+    if (r1 > d->rows_all) r1 = d->rows_all;
+    decode_column(d, r0, r1, u % d->cols);
+}
+
+/* src/iqr_decode.h:353-376: one unit per (run, column), chunk 16384 */
+int32_t orc_iqr_decode(const R97IqrDecodeDesc* d) {
+    if (orc_iqr_validate(d)) return 1;
+    const int64_t nruns = (d->rows + d->run_rows - 1) / d->run_rows;
+    decode_ctx ctx = {d};
+    parallel_for(nruns * d->cols, 16384, decode_unit, &ctx);
+    return 0;
+}
+
+/* src/iqr_form.h:203-216: bf16(row * factor), one rounding */
+void orc_fold_scale_col(const float* row, const float* factor, int64_t rows, int64_t nkb,
+                        uint16_t* out_scale) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t kb = 0; kb < nkb; ++kb) out_scale[r * nkb + kb] = orc_f32_to_bf16(row[r] * factor[kb]);
+}
+
+/* ------------------------------------------------------------------ gemm_nt over a stored weight */
+typedef struct {
+    int64_t M, N, K, groups;
+    const double* a;      /* x or dy */
+    const int8_t* codes;
+    const uint16_t* scale;
+    double* out;
+    const int64_t* rows;
+} gemm_ctx;
+
+/* LinearWeight::value_at for a stored weight (src/adjoint/host/linear.cpp:158-162) */
+static inline double w_at(const gemm_ctx* g, int64_t n, int64_t k) {
+    const int64_t group = g->groups > 0 ? g->K / g->groups : g->K;
+    return (double)g->codes[n * g->K + k] *
+           (double)orc_bf16_to_f32(g->scale[n * g->groups + (group > 0 ? k / group : 0)]);
+}
+
+static void twin_row(void* p, int64_t i) {
+    const gemm_ctx* g = (const gemm_ctx*)p;
+    const int64_t m = g->rows ? g->rows[i] : i;
+    for (int64_t n = 0; n < g->N; ++n) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < g->K; ++k) acc += g->a[m * g->K + k] * w_at(g, n, k);
+        g->out[m * g->N + n] = acc;
+    }
+}
+
+/* src/adjoint/host/linear.cpp:193-219 (parallel_for(M, 2)) */
+void orc_gemm_nt_twin(int64_t M, int64_t N, int64_t K, const double* x, const int8_t* codes,
+                      const uint16_t* scale, double* y, const int64_t* rows, int64_t n_rows) {
+    gemm_ctx g = {M, N, K, K / 128, x, codes, scale, y, rows};
+    parallel_for(rows ? n_rows : M, 2, twin_row, &g);
+}
+
+static void adjoint_row(void* p, int64_t i) {
+    const gemm_ctx* g = (const gemm_ctx*)p;
+    const int64_t m = g->rows ? g->rows[i] : i;
+    for (int64_t k = 0; k < g->K; ++k) {
+        double acc = 0.0;
+        for (int64_t n = 0; n < g->N; ++n) acc += g->a[m * g->N + n] * w_at(g, n, k);
+        g->out[m * g->K + k] += acc;
+    }
+}
+
+/* src/adjoint/host/linear.cpp:221-243 (parallel_for(M, 2)) */
+void orc_gemm_nt_adjoint(int64_t M, int64_t N, int64_t K, const double* dy, const int8_t* codes,
+                         const uint16_t* scale, double* dx, const int64_t* rows, int64_t n_rows) {
+    gemm_ctx g = {M, N, K, K / 128, dy, codes, scale, dx, rows};
+    parallel_for(rows ? n_rows : M, 2, adjoint_row, &g);
+}
+
+/* ------------------------------------------------------------------ LoRA */
+/* src/adjoint/host/lora.cpp:197-202: 0..S-1, or -1 for a base row */
+static inline int64_t row_slot(const double* slot, int64_t S, int64_t m) {
+    const double v = slot[m];
+    if (!(v >= 0.0)) return -1;
+    const int64_t s = (int64_t)v;
+    return s < S ? s : -1;
+}
+
+typedef struct {
+    int64_t M, K, N, R, S;
+    const double *x, *slot, *la, *lb, *scale, *cot, *t;
+    double* out;
+    float* grad;
+    int fused, round_t;
+} lora_ctx;
+
+static void shrink_twin_row(void* p, int64_t m) {
+    const lora_ctx* c = (const lora_ctx*)p;
+    const int64_t s = row_slot(c->slot, c->S, m);
+    if (s < 0) return;
+    for (int64_t j = 0; j < c->R; ++j) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < c->K; ++k) acc += c->x[m * c->K + k] * c->la[(s * c->R + j) * c->K + k];
+        c->out[m * c->R + j] = acc;
+    }
+}
+
+void orc_lora_shrink_twin(int64_t M, int64_t K, int64_t R, int64_t S, const double* x,
+                          const double* slot, const double* lora_a, double* t) {
+    lora_ctx c = {M, K, 0, R, S, x, slot, lora_a, NULL, NULL, NULL, NULL, t, NULL, 0, 0};
+    parallel_for(M, 2, shrink_twin_row, &c);
+}
+
+static void shrink_dx_row(void* p, int64_t m) {
+    const lora_ctx* c = (const lora_ctx*)p;
+    const int64_t s = row_slot(c->slot, c->S, m);
+    if (s < 0) return;
+    double* g = (double*)calloc((size_t)c->K, sizeof(double));
+    for (int64_t j = 0; j < c->R; ++j) {
+        const double ct = c->cot[m * c->R + j];
+        if (ct == 0.0) continue;
+        for (int64_t k = 0; k < c->K; ++k) g[k] += ct * c->la[(s * c->R + j) * c->K + k];
+    }
+    for (int64_t k = 0; k < c->K; ++k) c->out[m * c->K + k] += g[k];
+    free(g);
+}
+
+static void shrink_da_pair(void* p, int64_t u) {
+    const lora_ctx* c = (const lora_ctx*)p;
+    const int64_t j = u / c->K, k = u % c->K;
+    for (int64_t m = 0; m < c->M; ++m) {
+        const int64_t s = row_slot(c->slot, c->S, m);
+        if (s < 0) continue;
+        const double ct = c->cot[m * c->R + j];
+        if (ct == 0.0) continue;
+        const int64_t row0 = c->fused ? s * c->R : 0;
+        c->grad[(row0 + j) * c->K + k] += (float)(ct * c->x[m * c->K + k]);
+    }
+}
+
+/* src/adjoint/host/lora.cpp:260-328 (float activation: no a_scale) */
+void orc_lora_shrink_adjoint(int64_t M, int64_t K, int64_t R, int64_t S, const double* x,
+                             const double* slot, const double* lora_a, const double* ct,
+                             double* dx, float* da, int fused) {
+    lora_ctx c = {M, K, 0, R, S, x, slot, lora_a, NULL, NULL, ct, NULL, dx, da, fused, 0};
+    parallel_for(M, 2, shrink_dx_row, &c);
+    if (da) parallel_for(R * K, 2, shrink_da_pair, &c);
+}
+
+double orc_rounded_bf16(double v) {
+    float f = (float)v;
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    memcpy(&f, &u, 4);
+    return (double)f;
+}
+
+static inline double expand_scale(const lora_ctx* c, int64_t s, int64_t n) {
+    return c->scale ? c->scale[s * c->N + n] : 1.0;
+}
+
+static void expand_twin_row(void* p, int64_t m) {
+    const lora_ctx* c = (const lora_ctx*)p;
+    const int64_t s = row_slot(c->slot, c->S, m);
+    if (s < 0) return;
+    for (int64_t n = 0; n < c->N; ++n) {
+        double acc = 0.0;
+        for (int64_t j = 0; j < c->R; ++j) {
+            const double tv = c->t[m * c->R + j];
+            acc += (c->round_t ? orc_rounded_bf16(tv) : tv) * c->lb[(s * c->N + n) * c->R + j];
+        }
+        c->out[m * c->N + n] += expand_scale(c, s, n) * acc;
+    }
+}
+
+/* src/adjoint/host/lora.cpp:416-441 */
+void orc_lora_expand_twin(int64_t M, int64_t N, int64_t R, int64_t S, const double* t,
+                          const double* slot, const double* lora_b, const double* scale,
+                          int round_t, double* y) {
+    lora_ctx c = {M, 0, N, R, S, NULL, slot, NULL, lora_b, scale, NULL, t, y, NULL, 0, round_t};
+    parallel_for(M, 2, expand_twin_row, &c);
+}
+
+static void expand_dt_row(void* p, int64_t m) {
+    const lora_ctx* c = (const lora_ctx*)p;
+    const int64_t s = row_slot(c->slot, c->S, m);
+    if (s < 0) return;
+    for (int64_t n = 0; n < c->N; ++n) {
+        const double cy = c->cot[m * c->N + n];
+        if (cy == 0.0) continue;
+        const double cs = cy * expand_scale(c, s, n);
+        const int64_t b0 = (s * c->N + n) * c->R;
+        for (int64_t j = 0; j < c->R; ++j) c->out[m * c->R + j] += cs * c->lb[b0 + j];
+    }
+}
+
+static void expand_db_pair(void* p, int64_t u) {
+    const lora_ctx* c = (const lora_ctx*)p;
+    const int64_t n = u / c->R, j = u % c->R;
+    const int64_t cols = c->fused ? c->S * c->R : c->R;
+    for (int64_t m = 0; m < c->M; ++m) {
+        const int64_t s = row_slot(c->slot, c->S, m);
+        if (s < 0) continue;
+        const double cy = c->cot[m * c->N + n];
+        if (cy == 0.0) continue;
+        const double cs = cy * expand_scale(c, s, n);
+        const int64_t col0 = c->fused ? s * c->R : 0;
+        c->grad[n * cols + col0 + j] += (float)(cs * c->t[m * c->R + j]);
+    }
+}
+
+/* src/adjoint/host/lora.cpp:451-521 */
+void orc_lora_expand_adjoint(int64_t M, int64_t N, int64_t R, int64_t S, const double* t,
+                             const double* slot, const double* lora_b, const double* scale,
+                             const double* cy, double* dt, float* db, int fused) {
+    lora_ctx c = {M, 0, N, R, S, NULL, slot, NULL, lora_b, scale, cy, t, dt, db, fused, 0};
+    parallel_for(M, 2, expand_dt_row, &c);
+    if (db) parallel_for(N * R, 2, expand_db_pair, &c);
+}

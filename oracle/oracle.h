@@ -1,0 +1,84 @@
+/* oracle/oracle.h -- CPU restatement of the reference's host path for the IQR linear + LoRA.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the product (r9700training_amd/) links, loads or calls
+ * this. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and only as
+ * the checker / the reported CPU baseline, never as the thing measured or shipped.
+ *
+ * Every function restates one reference function (file:line in its comment) in plain C with the
+ * reference's arithmetic: f64 accumulation in the reference's loop order, f32 accumulation of the
+ * dA / dB leaves per term, bf16 RNE with NaN quieting, the same tail-biting seam. Parity status of
+ * each function (what pins it) is listed in the header comment of oracle.c.
+ */
+#ifndef R97_ORACLE_H
+#define R97_ORACLE_H
+
+#include <stdint.h>
+
+#include "../include/r97q.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* threads the parallel loops use: R97_THREADS when set to an integer >= 1, else min(8, hw).
+ * (src/parallel.h:171-181) */
+int orc_thread_count(void);
+/* force a thread count (0 = back to the environment rule) */
+void orc_set_threads(int n);
+
+/* scalar formats (src/iqr_decode.h:118-188) */
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t b);
+float orc_f16_to_f32(uint16_t h);
+float orc_e4m3_to_f32(uint8_t b);
+
+/* the state's value (src/iqr_decode.h:205-212) */
+int32_t orc_state_value(const R97IqrDecodeDesc* d, uint32_t st);
+
+/* description rules, host decode, planes fold (src/iqr_decode.h:321-376, src/iqr_form.h:203-216) */
+int32_t orc_iqr_validate(const R97IqrDecodeDesc* d);
+int32_t orc_iqr_decode(const R97IqrDecodeDesc* d);
+/* out_scale[r*nkb+kb] = bf16(row[r] * factor[kb]) with one rounding */
+void orc_fold_scale_col(const float* row, const float* factor, int64_t rows, int64_t nkb,
+                        uint16_t* out_scale);
+
+/* gemm_nt twin over a stored weight (src/adjoint/host/linear.cpp:132-219):
+ * y[m,n] = sum_k x[m,k] * code[n,k] * bf16(scale[n,k/128]), f64. `rows` (optional, n_rows
+ * entries) restricts the twin to those rows m of x / y (y keeps its [M,N] shape). */
+void orc_gemm_nt_twin(int64_t M, int64_t N, int64_t K, const double* x, const int8_t* codes,
+                      const uint16_t* scale, double* y, const int64_t* rows, int64_t n_rows);
+/* gemm_nt adjoint (src/adjoint/host/linear.cpp:221-243): dx[m,k] += sum_n dy[m,n]*W(n,k) */
+void orc_gemm_nt_adjoint(int64_t M, int64_t N, int64_t K, const double* dy, const int8_t* codes,
+                         const uint16_t* scale, double* dx, const int64_t* rows, int64_t n_rows);
+
+/* float lora_shrink twin (src/adjoint/host/lora.cpp:197-244): t[m,j] = sum_k x[m,k]*A[s,j,k],
+ * s = slot[m] (a row outside [0,S) is a base row and is left untouched). */
+void orc_lora_shrink_twin(int64_t M, int64_t K, int64_t R, int64_t S, const double* x,
+                          const double* slot, const double* lora_a, double* t);
+/* float lora_shrink adjoint (src/adjoint/host/lora.cpp:260-328):
+ * dx[m,k] += sum_j ct[m,j]*A[s,j,k];  dA[(fused? s*R : 0)+j, k] += (float)(ct[m,j]*x[m,k]),
+ * f32 per term, rows serial. `da` may be NULL. */
+void orc_lora_shrink_adjoint(int64_t M, int64_t K, int64_t R, int64_t S, const double* x,
+                             const double* slot, const double* lora_a, const double* ct,
+                             double* dx, float* da, int fused);
+/* lora_expand twin (src/adjoint/host/lora.cpp:409-441):
+ * y[m,n] (+)= scale[s,n] * sum_j t[m,j]*B[s,n,j]; round_t rounds t to bf16 first (the _mm op);
+ * `scale` NULL reads 1.0. y holds the base value on entry (a zero buffer for a plain write). */
+void orc_lora_expand_twin(int64_t M, int64_t N, int64_t R, int64_t S, const double* t,
+                          const double* slot, const double* lora_b, const double* scale,
+                          int round_t, double* y);
+/* lora_expand adjoint (src/adjoint/host/lora.cpp:451-521):
+ * dt[m,j] += sum_n cy[m,n]*scale[s,n]*B[s,n,j];  dB[n, (fused? s*R:0)+j] += (float)(...),
+ * f32 per term. `db` may be NULL. */
+void orc_lora_expand_adjoint(int64_t M, int64_t N, int64_t R, int64_t S, const double* t,
+                             const double* slot, const double* lora_b, const double* scale,
+                             const double* cy, double* dt, float* db, int fused);
+
+/* bf16 rounding the _mm twin applies (src/adjoint/host/lora.cpp:127-135): no NaN quieting */
+double orc_rounded_bf16(double v);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,293 @@
+"""oracle/oracle.py -- ctypes front of the CPU checker (TEST INFRASTRUCTURE ONLY).
+
+Loads oracle/liboracle.so (this repo's C restatement of the reference host path) and, when it was
+built, oracle/_ref/libr97ref.so (the reference's own host rows). Only tests/, __graft_entry__.smoke()
+and bench.py's cpu_baseline leg import this module; the product never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libr97ref.so")
+
+
+class Desc(C.Structure):
+    """R97IqrDecodeDesc (include/r97q.h; the reference's src/iqr_decode.h:59-114), same layout."""
+
+    _fields_ = [
+        ("rows_all", C.c_int64), ("cols", C.c_int64), ("row0", C.c_int64), ("rows", C.c_int64),
+        ("bits", C.c_int32), ("state_bits", C.c_int32), ("run_rows", C.c_int32), ("rb", C.c_int32),
+        ("mad", C.c_int32), ("round_mad", C.c_int32), ("mad_a", C.c_uint32), ("mad_b", C.c_uint32),
+        ("lut", C.c_void_p),
+        ("codes", C.c_void_p), ("codes_row_bytes", C.c_int64),
+        ("scale", C.c_void_p), ("scale_dtype", C.c_int32), ("scale_block_cols", C.c_int64),
+        ("scale_row_bytes", C.c_int64),
+        ("affine", C.c_int32), ("zero", C.c_void_p), ("zero_bits", C.c_int32), ("zero_row_bytes", C.c_int64),
+        ("scale2", C.c_void_p), ("scale2_dtype", C.c_int32), ("scale2_row_bytes", C.c_int64),
+        ("scale2_block_rows", C.c_int64), ("scale2_block_cols", C.c_int64),
+        ("out_codes", C.c_void_p), ("out_scale", C.c_void_p),
+    ]
+
+
+_lib = None
+_ref = None
+_P = C.c_void_p
+_I = C.c_int64
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run make -C oracle)")
+        L = C.CDLL(LIB_PATH)
+        L.orc_f32_to_bf16.restype = C.c_uint16
+        L.orc_f32_to_bf16.argtypes = [C.c_float]
+        L.orc_bf16_to_f32.restype = C.c_float
+        L.orc_bf16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_e4m3_to_f32.restype = C.c_float
+        L.orc_e4m3_to_f32.argtypes = [C.c_uint8]
+        L.orc_state_value.restype = C.c_int32
+        L.orc_state_value.argtypes = [C.POINTER(Desc), C.c_uint32]
+        L.orc_iqr_validate.restype = C.c_int32
+        L.orc_iqr_validate.argtypes = [C.POINTER(Desc)]
+        L.orc_iqr_decode.restype = C.c_int32
+        L.orc_iqr_decode.argtypes = [C.POINTER(Desc)]
+        L.orc_fold_scale_col.argtypes = [_P, _P, _I, _I, _P]
+        L.orc_gemm_nt_twin.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P, _I]
+        L.orc_gemm_nt_adjoint.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P, _I]
+        L.orc_lora_shrink_twin.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P]
+        L.orc_lora_shrink_adjoint.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, C.c_int]
+        L.orc_lora_expand_twin.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, C.c_int, _P]
+        L.orc_lora_expand_adjoint.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, C.c_int]
+        L.orc_rounded_bf16.restype = C.c_double
+        L.orc_rounded_bf16.argtypes = [C.c_double]
+        L.orc_thread_count.restype = C.c_int
+        L.orc_set_threads.argtypes = [C.c_int]
+        _lib = L
+    return _lib
+
+
+def ref():
+    """The reference's own host rows, or None when oracle/_ref was not built."""
+    global _ref
+    if _ref is None and os.path.exists(REF_PATH):
+        R = C.CDLL(REF_PATH)
+        R.ref_last_error.restype = C.c_char_p
+        R.ref_iqr_validate.argtypes = [C.POINTER(Desc)]
+        R.ref_iqr_decode.argtypes = [C.POINTER(Desc)]
+        R.ref_gemm_nt_twin.argtypes = [_I, _I, _I, _P, _P, _P, _P]
+        R.ref_gemm_nt_adjoint.argtypes = [_I, _I, _I, _P, _P, _P, _P]
+        R.ref_lora_shrink_twin.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P]
+        R.ref_lora_shrink_adjoint.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, C.c_int]
+        R.ref_lora_expand_twin.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, C.c_int, _P]
+        R.ref_lora_expand_adjoint.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, C.c_int]
+        _ref = R
+    return _ref
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def thread_count() -> int:
+    return int(lib().orc_thread_count())
+
+
+# ------------------------------------------------------------------ decode
+def decode(desc: Desc, use_ref: bool = False):
+    """Decode `desc` (host planes) -> (int8 [rows, cols], uint16 bf16 bits [rows, cols/128]).
+
+    Returns None when the description is refused."""
+    rows, cols = int(desc.rows), int(desc.cols)
+    oc = np.zeros((rows, cols), np.int8)
+    os_ = np.zeros((rows, cols // 128), np.uint16)
+    d = Desc.from_buffer_copy(desc)
+    d.out_codes = oc.ctypes.data
+    d.out_scale = os_.ctypes.data
+    L = ref() if use_ref else lib()
+    fn = L.ref_iqr_decode if use_ref else L.orc_iqr_decode
+    rc = fn(C.byref(d))
+    if rc != 0:
+        return None
+    return oc, os_
+
+
+def validate(desc: Desc, use_ref: bool = False) -> int:
+    """The description rules; unset output pointers are given a placeholder (the rules require
+    both outputs, and this call writes nothing)."""
+    d = Desc.from_buffer_copy(desc)
+    one = np.zeros(1, np.int64)
+    if not d.out_codes:
+        d.out_codes = one.ctypes.data
+    if not d.out_scale:
+        d.out_scale = one.ctypes.data
+    return int((ref().ref_iqr_validate if use_ref else lib().orc_iqr_validate)(C.byref(d)))
+
+
+def fold_scale_col(row: np.ndarray, factor: np.ndarray) -> np.ndarray:
+    row = np.ascontiguousarray(row, np.float32)
+    factor = np.ascontiguousarray(factor, np.float32)
+    out = np.zeros((row.size, factor.size), np.uint16)
+    lib().orc_fold_scale_col(_ptr(row), _ptr(factor), row.size, factor.size, _ptr(out))
+    return out
+
+
+# ------------------------------------------------------------------ gemm_nt
+def _f64(a):
+    return np.ascontiguousarray(a, np.float64)
+
+
+def gemm_nt_twin(x, codes, scale, rows=None, use_ref=False):
+    x = _f64(x)
+    M, K = x.shape
+    N = codes.shape[0]
+    codes = np.ascontiguousarray(codes, np.int8)
+    scale = np.ascontiguousarray(scale, np.uint16)
+    y = np.zeros((M, N), np.float64)
+    if use_ref:
+        rc = ref().ref_gemm_nt_twin(M, N, K, _ptr(x), _ptr(codes), _ptr(scale), _ptr(y))
+        if rc:
+            raise RuntimeError(ref().ref_last_error().decode())
+        return y
+    r = None if rows is None else np.ascontiguousarray(rows, np.int64)
+    lib().orc_gemm_nt_twin(M, N, K, _ptr(x), _ptr(codes), _ptr(scale), _ptr(y), _ptr(r),
+                           0 if r is None else r.size)
+    return y
+
+
+def gemm_nt_adjoint(dy, codes, scale, dx=None, rows=None, use_ref=False):
+    dy = _f64(dy)
+    M, N = dy.shape
+    K = codes.shape[1]
+    codes = np.ascontiguousarray(codes, np.int8)
+    scale = np.ascontiguousarray(scale, np.uint16)
+    dx = np.zeros((M, K), np.float64) if dx is None else _f64(dx).copy()
+    if use_ref:
+        rc = ref().ref_gemm_nt_adjoint(M, N, K, _ptr(dy), _ptr(codes), _ptr(scale), _ptr(dx))
+        if rc:
+            raise RuntimeError(ref().ref_last_error().decode())
+        return dx
+    r = None if rows is None else np.ascontiguousarray(rows, np.int64)
+    lib().orc_gemm_nt_adjoint(M, N, K, _ptr(dy), _ptr(codes), _ptr(scale), _ptr(dx), _ptr(r),
+                              0 if r is None else r.size)
+    return dx
+
+
+# ------------------------------------------------------------------ LoRA
+def lora_shrink_twin(x, slot, lora_a, use_ref=False):
+    """x [M,K], slot [M], lora_a [S,R,K] -> t [M,R] (base rows left zero)."""
+    x, slot, la = _f64(x), _f64(slot), _f64(lora_a)
+    M, K = x.shape
+    S, R, _ = la.shape
+    t = np.zeros((M, R), np.float64)
+    if use_ref:
+        rc = ref().ref_lora_shrink_twin(M, K, R, S, _ptr(x), _ptr(slot), _ptr(la), _ptr(t))
+        if rc:
+            raise RuntimeError(ref().ref_last_error().decode())
+        return t
+    lib().orc_lora_shrink_twin(M, K, R, S, _ptr(x), _ptr(slot), _ptr(la), _ptr(t))
+    return t
+
+
+def lora_shrink_adjoint(x, slot, lora_a, ct, dx=None, da=None, fused=False, use_ref=False):
+    x, slot, la, ct = _f64(x), _f64(slot), _f64(lora_a), _f64(ct)
+    M, K = x.shape
+    S, R, _ = la.shape
+    dx = np.zeros((M, K), np.float64) if dx is None else _f64(dx).copy()
+    rows = S * R if fused else R
+    da = np.zeros((rows, K), np.float32) if da is None else np.ascontiguousarray(da, np.float32).copy()
+    if use_ref:
+        rc = ref().ref_lora_shrink_adjoint(M, K, R, S, _ptr(x), _ptr(slot), _ptr(la), _ptr(ct),
+                                           _ptr(dx), _ptr(da), int(fused))
+        if rc:
+            raise RuntimeError(ref().ref_last_error().decode())
+        return dx, da
+    lib().orc_lora_shrink_adjoint(M, K, R, S, _ptr(x), _ptr(slot), _ptr(la), _ptr(ct), _ptr(dx),
+                                  _ptr(da), int(fused))
+    return dx, da
+
+
+def lora_expand_twin(t, slot, lora_b, scale, y=None, mm=False, use_ref=False):
+    """t [M,R], slot [M], lora_b [S,N,R], scale [S,N] -> y [M,N] (+= onto y when given)."""
+    t, slot, lb = _f64(t), _f64(slot), _f64(lora_b)
+    sc = None if scale is None else _f64(scale)
+    M, R = t.shape
+    S, N, _ = lb.shape
+    out = np.zeros((M, N), np.float64) if y is None else _f64(y).copy()
+    if use_ref:
+        if y is not None or sc is None:
+            raise ValueError("the reference driver serves the 5-operand plain-write record only")
+        rc = ref().ref_lora_expand_twin(M, N, R, S, _ptr(t), _ptr(slot), _ptr(lb), _ptr(sc),
+                                        int(mm), _ptr(out))
+        if rc:
+            raise RuntimeError(ref().ref_last_error().decode())
+        return out
+    lib().orc_lora_expand_twin(M, N, R, S, _ptr(t), _ptr(slot), _ptr(lb), _ptr(sc), int(mm), _ptr(out))
+    return out
+
+
+def lora_expand_adjoint(t, slot, lora_b, scale, cy, dt=None, db=None, fused=False, use_ref=False):
+    t, slot, lb, cy = _f64(t), _f64(slot), _f64(lora_b), _f64(cy)
+    sc = None if scale is None else _f64(scale)
+    M, R = t.shape
+    S, N, _ = lb.shape
+    dt = np.zeros((M, R), np.float64) if dt is None else _f64(dt).copy()
+    cols = S * R if fused else R
+    db = np.zeros((N, cols), np.float32) if db is None else np.ascontiguousarray(db, np.float32).copy()
+    if use_ref:
+        rc = ref().ref_lora_expand_adjoint(M, N, R, S, _ptr(t), _ptr(slot), _ptr(lb), _ptr(sc),
+                                           _ptr(cy), _ptr(dt), _ptr(db), int(fused))
+        if rc:
+            raise RuntimeError(ref().ref_last_error().decode())
+        return dt, db
+    lib().orc_lora_expand_adjoint(M, N, R, S, _ptr(t), _ptr(slot), _ptr(lb), _ptr(sc), _ptr(cy),
+                                  _ptr(dt), _ptr(db), int(fused))
+    return dt, db
+
+
+# ------------------------------------------------------------------ the whole path
+def qlinear_lora_reference(x, codes, scale, A, B, s, dy, rows=None):
+    """The host path of one adapted linear, composed the way the walk composes its three records
+    (src/backward.cpp:556-737, reverse order expand -> shrink -> gemm_nt), single adapter, all rows
+    on slot 0. Returns dict(y, t, dx, dA, dB) in f64 (dA, dB f32 leaves).
+
+    `rows` (optional) restricts the row-local outputs (y, t, dx) to those token rows; dA and dB
+    need every row and are then None."""
+    x = _f64(x)
+    M, K = x.shape
+    N = codes.shape[0]
+    R = A.shape[0]
+    slot = np.zeros(M, np.float64)
+    scale_n = np.full((1, N), float(s), np.float64)
+    la = _f64(A).reshape(1, R, K)
+    lb = _f64(B).reshape(1, N, R)
+    if rows is not None:
+        rows = np.asarray(rows, np.int64)
+        xs, dys = x[rows], _f64(dy)[rows]
+        sl = np.zeros(rows.size, np.float64)
+        y = gemm_nt_twin(xs, codes, scale)
+        t = lora_shrink_twin(xs, sl, la)
+        y = lora_expand_twin(t, sl, lb, scale_n, y=y)
+        dt, _ = lora_expand_adjoint(t, sl, lb, scale_n, dys, db=None)
+        dx, _ = lora_shrink_adjoint(xs, sl, la, dt)
+        dx = gemm_nt_adjoint(dys, codes, scale, dx=dx)
+        return dict(y=y, t=t, dx=dx, dA=None, dB=None)
+    y = gemm_nt_twin(x, codes, scale)
+    t = lora_shrink_twin(x, slot, la)
+    y = lora_expand_twin(t, slot, lb, scale_n, y=y)
+    dt, dB = lora_expand_adjoint(t, slot, lb, scale_n, dy)
+    dx, dA = lora_shrink_adjoint(x, slot, la, dt)
+    dx = gemm_nt_adjoint(dy, codes, scale, dx=dx)
+    return dict(y=y, t=t, dx=dx, dA=dA, dB=dB)

@@ -1,0 +1,253 @@
+// oracle/ref_driver.cpp -- a C ABI over the reference's own host rows, for golden vectors.
+//
+// TEST INFRASTRUCTURE ONLY. Built by oracle/Makefile together with the reference's sources where
+// they lie under /root/reference (nothing is copied) into oracle/_ref/libr97ref.so, which only
+// tests/golden/make_golden.py, the oracle's tests and bench.py's cpu_baseline leg load.
+//
+// Each entry builds the OpRecord the reference's own tests build (tests/host/adjoint_linear.cpp:
+// 96-106, tests/host/adjoint_lora.cpp:90-121), looks the row up through the reference registry
+// (twin_find / adjoint_find, src/adjoint_registry.cpp:99-113) and calls it. A stored IQR weight
+// reaches the rows the way the join hands it: a StoredWeight put under an encoding pointer
+// (src/stored_weight.h:35-47) and an operand with `raw`/`enc` set and no values.
+#include "r97/adjoint.h"
+
+#include "iqr_decode.h"
+#include "stored_weight.h"
+
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+using namespace r97;
+
+namespace {
+
+const int kEncToken = 0;  // the encoding pointer the stored weight is keyed by
+
+AdValue values(const char* dtype, std::vector<int64_t> shape, const double* v) {
+    AdValue a;
+    a.dtype = dtype;
+    a.shape = std::move(shape);
+    int64_t n = 1;
+    for (int64_t d : a.shape) n *= d;
+    if (v) a.value.assign(v, v + n);
+    else a.value.assign((size_t)n, 0.0);
+    return a;
+}
+
+OpRecord gemm_nt_rec(int64_t M, int64_t N, int64_t K) {
+    OpRecord rec;
+    rec.op = "gemm_nt";
+    rec.params = {{"M", M}, {"N", N}, {"K", K}, {"dtype", "bf16"}};
+    rec.operands = {
+        {"a", "bf16", {M, K}, 0, M, false},
+        {"b", "bf16", {N, K}, 0, N, false},
+        {"y", "f32", {M, N}, 0, M, true},
+    };
+    return rec;
+}
+
+void put_weight(int64_t N, int64_t K, const int8_t* codes, const uint16_t* scale) {
+    StoredWeight w;
+    w.rows = N;
+    w.cols = K;
+    w.groups = K / 128;
+    w.codes.assign(codes, codes + N * K);
+    w.scale.assign(scale, scale + N * (K / 128));
+    stored_weight_put(&kEncToken, std::move(w));
+}
+
+AdValue stored_operand(int64_t N, int64_t K) {
+    AdValue b;
+    b.dtype = "bf16";
+    b.shape = {N, K};
+    b.raw = &kEncToken;
+    b.enc = &kEncToken;
+    return b;
+}
+
+OpRecord shrink_rec(int64_t M, int64_t K, int64_t R, int64_t S) {
+    OpRecord rec;
+    rec.op = "lora_shrink";
+    rec.params = {{"M", M}, {"K", K}, {"R", R}, {"S", S}, {"group", 0}, {"dtype", "bf16"}};
+    rec.operands = {{"a", "bf16", {M, K}, 0, M, false},
+                    {"a_scale", "invalid", {}, 0, 0, false},
+                    {"slot", "i32", {M}, 0, M, false},
+                    {"lora_a", "bf16", {S, R, K}, 0, S, false},
+                    {"t", "f32", {M, R}, 0, M, true}};
+    return rec;
+}
+
+OpRecord expand_rec(int64_t M, int64_t N, int64_t R, int64_t S, bool mm) {
+    OpRecord rec;
+    rec.op = mm ? "lora_expand_mm" : "lora_expand";
+    rec.params = {{"M", M}, {"N", N}, {"R", R}, {"S", S}, {"dtype", "bf16"}};
+    rec.operands = {{"t", "f32", {M, R}, 0, M, false},
+                    {"slot", "i32", {M}, 0, M, false},
+                    {"lora_b", "bf16", {S, N, R}, 0, S, false},
+                    {"scale", "f32", {S, N}, 0, S, false},
+                    {"y", "bf16", {M, N}, 0, M, true}};
+    return rec;
+}
+
+thread_local std::string g_err;
+
+}  // namespace
+
+extern "C" {
+
+const char* ref_last_error() { return g_err.c_str(); }
+
+int ref_iqr_validate(const R97IqrDecodeDesc* d) { return r97_iqr_validate(*d); }
+int ref_iqr_decode(const R97IqrDecodeDesc* d) { return r97_iqr_decode_host(*d); }
+
+int ref_gemm_nt_twin(int64_t M, int64_t N, int64_t K, const double* x, const int8_t* codes,
+                     const uint16_t* scale, double* y) {
+    try {
+        put_weight(N, K, codes, scale);
+        OpRecord rec = gemm_nt_rec(M, N, K);
+        std::vector<AdValue> reads = {values("bf16", {M, K}, x), stored_operand(N, K)};
+        std::vector<AdValue> out;
+        TwinFn fn = twin_find(rec.op, rec.params, &g_err);
+        if (!fn) return 1;
+        fn(rec, reads, &out);
+        stored_weight_clear();
+        if (out.size() != 1 || (int64_t)out[0].value.size() != M * N) return 2;
+        std::memcpy(y, out[0].value.data(), sizeof(double) * (size_t)(M * N));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+int ref_gemm_nt_adjoint(int64_t M, int64_t N, int64_t K, const double* dy, const int8_t* codes,
+                        const uint16_t* scale, double* dx) {
+    try {
+        put_weight(N, K, codes, scale);
+        OpRecord rec = gemm_nt_rec(M, N, K);
+        std::vector<AdValue> fwd = {values("bf16", {M, K}, nullptr), stored_operand(N, K),
+                                    values("f32", {M, N}, nullptr)};
+        std::vector<AdValue> cot = {values("f32", {M, N}, dy)};
+        std::vector<AdValue> dc = {values("bf16", {M, K}, dx), AdValue{}, AdValue{}};
+        AdjointFn fn = adjoint_find(rec.op, Side::host, rec.params, &g_err);
+        if (!fn) return 1;
+        AdjointCall call{rec, fwd, cot, &dc, nullptr, ""};
+        fn(call);
+        stored_weight_clear();
+        std::memcpy(dx, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+int ref_lora_shrink_twin(int64_t M, int64_t K, int64_t R, int64_t S, const double* x,
+                         const double* slot, const double* la, double* t) {
+    try {
+        OpRecord rec = shrink_rec(M, K, R, S);
+        AdValue absent;
+        absent.dtype = "invalid";
+        std::vector<AdValue> reads = {values("bf16", {M, K}, x), absent, values("i32", {M}, slot),
+                                      values("bf16", {S, R, K}, la)};
+        std::vector<AdValue> out;
+        TwinFn fn = twin_find(rec.op, rec.params, &g_err);
+        if (!fn) return 1;
+        fn(rec, reads, &out);
+        if (out.size() != 1) return 2;
+        std::memcpy(t, out[0].value.data(), sizeof(double) * (size_t)(M * R));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+int ref_lora_shrink_adjoint(int64_t M, int64_t K, int64_t R, int64_t S, const double* x,
+                            const double* slot, const double* la, const double* ct, double* dx,
+                            float* da, int fused) {
+    try {
+        OpRecord rec = shrink_rec(M, K, R, S);
+        AdValue absent;
+        absent.dtype = "invalid";
+        std::vector<AdValue> fwd = {values("bf16", {M, K}, x), absent, values("i32", {M}, slot),
+                                    values("bf16", {S, R, K}, la), values("f32", {M, R}, nullptr)};
+        std::vector<AdValue> cot = {values("f32", {M, R}, ct)};
+        std::vector<AdValue> dc = {values("bf16", {M, K}, dx), AdValue{}, AdValue{}, AdValue{},
+                                   AdValue{}};
+        ParamSet grads;
+        Param p;
+        p.name = "site.lora_A";
+        p.shape = fused ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
+        const int64_t na = (fused ? S * R : R) * K;
+        p.value.assign(da, da + na);
+        grads.push_back(std::move(p));
+        AdjointFn fn = adjoint_find(rec.op, Side::host, rec.params, &g_err);
+        if (!fn) return 1;
+        AdjointCall call{rec, fwd, cot, &dc, &grads, "site"};
+        call.fused_slots = fused != 0;
+        fn(call);
+        std::memcpy(dx, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
+        std::memcpy(da, grads[0].value.data(), sizeof(float) * (size_t)na);
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+int ref_lora_expand_twin(int64_t M, int64_t N, int64_t R, int64_t S, const double* t,
+                         const double* slot, const double* lb, const double* scale, int mm,
+                         double* y) {
+    try {
+        OpRecord rec = expand_rec(M, N, R, S, mm != 0);
+        std::vector<AdValue> reads = {values("f32", {M, R}, t), values("i32", {M}, slot),
+                                      values("bf16", {S, N, R}, lb), values("f32", {S, N}, scale)};
+        std::vector<AdValue> out;
+        TwinFn fn = twin_find(rec.op, rec.params, &g_err);
+        if (!fn) return 1;
+        fn(rec, reads, &out);
+        if (out.size() != 1) return 2;
+        std::memcpy(y, out[0].value.data(), sizeof(double) * (size_t)(M * N));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+int ref_lora_expand_adjoint(int64_t M, int64_t N, int64_t R, int64_t S, const double* t,
+                            const double* slot, const double* lb, const double* scale,
+                            const double* cy, double* dt, float* db, int fused) {
+    try {
+        OpRecord rec = expand_rec(M, N, R, S, false);
+        std::vector<AdValue> fwd = {values("f32", {M, R}, t), values("i32", {M}, slot),
+                                    values("bf16", {S, N, R}, lb), values("f32", {S, N}, scale),
+                                    values("bf16", {M, N}, nullptr)};
+        std::vector<AdValue> cot = {values("bf16", {M, N}, cy)};
+        std::vector<AdValue> dc = {values("f32", {M, R}, dt), AdValue{}, AdValue{}, AdValue{},
+                                   AdValue{}};
+        ParamSet grads;
+        Param p;
+        p.name = "site.lora_B";
+        p.shape = fused ? std::vector<int64_t>{N, S * R} : std::vector<int64_t>{N, R};
+        const int64_t nb = N * (fused ? S * R : R);
+        p.value.assign(db, db + nb);
+        grads.push_back(std::move(p));
+        AdjointFn fn = adjoint_find(rec.op, Side::host, rec.params, &g_err);
+        if (!fn) return 1;
+        AdjointCall call{rec, fwd, cot, &dc, &grads, "site"};
+        call.fused_slots = fused != 0;
+        fn(call);
+        std::memcpy(dt, dc[0].value.data(), sizeof(double) * (size_t)(M * R));
+        std::memcpy(db, grads[0].value.data(), sizeof(float) * (size_t)nb);
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+}  // extern "C"
