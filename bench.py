@@ -1,0 +1,268 @@
+#!/usr/bin/env python3
+"""bench.py -- the fused IQR-linear + LoRA forward+backward on one MI355X.
+
+One step = one forward and one backward of the adapted linear on one batch of synthetic input:
+  forward   t = X.A^T, Y = X.W^T + s.t.B^T                 (r97q_lora_fwd_prep, r97q_qlinear_fwd_base)
+  backward  dt = s.dY.B, dA += dt^T.X, dB += s.dY^T.t,
+            dX = dY.W + dt.A                               (r97q_lora_bwd_prep, _grads, r97q_qlinear_dx_base)
+W is an IQR trunk-form weight (b5 trellis.mad, L 16, 256-row runs, f32 row scale + scale.col)
+quantized from W ~ N(0, 0.02) by this repo's quantizer; X, dY bf16 N(0,1); A, B bf16 N(0, 0.01).
+Default workload: BASELINE.json configs[1] (C2: 4096 x 4096, T 4096, rank 16, alpha 32).
+
+Prints ONE JSON line (rank 0): the step's whole-job TFLOP/s, the dominant kernel's roofline
+(HIP events around its launches inside the timed region) and a CPU baseline (the reference's own
+host rows, oracle/_ref, on the box's host cores, over a bounded row sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+CONFIGS = {
+    # name: (T, N, K, rank, alpha)
+    "c1": (128, 1024, 1024, 8, 16.0),
+    "c2": (4096, 4096, 4096, 16, 32.0),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--out-dtype", default="f32", choices=["f32", "bf16"],
+                    help="Y and dX dtype (f32: the parity contract's single rounding)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="target CPU work for the cpu_baseline sample (0 = skip)")
+    ap.add_argument("--seed", type=int, default=2001)
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="run only a plain device copy of this many MiB (3 launches), the known-size "
+                         "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
+    return ap.parse_args()
+
+
+def flops(T, N, K, r):
+    """Algorithmic FLOPs of one fwd+bwd (the base weight is frozen: no dW)."""
+    return 4 * T * N * K + 6 * T * r * (K + N)
+
+
+def make_inputs(T, N, K, r, seed, device):
+    import numpy as np
+    import torch
+
+    from r9700training_amd.qlinear import QWeight, device_desc
+    from r9700training_amd.quantize import quantize_trellis
+
+    rng = np.random.default_rng(seed)
+    W = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+    q = quantize_trellis(W, bits=5, state_bits=16, run_rows=256)
+    codes = torch.from_numpy(q["codes"]).to(device)
+    scale = torch.from_numpy(q["row_scale"].view(np.uint8).reshape(N, 4).copy()).to(device)
+    col = torch.from_numpy(q["col_factor"]).to(device)
+    d = device_desc(dict(codes=codes, scale=scale), N, K, dict(
+        bits=5, state_bits=16, run_rows=256, rb=1, mad=1, round_mad=1, mad_a=q["mad_a"], mad_b=q["mad_b"],
+        codes_row_bytes=q["codes"].shape[1], scale_dtype=0, scale_block_cols=0, scale_row_bytes=4))
+    w = QWeight(d, scale_col=col)
+    g = torch.Generator(device="cpu").manual_seed(seed + 1)
+    X = torch.randn((T, K), generator=g).to(torch.bfloat16).to(device)
+    dY = torch.randn((T, N), generator=g).to(torch.bfloat16).to(device)
+    A = (0.01 * torch.randn((r, K), generator=g)).to(torch.bfloat16).to(device)
+    B = (0.01 * torch.randn((N, r), generator=g)).to(torch.bfloat16).to(device)
+    return dict(w=w, q=q, X=X, dY=dY, A=A, B=B, keep=(codes, scale, col))
+
+
+def cpu_baseline(inp, T, N, K, r, s, target_s):
+    """The reference's own host path (oracle/_ref: its r97_iqr_decode_host, gemm_nt twin and
+    adjoint, float lora_shrink / lora_expand twins and adjoints, f64 with its parallel_for) on a
+    row sample of the same workload, extrapolated linearly in tokens to the whole step."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    use_ref = O.ref() is not None
+    nthreads = min(8, os.cpu_count() or 1)
+    os.environ["R97_THREADS"] = str(nthreads)
+    O.set_threads(nthreads)
+    q = inp["q"]
+    # the decode (once): the stored planes to the int8 grid + folded scale
+    import ctypes as C
+    from oracle.oracle import Desc
+
+    codes_p = np.ascontiguousarray(q["codes"])
+    rs = np.ascontiguousarray(q["row_scale"])
+    d = Desc()
+    d.rows_all, d.cols, d.row0, d.rows = N, K, 0, N
+    d.bits, d.state_bits, d.run_rows, d.rb, d.mad, d.round_mad = 5, 16, 256, 1, 1, 1
+    d.mad_a, d.mad_b = q["mad_a"], q["mad_b"]
+    d.codes, d.codes_row_bytes = codes_p.ctypes.data, codes_p.shape[1]
+    d.scale, d.scale_dtype, d.scale_block_cols, d.scale_row_bytes = rs.ctypes.data, 0, 0, 4
+    t0 = time.perf_counter()
+    codes, _ = O.decode(d, use_ref=use_ref)
+    scale = O.fold_scale_col(rs, q["col_factor"])
+    t_decode = time.perf_counter() - t0
+
+    X = inp["X"].float().cpu().numpy().astype(np.float64)
+    dY = inp["dY"].float().cpu().numpy().astype(np.float64)
+    A = inp["A"].float().cpu().numpy().astype(np.float64)
+    B = inp["B"].float().cpu().numpy().astype(np.float64)
+
+    def path(rows):
+        x, dy = X[rows], dY[rows]
+        M = len(rows)
+        slot = np.zeros(M)
+        sc = np.full((1, N), s)
+        O.gemm_nt_twin(x, codes, scale, use_ref=use_ref)
+        t = O.lora_shrink_twin(x, slot, A.reshape(1, r, K), use_ref=use_ref)
+        O.lora_expand_twin(t, slot, B.reshape(1, N, r), sc, use_ref=use_ref)
+        dt, _ = O.lora_expand_adjoint(t, slot, B.reshape(1, N, r), sc, dy, use_ref=use_ref)
+        O.lora_shrink_adjoint(x, slot, A.reshape(1, r, K), dt, use_ref=use_ref)
+        O.gemm_nt_adjoint(dy, codes, scale, use_ref=use_ref)
+
+    probe = list(range(min(T, 2 * nthreads)))
+    t0 = time.perf_counter()
+    path(probe)
+    per_row = (time.perf_counter() - t0) / len(probe)
+    n = int(max(len(probe), min(T, target_s / max(per_row, 1e-9))))
+    n = max(2 * nthreads, (n // (2 * nthreads)) * (2 * nthreads))
+    rows = np.linspace(0, T - 1, n).astype(np.int64)
+    t0 = time.perf_counter()
+    path(rows)
+    t_rows = time.perf_counter() - t0
+    step_s = t_decode + t_rows * (T / n)
+    return {
+        "value": round(flops(T, N, K, r) / step_s / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": nthreads,
+        "kind": "reference" if use_ref else "port",
+        "sample": f"{n} of {T} token rows (evenly spaced) through decode + gemm_nt twin/adjoint + "
+                  f"lora shrink/expand twins/adjoints, f64, {nthreads} threads; extrapolated "
+                  f"linearly in tokens ({t_rows:.1f} s sampled + {t_decode:.2f} s decode; "
+                  f"{step_s:.1f} s per full step; nproc {os.cpu_count()})",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import ctypes as C
+
+    import torch
+
+    if args.calibrate_copy_mib > 0:
+        n = args.calibrate_copy_mib << 18  # int32 elements
+        src = torch.ones(n, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_mib": args.calibrate_copy_mib, "launches": 3}), flush=True)
+        return
+
+    from r9700training_amd import R97Q_BF16, R97Q_F32, _ptr, _stream, check, lib
+    from r9700training_amd.qlinear import bwd_workspace, fwd_workspace
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    T, N, K, r, alpha = CONFIGS[args.config]
+    s = alpha / r
+    inp = make_inputs(T, N, K, r, args.seed, dev)
+    w = inp["w"]
+    out_dt = torch.float32 if args.out_dtype == "f32" else torch.bfloat16
+    code = R97Q_F32 if args.out_dtype == "f32" else R97Q_BF16
+    Y = torch.empty((T, N), dtype=out_dt, device=dev)
+    dX = torch.empty((T, K), dtype=out_dt, device=dev)
+    t = torch.empty((T, r), dtype=torch.float32, device=dev)
+    dA = torch.zeros((r, K), dtype=torch.float32, device=dev)
+    dB = torch.zeros((N, r), dtype=torch.float32, device=dev)
+    wsf = fwd_workspace(T, N, K, r, dev)
+    wsb = bwd_workspace(T, N, K, r, dev)
+    L = lib()
+    stream = torch.cuda.current_stream()
+    st = _stream(stream)
+    P = lambda x: _ptr(x)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+
+    def step(e=None):
+        check(L.r97q_lora_fwd_prep(T, N, K, P(inp["X"]), P(inp["A"]), r, s, P(t), P(wsf), wsf.numel(), st), "fwd_prep")
+        if e: e[0].record(stream)
+        check(L.r97q_qlinear_fwd_base(C.byref(w.w), P(inp["X"]), T, P(inp["B"]), r, P(Y), code, P(wsf),
+                                      wsf.numel(), st), "fwd_base")
+        if e: e[1].record(stream)
+        check(L.r97q_lora_bwd_prep(T, N, K, P(inp["dY"]), P(inp["A"]), P(inp["B"]), P(t), r, s, P(wsb),
+                                   wsb.numel(), st), "bwd_prep")
+        check(L.r97q_lora_bwd_grads(T, N, K, P(inp["X"]), P(inp["dY"]), r, P(dA), P(dB), P(wsb), wsb.numel(), st),
+              "bwd_grads")
+        if e: e[2].record(stream)
+        check(L.r97q_qlinear_dx_base(C.byref(w.w), P(inp["dY"]), T, r, P(dX), code, 0, P(wsb), wsb.numel(), st),
+              "dx_base")
+        if e: e[3].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(ev[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed * 1e3 / args.steps
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    dx_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    total_flops = flops(T, N, K, r)
+    value = total_flops / (ms_step * 1e-3) / 1e12
+    # the dominant kernel and its algorithmic work per launch
+    kern = {"qlinear_fwd_kernel": (fwd_ms, 2 * T * N * K + 2 * T * N * r),
+            "qlinear_dx_kernel": (dx_ms, 2 * T * N * K + 2 * T * K * r)}
+    name = max(kern, key=lambda k: kern[k][0])
+    kms, kfl = kern[name]
+    achieved = kfl / (kms * 1e-3) / 1e12
+    packed_bytes = N * K * 5 // 8
+    line = {
+        "metric": "qlinear+LoRA fwd+bwd TFLOP/s, % MFMA/HBM roofline; LoRA-step tokens/s",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: W ~ N(0,0.02) quantized by this repo's trellis quantizer; X, dY ~ N(0,1) bf16; "
+                "A, B ~ N(0,0.01) bf16",
+        "config": {"workload": f"{args.config.upper()}: IQR linear {N}x{K} (b5 trellis.mad L16, 256-row runs, "
+                               f"f32 row scale + scale.col) + LoRA r{r} alpha {alpha:g}, T={T}, fwd+bwd, "
+                               f"Y/dX {args.out_dtype}",
+                   "T": T, "N": N, "K": K, "rank": r, "alpha": alpha, "out_dtype": args.out_dtype},
+        "tokens_per_s": round(T / (ms_step * 1e-3), 1),
+        "flops_per_step": total_flops,
+        "kernels_ms": {"qlinear_fwd_kernel": round(fwd_ms, 4), "qlinear_dx_kernel": round(dx_ms, 4),
+                       "other": round(ms_step - fwd_ms - dx_ms, 4)},
+        "roofline": {"bound": "mfma", "kernel": name, "achieved": round(achieved, 3),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None,
+                     "packed_weight_GBs": round(packed_bytes / (kms * 1e-3) / 1e9, 2)},
+        "quantizer_rel_err": round(inp["q"]["rel_err"], 4),
+    }
+    if args.cpu_seconds > 0:
+        line["cpu_baseline"] = cpu_baseline(inp, T, N, K, r, s, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

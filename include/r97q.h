@@ -108,13 +108,15 @@ int r97_iqr_decode(const R97IqrDecodeDesc* desc, R97IqrStream stream);
  *             descending row order, packed LSB first, so that the trellis state of row n is the
  *             `state_bits`-wide bit window that starts at row n's code. Grouped in 32-row
  *             segments of `bits` dwords; dword d of a segment is stored for 4 consecutive columns
- *             together (one 128-bit load), see the layout in csrc/iqr_layout.h. Same size as
- *             the canonical codes plane: no halo is stored.
+ *             together (one 128-bit load); r9700training_amd/csrc/iqr_device.h states the
+ *             layout. Same size as the canonical codes plane: no halo is stored.
  *   scale_t : the effective bf16 scale of every (row, 128-column block), transposed to
  *             [cols/128][rows]: the block scale with scale.1 settled (src/iqr_decode.h:223-235) and
  *             the optional scale.col factor folded in with one rounding (src/iqr_form.h:203-216).
- * The fused path serves trellis forms with rb = 1 (computed `mad` or stored `lut` codebook, any
- * scale dtype, optional scale.1 / scale.col), cols % 128 == 0, rows % 32 == 0 and run_rows % 32 == 0. */
+ * The fused path serves trellis forms with rb = 1, the computed `trellis.mad` codebook, bits 3..6,
+ * state_bits 16, any scale dtype with optional scale.1 / scale.col, cols % 128 == 0,
+ * rows % 32 == 0 and run_rows % 32 == 0; other forms are refused with R97Q_EUNSUPPORTED (the
+ * standalone r97_iqr_decode serves every form). */
 typedef struct R97qWeight {
     int64_t rows;          /* N */
     int64_t cols;          /* K */
@@ -174,6 +176,57 @@ int r97q_qlinear_lora_bwd(const R97qWeight* w, const uint16_t* X, const uint16_t
                           const float* t, void* dX, int32_t dx_dtype, int32_t dx_accumulate,
                           float* dA, float* dB, void* workspace, int64_t workspace_bytes,
                           R97IqrStream stream);
+
+/* ------------------------------------------------------------------ the quantizer
+ *
+ * Quantize W [N, K] (HOST f32, row-major) to the trunk IQR form: trellis.mad codes of `bits` with
+ * a `state_bits` state over tail-biting runs of `run_rows`, one f32 scale a row and one f32
+ * scale.col factor a 128-column block. Outputs are host buffers: codes [N, ceil(K*bits/8)] packed
+ * LSB first, row_scale [N], col_factor [K/128]; rel_err (optional) receives the decoded weight's
+ * relative RMS error. threads <= 0 uses every hardware thread. The reference's quantizer
+ * (radiance's libquant, absent from the reference tree) has no counterpart here to match: the
+ * output is a valid stored weight of the reference's format (src/iqr_decode.h), and its error is
+ * reported, not matched. */
+int r97q_iqr_encode_trellis(const float* W, int64_t N, int64_t K, int32_t bits, int32_t state_bits,
+                            int32_t run_rows, uint32_t mad_a, uint32_t mad_b, uint8_t* codes,
+                            float* row_scale, float* col_factor, int32_t threads, double* rel_err);
+
+/* ------------------------------------------------------------------ the stages
+ *
+ * The two calls above are these stages in order on one stream; a caller may issue them itself
+ * (to time, overlap or reorder them). The workspace carries the adapter's activations between the
+ * stages of one direction, so every stage of a direction gets the same workspace. Each is the part
+ * of the reference rows named beside it.
+ *
+ * Forward: t = X.A^T (f32 into t_out) and the adapter operand of the fused kernel
+ *          (lora_shrink_twin, src/adjoint/host/lora.cpp:226-244). rank 0: a no-op. */
+int r97q_lora_fwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* X, const uint16_t* A,
+                       int32_t rank, float scale, float* t_out, void* workspace,
+                       int64_t workspace_bytes, R97IqrStream stream);
+/* Forward: the fused decode + MFMA kernel, Y = X.W^T (+ scale.t.B^T read from the workspace)
+ * (gemm_nt_twin + lora_expand_twin, src/adjoint/host/linear.cpp:193-219, lora.cpp:416-441). */
+int r97q_qlinear_fwd_base(const R97qWeight* w, const uint16_t* X, int64_t T, const uint16_t* B,
+                          int32_t rank, void* Y, int32_t y_dtype, void* workspace,
+                          int64_t workspace_bytes, R97IqrStream stream);
+/* Backward: dt = scale.dY.B (in the workspace, as the adapter operands of the fused dX kernel and of
+ * dA) (lora_expand_host_adjoint's dt, src/adjoint/host/lora.cpp:495-506), and, when t is given,
+ * scale.t as dB's operand. rank 0: a no-op. */
+int r97q_lora_bwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* dY, const uint16_t* A,
+                       const uint16_t* B, const float* t, int32_t rank, float scale, void* workspace,
+                       int64_t workspace_bytes, R97IqrStream stream);
+/* Backward: dA += dt^T.X and dB += scale.dY^T.t (the leaves of lora_shrink_host_adjoint and
+ * lora_expand_host_adjoint, src/adjoint/host/lora.cpp:316-327, 507-520), after r97q_lora_bwd_prep
+ * on the same workspace (dB needs that prep to have had t). Either output may be NULL. The sums
+ * over token chunks are combined with f32 atomic adds, so their order (and the last bits of a
+ * gradient) may differ from call to call. */
+int r97q_lora_bwd_grads(int64_t T, int64_t N, int64_t K, const uint16_t* X, const uint16_t* dY,
+                        int32_t rank, float* dA, float* dB, void* workspace, int64_t workspace_bytes,
+                        R97IqrStream stream);
+/* Backward: the fused decode + MFMA dX kernel, dX = dY.W (+ dt.A from the workspace)
+ * (gemm_nt_adjoint + the shrink's dx, src/adjoint/host/linear.cpp:221-243, lora.cpp:295-315). */
+int r97q_qlinear_dx_base(const R97qWeight* w, const uint16_t* dY, int64_t T, int32_t rank, void* dX,
+                         int32_t dx_dtype, int32_t dx_accumulate, void* workspace,
+                         int64_t workspace_bytes, R97IqrStream stream);
 
 #ifdef __cplusplus
 }

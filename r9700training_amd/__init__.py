@@ -1,0 +1,111 @@
+"""r9700training_amd -- MI355X (gfx950) IQR-quantized linear + LoRA, forward and backward.
+
+A thin Python front over libr97q.so's C ABI (include/r97q.h). Device memory and streams come
+from torch (plumbing only: every byte of arithmetic happens in the HIP kernels of csrc/). There
+is no CPU fallback: when the library is missing or cannot load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libr97q.so")
+
+R97Q_F32 = 0
+R97Q_BF16 = 1
+
+
+class R97qError(RuntimeError):
+    pass
+
+
+class Desc(C.Structure):
+    """R97IqrDecodeDesc (include/r97q.h), the reference's src/iqr_decode.h:59-114 layout."""
+
+    _fields_ = [
+        ("rows_all", C.c_int64), ("cols", C.c_int64), ("row0", C.c_int64), ("rows", C.c_int64),
+        ("bits", C.c_int32), ("state_bits", C.c_int32), ("run_rows", C.c_int32), ("rb", C.c_int32),
+        ("mad", C.c_int32), ("round_mad", C.c_int32), ("mad_a", C.c_uint32), ("mad_b", C.c_uint32),
+        ("lut", C.c_void_p),
+        ("codes", C.c_void_p), ("codes_row_bytes", C.c_int64),
+        ("scale", C.c_void_p), ("scale_dtype", C.c_int32), ("scale_block_cols", C.c_int64),
+        ("scale_row_bytes", C.c_int64),
+        ("affine", C.c_int32), ("zero", C.c_void_p), ("zero_bits", C.c_int32), ("zero_row_bytes", C.c_int64),
+        ("scale2", C.c_void_p), ("scale2_dtype", C.c_int32), ("scale2_row_bytes", C.c_int64),
+        ("scale2_block_rows", C.c_int64), ("scale2_block_cols", C.c_int64),
+        ("out_codes", C.c_void_p), ("out_scale", C.c_void_p),
+    ]
+
+
+class Weight(C.Structure):
+    """R97qWeight (include/r97q.h): a prepared weight on the device."""
+
+    _fields_ = [
+        ("rows", C.c_int64), ("cols", C.c_int64), ("bits", C.c_int32), ("state_bits", C.c_int32),
+        ("run_rows", C.c_int32), ("mad", C.c_int32), ("mad_a", C.c_uint32), ("mad_b", C.c_uint32),
+        ("lut", C.c_void_p), ("stream", C.c_void_p), ("scale_t", C.c_void_p),
+    ]
+
+
+# every symbol include/r97q.h declares, with its ctypes signature
+_P, _I, _i = C.c_void_p, C.c_int64, C.c_int32
+SIGNATURES = {
+    "r97q_last_error": (C.c_char_p, []),
+    "r97q_iqr_validate": (C.c_int, [C.POINTER(Desc)]),
+    "r97_iqr_decode": (C.c_int, [C.POINTER(Desc), _P]),
+    "r97q_weight_stream_bytes": (C.c_int64, [C.POINTER(Desc)]),
+    "r97q_weight_prepare": (C.c_int, [C.POINTER(Desc), _P, _P, _P, C.POINTER(Weight), _P]),
+    "r97q_fwd_workspace_bytes": (C.c_int64, [_I, _I, _I, _i]),
+    "r97q_bwd_workspace_bytes": (C.c_int64, [_I, _I, _I, _i]),
+    "r97q_qlinear_lora_fwd": (C.c_int, [C.POINTER(Weight), _P, _I, _P, _P, _i, C.c_float, _P, _i, _P, _P, _I, _P]),
+    "r97q_qlinear_lora_bwd": (C.c_int, [C.POINTER(Weight), _P, _P, _I, _P, _P, _i, C.c_float, _P, _P, _i, _i,
+                                        _P, _P, _P, _I, _P]),
+    "r97q_iqr_encode_trellis": (C.c_int, [_P, _I, _I, _i, _i, _i, C.c_uint32, C.c_uint32, _P, _P, _P, _i,
+                                          C.POINTER(C.c_double)]),
+    "r97q_lora_fwd_prep": (C.c_int, [_I, _I, _I, _P, _P, _i, C.c_float, _P, _P, _I, _P]),
+    "r97q_qlinear_fwd_base": (C.c_int, [C.POINTER(Weight), _P, _I, _P, _i, _P, _i, _P, _I, _P]),
+    "r97q_lora_bwd_prep": (C.c_int, [_I, _I, _I, _P, _P, _P, _P, _i, C.c_float, _P, _I, _P]),
+    "r97q_lora_bwd_grads": (C.c_int, [_I, _I, _I, _P, _P, _i, _P, _P, _P, _I, _P]),
+    "r97q_qlinear_dx_base": (C.c_int, [C.POINTER(Weight), _P, _I, _i, _P, _i, _i, _P, _I, _P]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded libr97q.so (raises R97qError when it is missing or incomplete)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise R97qError(f"libr97q.so is not built ({LIB_PATH}); run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().r97q_last_error().decode()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise R97qError(f"{what} failed (status {rc}): {last_error()}")
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+from .qlinear import QWeight, qlinear_lora_fwd, qlinear_lora_bwd, iqr_decode  # noqa: E402,F401

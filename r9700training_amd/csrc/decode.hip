@@ -1,0 +1,321 @@
+// decode.hip -- the standalone IQR decode (canonical planes -> int8 grid + bf16 scale) and the
+// one-time preparation of a weight for the fused kernels (canonical planes -> column streams +
+// transposed effective scale), with their C-ABI entry points.
+//
+// The decode is the reference's r97_iqr_decode (src/iqr_decode.h:278-386): same rules, same
+// values, bit for bit. It is not the reference's schedule: instead of one thread walking a whole
+// 256-row run of one column, each thread decodes an 8-row chunk of a column and seeds its state
+// from the ceil(L/b) codes above the chunk (wrapping inside the run, which is exactly the
+// tail-biting seam), so a launch has rows/8 x cols independent threads and consecutive threads
+// write consecutive columns.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "iqr_device.h"
+#include "status.h"
+
+namespace r97q {
+
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+}
+
+void clear_error() { g_error.clear(); }
+
+const char* last_error() { return g_error.c_str(); }
+
+// ---------------------------------------------------------------- the description's rules
+// src/iqr_decode.h:321-349
+int32_t validate(const R97IqrDecodeDesc& d) {
+    if (!d.codes || !d.out_codes || !d.out_scale) return 1;
+    if (d.rows <= 0 || d.row0 < 0 || d.rows_all <= 0 || d.rows > d.rows_all - d.row0) return 1;
+    if (d.cols <= 0 || (d.cols & 127) != 0) return 1;
+    if (d.run_rows <= 0 || d.rb <= 0 || d.run_rows % d.rb != 0) return 1;
+    if (d.row0 % d.run_rows != 0) return 1;
+    if (d.rows % d.run_rows != 0 && d.row0 + d.rows != d.rows_all) return 1;
+    const int64_t bc = d.scale_block_cols > 0 ? d.scale_block_cols : d.cols;
+    if (bc != 128 && bc != d.cols) return 1;
+    if (d.affine) {
+        if (!d.zero || d.bits < 1 || d.bits > 7 || d.zero_bits < 1 || d.zero_bits > 8) return 1;
+        if (d.run_rows != 1 || d.rb != 1 || d.scale2) return 1;
+        return 0;
+    }
+    if (d.bits < 1 || d.bits > 16 || d.state_bits < 1 || d.state_bits > 24) return 1;
+    if (!d.mad && !d.lut) return 1;
+    if (d.scale2 && (d.scale2_block_rows < 0 || d.scale2_block_cols < 0)) return 1;
+    if (d.scale2 && d.scale2_block_cols > 0 && d.scale2_block_cols % 128 != 0) return 1;
+    const int32_t c = (d.state_bits + d.bits - 1) / d.bits;
+    for (int64_t r0 = d.row0; r0 < d.row0 + d.rows; r0 += d.run_rows) {
+        int64_t r1 = r0 + d.run_rows;
+        if (r1 > d.rows_all) r1 = d.rows_all;
+        if (r1 - r0 < c) return 1;
+    }
+    return 0;
+}
+
+namespace {
+
+// ---------------------------------------------------------------- the decode kernel
+constexpr int kDecodeThreads = 256;
+
+__device__ inline int32_t state_value(const R97IqrDecodeDesc& d, uint32_t st) {
+    if (d.mad) return mad_value(st & 0xFFFFFFu, d.mad_a & 0xFFFFFFu, d.mad_b);
+    return (int32_t)d.lut[st];
+}
+
+// src/iqr_decode.h:239-250
+__device__ float block_max(const R97IqrDecodeDesc& d, int64_t r, int64_t kb) {
+    const int64_t r0 = (r / d.rb) * d.rb;
+    int64_t r1 = r0 + d.rb;
+    if (r1 > d.rows_all) r1 = d.rows_all;
+    float m = 0.0f;
+    for (int64_t q = r0; q < r1; ++q) {
+        const float v = block_scale(d, q, kb);
+        m = v > m ? v : m;
+    }
+    return m;
+}
+
+// src/iqr_decode.h:253-256
+__device__ inline int32_t rb_round(int32_t v, float ratio, int32_t mad) {
+    if (mad) return (int32_t)(__builtin_fmaf((float)v, ratio, 12582912.0f) - 12582912.0f);
+    return (int32_t)__builtin_rintf((float)v * ratio);
+}
+
+// One thread: column j, rows [r, r_end) of the run [run_start, run_end).
+__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDecodeDesc d,
+                                                                int64_t chunk_rows,
+                                                                int64_t chunks) {
+    const int64_t j = (int64_t)blockIdx.x * kDecodeThreads + threadIdx.x;
+    const int64_t ch = blockIdx.y + (int64_t)blockIdx.z * gridDim.y;
+    if (j >= d.cols || ch >= chunks) return;
+    const int64_t r = d.row0 + ch * chunk_rows;
+    const int64_t run_start = (r / d.run_rows) * d.run_rows;
+    int64_t run_end = run_start + d.run_rows;
+    if (run_end > d.rows_all) run_end = d.rows_all;
+    int64_t r_end = r + chunk_rows;
+    if (r_end > run_end) r_end = run_end;
+    if (r_end > d.row0 + d.rows) r_end = d.row0 + d.rows;
+    const int64_t kb = j >> 7;
+    const int64_t nkb = d.cols >> 7;
+    const bool first = (j & 127) == 0;
+
+    if (d.affine) {
+        for (int64_t q = r; q < r_end; ++q) {
+            const uint32_t code = load_bits(d.codes + (q - d.row0) * d.codes_row_bytes, d.bits, j);
+            const int64_t bc = d.scale_block_cols > 0 ? d.scale_block_cols : d.cols;
+            const int64_t gb = bc == d.cols ? 0 : (kb * 128) / bc;
+            const uint32_t zero = load_bits(d.zero + (q - d.row0) * d.zero_row_bytes, d.zero_bits, gb);
+            d.out_codes[(q - d.row0) * d.cols + j] = (int8_t)((int32_t)code - (int32_t)zero);
+            if (first) d.out_scale[(q - d.row0) * nkb + kb] = f32_to_bf16(block_scale(d, q, kb));
+        }
+        return;
+    }
+
+    // The state before row r: the c codes above it, wrapping inside the run (the seam when r is
+    // the run's first row, the plain shift register otherwise).
+    const int32_t c = (d.state_bits + d.bits - 1) / d.bits;
+    const uint32_t mask = (1u << d.state_bits) - 1u;
+    const int64_t len = run_end - run_start;
+    uint32_t st = 0;
+    for (int32_t q = c; q >= 1; --q) {
+        int64_t t = r - q;
+        if (t < run_start) t += len;
+        st = ((st << d.bits) | load_bits(d.codes + (t - d.row0) * d.codes_row_bytes, d.bits, j)) & mask;
+    }
+    // rb > 1: the block's shared scale is set at the block's first row; a chunk that starts inside
+    // a block takes the block's value, which is what the serial walk carried there.
+    float cur = 0.0f;
+    if (d.rb > 1 && (r % d.rb) != 0) cur = block_max(d, (r / d.rb) * d.rb, kb);
+    for (int64_t q = r; q < r_end; ++q) {
+        st = ((st << d.bits) | load_bits(d.codes + (q - d.row0) * d.codes_row_bytes, d.bits, j)) & mask;
+        const int32_t v = state_value(d, st);
+        int32_t out;
+        float sc;
+        if (d.rb > 1) {
+            if (q % d.rb == 0) cur = block_max(d, q, kb);
+            const float sr = block_scale(d, q, kb);
+            sc = cur;
+            out = cur <= 0.0f ? 0 : rb_round(v, sr / cur, d.round_mad);
+        } else {
+            sc = block_scale(d, q, kb);
+            out = v;
+        }
+        d.out_codes[(q - d.row0) * d.cols + j] = (int8_t)out;
+        if (first) d.out_scale[(q - d.row0) * nkb + kb] = f32_to_bf16(sc);
+    }
+}
+
+// ---------------------------------------------------------------- preparation
+// One thread per (segment g, column): the segment's 32 codes of the column, assembled into its
+// `bits` stream dwords (row 32g+i's code at bit bits*(31-i)).
+__global__ __launch_bounds__(256) void prepare_stream_kernel(const R97IqrDecodeDesc d,
+                                                             uint32_t* __restrict__ stream) {
+    const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t g = blockIdx.y;
+    if (col >= d.cols) return;
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = 0;
+    for (int i = 0; i < 32; ++i) {
+        const uint32_t code = load_bits(d.codes + (g * 32 + i) * d.codes_row_bytes, d.bits, col);
+        const int pos = d.bits * (31 - i);
+        const int wi = pos >> 5, sh = pos & 31;
+        // a code may straddle two dwords
+        for (int q = 0; q < 16; ++q) {
+            if (q == wi) w[q] |= code << sh;
+            if (q == wi + 1 && sh + d.bits > 32) w[q] |= code >> (32 - sh);
+        }
+    }
+    for (int q = 0; q < d.bits; ++q) stream[stream_index(g, d.bits, q, d.cols, col)] = w[q];
+}
+
+// One thread per (row, 128-column block): the effective bf16 scale, transposed to [cols/128][rows].
+__global__ __launch_bounds__(256) void prepare_scale_kernel(const R97IqrDecodeDesc d,
+                                                            const float* __restrict__ scale_col,
+                                                            uint16_t* __restrict__ scale_t) {
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t kb = blockIdx.y;
+    if (n >= d.rows_all) return;
+    uint16_t s;
+    if (scale_col) {
+        // src/iqr_form.h:203-216: one f32 a row times one f32 a block, rounded once
+        const float row = __builtin_bit_cast(float, ((const uint32_t*)(d.scale + n * d.scale_row_bytes))[0]);
+        s = f32_to_bf16(row * scale_col[kb]);
+    } else {
+        s = f32_to_bf16(block_scale(d, n, kb));
+    }
+    scale_t[kb * d.rows_all + n] = s;
+}
+
+}  // namespace
+
+// Whether `d` is a form the fused kernels serve; the reason goes to the error message.
+bool fused_form(const R97IqrDecodeDesc& d, const float* scale_col) {
+    if (d.affine) {
+        set_error("fused path: the affine grid has no trellis (decode it with r97_iqr_decode)");
+        return false;
+    }
+    if (!d.mad) {
+        set_error("fused path: a stored-LUT codebook is not served (trellis.mad only)");
+        return false;
+    }
+    if (d.rb != 1) {
+        set_error("fused path: rb = %d row blocks are not served (rb = 1 only)", (int)d.rb);
+        return false;
+    }
+    if (d.state_bits != 16 || d.bits < 3 || d.bits > 6) {
+        set_error("fused path: bits %d state_bits %d not served (bits 3..6, L = 16)", (int)d.bits,
+                  (int)d.state_bits);
+        return false;
+    }
+    if (d.rows_all % 32 != 0 || d.run_rows % 32 != 0 || d.cols % 128 != 0) {
+        set_error("fused path: rows %lld / run %d must be multiples of 32, cols %lld of 128",
+                  (long long)d.rows_all, (int)d.run_rows, (long long)d.cols);
+        return false;
+    }
+    if (scale_col && (d.scale_dtype != R97_IQR_F32 || d.scale_block_cols > 0)) {
+        set_error("fused path: scale.col needs one f32 scale a row (src/iqr_form.h:209)");
+        return false;
+    }
+    return true;
+}
+
+}  // namespace r97q
+
+using namespace r97q;
+
+extern "C" {
+
+const char* r97q_last_error(void) { return r97q::last_error(); }
+
+int r97q_iqr_validate(const R97IqrDecodeDesc* desc) { return desc ? r97q::validate(*desc) : 1; }
+
+int r97_iqr_decode(const R97IqrDecodeDesc* desc, R97IqrStream stream) {
+    clear_error();
+    if (!desc || validate(*desc)) {
+        set_error("r97_iqr_decode: the description is outside the decode's rules");
+        return 1;
+    }
+    const R97IqrDecodeDesc& d = *desc;
+    const int64_t chunk_rows = (d.run_rows % 8 == 0) ? 8 : 1;
+    // chunks never straddle a run: runs start at multiples of run_rows and chunk_rows divides it
+    const int64_t chunks = (d.rows + chunk_rows - 1) / chunk_rows;
+    const int64_t gy = chunks < 65535 ? chunks : 65535;
+    const int64_t gz = (chunks + gy - 1) / gy;
+    dim3 grid((unsigned)((d.cols + kDecodeThreads - 1) / kDecodeThreads), (unsigned)gy, (unsigned)gz);
+    hipLaunchKernelGGL(decode_kernel, grid, dim3(kDecodeThreads), 0, (hipStream_t)stream, d,
+                       chunk_rows, chunks);
+    return launch_status("r97_iqr_decode") == R97Q_OK ? 0 : 1;
+}
+
+int64_t r97q_weight_stream_bytes(const R97IqrDecodeDesc* desc) {
+    clear_error();
+    if (!desc) {
+        set_error("r97q_weight_stream_bytes: null description");
+        return -1;
+    }
+    if (!fused_form(*desc, nullptr)) return -1;
+    return desc->rows_all / 32 * desc->bits * desc->cols * 4;
+}
+
+int r97q_weight_prepare(const R97IqrDecodeDesc* desc, const float* scale_col,
+                        uint32_t* stream_out, uint16_t* scale_t_out, R97qWeight* w,
+                        R97IqrStream stream) {
+    clear_error();
+    if (!desc || !stream_out || !scale_t_out || !w) {
+        set_error("r97q_weight_prepare: null argument");
+        return R97Q_EINVAL;
+    }
+    R97IqrDecodeDesc d = *desc;
+    if (d.row0 != 0 || d.rows != d.rows_all) {
+        set_error("r97q_weight_prepare: the whole weight is prepared at once (row0 0, rows = rows_all)");
+        return R97Q_EINVAL;
+    }
+    // the rules need output pointers; preparation writes its own planes instead
+    d.out_codes = reinterpret_cast<int8_t*>(stream_out);
+    d.out_scale = scale_t_out;
+    if (validate(d)) {
+        set_error("r97q_weight_prepare: the description is outside the decode's rules");
+        return R97Q_EINVAL;
+    }
+    if (!fused_form(d, scale_col)) return R97Q_EUNSUPPORTED;
+    const hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(prepare_stream_kernel,
+                       dim3((unsigned)((d.cols + 255) / 256), (unsigned)(d.rows_all / 32)), dim3(256),
+                       0, s, d, stream_out);
+    if (int e = launch_status("prepare_stream_kernel")) return e;
+    hipLaunchKernelGGL(prepare_scale_kernel,
+                       dim3((unsigned)((d.rows_all + 255) / 256), (unsigned)(d.cols / 128)),
+                       dim3(256), 0, s, d, scale_col, scale_t_out);
+    if (int e = launch_status("prepare_scale_kernel")) return e;
+    R97qWeight out{};
+    out.rows = d.rows_all;
+    out.cols = d.cols;
+    out.bits = d.bits;
+    out.state_bits = d.state_bits;
+    out.run_rows = d.run_rows;
+    out.mad = d.mad;
+    out.mad_a = d.mad_a;
+    out.mad_b = d.mad_b;
+    out.lut = d.lut;
+    out.stream = stream_out;
+    out.scale_t = scale_t_out;
+    *w = out;
+    return R97Q_OK;
+}
+
+}  // extern "C"

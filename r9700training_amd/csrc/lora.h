@@ -1,0 +1,52 @@
+// lora.h -- launchers of the adapter's skinny kernels (lora.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace r97q {
+
+// v[m][j] = sum_k In[m][k] W[j][k] for m < T, j < r (W row-major [down_rank(r), Kin], rows past r
+// zero; Kin a multiple of 128). Writes, each when non-null:
+//   out [T, r] f32    = sa * v
+//   P   [T, 2r] bf16  = [hi | lo](sb * v)                    (row-major)
+//   Pt  [2r, ldt] bf16 = [hi | lo](sb * v), transposed       (zero for T <= m < ldt)
+//   Pt2 [2r, ldt] bf16 = [hi | lo](s2 * U2[m][j]), transposed (U2 f32 [T, r])
+struct DownArgs {
+    const uint16_t* In;
+    const uint16_t* W;
+    int64_t T, Kin, ldt;
+    int r;
+    float sa, sb;
+    float* out;
+    uint16_t* P;
+    uint16_t* Pt;
+    const float* U2;
+    float s2;
+    uint16_t* Pt2;
+};
+
+// out (+=, f32 atomics) scale * sum_m (Pt[j][m] + Pt[r+j][m]) V[m][c]: V bf16 [T, C] (C a multiple
+// of 64), out [r, C] row-major or, `transposed`, [C, r].
+struct GradOne {
+    const uint16_t* Pt;
+    const uint16_t* V;
+    int64_t C;
+    float* out;
+    float scale;
+    int transposed;
+};
+struct GradArgs {
+    GradOne one[2];
+    int64_t T, ldt, chunk;
+};
+
+int down_rank(int r);          // r rounded up to a multiple of 16
+int64_t grad_ld(int64_t T);    // the transposed splits' row length: T rounded up to 32
+
+int launch_lora_down(const DownArgs& a, hipStream_t s);
+int launch_lora_grads(int r, GradArgs g, int nz, hipStream_t s);
+int launch_transpose2(const uint16_t* B, uint16_t* Bt, int64_t N, const uint16_t* A, uint16_t* At,
+                      int64_t K, int r, hipStream_t s);
+
+}  // namespace r97q

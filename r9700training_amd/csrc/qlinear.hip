@@ -1,0 +1,398 @@
+// qlinear.hip -- the C-ABI of the fused IQR-linear + LoRA forward and backward (include/r97q.h):
+// argument checks, workspace layout and the launch order of the stages.
+//
+//   forward   t = X.A^T; Y = X.W^T + s.t.B^T          (reference twins: src/adjoint/host/linear.cpp:
+//                                                      193-219, lora.cpp:226-244, 416-441)
+//   backward  dt = s.dY.B;  dX = dY.W + dt.A;          (linear.cpp:221-243, lora.cpp:260-328,
+//             dA += dt^T.X;  dB += s.dY^T.t            451-521)
+//
+// Kernels: the fused decode + MFMA base products (qlinear_fused.hip) carry the adapter's
+// up-projection in their epilogue; the adapter's down products and factor gradients are
+// lora.hip's. A step is 2 launches forward (down, fused) and 4 backward (transposes, down, grads,
+// fused).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+
+#include "iqr_device.h"
+#include "lora.h"
+#include "qlinear_fused.h"
+#include "status.h"
+
+using namespace r97q;
+
+namespace {
+
+int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
+bool rank_ok(int r) { return r == 0 || r == 8 || r == 16 || r == 32 || r == 64; }
+
+struct Shape {
+    int64_t T, N, K;
+    int r;
+};
+
+// Workspace layout. Forward: P [T, 2r] | Apad [rd, K] (when r is not a multiple of 16).
+// Backward: Bt [rd, N] | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt].
+struct FwdWs {
+    int64_t P, Apad, total;
+};
+FwdWs fwd_ws(const Shape& s) {
+    FwdWs w{};
+    if (s.r == 0) return w;
+    const int rd = down_rank(s.r);
+    w.P = 0;
+    w.Apad = w.P + align256(s.T * 2 * s.r * 2);
+    w.total = w.Apad + (rd != s.r ? align256((int64_t)rd * s.K * 2) : 0);
+    return w;
+}
+struct BwdWs {
+    int64_t Bt, At, P, PtA, PtB, total;
+};
+BwdWs bwd_ws(const Shape& s) {
+    BwdWs w{};
+    if (s.r == 0) return w;
+    const int rd = down_rank(s.r);
+    const int64_t ldt = grad_ld(s.T);
+    w.Bt = 0;
+    w.At = w.Bt + align256((int64_t)rd * s.N * 2);
+    w.P = w.At + align256(s.K * s.r * 2);
+    w.PtA = w.P + align256(s.T * 2 * s.r * 2);
+    w.PtB = w.PtA + align256(2 * s.r * ldt * 2);
+    w.total = w.PtB + align256(2 * s.r * ldt * 2);
+    return w;
+}
+
+// zero-fill + copy of a [r, cols] bf16 matrix into [rd, cols] (rows r..rd-1 zero)
+__global__ __launch_bounds__(256) void pad_rows16(const uint16_t* __restrict__ in, int r, int rd,
+                                                  int64_t cols, uint16_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)rd * cols) return;
+    const int64_t row = i / cols;
+    out[i] = row < r ? in[i] : (uint16_t)0;
+}
+
+int check_weight(const R97qWeight* w) {
+    if (!w || !w->stream || !w->scale_t) {
+        set_error("qlinear: null weight");
+        return R97Q_EINVAL;
+    }
+    if (!w->mad || w->state_bits != 16 || w->bits < 3 || w->bits > 6) {
+        set_error("qlinear: weight form not served (trellis.mad, L 16, bits 3..6)");
+        return R97Q_EUNSUPPORTED;
+    }
+    if (w->rows % kBN != 0 || w->cols % kBN != 0 || w->run_rows % 32 != 0) {
+        set_error("qlinear: N %lld and K %lld must be multiples of 128, run %d of 32",
+                  (long long)w->rows, (long long)w->cols, (int)w->run_rows);
+        return R97Q_EUNSUPPORTED;
+    }
+    return R97Q_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- the stages
+namespace {
+
+int check_rank(int32_t rank, const char* who) {
+    if (!rank_ok(rank)) {
+        set_error("%s: rank %d not served (0, 8, 16, 32, 64)", who, (int)rank);
+        return R97Q_EUNSUPPORTED;
+    }
+    return R97Q_OK;
+}
+
+int check_ws(int64_t have, int64_t need, const void* ws, const char* who) {
+    if (have < need || (need > 0 && !ws)) {
+        set_error("%s: workspace %lld bytes, needs %lld", who, (long long)have, (long long)need);
+        return R97Q_EWORKSPACE;
+    }
+    return R97Q_OK;
+}
+
+// t = X.A^T (f32, kept for the backward), P = [hi | lo](s.t) in the forward workspace
+int fwd_prep(const Shape& sh, const uint16_t* X, const uint16_t* A, float scale, float* t_out,
+             uint8_t* wsb, hipStream_t s) {
+    const FwdWs ws = fwd_ws(sh);
+    const int rank = sh.r, rd = down_rank(rank);
+    const uint16_t* Wd = A;
+    if (rd != rank) {
+        uint16_t* Apad = reinterpret_cast<uint16_t*>(wsb + ws.Apad);
+        hipLaunchKernelGGL(pad_rows16, dim3((unsigned)((rd * sh.K + 255) / 256)), dim3(256), 0, s, A,
+                           rank, rd, sh.K, Apad);
+        if (int e = launch_status("pad_rows16")) return e;
+        Wd = Apad;
+    }
+    DownArgs a{};
+    a.In = X;
+    a.W = Wd;
+    a.T = sh.T;
+    a.Kin = sh.K;
+    a.ldt = sh.T;
+    a.r = rank;
+    a.sa = 1.0f;
+    a.sb = scale;
+    a.out = t_out;
+    a.P = reinterpret_cast<uint16_t*>(wsb + ws.P);
+    return launch_lora_down(a, s);
+}
+
+int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* X, const uint16_t* B, void* Y,
+             int32_t y_dtype, uint8_t* wsb, hipStream_t s) {
+    FwdParams p{};
+    p.X = X;
+    p.T = sh.T;
+    p.N = sh.N;
+    p.K = sh.K;
+    p.stream = w->stream;
+    p.scale_t = w->scale_t;
+    p.a24 = w->mad_a & 0xFFFFFFu;
+    p.b = w->mad_b;
+    p.run_rows = w->run_rows;
+    p.P = sh.r > 0 ? reinterpret_cast<const uint16_t*>(wsb + fwd_ws(sh).P) : nullptr;
+    p.B = B;
+    p.rank = sh.r;
+    p.Y = Y;
+    p.y_f32 = y_dtype == R97Q_F32;
+    p.mtiles = (int)((sh.T + kBM - 1) / kBM);
+    p.ntiles = (int)(sh.N / kBN);
+    switch (w->bits) {
+        case 3: launch_fwd<3>(p, s); break;
+        case 4: launch_fwd<4>(p, s); break;
+        case 5: launch_fwd<5>(p, s); break;
+        default: launch_fwd<6>(p, s); break;
+    }
+    return launch_status("qlinear_fwd_kernel");
+}
+
+// B^T [rd, N] (zero rows past r), A^T [K, r]; dt = s.dY.B as P = [hi | lo](dt) for the fused dX
+// epilogue and PtA (the same, transposed) for dA; PtB = [hi | lo](s.t) transposed for dB.
+int bwd_prep(const Shape& sh, const uint16_t* dY, const uint16_t* A, const uint16_t* B, const float* t,
+             float scale, uint8_t* wsb, hipStream_t s) {
+    const BwdWs ws = bwd_ws(sh);
+    uint16_t* Bt = reinterpret_cast<uint16_t*>(wsb + ws.Bt);
+    uint16_t* At = reinterpret_cast<uint16_t*>(wsb + ws.At);
+    if (int e = launch_transpose2(B, Bt, sh.N, A, At, sh.K, sh.r, s)) return e;
+    DownArgs a{};
+    a.In = dY;
+    a.W = Bt;
+    a.T = sh.T;
+    a.Kin = sh.N;
+    a.ldt = grad_ld(sh.T);
+    a.r = sh.r;
+    a.sa = scale;
+    a.sb = scale;
+    a.P = reinterpret_cast<uint16_t*>(wsb + ws.P);
+    a.Pt = reinterpret_cast<uint16_t*>(wsb + ws.PtA);
+    if (t) {
+        a.U2 = t;
+        a.s2 = scale;
+        a.Pt2 = reinterpret_cast<uint16_t*>(wsb + ws.PtB);
+    }
+    return launch_lora_down(a, s);
+}
+
+// dA[j][k] += sum_m dt[m][j] X[m][k];  dB[n][j] += s . sum_m dY[m][n] t[m][j]
+int bwd_grads(const Shape& sh, const uint16_t* X, const uint16_t* dY, float* dA, float* dB, uint8_t* wsb,
+              hipStream_t s) {
+    const BwdWs ws = bwd_ws(sh);
+    GradArgs g{};
+    g.T = sh.T;
+    g.ldt = grad_ld(sh.T);
+    int nz = 0;
+    if (dA) g.one[nz++] = GradOne{reinterpret_cast<const uint16_t*>(wsb + ws.PtA), X, sh.K, dA, 1.0f, 0};
+    if (dB) g.one[nz++] = GradOne{reinterpret_cast<const uint16_t*>(wsb + ws.PtB), dY, sh.N, dB, 1.0f, 1};
+    if (nz == 0) return R97Q_OK;
+    return launch_lora_grads(sh.r, g, nz, s);
+}
+
+int dx_base(const R97qWeight* w, const Shape& sh, const uint16_t* dY, void* dX, int32_t dx_dtype,
+            int32_t accumulate, uint8_t* wsb, hipStream_t s) {
+    const BwdWs ws = bwd_ws(sh);
+    DxParams p{};
+    p.dY = dY;
+    p.T = sh.T;
+    p.N = sh.N;
+    p.K = sh.K;
+    p.stream = w->stream;
+    p.scale_t = w->scale_t;
+    p.a24 = w->mad_a & 0xFFFFFFu;
+    p.b = w->mad_b;
+    p.run_rows = w->run_rows;
+    p.P = sh.r > 0 ? reinterpret_cast<const uint16_t*>(wsb + ws.P) : nullptr;
+    p.At = sh.r > 0 ? reinterpret_cast<const uint16_t*>(wsb + ws.At) : nullptr;
+    p.rank = sh.r;
+    p.dX = dX;
+    p.dx_f32 = dx_dtype == R97Q_F32;
+    p.accumulate = accumulate != 0;
+    p.mtiles = (int)((sh.T + kBM - 1) / kBM);
+    p.ktiles = (int)(sh.K / kBN);
+    switch (w->bits) {
+        case 3: launch_dx<3>(p, s); break;
+        case 4: launch_dx<4>(p, s); break;
+        case 5: launch_dx<5>(p, s); break;
+        default: launch_dx<6>(p, s); break;
+    }
+    return launch_status("qlinear_dx_kernel");
+}
+
+int shape_ok(int64_t T, int64_t N, int64_t K, const char* who) {
+    if (T <= 0 || N <= 0 || K <= 0 || N % kBN || K % kBN) {
+        set_error("%s: T %lld N %lld K %lld (T > 0, N and K multiples of 128)", who, (long long)T,
+                  (long long)N, (long long)K);
+        return R97Q_EINVAL;
+    }
+    return R97Q_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t r97q_fwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank) {
+    return fwd_ws(Shape{T, N, K, rank}).total;
+}
+
+int64_t r97q_bwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank) {
+    return bwd_ws(Shape{T, N, K, rank}).total;
+}
+
+int r97q_lora_fwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* X, const uint16_t* A,
+                       int32_t rank, float scale, float* t_out, void* workspace,
+                       int64_t workspace_bytes, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_lora_fwd_prep";
+    if (int e = shape_ok(T, N, K, who)) return e;
+    if (int e = check_rank(rank, who)) return e;
+    if (rank == 0) return R97Q_OK;
+    if (!X || !A || !t_out) {
+        set_error("%s: null X, A or t_out", who);
+        return R97Q_EINVAL;
+    }
+    const Shape sh{T, N, K, rank};
+    if (int e = check_ws(workspace_bytes, fwd_ws(sh).total, workspace, who)) return e;
+    return fwd_prep(sh, X, A, scale, t_out, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
+}
+
+int r97q_qlinear_fwd_base(const R97qWeight* w, const uint16_t* X, int64_t T, const uint16_t* B,
+                          int32_t rank, void* Y, int32_t y_dtype, void* workspace,
+                          int64_t workspace_bytes, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_qlinear_fwd_base";
+    if (int e = check_weight(w)) return e;
+    if (int e = check_rank(rank, who)) return e;
+    if (!X || !Y || T <= 0 || (rank > 0 && !B)) {
+        set_error("%s: null X / Y (or B with rank > 0), or T <= 0", who);
+        return R97Q_EINVAL;
+    }
+    const Shape sh{T, w->rows, w->cols, rank};
+    if (int e = check_ws(workspace_bytes, fwd_ws(sh).total, workspace, who)) return e;
+    return fwd_base(w, sh, X, B, Y, y_dtype, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
+}
+
+int r97q_qlinear_lora_fwd(const R97qWeight* w, const uint16_t* X, int64_t T, const uint16_t* A,
+                          const uint16_t* B, int32_t rank, float scale, void* Y, int32_t y_dtype,
+                          float* t_out, void* workspace, int64_t workspace_bytes,
+                          R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_qlinear_lora_fwd";
+    if (int e = check_weight(w)) return e;
+    if (int e = check_rank(rank, who)) return e;
+    if (!X || !Y || T <= 0) {
+        set_error("%s: null X / Y or T <= 0", who);
+        return R97Q_EINVAL;
+    }
+    if (rank > 0 && (!A || !B || !t_out)) {
+        set_error("%s: rank %d needs A, B and t_out", who, (int)rank);
+        return R97Q_EINVAL;
+    }
+    const Shape sh{T, w->rows, w->cols, rank};
+    if (int e = check_ws(workspace_bytes, fwd_ws(sh).total, workspace, who)) return e;
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    const hipStream_t s = (hipStream_t)stream;
+    if (rank > 0)
+        if (int e = fwd_prep(sh, X, A, scale, t_out, wsb, s)) return e;
+    return fwd_base(w, sh, X, B, Y, y_dtype, wsb, s);
+}
+
+int r97q_lora_bwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* dY, const uint16_t* A,
+                       const uint16_t* B, const float* t, int32_t rank, float scale, void* workspace,
+                       int64_t workspace_bytes, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_lora_bwd_prep";
+    if (int e = shape_ok(T, N, K, who)) return e;
+    if (int e = check_rank(rank, who)) return e;
+    if (rank == 0) return R97Q_OK;
+    if (!dY || !A || !B) {
+        set_error("%s: null dY, A or B", who);
+        return R97Q_EINVAL;
+    }
+    const Shape sh{T, N, K, rank};
+    if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
+    return bwd_prep(sh, dY, A, B, t, scale, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
+}
+
+int r97q_lora_bwd_grads(int64_t T, int64_t N, int64_t K, const uint16_t* X, const uint16_t* dY,
+                        int32_t rank, float* dA, float* dB, void* workspace, int64_t workspace_bytes,
+                        R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_lora_bwd_grads";
+    if (int e = shape_ok(T, N, K, who)) return e;
+    if (int e = check_rank(rank, who)) return e;
+    if (rank == 0) return R97Q_OK;
+    if ((dA && !X) || (dB && !dY)) {
+        set_error("%s: dA needs X, dB needs dY", who);
+        return R97Q_EINVAL;
+    }
+    const Shape sh{T, N, K, rank};
+    if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
+    return bwd_grads(sh, X, dY, dA, dB, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
+}
+
+int r97q_qlinear_dx_base(const R97qWeight* w, const uint16_t* dY, int64_t T, int32_t rank, void* dX,
+                         int32_t dx_dtype, int32_t dx_accumulate, void* workspace,
+                         int64_t workspace_bytes, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_qlinear_dx_base";
+    if (int e = check_weight(w)) return e;
+    if (int e = check_rank(rank, who)) return e;
+    if (!dY || !dX || T <= 0) {
+        set_error("%s: null dY / dX or T <= 0", who);
+        return R97Q_EINVAL;
+    }
+    const Shape sh{T, w->rows, w->cols, rank};
+    if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
+    return dx_base(w, sh, dY, dX, dx_dtype, dx_accumulate, static_cast<uint8_t*>(workspace),
+                   (hipStream_t)stream);
+}
+
+int r97q_qlinear_lora_bwd(const R97qWeight* w, const uint16_t* X, const uint16_t* dY, int64_t T,
+                          const uint16_t* A, const uint16_t* B, int32_t rank, float scale,
+                          const float* t, void* dX, int32_t dx_dtype, int32_t dx_accumulate,
+                          float* dA, float* dB, void* workspace, int64_t workspace_bytes,
+                          R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_qlinear_lora_bwd";
+    if (int e = check_weight(w)) return e;
+    if (int e = check_rank(rank, who)) return e;
+    if (!dY || !dX || T <= 0) {
+        set_error("%s: null dY / dX or T <= 0", who);
+        return R97Q_EINVAL;
+    }
+    if (rank > 0 && (!A || !B || !t || !X)) {
+        set_error("%s: rank %d needs X, A, B and t", who, (int)rank);
+        return R97Q_EINVAL;
+    }
+    const Shape sh{T, w->rows, w->cols, rank};
+    if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    const hipStream_t s = (hipStream_t)stream;
+    if (rank > 0) {
+        if (int e = bwd_prep(sh, dY, A, B, t, scale, wsb, s)) return e;
+        if (int e = bwd_grads(sh, X, dY, dA, dB, wsb, s)) return e;
+    }
+    return dx_base(w, sh, dY, dX, dx_dtype, dx_accumulate, wsb, s);
+}
+
+}  // extern "C"

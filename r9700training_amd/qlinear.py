@@ -1,0 +1,114 @@
+"""The fused IQR-linear + LoRA path on device tensors (a front over include/r97q.h).
+
+Shapes and dtypes follow the C ABI: X, dY bf16 [T, K] / [T, N]; A bf16 [r, K]; B bf16 [N, r];
+t f32 [T, r]; dA f32 [r, K]; dB f32 [N, r]. Planes are uint8 device tensors.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import Desc, R97Q_BF16, R97Q_F32, Weight, _ptr, _stream, check, lib
+
+
+def device_desc(planes: dict, rows: int, cols: int, fields: dict) -> Desc:
+    """A description over device planes. `planes` maps codes / scale / lut / scale2 / zero to
+    uint8 (or int8) device tensors; `fields` holds the scalar fields (bits, state_bits, ...)."""
+    d = Desc()
+    d.rows_all, d.cols, d.row0, d.rows = rows, cols, 0, rows
+    for k, v in fields.items():
+        setattr(d, k, v)
+    for k in ("codes", "scale", "lut", "scale2", "zero"):
+        t = planes.get(k)
+        if t is not None:
+            setattr(d, k, t.data_ptr())
+    return d
+
+
+def iqr_decode(desc: Desc, out_codes: torch.Tensor, out_scale: torch.Tensor, stream=None) -> None:
+    """r97_iqr_decode over `desc` (device planes) into out_codes int8 [rows, cols] and out_scale
+    int16 (bf16 bits) [rows, cols/128]."""
+    d = Desc.from_buffer_copy(desc)
+    d.out_codes = out_codes.data_ptr()
+    d.out_scale = out_scale.data_ptr()
+    rc = lib().r97_iqr_decode(C.byref(d), _stream(stream))
+    check(rc, "r97_iqr_decode")
+
+
+class QWeight:
+    """A prepared IQR weight on the device: the column streams and the transposed effective scale
+    (made once: the base weight is frozen)."""
+
+    def __init__(self, desc: Desc, scale_col: torch.Tensor | None = None, device="cuda", stream=None):
+        L = lib()
+        d = Desc.from_buffer_copy(desc)
+        nbytes = L.r97q_weight_stream_bytes(C.byref(d))
+        if nbytes < 0:
+            check(2, "r97q_weight_stream_bytes")
+        self.rows, self.cols = int(d.rows_all), int(d.cols)
+        self.stream_plane = torch.empty(nbytes // 4, dtype=torch.int32, device=device)
+        self.scale_t = torch.empty((self.cols // 128) * self.rows, dtype=torch.int16, device=device)
+        self.w = Weight()
+        self._scale_col = scale_col
+        rc = L.r97q_weight_prepare(C.byref(d), _ptr(scale_col), _ptr(self.stream_plane),
+                                   _ptr(self.scale_t), C.byref(self.w), _stream(stream))
+        check(rc, "r97q_weight_prepare")
+
+    @property
+    def N(self):
+        return self.rows
+
+    @property
+    def K(self):
+        return self.cols
+
+
+def fwd_workspace(T, N, K, rank, device="cuda"):
+    n = lib().r97q_fwd_workspace_bytes(T, N, K, rank)
+    return torch.empty(max(n, 1), dtype=torch.uint8, device=device)
+
+
+def bwd_workspace(T, N, K, rank, device="cuda"):
+    n = lib().r97q_bwd_workspace_bytes(T, N, K, rank)
+    return torch.empty(max(n, 1), dtype=torch.uint8, device=device)
+
+
+def qlinear_lora_fwd(w: QWeight, X, A=None, B=None, scale=1.0, y_dtype=torch.bfloat16, workspace=None,
+                     out=None, t_out=None, stream=None):
+    """Y = X.W^T + scale.(X.A^T).B^T; returns (Y, t)."""
+    T = X.shape[0]
+    rank = 0 if A is None else A.shape[0]
+    if out is None:
+        out = torch.empty((T, w.N), dtype=y_dtype, device=X.device)
+    if rank and t_out is None:
+        t_out = torch.empty((T, rank), dtype=torch.float32, device=X.device)
+    if workspace is None:
+        workspace = fwd_workspace(T, w.N, w.K, rank, X.device)
+    rc = lib().r97q_qlinear_lora_fwd(
+        C.byref(w.w), _ptr(X), T, _ptr(A), _ptr(B), rank, float(scale), _ptr(out),
+        R97Q_F32 if out.dtype == torch.float32 else R97Q_BF16, _ptr(t_out), _ptr(workspace),
+        workspace.numel(), _stream(stream))
+    check(rc, "r97q_qlinear_lora_fwd")
+    return out, t_out
+
+
+def qlinear_lora_bwd(w: QWeight, X, dY, A=None, B=None, t=None, scale=1.0, dx_dtype=torch.bfloat16,
+                     dX=None, accumulate=False, dA=None, dB=None, workspace=None, stream=None):
+    """dX (written or added to), dA += ..., dB += ...; returns (dX, dA, dB)."""
+    T = dY.shape[0]
+    rank = 0 if A is None else A.shape[0]
+    if dX is None:
+        dX = torch.empty((T, w.K), dtype=dx_dtype, device=dY.device)
+    if rank and dA is None:
+        dA = torch.zeros((rank, w.K), dtype=torch.float32, device=dY.device)
+    if rank and dB is None:
+        dB = torch.zeros((w.N, rank), dtype=torch.float32, device=dY.device)
+    if workspace is None:
+        workspace = bwd_workspace(T, w.N, w.K, rank, dY.device)
+    rc = lib().r97q_qlinear_lora_bwd(
+        C.byref(w.w), _ptr(X), _ptr(dY), T, _ptr(A), _ptr(B), rank, float(scale), _ptr(t), _ptr(dX),
+        R97Q_F32 if dX.dtype == torch.float32 else R97Q_BF16, int(bool(accumulate)), _ptr(dA),
+        _ptr(dB), _ptr(workspace), workspace.numel(), _stream(stream))
+    check(rc, "r97q_qlinear_lora_bwd")
+    return dX, dA, dB
