@@ -7,11 +7,13 @@ One step = one forward and one backward of the adapted linear on one batch of sy
             dX = dY.W + dt.A                               (r97q_lora_bwd_prep, _grads, r97q_qlinear_dx_base)
 W is an IQR trunk-form weight (b5 trellis.mad, L 16, 256-row runs, f32 row scale + scale.col)
 quantized from W ~ N(0, 0.02) by this repo's quantizer; X, dY bf16 N(0,1); A, B bf16 N(0, 0.01).
-Default workload: BASELINE.json configs[1] (C2: 4096 x 4096, T 4096, rank 16, alpha 32).
+Default workload: C2, 4096 x 4096, T 4096, rank 16, alpha 32.
 
 Prints ONE JSON line (rank 0): the step's whole-job TFLOP/s, the dominant kernel's roofline
-(HIP events around its launches inside the timed region) and a CPU baseline (the reference's own
-host rows, oracle/_ref, on the box's host cores, over a bounded row sample).
+(HIP events around its launches inside the timed region), its HBM traffic per launch from the
+committed FETCH_SIZE / WRITE_SIZE profile of the same sources (null when the sources changed since)
+and a CPU baseline (the reference's own host rows, oracle/_ref, on the box's host cores, over a
+bounded row sample).
 """
 from __future__ import annotations
 
@@ -49,6 +51,32 @@ def parse():
                     help="run only a plain device copy of this many MiB (3 launches), the known-size "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
     return ap.parse_args()
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qlinear_c2_traffic.json")
+
+
+def profiled_traffic(kernel, config):
+    """HBM bytes per launch of `kernel` from the committed counter profile, if it was taken on this
+    config and on the kernel sources as they are now; else None."""
+    import hashlib
+
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            prof = json.load(f)
+    except (OSError, ValueError):
+        return None
+    h = hashlib.sha256()
+    for src in prof.get("sources", []):
+        try:
+            with open(os.path.join(ROOT, src), "rb") as f:
+                h.update(f.read())
+        except OSError:
+            return None
+    if config != "c2" or h.hexdigest()[:16] != prof.get("sources_sha256_16"):
+        return None
+    k = prof.get("kernels", {}).get(kernel)
+    return None if k is None else k["traffic_bytes"]
 
 
 def flops(T, N, K, r):
@@ -255,7 +283,7 @@ def main():
                        "other": round(ms_step - fwd_ms - dx_ms, 4)},
         "roofline": {"bound": "mfma", "kernel": name, "achieved": round(achieved, 3),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None,
+                     "traffic": profiled_traffic(name, args.config),
                      "packed_weight_GBs": round(packed_bytes / (kms * 1e-3) / 1e9, 2)},
         "quantizer_rel_err": round(inp["q"]["rel_err"], 4),
     }
