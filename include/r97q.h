@@ -216,9 +216,8 @@ int r97q_lora_bwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* dY, cons
                        int64_t workspace_bytes, R97IqrStream stream);
 /* Backward: dA += dt^T.X and dB += scale.dY^T.t (the leaves of lora_shrink_host_adjoint and
  * lora_expand_host_adjoint, src/adjoint/host/lora.cpp:316-327, 507-520), after r97q_lora_bwd_prep
- * on the same workspace (dB needs that prep to have had t). Either output may be NULL. The sums
- * over token chunks are combined with f32 atomic adds, so their order (and the last bits of a
- * gradient) may differ from call to call. */
+ * on the same workspace (dB needs that prep to have had t). Either output may be NULL. The token
+ * chunks' partial sums are added in a fixed order: repeated calls give the same bits. */
 int r97q_lora_bwd_grads(int64_t T, int64_t N, int64_t K, const uint16_t* X, const uint16_t* dY,
                         int32_t rank, float* dA, float* dB, void* workspace, int64_t workspace_bytes,
                         R97IqrStream stream);

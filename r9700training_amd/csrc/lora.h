@@ -26,8 +26,9 @@ struct DownArgs {
     uint16_t* Pt2;
 };
 
-// out (+=, f32 atomics) scale * sum_m (Pt[j][m] + Pt[r+j][m]) V[m][c]: V bf16 [T, C] (C a multiple
-// of 64), out [r, C] row-major or, `transposed`, [C, r].
+// out += scale * sum_m (Pt[j][m] + Pt[r+j][m]) V[m][c]: V bf16 [T, C] (C a multiple of 128), out
+// [r, C] row-major or, `transposed`, [C, r]; Pt bf16 [2r, ldt]. The token chunks' partial sums go
+// to `part` (f32 [grad_chunks, r, C]) and are added into out in chunk order.
 struct GradOne {
     const uint16_t* Pt;
     const uint16_t* V;
@@ -35,17 +36,23 @@ struct GradOne {
     float* out;
     float scale;
     int transposed;
+    float* part;
 };
 struct GradArgs {
     GradOne one[2];
-    int64_t T, ldt, chunk;
+    int64_t T, ldt;
+    int64_t chunk;  // tokens a chunk: grad_chunk_rows(T, K, N), the size the partial buffers assume
 };
 
 int down_rank(int r);          // r rounded up to a multiple of 16
-int64_t grad_ld(int64_t T);    // the transposed splits' row length: T rounded up to 32
+int64_t grad_ld(int64_t T);    // the transposed splits' row length: T rounded up to 64
+// the gradient launch's token chunks (at most this many) and their length in tokens, for dA over K
+// columns and dB over N
+int64_t grad_chunks(int64_t T, int64_t K, int64_t N);
+int64_t grad_chunk_rows(int64_t T, int64_t K, int64_t N);
 
 int launch_lora_down(const DownArgs& a, hipStream_t s);
-int launch_lora_grads(int r, GradArgs g, int nz, hipStream_t s);
+int launch_lora_grads(int r, const GradArgs& g, int nz, hipStream_t s);
 int launch_transpose2(const uint16_t* B, uint16_t* Bt, int64_t N, const uint16_t* A, uint16_t* At,
                       int64_t K, int r, hipStream_t s);
 

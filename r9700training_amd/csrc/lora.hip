@@ -7,15 +7,19 @@
 // [hi | lo] pair of bf16 (hi = bf16(v), lo = bf16(v - hi)) wherever they enter an MFMA, so the
 // adapter path keeps ~16 significant bits.
 //
-//   lora_down_kernel   one workgroup = 16 token rows x the whole reduction, its 4 waves a quarter
-//                      each (v_mfma_f32_16x16x32_bf16), reduced through LDS in a fixed order; it
-//                      writes the f32 result and its [hi | lo] splits for the fused kernels'
-//                      epilogues (row-major) and for the gradient kernel (transposed).
-//   lora_grads_kernel  dA and dB in one launch: a workgroup = 64 output columns x a token chunk;
-//                      the token tile (X or dY) is staged in LDS with coalesced loads and read
-//                      back transposed with ds_read_b64_tr_b16, the [hi | lo] split of dt or s.t
-//                      is the other operand; chunks combine with f32 atomics (as the reference's
-//                      device rows add into the step's f32 gradient stage).
+//   lora_down_kernel   one workgroup = 16 token rows x the whole reduction, its 8 (or 4) waves an
+//                      eighth (quarter) each (v_mfma_f32_16x16x32_bf16), reduced through LDS in a
+//                      fixed order; it writes the f32 result and its [hi | lo] splits for the
+//                      fused kernels' epilogues (row-major) and for the gradient kernel
+//                      (transposed).
+//   lora_grads_kernel  dA and dB in one launch: a workgroup = 512 output columns x a token
+//                      chunk; the token tile (X or dY) and the Pt rows stream through registers
+//                      into two LDS slots, loaded three tiles ahead; the token tile is read back
+//                      transposed with ds_read_b64_tr_b16, the [hi | lo] split of dt or s.t is
+//                      the other operand; each chunk writes its own partial sums.
+//   grad_reduce_kernel adds the chunks' partials into dA and dB in chunk order (deterministic; the
+//                      leaves are added into, as the reference's rows add into the step's f32
+//                      gradients).
 //   transpose2_kernel  B [N, r] -> B^T [rd, N] (zero rows up to the 16-wide rank) and
 //                      A [r, K] -> A^T [K, r], in one launch.
 #include <hip/hip_runtime.h>
@@ -33,6 +37,7 @@ typedef __bf16 bf16x8 __attribute__((__vector_size__(16)));
 typedef float f32x4 __attribute__((__vector_size__(16)));
 typedef short s16x4 __attribute__((__vector_size__(4 * sizeof(short))));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // a native 16-byte vector (registers)
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -46,16 +51,30 @@ __device__ __forceinline__ void split(float v, uint16_t& hi, uint16_t& lo) {
     lo = f32_to_bf16(v - bf16_to_f32(hi));
 }
 
+// the two transposing reads of a B operand (k = 8g..8g+3, then 8g+4..8g+7) as one bf16x8
+__device__ __forceinline__ bf16x8 tr_pair(s16x4 lo4, s16x4 hi4) {
+    const uint4 w = {(uint32_t)(uint16_t)lo4[0] | ((uint32_t)(uint16_t)lo4[1] << 16),
+                     (uint32_t)(uint16_t)lo4[2] | ((uint32_t)(uint16_t)lo4[3] << 16),
+                     (uint32_t)(uint16_t)hi4[0] | ((uint32_t)(uint16_t)hi4[1] << 16),
+                     (uint32_t)(uint16_t)hi4[2] | ((uint32_t)(uint16_t)hi4[3] << 16)};
+    return as_bf16x8(w);
+}
+
 // ---------------------------------------------------------------- down
+// One workgroup = 16 token rows; its nw waves (8, or 4 when Kin is not a multiple of 256) each
+// reduce a contiguous nw-th of Kin, then the partial sums are added in wave order through LDS.
+constexpr int kDownWavesMax = 8;
+
 template <int RD>
-__global__ __launch_bounds__(256) void lora_down_kernel(DownArgs a) {
-    __shared__ float red[4][16][RD];
+__global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
+    __shared__ float red[kDownWavesMax][16][RD];
+    const int nw = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row16 = lane & 15, grp = lane >> 4;
     const int64_t m0 = (int64_t)blockIdx.x * 16;
     int64_t row = m0 + row16;
     if (row > a.T - 1) row = a.T - 1;
-    const int64_t kq = a.Kin / 4;  // a multiple of 32
+    const int64_t kq = a.Kin / nw;  // a multiple of 32
     const uint16_t* ap = a.In + row * a.Kin + wave * kq + 8 * grp;
     const uint16_t* wp = a.W + (int64_t)row16 * a.Kin + wave * kq + 8 * grp;
     constexpr int NB = RD / 16;
@@ -89,11 +108,12 @@ __global__ __launch_bounds__(256) void lora_down_kernel(DownArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) red[wave][4 * grp + e][16 * nb + row16] = acc[nb][e];
     __syncthreads();
-    for (int i = threadIdx.x; i < 16 * RD; i += 256) {
+    for (int i = threadIdx.x; i < 16 * RD; i += blockDim.x) {
         const int ml = i / RD, j = i % RD;
         const int64_t m = m0 + ml;
         if (j >= a.r || m >= a.ldt) continue;
-        const float v = ((red[0][ml][j] + red[1][ml][j]) + red[2][ml][j]) + red[3][ml][j];
+        float v = red[0][ml][j];
+        for (int w = 1; w < nw; ++w) v += red[w][ml][j];
         uint16_t hi = 0, lo = 0;
         if (m < a.T) {
             if (a.out) a.out[m * a.r + j] = a.sa * v;
@@ -118,74 +138,183 @@ __global__ __launch_bounds__(256) void lora_down_kernel(DownArgs a) {
 }
 
 // ---------------------------------------------------------------- grads
-// C[v][c] = sum_m Pt[v][m] V[m][c] over the chunk's rows, v = 0..2r-1 (hi rows then lo rows);
-// out gets scale * (C[j][c] + C[r+j][c]).
+// part[chunk][j][c] = scale * sum_{m in chunk} (Pt[j][m] + Pt[r+j][m]) V[m][c]   (j < r)
+// computed as C[v][c] = sum_m Pt[v][m] V[m][c] over the 2r [hi | lo] rows v, then out (+)= the
+// sum of the chunks' parts in chunk order (grad_reduce_kernel): no atomics, so dA and dB are the
+// same bits on every call.
+//
+// A workgroup = 512 columns (8 waves x 64) x a token chunk, walked TOK tokens at a time. Tiles
+// stream global -> registers -> LDS: each wave loads TOK/8 token rows (one 1 KiB row each) of a
+// tile and NP 1 KiB pieces of the tile's Pt rows (2r rows x TOK tokens); a tile is loaded three
+// iterations before it is multiplied (two register sets in flight) and written to one of two LDS
+// slots the iteration before. The token tile is read back transposed with ds_read_b64_tr_b16
+// (the MFMA's B operand), the Pt rows straight (the A operand). Token rows are padded to 1088
+// bytes so the transposing reads of four consecutive rows land on distinct banks.
+constexpr int kGradCols = 512;
+constexpr int kGradRow = 2 * kGradCols + 64;
+
 template <int R>
-__global__ __launch_bounds__(256) void lora_grads_kernel(GradArgs ga) {
-    constexpr int R2 = 2 * R;
-    constexpr int VB = (R2 + 15) / 16;  // 16-row blocks of the [hi | lo] operand
-    __shared__ __attribute__((aligned(16))) uint16_t tile[32 * 64];
-    __shared__ float cred[R2 < 16 ? 16 : R2][64];
+struct GradShape {
+    static constexpr int R2 = 2 * R;
+    static constexpr int VB = R2 / 16;                  // 16-row blocks of Pt (R is 8, 16, 32 or 64)
+    static constexpr int TOK = R == 64 ? 32 : 64;       // tokens a tile (two LDS slots fit 160 KiB)
+    static constexpr int ROWS = TOK / 8;                // token rows a wave loads
+    static constexpr int PTB = R2 * TOK * 2;            // Pt bytes a tile
+    static constexpr int NP = (PTB / 1024 + 7) / 8;     // 1 KiB Pt pieces a wave loads
+    static constexpr int NREG = ROWS + NP;
+    static constexpr int VTILE = TOK * kGradRow;
+    static constexpr int SLOT = VTILE + PTB;
+};
+
+// one lane's loads of a gradient tile: its token rows (16 bytes each) and Pt pieces
+struct GradLane {
+    const uint16_t* V;
+    const uint16_t* Pt;
+    int64_t C, T, ldt, mb, gcol;
+    int wave, lane, niter;
+};
+
+template <int R>
+__device__ __forceinline__ void grad_load(const GradLane& L, int it, u32x4 (&r)[GradShape<R>::NREG]) {
+    using S = GradShape<R>;
+    if (it > L.niter - 1) it = L.niter - 1;  // past the chunk: its last tile again (never multiplied)
+#pragma unroll
+    for (int q = 0; q < S::ROWS; ++q) {  // token rows ROWS*wave + q
+        int64_t row = L.mb + S::TOK * it + S::ROWS * L.wave + q;
+        if (row > L.T - 1) row = L.T - 1;  // rows past T meet zero splits
+        r[q] = *reinterpret_cast<const u32x4*>(L.V + row * L.C + L.gcol);
+    }
+    // Pt piece p (1 KiB = 64 lanes x 16 bytes): byte 1024p + 16*lane of the tile's [2r][TOK]
+    // block; pieces past the block (waves with nothing to load) reload piece 0 and do not store
+#pragma unroll
+    for (int u = 0; u < S::NP; ++u) {
+        int piece = L.wave + 8 * u;
+        if (piece >= S::PTB / 1024) piece = 0;
+        const int byte = 1024 * piece + 16 * L.lane;
+        const int v = byte / (2 * S::TOK), m = (byte % (2 * S::TOK)) / 2;
+        r[S::ROWS + u] = *reinterpret_cast<const u32x4*>(L.Pt + (int64_t)v * L.ldt + L.mb + S::TOK * it + m);
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void grad_store(const GradLane& L, const u32x4 (&r)[GradShape<R>::NREG], uint8_t* st) {
+    using S = GradShape<R>;
+#pragma unroll
+    for (int q = 0; q < S::ROWS; ++q)
+        *reinterpret_cast<u32x4*>(st + (S::ROWS * L.wave + q) * kGradRow + 16 * L.lane) = r[q];
+#pragma unroll
+    for (int u = 0; u < S::NP; ++u) {
+        const int piece = L.wave + 8 * u;
+        if (piece < S::PTB / 1024) *reinterpret_cast<u32x4*>(st + S::VTILE + 1024 * piece + 16 * L.lane) = r[S::ROWS + u];
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void grad_multiply(const uint8_t* st, int wave, int i16, int grp,
+                                              f32x4 (&acc)[GradShape<R>::VB][4]) {
+    using S = GradShape<R>;
+#pragma unroll
+    for (int ks = 0; ks < S::TOK / 32; ++ks) {
+        bf16x8 pa[S::VB];  // lane (i, grp): Pt row 16vb + i, tokens 32ks + 8grp .. +8
+#pragma unroll
+        for (int vb = 0; vb < S::VB; ++vb)
+            pa[vb] = as_bf16x8(*reinterpret_cast<const uint4*>(st + S::VTILE + (16 * vb + i16) * (2 * S::TOK) +
+                                                                2 * (32 * ks + 8 * grp)));
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            const int col = 64 * wave + 16 * cb;
+            const int e = i16 >> 2, q = i16 & 3;
+            const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(st + (32 * ks + 8 * grp + e) * kGradRow + (col + 4 * q) * 2));
+            const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(st + (32 * ks + 8 * grp + 4 + e) * kGradRow + (col + 4 * q) * 2));
+            const bf16x8 bv = tr_pair(lo4, hi4);
+#pragma unroll
+            for (int vb = 0; vb < S::VB; ++vb) acc[vb][cb] = mfma16(pa[vb], bv, acc[vb][cb]);
+        }
+    }
+}
+
+template <int R>
+__global__ __launch_bounds__(512) void lora_grads_kernel(GradArgs ga) {
+    using S = GradShape<R>;
+    constexpr int VB = S::VB;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * S::SLOT];
     const GradOne& g = ga.one[blockIdx.z];
     const int64_t C = g.C;
-    const int64_t c0 = (int64_t)blockIdx.x * 64;
+    const int64_t c0 = (int64_t)blockIdx.x * kGradCols;
     if (c0 >= C) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i16 = lane & 15, grp = lane >> 4;
     const int64_t mb = (int64_t)blockIdx.y * ga.chunk;
     int64_t me = mb + ga.chunk;
     if (me > ga.ldt) me = ga.ldt;
-    f32x4 acc[VB];
-#pragma unroll
-    for (int vb = 0; vb < VB; ++vb) acc[vb] = (f32x4){};
-    // staging: thread t loads row t/8 (of 32), 16 bytes at column chunk t%8 (of 8): coalesced
-    const int lr = threadIdx.x >> 3, lc = threadIdx.x & 7;
-    for (int64_t m = mb; m < me; m += 32) {
-        int64_t row = m + lr;
-        if (row > ga.T - 1) row = ga.T - 1;  // rows past T meet zero splits
-        const uint4 v = *reinterpret_cast<const uint4*>(g.V + row * C + c0 + 8 * lc);
-        __syncthreads();
-        *reinterpret_cast<uint4*>(&tile[lr * 64 + 8 * lc]) = v;
-        __syncthreads();
-        // B operand (m x c): lane 16*grp + i needs V[m + 8*grp + 0..7][c0 + 16*wave + i]; two
-        // transposing reads give rows 4h..4h+3 of the group: lane 16*grp + 4e + q addresses
-        // row 8*grp + 4h + e, columns 16*wave + 4q .. +3
-        const int e = i16 >> 2, q = i16 & 3;
-        s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)((__attribute__((address_space(3))) uint16_t*)tile + (8 * grp + e) * 64 + 16 * wave + 4 * q));
-        s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)((__attribute__((address_space(3))) uint16_t*)tile + (8 * grp + 4 + e) * 64 + 16 * wave + 4 * q));
-        const uint4 bw = {(uint32_t)(uint16_t)lo4[0] | ((uint32_t)(uint16_t)lo4[1] << 16),
-                          (uint32_t)(uint16_t)lo4[2] | ((uint32_t)(uint16_t)lo4[3] << 16),
-                          (uint32_t)(uint16_t)hi4[0] | ((uint32_t)(uint16_t)hi4[1] << 16),
-                          (uint32_t)(uint16_t)hi4[2] | ((uint32_t)(uint16_t)hi4[3] << 16)};
-        const bf16x8 bv = as_bf16x8(bw);
-        // A operand (v x m): lane 16*grp + i holds Pt[16*vb + i][m + 8*grp .. +7]
-#pragma unroll
-        for (int vb = 0; vb < VB; ++vb) {
-            const int vr = 16 * vb + i16;
-            uint4 aw = {0u, 0u, 0u, 0u};
-            if (vr < R2) aw = *reinterpret_cast<const uint4*>(g.Pt + (int64_t)vr * ga.ldt + m + 8 * grp);
-            acc[vb] = mfma16(as_bf16x8(aw), bv, acc[vb]);
-        }
-    }
-    // acc element e of block vb: row v = 16*vb + 4*grp + e, column 16*wave + i16
+    const int niter = (int)((me - mb) / S::TOK);
+    // the lane's 8 columns of every row it loads (columns past C read column c0 instead and their
+    // results are never stored)
+    const int64_t gcol = c0 + 8 * lane < C ? c0 + 8 * lane : c0;
+
+    f32x4 acc[VB][4];
 #pragma unroll
     for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int vr = 16 * vb + 4 * grp + e;
-            if (vr < R2) cred[vr][16 * wave + i16] = acc[vb][e];
-        }
+        for (int cb = 0; cb < 4; ++cb) acc[vb][cb] = (f32x4){};
+    const GradLane L{g.V, g.Pt, C, ga.T, ga.ldt, mb, gcol, wave, lane, niter};
+    // iteration it: multiply slot it&1, write tile it+1 (its registers) into the other slot (a
+    // tile past the chunk's end goes into the slot no wave reads again), one barrier, then reload
+    // those registers with tile it+3. Unrolled by two so the register sets keep fixed names.
+    u32x4 ra[S::NREG], rb[S::NREG];
+    grad_load<R>(L, 0, ra);
+    grad_load<R>(L, 1, rb);
+    grad_store<R>(L, ra, lds);
+    grad_load<R>(L, 2, ra);
     __syncthreads();
-    for (int i = threadIdx.x; i < R * 64; i += 256) {
-        const int j = i / 64, cc = i % 64;
-        const int64_t c = c0 + cc;
-        if (c >= C) continue;
-        const float v = g.scale * (cred[j][cc] + cred[R + j][cc]);
-        float* d = g.transposed ? g.out + c * R + j : g.out + (int64_t)j * C + c;
-        atomicAdd(d, v);
+    for (int it = 0; it < niter; it += 2) {
+        grad_multiply<R>(lds, wave, i16, grp, acc);
+        grad_store<R>(L, rb, lds + S::SLOT);
+        __syncthreads();
+        grad_load<R>(L, it + 3, rb);
+        if (it + 1 >= niter) break;
+        grad_multiply<R>(lds + S::SLOT, wave, i16, grp, acc);
+        grad_store<R>(L, ra, lds);
+        __syncthreads();
+        grad_load<R>(L, it + 4, ra);
     }
+    // acc element e of block (vb, cb): row v = 16vb + 4grp + e, column c0 + 64*wave + 16cb + i16.
+    // Row j (< R) pairs with row R + j: the same lane and element VB/2 blocks on, or, for R = 8
+    // (one block), the lane 32 on.
+    float* part = g.part + (int64_t)blockIdx.y * R * C;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+        const int64_t c = c0 + 64 * wave + 16 * cb + i16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if constexpr (R >= 16) {
+#pragma unroll
+                for (int vb = 0; vb < VB / 2; ++vb) {
+                    const int j = 16 * vb + 4 * grp + e;
+                    if (c < C) part[(int64_t)j * C + c] = g.scale * (acc[vb][cb][e] + acc[vb + VB / 2][cb][e]);
+                }
+            } else {
+                const float other = __shfl_xor(acc[0][cb][e], 32);
+                const int j = 4 * grp + e;
+                if (grp < 2 && c < C) part[(int64_t)j * C + c] = g.scale * (acc[0][cb][e] + other);
+            }
+        }
+    }
+}
+
+// out (+)= sum over chunks, in chunk order, of part[chunk][j][c]; out is [r, C] row-major or,
+// `transposed`, [C, r]. One thread a (j, c).
+__global__ __launch_bounds__(256) void grad_reduce_kernel(GradArgs ga, int r, int nchunks) {
+    const GradOne& g = ga.one[blockIdx.y];
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)r * g.C) return;
+    const int64_t j = i / g.C, c = i % g.C;
+    float v = 0.0f;
+    for (int ch = 0; ch < nchunks; ++ch) v += g.part[((int64_t)ch * r + j) * g.C + c];
+    float* d = g.transposed ? g.out + c * r + j : g.out + i;
+    *d += v;
 }
 
 // ---------------------------------------------------------------- transposes
@@ -209,23 +338,28 @@ __global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* __restr
 
 template <int RD>
 int down_r(const DownArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(lora_down_kernel<RD>, dim3((unsigned)((a.ldt + 15) / 16)), dim3(256), 0, s, a);
+    const int nw = a.Kin % 256 == 0 ? kDownWavesMax : 4;
+    hipLaunchKernelGGL(lora_down_kernel<RD>, dim3((unsigned)((a.ldt + 15) / 16)), dim3(64 * nw), 0, s, a);
     return launch_status("lora_down_kernel");
 }
 
 template <int R>
 int grads_r(const GradArgs& g, int64_t cmax, int nz, hipStream_t s) {
     const int64_t chunks = (g.ldt + g.chunk - 1) / g.chunk;
-    hipLaunchKernelGGL(lora_grads_kernel<R>, dim3((unsigned)((cmax + 63) / 64), (unsigned)chunks, (unsigned)nz),
-                       dim3(256), 0, s, g);
-    return launch_status("lora_grads_kernel");
+    hipLaunchKernelGGL(lora_grads_kernel<R>, dim3((unsigned)((cmax + kGradCols - 1) / kGradCols), (unsigned)chunks,
+                                                  (unsigned)nz),
+                       dim3(512), 0, s, g);
+    if (int e = launch_status("lora_grads_kernel")) return e;
+    hipLaunchKernelGGL(grad_reduce_kernel, dim3((unsigned)((R * cmax + 255) / 256), (unsigned)nz), dim3(256), 0, s, g,
+                       R, (int)chunks);
+    return launch_status("grad_reduce_kernel");
 }
 
 }  // namespace
 
 int down_rank(int r) { return (r + 15) / 16 * 16; }
 
-int64_t grad_ld(int64_t T) { return (T + 31) / 32 * 32; }
+int64_t grad_ld(int64_t T) { return (T + 63) / 64 * 64; }
 
 int launch_lora_down(const DownArgs& a, hipStream_t s) {
     switch (down_rank(a.r)) {
@@ -238,15 +372,27 @@ int launch_lora_down(const DownArgs& a, hipStream_t s) {
     }
 }
 
-int launch_lora_grads(int r, GradArgs g, int nz, hipStream_t s) {
+int64_t grad_chunks(int64_t T, int64_t K, int64_t N) {
+    // about 256 workgroups over dA's and dB's column blocks (one a CU)
+    const int64_t cols = (K + kGradCols - 1) / kGradCols + (N + kGradCols - 1) / kGradCols;
+    int64_t chunks = (256 + cols - 1) / cols;
+    const int64_t tiles = grad_ld(T) / 64;  // no chunk smaller than one 64-token tile
+    if (chunks > tiles) chunks = tiles;
+    return chunks < 1 ? 1 : chunks;
+}
+
+int64_t grad_chunk_rows(int64_t T, int64_t K, int64_t N) {
+    const int64_t chunks = grad_chunks(T, K, N);
+    const int64_t ldt = grad_ld(T);
+    return ((ldt + chunks - 1) / chunks + 63) / 64 * 64;  // whole 64-token tiles
+}
+
+int launch_lora_grads(int r, const GradArgs& g, int nz, hipStream_t s) {
     const int64_t cmax = nz > 1 && g.one[1].C > g.one[0].C ? g.one[1].C : g.one[0].C;
-    // about 512 workgroups: chunks of whole 32-row steps
-    const int64_t cols = (cmax + 63) / 64 * nz;
-    int64_t chunks = (512 + cols - 1) / cols;
-    if (chunks < 1) chunks = 1;
-    int64_t chunk = (g.ldt + chunks - 1) / chunks;
-    chunk = (chunk + 31) / 32 * 32;
-    g.chunk = chunk;
+    if (g.chunk <= 0 || g.chunk % 64 != 0) {
+        set_error("lora grads: chunk %lld is not a positive multiple of 64", (long long)g.chunk);
+        return R97Q_EINVAL;
+    }
     switch (r) {
         case 8: return grads_r<8>(g, cmax, nz, s);
         case 16: return grads_r<16>(g, cmax, nz, s);

@@ -34,7 +34,8 @@ struct Shape {
 };
 
 // Workspace layout. Forward: P [T, 2r] | Apad [rd, K] (when r is not a multiple of 16).
-// Backward: Bt [rd, N] | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt].
+// Backward: Bt [rd, N] | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt] | partA [chunks, r, K]
+// | partB [chunks, r, N] (f32 partial sums of the factor gradients).
 struct FwdWs {
     int64_t P, Apad, total;
 };
@@ -48,7 +49,7 @@ FwdWs fwd_ws(const Shape& s) {
     return w;
 }
 struct BwdWs {
-    int64_t Bt, At, P, PtA, PtB, total;
+    int64_t Bt, At, P, PtA, PtB, partA, partB, total;
 };
 BwdWs bwd_ws(const Shape& s) {
     BwdWs w{};
@@ -60,7 +61,10 @@ BwdWs bwd_ws(const Shape& s) {
     w.P = w.At + align256(s.K * s.r * 2);
     w.PtA = w.P + align256(s.T * 2 * s.r * 2);
     w.PtB = w.PtA + align256(2 * s.r * ldt * 2);
-    w.total = w.PtB + align256(2 * s.r * ldt * 2);
+    const int64_t chunks = grad_chunks(s.T, s.K, s.N);
+    w.partA = w.PtB + align256(2 * s.r * ldt * 2);
+    w.partB = w.partA + align256(chunks * s.r * s.K * 4);
+    w.total = w.partB + align256(chunks * s.r * s.N * 4);
     return w;
 }
 
@@ -200,9 +204,14 @@ int bwd_grads(const Shape& sh, const uint16_t* X, const uint16_t* dY, float* dA,
     GradArgs g{};
     g.T = sh.T;
     g.ldt = grad_ld(sh.T);
+    g.chunk = grad_chunk_rows(sh.T, sh.K, sh.N);
     int nz = 0;
-    if (dA) g.one[nz++] = GradOne{reinterpret_cast<const uint16_t*>(wsb + ws.PtA), X, sh.K, dA, 1.0f, 0};
-    if (dB) g.one[nz++] = GradOne{reinterpret_cast<const uint16_t*>(wsb + ws.PtB), dY, sh.N, dB, 1.0f, 1};
+    if (dA)
+        g.one[nz++] = GradOne{reinterpret_cast<const uint16_t*>(wsb + ws.PtA), X, sh.K, dA, 1.0f, 0,
+                              reinterpret_cast<float*>(wsb + ws.partA)};
+    if (dB)
+        g.one[nz++] = GradOne{reinterpret_cast<const uint16_t*>(wsb + ws.PtB), dY, sh.N, dB, 1.0f, 1,
+                              reinterpret_cast<float*>(wsb + ws.partB)};
     if (nz == 0) return R97Q_OK;
     return launch_lora_grads(sh.r, g, nz, s);
 }
