@@ -227,6 +227,28 @@ int r97q_qlinear_dx_base(const R97qWeight* w, const uint16_t* dY, int64_t T, int
                          int32_t dx_dtype, int32_t dx_accumulate, void* workspace,
                          int64_t workspace_bytes, R97IqrStream stream);
 
+/* ------------------------------------------------------------------ the adapter's rows on their own
+ *
+ * The shrink's and the expand's adjoints as separate calls, for a caller whose backward walk runs
+ * them as separate rows (the reference's device rows lora_shrink_device_adjoint and
+ * lora_expand_device_adjoint, src/adjoint/device/lora.hip:439-571, whose host twins are
+ * src/adjoint/host/lora.cpp:260-328 and 451-521). One adapter slot, every row served; the caller
+ * masks base rows by zeroing their cotangent rows.
+ *
+ * Shrink: dX (+)= t_cot . A (f32 [T, K]; added into when dx_accumulate) and dA += t_cot^T . X
+ * (f32 [r, K]); t_cot f32 [T, r] enters the MFMAs as an [hi | lo] bf16 pair. Either output may be
+ * NULL (dA needs X). */
+int64_t r97q_lora_shrink_bwd_workspace_bytes(int64_t T, int64_t K, int32_t rank);
+int r97q_lora_shrink_bwd(int64_t T, int64_t K, const uint16_t* X, const uint16_t* A, int32_t rank,
+                         const float* t_cot, float* dX, int32_t dx_accumulate, float* dA, void* workspace,
+                         int64_t workspace_bytes, R97IqrStream stream);
+/* Expand: t_cot += scale . dY . B (f32 [T, r]) and dB += scale . dY^T . t (f32 [N, r]). Either
+ * output may be NULL (dB needs t). */
+int64_t r97q_lora_expand_bwd_workspace_bytes(int64_t T, int64_t N, int32_t rank);
+int r97q_lora_expand_bwd(int64_t T, int64_t N, const uint16_t* dY, const uint16_t* B, int32_t rank, float scale,
+                         const float* t, float* t_cot, float* dB, void* workspace, int64_t workspace_bytes,
+                         R97IqrStream stream);
+
 #ifdef __cplusplus
 }
 #endif

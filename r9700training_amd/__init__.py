@@ -67,6 +67,10 @@ SIGNATURES = {
     "r97q_qlinear_fwd_base": (C.c_int, [C.POINTER(Weight), _P, _I, _P, _i, _P, _i, _P, _I, _P]),
     "r97q_lora_bwd_prep": (C.c_int, [_I, _I, _I, _P, _P, _P, _P, _i, C.c_float, _P, _I, _P]),
     "r97q_lora_bwd_grads": (C.c_int, [_I, _I, _I, _P, _P, _i, _P, _P, _P, _I, _P]),
+    "r97q_lora_shrink_bwd_workspace_bytes": (_I, [_I, _I, _i]),
+    "r97q_lora_shrink_bwd": (C.c_int, [_I, _I, _P, _P, _i, _P, _P, _i, _P, _P, _I, _P]),
+    "r97q_lora_expand_bwd_workspace_bytes": (_I, [_I, _I, _i]),
+    "r97q_lora_expand_bwd": (C.c_int, [_I, _I, _P, _P, _i, C.c_float, _P, _P, _P, _P, _I, _P]),
     "r97q_qlinear_dx_base": (C.c_int, [C.POINTER(Weight), _P, _I, _i, _P, _i, _i, _P, _I, _P]),
 }
 

@@ -8,7 +8,7 @@ namespace r97q {
 
 // v[m][j] = sum_k In[m][k] W[j][k] for m < T, j < r (W row-major [down_rank(r), Kin], rows past r
 // zero; Kin a multiple of 128). Writes, each when non-null:
-//   out [T, r] f32    = sa * v
+//   out [T, r] f32    = sa * v   (+= when out_add)
 //   P   [T, 2r] bf16  = [hi | lo](sb * v)                    (row-major)
 //   Pt  [2r, ldt] bf16 = [hi | lo](sb * v), transposed       (zero for T <= m < ldt)
 //   Pt2 [2r, ldt] bf16 = [hi | lo](s2 * U2[m][j]), transposed (U2 f32 [T, r])
@@ -24,6 +24,7 @@ struct DownArgs {
     const float* U2;
     float s2;
     uint16_t* Pt2;
+    int out_add;  // out += (instead of =)
 };
 
 // out += scale * sum_m (Pt[j][m] + Pt[r+j][m]) V[m][c]: V bf16 [T, C] (C a multiple of 128), out
@@ -55,5 +56,11 @@ int launch_lora_down(const DownArgs& a, hipStream_t s);
 int launch_lora_grads(int r, const GradArgs& g, int nz, hipStream_t s);
 int launch_transpose2(const uint16_t* B, uint16_t* Bt, int64_t N, const uint16_t* A, uint16_t* At,
                       int64_t K, int r, hipStream_t s);
+// P [T, 2r] / Pt [2r, ldt] = [hi | lo](scale * U), U f32 [T, r]; either output may be null
+int launch_split(const float* U, int64_t T, int r, int64_t ldt, float scale, uint16_t* P, uint16_t* Pt,
+                 hipStream_t s);
+// out [T, C] f32 (+)= [hi | lo](P) . [Q | Q]^T: P [T, 2r] bf16, Q [C, r] bf16 (C a multiple of 128)
+int launch_lora_up(const uint16_t* P, const uint16_t* Q, int64_t T, int64_t C, int r, float* out, int accumulate,
+                   hipStream_t s);
 
 }  // namespace r97q

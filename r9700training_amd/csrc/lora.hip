@@ -20,6 +20,9 @@
 //   grad_reduce_kernel adds the chunks' partials into dA and dB in chunk order (deterministic; the
 //                      leaves are added into, as the reference's rows add into the step's f32
 //                      gradients).
+//   split_kernel       an f32 [T, r] operand (a cotangent handed in) -> its [hi | lo] splits.
+//   lora_up_kernel     the up-projection t_cot . A of the shrink's adjoint, on its own (the fused
+//                      dX kernel carries it in its epilogue when the base product runs too).
 //   transpose2_kernel  B [N, r] -> B^T [rd, N] (zero rows up to the 16-wide rank) and
 //                      A [r, K] -> A^T [K, r], in one launch.
 #include <hip/hip_runtime.h>
@@ -116,7 +119,7 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
         for (int w = 1; w < nw; ++w) v += red[w][ml][j];
         uint16_t hi = 0, lo = 0;
         if (m < a.T) {
-            if (a.out) a.out[m * a.r + j] = a.sa * v;
+            if (a.out) a.out[m * a.r + j] = a.out_add ? a.out[m * a.r + j] + a.sa * v : a.sa * v;
             split(a.sb * v, hi, lo);
             if (a.P) {
                 a.P[m * 2 * a.r + j] = hi;
@@ -317,6 +320,81 @@ __global__ __launch_bounds__(256) void grad_reduce_kernel(GradArgs ga, int r, in
     *d += v;
 }
 
+// ---------------------------------------------------------------- split and up
+// P [T, 2r] = [hi | lo](s * U[m][j]) row-major, Pt [2r, ldt] the same transposed (zero for
+// T <= m < ldt). One thread an (m, j), m < ldt.
+__global__ __launch_bounds__(256) void split_kernel(const float* __restrict__ U, int64_t T, int r, int64_t ldt,
+                                                    float s, uint16_t* __restrict__ P, uint16_t* __restrict__ Pt) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= ldt * r) return;
+    const int64_t m = i / r;
+    const int j = (int)(i % r);
+    uint16_t hi = 0, lo = 0;
+    if (m < T) split(s * U[m * r + j], hi, lo);
+    if (m < T && P) {
+        P[m * 2 * r + j] = hi;
+        P[m * 2 * r + r + j] = lo;
+    }
+    if (Pt) {
+        Pt[(int64_t)j * ldt + m] = hi;
+        Pt[(int64_t)(r + j) * ldt + m] = lo;
+    }
+}
+
+// out[m][c] (+)= sum_{v < 2r} P[m][v] Q[c][v mod r]: the up-projection of an [hi | lo] split
+// through a factor held output-major (Q = A^T [C, r] for dx = t_cot . A). A workgroup = 4 waves =
+// 32 token rows x 256 columns; a wave's 32 x 64 tile is 2 x 4 v_mfma_f32_16x16x32_bf16 blocks.
+__global__ __launch_bounds__(256) void lora_up_kernel(const uint16_t* __restrict__ P, const uint16_t* __restrict__ Q,
+                                                      int64_t T, int64_t C, int r, float* __restrict__ out,
+                                                      int accumulate) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i16 = lane & 15, g = lane >> 4;
+    const int64_t m0 = (int64_t)blockIdx.y * 32;
+    const int64_t c0 = (int64_t)blockIdx.x * 256 + 64 * wave;
+    if (c0 >= C) return;
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[mb][cb] = (f32x4){};
+    for (int kk = 0; kk < 2 * r; kk += 32) {
+        const int kq = kk + 8 * g;
+        const bool live = kq < 2 * r;  // rank 8: 2r = 16 fills half of the 32-deep slice
+        bf16x8 pa[2], qb[4];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            int64_t row = m0 + 16 * mb + i16;
+            if (row > T - 1) row = T - 1;
+            pa[mb] = as_bf16x8(live ? *reinterpret_cast<const uint4*>(P + row * 2 * r + kq) : uint4{0u, 0u, 0u, 0u});
+        }
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            int64_t c = c0 + 16 * cb + i16;
+            if (c > C - 1) c = C - 1;
+            qb[cb] = as_bf16x8(live ? *reinterpret_cast<const uint4*>(Q + c * r + (kq % r)) : uint4{0u, 0u, 0u, 0u});
+        }
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) acc[mb][cb] = mfma16(pa[mb], qb[cb], acc[mb][cb]);
+    }
+    // element e of block (mb, cb): row 16mb + 4g + e, column 16cb + i16
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t m = m0 + 16 * mb + 4 * g + e;
+            if (m >= T) continue;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                const int64_t c = c0 + 16 * cb + i16;
+                if (c >= C) continue;
+                float* d = out + m * C + c;
+                *d = accumulate ? *d + acc[mb][cb][e] : acc[mb][cb][e];
+            }
+        }
+}
+
 // ---------------------------------------------------------------- transposes
 // y 0: Bt[q][n] = B[n][q] for q < r, 0 for r <= q < rd;  y 1: At[k][j] = A[j][k]
 __global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* __restrict__ B,
@@ -402,6 +480,20 @@ int launch_lora_grads(int r, const GradArgs& g, int nz, hipStream_t s) {
             set_error("lora grads: rank %d not served", r);
             return R97Q_EUNSUPPORTED;
     }
+}
+
+int launch_split(const float* U, int64_t T, int r, int64_t ldt, float scale, uint16_t* P, uint16_t* Pt,
+                 hipStream_t s) {
+    hipLaunchKernelGGL(split_kernel, dim3((unsigned)((ldt * r + 255) / 256)), dim3(256), 0, s, U, T, r, ldt, scale, P,
+                       Pt);
+    return launch_status("split_kernel");
+}
+
+int launch_lora_up(const uint16_t* P, const uint16_t* Q, int64_t T, int64_t C, int r, float* out, int accumulate,
+                   hipStream_t s) {
+    hipLaunchKernelGGL(lora_up_kernel, dim3((unsigned)((C + 255) / 256), (unsigned)((T + 31) / 32)), dim3(256), 0, s,
+                       P, Q, T, C, r, out, accumulate);
+    return launch_status("lora_up_kernel");
 }
 
 int launch_transpose2(const uint16_t* B, uint16_t* Bt, int64_t N, const uint16_t* A, uint16_t* At,

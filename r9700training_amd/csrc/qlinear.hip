@@ -68,6 +68,37 @@ BwdWs bwd_ws(const Shape& s) {
     return w;
 }
 
+// The adapter rows on their own (the shrink's and the expand's adjoints), workspace layouts:
+// shrink: P [T, 2r] | Pt [2r, ldt] | At [K, r] | part [chunks, r, K]
+// expand: Bt [rd, N] | Pt2 [2r, ldt] | part [chunks, r, N]
+struct ShrinkWs {
+    int64_t P, Pt, At, part, total;
+};
+ShrinkWs shrink_ws(int64_t T, int64_t K, int r) {
+    ShrinkWs w{};
+    if (r == 0) return w;
+    const int64_t ldt = grad_ld(T);
+    w.P = 0;
+    w.Pt = w.P + align256(T * 2 * r * 2);
+    w.At = w.Pt + align256(2 * r * ldt * 2);
+    w.part = w.At + align256(K * r * 2);
+    w.total = w.part + align256(grad_chunks(T, K, 0) * r * K * 4);
+    return w;
+}
+struct ExpandWs {
+    int64_t Bt, Pt2, part, total;
+};
+ExpandWs expand_ws(int64_t T, int64_t N, int r) {
+    ExpandWs w{};
+    if (r == 0) return w;
+    const int64_t ldt = grad_ld(T);
+    w.Bt = 0;
+    w.Pt2 = w.Bt + align256((int64_t)down_rank(r) * N * 2);
+    w.part = w.Pt2 + align256(2 * r * ldt * 2);
+    w.total = w.part + align256(grad_chunks(T, 0, N) * r * N * 4);
+    return w;
+}
+
 // zero-fill + copy of a [r, cols] bf16 matrix into [rd, cols] (rows r..rd-1 zero)
 __global__ __launch_bounds__(256) void pad_rows16(const uint16_t* __restrict__ in, int r, int rd,
                                                   int64_t cols, uint16_t* __restrict__ out) {
@@ -402,6 +433,104 @@ int r97q_qlinear_lora_bwd(const R97qWeight* w, const uint16_t* X, const uint16_t
         if (int e = bwd_grads(sh, X, dY, dA, dB, wsb, s)) return e;
     }
     return dx_base(w, sh, dY, dX, dx_dtype, dx_accumulate, wsb, s);
+}
+
+int64_t r97q_lora_shrink_bwd_workspace_bytes(int64_t T, int64_t K, int32_t rank) {
+    return rank_ok(rank) && T > 0 && K > 0 ? shrink_ws(T, K, rank).total : -1;
+}
+
+int r97q_lora_shrink_bwd(int64_t T, int64_t K, const uint16_t* X, const uint16_t* A, int32_t rank,
+                         const float* t_cot, float* dX, int32_t dx_accumulate, float* dA, void* workspace,
+                         int64_t workspace_bytes, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_lora_shrink_bwd";
+    if (T <= 0 || K <= 0 || K % kBN) {
+        set_error("%s: T %lld K %lld (T > 0, K a multiple of 128)", who, (long long)T, (long long)K);
+        return R97Q_EINVAL;
+    }
+    if (int e = check_rank(rank, who)) return e;
+    if (rank == 0 || (!dX && !dA)) return R97Q_OK;
+    if (!A || !t_cot || (dA && !X)) {
+        set_error("%s: null A or t_cot, or dA without X", who);
+        return R97Q_EINVAL;
+    }
+    const ShrinkWs ws = shrink_ws(T, K, rank);
+    if (int e = check_ws(workspace_bytes, ws.total, workspace, who)) return e;
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    const hipStream_t s = (hipStream_t)stream;
+    const int64_t ldt = grad_ld(T);
+    uint16_t* P = reinterpret_cast<uint16_t*>(wsb + ws.P);
+    uint16_t* Pt = reinterpret_cast<uint16_t*>(wsb + ws.Pt);
+    uint16_t* At = reinterpret_cast<uint16_t*>(wsb + ws.At);
+    if (int e = launch_split(t_cot, T, rank, ldt, 1.0f, P, dA ? Pt : nullptr, s)) return e;
+    if (dX) {
+        if (int e = launch_transpose2(nullptr, nullptr, 0, A, At, K, rank, s)) return e;
+        if (int e = launch_lora_up(P, At, T, K, rank, dX, dx_accumulate, s)) return e;
+    }
+    if (dA) {
+        GradArgs g{};
+        g.T = T;
+        g.ldt = ldt;
+        g.chunk = grad_chunk_rows(T, K, 0);
+        g.one[0] = GradOne{Pt, X, K, dA, 1.0f, 0, reinterpret_cast<float*>(wsb + ws.part)};
+        if (int e = launch_lora_grads(rank, g, 1, s)) return e;
+    }
+    return R97Q_OK;
+}
+
+int64_t r97q_lora_expand_bwd_workspace_bytes(int64_t T, int64_t N, int32_t rank) {
+    return rank_ok(rank) && T > 0 && N > 0 ? expand_ws(T, N, rank).total : -1;
+}
+
+int r97q_lora_expand_bwd(int64_t T, int64_t N, const uint16_t* dY, const uint16_t* B, int32_t rank, float scale,
+                         const float* t, float* t_cot, float* dB, void* workspace, int64_t workspace_bytes,
+                         R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_lora_expand_bwd";
+    if (T <= 0 || N <= 0 || N % kBN) {
+        set_error("%s: T %lld N %lld (T > 0, N a multiple of 128)", who, (long long)T, (long long)N);
+        return R97Q_EINVAL;
+    }
+    if (int e = check_rank(rank, who)) return e;
+    if (rank == 0 || (!t_cot && !dB)) return R97Q_OK;
+    if (!dY || !B || (dB && !t)) {
+        set_error("%s: null dY or B, or dB without t", who);
+        return R97Q_EINVAL;
+    }
+    const ExpandWs ws = expand_ws(T, N, rank);
+    if (int e = check_ws(workspace_bytes, ws.total, workspace, who)) return e;
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    const hipStream_t s = (hipStream_t)stream;
+    const int64_t ldt = grad_ld(T);
+    uint16_t* Bt = reinterpret_cast<uint16_t*>(wsb + ws.Bt);
+    uint16_t* Pt2 = reinterpret_cast<uint16_t*>(wsb + ws.Pt2);
+    if (int e = launch_transpose2(B, Bt, N, nullptr, nullptr, 0, rank, s)) return e;
+    DownArgs a{};
+    a.In = dY;
+    a.W = Bt;
+    a.T = T;
+    a.Kin = N;
+    a.ldt = dB ? ldt : T;
+    a.r = rank;
+    a.sa = scale;
+    a.sb = scale;
+    a.out = t_cot;
+    a.out_add = 1;
+    if (dB) {
+        a.U2 = t;
+        a.s2 = scale;
+        a.Pt2 = Pt2;
+    }
+    if (int e = launch_lora_down(a, s)) return e;
+    if (dB) {
+        GradArgs g{};
+        g.T = T;
+        g.ldt = ldt;
+        g.chunk = grad_chunk_rows(T, 0, N);
+        g.one[0] = GradOne{Pt2, dY, N, dB, 1.0f, 1, reinterpret_cast<float*>(wsb + ws.part)};
+        if (int e = launch_lora_grads(rank, g, 1, s)) return e;
+    }
+    return R97Q_OK;
 }
 
 }  // extern "C"

@@ -112,3 +112,43 @@ def qlinear_lora_bwd(w: QWeight, X, dY, A=None, B=None, t=None, scale=1.0, dx_dt
         _ptr(dB), _ptr(workspace), workspace.numel(), _stream(stream))
     check(rc, "r97q_qlinear_lora_bwd")
     return dX, dA, dB
+
+
+def _workspace(nbytes: int, device, what: str) -> torch.Tensor:
+    if nbytes < 0:
+        raise ValueError(f"{what}: shape or rank not served")
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+
+
+def lora_shrink_bwd(X, A, t_cot, dX=None, accumulate=False, dA=None, want_dA=True, workspace=None, stream=None):
+    """The shrink's adjoint on its own: dX (+)= t_cot . A (f32 [T, K]), dA += t_cot^T . X (f32 [r, K]).
+    X bf16 [T, K] (may be None when no dA is wanted), A bf16 [r, K], t_cot f32 [T, r]. Returns (dX, dA)."""
+    T, rank = t_cot.shape
+    K = A.shape[1]
+    if dX is None:
+        dX = torch.zeros((T, K), dtype=torch.float32, device=t_cot.device)
+    if want_dA and dA is None:
+        dA = torch.zeros((rank, K), dtype=torch.float32, device=t_cot.device)
+    if workspace is None:
+        workspace = _workspace(lib().r97q_lora_shrink_bwd_workspace_bytes(T, K, rank), t_cot.device, "lora_shrink_bwd")
+    rc = lib().r97q_lora_shrink_bwd(T, K, _ptr(X), _ptr(A), rank, _ptr(t_cot), _ptr(dX), int(bool(accumulate)),
+                                    _ptr(dA if want_dA else None), _ptr(workspace), workspace.numel(), _stream(stream))
+    check(rc, "r97q_lora_shrink_bwd")
+    return dX, dA
+
+
+def lora_expand_bwd(dY, B, scale, t=None, t_cot=None, dB=None, want_dB=True, workspace=None, stream=None):
+    """The expand's adjoint on its own: t_cot += scale . dY . B (f32 [T, r]), dB += scale . dY^T . t
+    (f32 [N, r]). dY bf16 [T, N], B bf16 [N, r], t f32 [T, r]. Returns (t_cot, dB)."""
+    T, N = dY.shape
+    rank = B.shape[1]
+    if t_cot is None:
+        t_cot = torch.zeros((T, rank), dtype=torch.float32, device=dY.device)
+    if want_dB and dB is None:
+        dB = torch.zeros((N, rank), dtype=torch.float32, device=dY.device)
+    if workspace is None:
+        workspace = _workspace(lib().r97q_lora_expand_bwd_workspace_bytes(T, N, rank), dY.device, "lora_expand_bwd")
+    rc = lib().r97q_lora_expand_bwd(T, N, _ptr(dY), _ptr(B), rank, float(scale), _ptr(t), _ptr(t_cot),
+                                    _ptr(dB if want_dB else None), _ptr(workspace), workspace.numel(), _stream(stream))
+    check(rc, "r97q_lora_expand_bwd")
+    return t_cot, dB
