@@ -1,0 +1,430 @@
+// rows.cpp -- the MI355X device rows of the quantized linear and its LoRA adapter, registered
+// through r97/adjoint.h so the reference's backward walk finds them where it finds its own
+// device rows (src/adjoint/device/linear.hip:744-762, src/adjoint/device/lora.hip:439-579):
+//
+//   gemm_nt      device, dtype bf16, frozen {1}     dc[a] += dy . W
+//                  W a stored IQR weight (AdValue raw + enc): the fused decode + MFMA dX kernel;
+//                  W dense bf16 values: one rocBLAS bf16 GEMM (a plain library product)
+//   lora_shrink  device, float activations, frozen {1, 2, 3}
+//                  dc[a] += t_cot . A_s,   leaf lora_A += t_cot^T . x        (per slot s)
+//   lora_expand  device, frozen {1, 2, 3}
+//                  dc[t] += (y_cot * scale_s) . B_s, leaf lora_B += (y_cot * scale_s)^T . t
+//                  and, for an in-place write, the write's own slot passes y_cot through
+//
+// Every row follows the contract's ownership rules: it adds into `dc` and the leaves, never
+// overwrites, never writes a frozen slot, and returns with its results host-visible (one
+// process-wide stream, synchronised before return). A record whose layout is malformed is left
+// untouched, as the reference's rows do; a well-formed record this build's kernels cannot serve
+// (a rank outside 8/16/32/64, a K or N not a multiple of 128, a stored form the fused kernels do not
+// decode) throws std::runtime_error naming the op and the shape, instead of dropping a gradient.
+//
+// Numerics: activations and weights arrive as f64 copies of bf16 values and are uploaded exactly;
+// a cotangent (an arbitrary f64) is split into a bf16 [hi | lo] pair and both halves are
+// multiplied (linearity), so the products carry ~16 significant bits of it; sums accumulate in f32
+// on the card and are added into the f64 slots on the host.
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "r97/adjoint.h"
+#include "r97/adjoint_family.h"
+#include "r97/stored_weight.h"
+#include "r97q.h"
+
+namespace r97 {
+namespace {
+
+// ---------------------------------------------------------------- record helpers
+int operand_pos(const OpRecord& rec, const char* name) {
+    for (size_t i = 0; i < rec.operands.size(); ++i)
+        if (rec.operands[i].buffer == name) return (int)i;
+    return -1;
+}
+
+const OpParam* find_param(const std::vector<OpParam>& params, const char* name) {
+    for (const OpParam& p : params)
+        if (p.first == name) return &p;
+    return nullptr;
+}
+
+int64_t param_int(const OpRecord& rec, const char* name, int64_t fallback) {
+    const OpParam* p = find_param(rec.params, name);
+    if (!p) return fallback;
+    const int64_t* v = std::get_if<int64_t>(&p->second);
+    return v ? *v : fallback;
+}
+
+bool param_is(const std::vector<OpParam>& params, const char* name, const char* value) {
+    const OpParam* p = find_param(params, name);
+    if (!p) return false;
+    const std::string* s = std::get_if<std::string>(&p->second);
+    return s && *s == value;
+}
+
+bool serves_bf16(const std::vector<OpParam>& params) { return param_is(params, "dtype", "bf16"); }
+
+// the activation the shrink reads is a float tensor (not int8 / fp8 codes with a group scale)
+bool float_act(const std::vector<OpParam>& params) {
+    return !(param_is(params, "dtype", "i8") || param_is(params, "dtype", "fp8_e4m3") ||
+             param_is(params, "dtype", "fp8_e5m2"));
+}
+
+bool rank_served(int64_t r) { return r == 8 || r == 16 || r == 32 || r == 64; }
+
+[[noreturn]] void refuse(const std::string& op, const std::string& why) {
+    throw std::runtime_error(op + " (MI355X device row): " + why);
+}
+
+std::string dims(std::initializer_list<int64_t> d) {
+    std::string s = "[";
+    for (int64_t v : d) s += (s.size() > 1 ? ", " : "") + std::to_string(v);
+    return s + "]";
+}
+
+// ---------------------------------------------------------------- leaves
+Param& grad_entry(ParamSet* grads, const std::string& name, const std::vector<int64_t>& shape) {
+    for (Param& p : *grads)
+        if (p.name == name) return p;
+    Param p;
+    p.name = name;
+    p.shape = shape;
+    int64_t n = 1;
+    for (int64_t d : shape) n *= d;
+    p.value.assign((size_t)n, 0.0f);
+    grads->push_back(std::move(p));
+    return grads->back();
+}
+
+std::string grad_name(const char* prefix, const char* leaf) {
+    if (!prefix || !*prefix) return leaf;
+    return std::string(prefix) + "." + leaf;
+}
+
+// a slot's factor leaf: the record's fused name, the slot's module, or the record's prefix
+std::string factor_grad_name(const AdjointCall& call, const char* leaf, int64_t slot) {
+    if (call.fused_slots) return grad_name(call.prefix, leaf);
+    if (call.slot_prefix) return grad_name(call.slot_prefix(slot).c_str(), leaf);
+    return grad_name(call.prefix, leaf);
+}
+
+// row m's adapter slot, or -1 for a base row (negative, NaN or past the pool)
+int64_t row_slot(const AdValue& slot, int64_t m, int64_t S) {
+    const double v = slot.value[(size_t)m];
+    if (!(v >= 0.0)) return -1;
+    const int64_t s = (int64_t)v;
+    return s < S ? s : -1;
+}
+
+// ---------------------------------------------------------------- bf16 on the host
+uint16_t to_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return (uint16_t)((u >> 16) | 0x0040u);  // quiet NaN
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float from_bf16(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+void to_bf16(const double* v, size_t n, std::vector<uint16_t>& out) {
+    out.resize(n);
+    for (size_t i = 0; i < n; ++i) out[i] = to_bf16((float)v[i]);
+}
+
+// v ~ hi + lo, both bf16 (~16 significant bits)
+void split_bf16(const std::vector<double>& v, std::vector<uint16_t>& hi, std::vector<uint16_t>& lo) {
+    hi.resize(v.size());
+    lo.resize(v.size());
+    for (size_t i = 0; i < v.size(); ++i) {
+        hi[i] = to_bf16((float)v[i]);
+        lo[i] = to_bf16((float)(v[i] - (double)from_bf16(hi[i])));
+    }
+}
+
+// ---------------------------------------------------------------- the card
+// One stream, grow-only buffers by role, one rocBLAS handle; created on first use, kept for the
+// process. A mutex serialises rows called from more than one thread.
+struct Card {
+    std::mutex mu;
+    hipStream_t stream = nullptr;
+    rocblas_handle blas = nullptr;
+    std::map<std::string, std::pair<void*, size_t>> bufs;
+};
+
+Card& card() {
+    static Card* c = new Card;
+    return *c;
+}
+
+void hip_ok(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void r97q_ok(int rc, const char* what) {
+    if (rc != R97Q_OK) throw std::runtime_error(std::string(what) + ": " + r97q_last_error());
+}
+
+hipStream_t stream_of(Card& c) {
+    if (!c.stream) hip_ok(hipStreamCreate(&c.stream), "hipStreamCreate");
+    return c.stream;
+}
+
+void* buffer(Card& c, const std::string& role, size_t bytes) {
+    auto& b = c.bufs[role];
+    if (b.second < bytes || !b.first) {
+        if (b.first) hip_ok(hipFree(b.first), "hipFree");
+        b = {nullptr, 0};
+        hip_ok(hipMalloc(&b.first, bytes ? bytes : 1), "hipMalloc");
+        b.second = bytes;
+    }
+    return b.first;
+}
+
+// uploads complete before return: the host vectors are temporaries of the row
+template <class T>
+T* upload(Card& c, const std::string& role, const std::vector<T>& h) {
+    void* d = buffer(c, role, h.size() * sizeof(T));
+    hip_ok(hipMemcpyAsync(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice, stream_of(c)), "upload");
+    hip_ok(hipStreamSynchronize(stream_of(c)), "hipStreamSynchronize");
+    return static_cast<T*>(d);
+}
+
+float* zeros(Card& c, const std::string& role, size_t n) {
+    void* d = buffer(c, role, n * sizeof(float));
+    hip_ok(hipMemsetAsync(d, 0, n * sizeof(float), stream_of(c)), "hipMemsetAsync");
+    return static_cast<float*>(d);
+}
+
+std::vector<float> download(Card& c, const float* d, size_t n) {
+    std::vector<float> h(n);
+    hip_ok(hipMemcpyAsync(h.data(), d, n * sizeof(float), hipMemcpyDeviceToHost, stream_of(c)), "download");
+    hip_ok(hipStreamSynchronize(stream_of(c)), "hipStreamSynchronize");
+    return h;
+}
+
+// ---------------------------------------------------------------- gemm_nt
+// The reference's gemm_nt adjoint (src/adjoint/host/linear.cpp:221-243, device row
+// src/adjoint/device/linear.hip:745): dx[m, k] += sum_n dy[m, n] W(n, k).
+void gemm_nt_device(const AdjointCall& call) {
+    const OpRecord& rec = call.rec;
+    const int ia = operand_pos(rec, "a"), ib = operand_pos(rec, "b");
+    if (ia < 0 || ib < 0 || call.cot.empty() || !call.dc || (size_t)std::max(ia, ib) >= call.fwd.size()) return;
+    const AdValue& a = call.fwd[(size_t)ia];
+    const AdValue& b = call.fwd[(size_t)ib];
+    const AdValue& dy = call.cot[0];
+    const int64_t K = param_int(rec, "K", a.shape.size() >= 2 ? a.shape[1] : 0);
+    const int64_t N = param_int(rec, "N", b.shape.size() >= 2 ? b.shape[0] : 0);
+    const int64_t M = param_int(rec, "M", a.shape.empty() ? 0 : a.shape[0]);
+    AdValue& dx = (*call.dc)[(size_t)ia];
+    if (M <= 0 || N <= 0 || K <= 0 || (int64_t)dy.value.size() != M * N || (int64_t)dx.value.size() != M * K) return;
+    const bool stored = b.raw != nullptr || b.enc != nullptr;
+    if (!stored && (int64_t)b.value.size() != N * K) return;
+
+    Card& c = card();
+    std::lock_guard<std::mutex> lock(c.mu);
+    const hipStream_t s = stream_of(c);
+    std::vector<uint16_t> hi, lo;
+    split_bf16(dy.value, hi, lo);
+    const uint16_t* d_hi = upload(c, "dy_hi", hi);
+    const uint16_t* d_lo = upload(c, "dy_lo", lo);
+    float* d_dx = static_cast<float*>(buffer(c, "dx", (size_t)(M * K) * 4));
+    if (stored) {
+        if (!b.enc) refuse(rec.op, "a stored weight operand carries no encoding");
+        if (K % 128 || N % 128) refuse(rec.op, "stored weight " + dims({N, K}) + ": N and K must be multiples of 128");
+        const R97qWeight* w = device_weight_get(static_cast<const IqrStoredEnc*>(b.enc), N, K, s);
+        r97q_ok(r97q_qlinear_dx_base(w, d_hi, M, 0, d_dx, R97Q_F32, 0, nullptr, 0, s), "gemm_nt dX");
+        r97q_ok(r97q_qlinear_dx_base(w, d_lo, M, 0, d_dx, R97Q_F32, 1, nullptr, 0, s), "gemm_nt dX");
+    } else {
+        std::vector<uint16_t> wb;
+        to_bf16(b.value.data(), b.value.size(), wb);
+        const uint16_t* d_w = upload(c, "w", wb);
+        if (!c.blas) {
+            if (rocblas_create_handle(&c.blas) != rocblas_status_success) refuse(rec.op, "rocblas_create_handle failed");
+        }
+        rocblas_set_stream(c.blas, s);
+        // row-major dx[M, K] = dy[M, N] . W[N, K] is column-major dx^T[K, M] = W^T[K, N] . dy^T[N, M]
+        const float one = 1.0f, zero = 0.0f;
+        for (int half = 0; half < 2; ++half) {
+            const rocblas_status st = rocblas_gemm_ex(
+                c.blas, rocblas_operation_none, rocblas_operation_none, (rocblas_int)K, (rocblas_int)M, (rocblas_int)N,
+                &one, d_w, rocblas_datatype_bf16_r, (rocblas_int)K, half ? d_lo : d_hi, rocblas_datatype_bf16_r,
+                (rocblas_int)N, half ? &one : &zero, d_dx, rocblas_datatype_f32_r, (rocblas_int)K, d_dx,
+                rocblas_datatype_f32_r, (rocblas_int)K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+            if (st != rocblas_status_success) refuse(rec.op, std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(st));
+        }
+    }
+    const std::vector<float> h = download(c, d_dx, (size_t)(M * K));
+    for (size_t i = 0; i < h.size(); ++i) dx.value[i] += (double)h[i];
+}
+
+// ---------------------------------------------------------------- lora_shrink
+// The float shrink's adjoint (src/adjoint/host/lora.cpp:260-328): schema a, a_scale (absent, dtype
+// "invalid"), slot, lora_a [S, R, K], t. Per slot s, over that slot's rows:
+//   dc[a][m, k] += sum_j t_cot[m, j] A[s, j, k];   lora_A(s)[j, k] += sum_m t_cot[m, j] x[m, k]
+void lora_shrink_device(const AdjointCall& call) {
+    const std::vector<AdValue>& v = call.fwd;
+    if ((v.size() != 4 && v.size() != 5) || call.cot.empty() || !call.dc) return;
+    const AdValue &a = v[0], &held = v[1], &slot = v[2], &la = v[3];
+    if (held.dtype != "invalid") return;  // a coded activation: the coded row's record
+    if (a.shape.size() != 2 || slot.shape.size() != 1 || la.shape.size() != 3) return;
+    const int64_t M = a.shape[0], K = a.shape[1], S = la.shape[0], R = la.shape[1];
+    if (M <= 0 || K <= 0 || R <= 0 || S <= 0 || la.shape[2] != K || slot.shape[0] != M) return;
+    if ((int64_t)a.value.size() != M * K || (int64_t)slot.value.size() != M || (int64_t)la.value.size() != S * R * K)
+        return;
+    const AdValue& t_cot = call.cot[0];
+    AdValue& a_cot = call.dc->at(0);
+    if ((int64_t)t_cot.value.size() != M * R || (int64_t)a_cot.value.size() != M * K) return;
+    if (!rank_served(R) || K % 128)
+        refuse(call.rec.op, "rank " + std::to_string(R) + ", K " + std::to_string(K) +
+                                " not served (ranks 8, 16, 32, 64; K a multiple of 128)");
+    std::vector<char> used((size_t)S, 0);
+    for (int64_t m = 0; m < M; ++m) {
+        const int64_t sl = row_slot(slot, m, S);
+        if (sl >= 0) used[(size_t)sl] = 1;
+    }
+
+    Card& c = card();
+    std::lock_guard<std::mutex> lock(c.mu);
+    const hipStream_t s = stream_of(c);
+    std::vector<uint16_t> xb;
+    to_bf16(a.value.data(), a.value.size(), xb);
+    const uint16_t* d_x = upload(c, "x", xb);
+    float* d_dx = static_cast<float*>(buffer(c, "dx", (size_t)(M * K) * 4));
+    const int64_t wsb = r97q_lora_shrink_bwd_workspace_bytes(M, K, (int32_t)R);
+    void* d_ws = buffer(c, "ws", (size_t)wsb);
+    bool first = true;
+    for (int64_t sl = 0; sl < S; ++sl) {
+        if (!used[(size_t)sl]) continue;
+        std::vector<uint16_t> ab;
+        to_bf16(la.value.data() + sl * R * K, (size_t)(R * K), ab);
+        const uint16_t* d_a = upload(c, "a_s", ab);
+        std::vector<float> tc((size_t)(M * R), 0.0f);
+        for (int64_t m = 0; m < M; ++m)
+            if (row_slot(slot, m, S) == sl)
+                for (int64_t j = 0; j < R; ++j) tc[(size_t)(m * R + j)] = (float)t_cot.value[(size_t)(m * R + j)];
+        const float* d_tc = upload(c, "t_cot", tc);
+        float* d_da = call.grads ? zeros(c, "da", (size_t)(R * K)) : nullptr;
+        r97q_ok(r97q_lora_shrink_bwd(M, K, d_x, d_a, (int32_t)R, d_tc, d_dx, first ? 0 : 1, d_da, d_ws, wsb, s),
+                "lora_shrink adjoint");
+        first = false;
+        if (call.grads) {
+            const std::vector<float> da = download(c, d_da, (size_t)(R * K));
+            const std::vector<int64_t> shape = call.fused_slots ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
+            Param& leaf = grad_entry(call.grads, factor_grad_name(call, "lora_A", sl), shape);
+            const int64_t row0 = call.fused_slots ? sl * R : 0;
+            for (int64_t j = 0; j < R; ++j)
+                for (int64_t k = 0; k < K; ++k) leaf.value[(size_t)((row0 + j) * K + k)] += da[(size_t)(j * K + k)];
+        }
+    }
+    if (first) return;  // every row a base row
+    const std::vector<float> h = download(c, d_dx, (size_t)(M * K));
+    for (size_t i = 0; i < h.size(); ++i) a_cot.value[i] += (double)h[i];
+}
+
+// ---------------------------------------------------------------- lora_expand
+// The expand's adjoint (src/adjoint/host/lora.cpp:451-521): schema t, slot, lora_b [S, N, R],
+// scale [S, N] (absent in a float trunk's 4-operand record: 1), y. Per slot s, over its rows:
+//   dc[t][m, j] += sum_n y_cot[m, n] scale[s, n] B[s, n, j]
+//   lora_B(s)[n, j] += sum_m y_cot[m, n] scale[s, n] t[m, j]
+// and an in-place write's slot takes y_cot back unchanged.
+void lora_expand_device(const AdjointCall& call) {
+    const OpRecord& rec = call.rec;
+    const std::vector<AdValue>& v = call.fwd;
+    const size_t n = v.size();
+    if ((n != 4 && n != 5) || call.cot.empty() || !call.dc || rec.operands.size() < 4) return;
+    const AdValue &t = v[0], &slot = v[1], &lb = v[2];
+    const bool has_scale = n == 5 || !rec.operands[3].written;
+    const AdValue* sc = has_scale ? &v[3] : nullptr;
+    if (t.shape.size() != 2 || slot.shape.size() != 1 || lb.shape.size() != 3) return;
+    const int64_t M = t.shape[0], R = t.shape[1], S = lb.shape[0], N = lb.shape[1];
+    if (M <= 0 || N <= 0 || R <= 0 || S <= 0 || lb.shape[2] != R || slot.shape[0] != M) return;
+    if ((int64_t)t.value.size() != M * R || (int64_t)slot.value.size() != M || (int64_t)lb.value.size() != S * N * R)
+        return;
+    if (sc && (sc->shape.size() != 2 || sc->shape[0] != S || sc->shape[1] != N || (int64_t)sc->value.size() != S * N))
+        return;
+    const AdValue& y_cot = call.cot[0];
+    AdValue& t_cot = call.dc->at(0);
+    if ((int64_t)y_cot.value.size() != M * N || (int64_t)t_cot.value.size() != M * R) return;
+    if (!rank_served(R) || N % 128)
+        refuse(rec.op, "rank " + std::to_string(R) + ", N " + std::to_string(N) +
+                           " not served (ranks 8, 16, 32, 64; N a multiple of 128)");
+    // the in-place write's direct path
+    for (size_t i = 0; i < rec.operands.size() && i < call.dc->size(); ++i)
+        if (rec.operands[i].written && rec.operands[i].in_place) {
+            AdValue& d = call.dc->at(i);
+            if (d.value.size() == y_cot.value.size())
+                for (size_t e = 0; e < y_cot.value.size(); ++e) d.value[e] += y_cot.value[e];
+        }
+    std::vector<char> used((size_t)S, 0);
+    for (int64_t m = 0; m < M; ++m) {
+        const int64_t sl = row_slot(slot, m, S);
+        if (sl >= 0) used[(size_t)sl] = 1;
+    }
+
+    Card& c = card();
+    std::lock_guard<std::mutex> lock(c.mu);
+    const hipStream_t s = stream_of(c);
+    std::vector<float> tf(t.value.begin(), t.value.end());
+    const float* d_t = upload(c, "t", tf);
+    float* d_tc = zeros(c, "t_cot", (size_t)(M * R));
+    const int64_t wsb = r97q_lora_expand_bwd_workspace_bytes(M, N, (int32_t)R);
+    void* d_ws = buffer(c, "ws", (size_t)wsb);
+    bool any = false;
+    for (int64_t sl = 0; sl < S; ++sl) {
+        if (!used[(size_t)sl]) continue;
+        any = true;
+        std::vector<double> dys((size_t)(M * N), 0.0);
+        for (int64_t m = 0; m < M; ++m) {
+            if (row_slot(slot, m, S) != sl) continue;
+            for (int64_t k = 0; k < N; ++k)
+                dys[(size_t)(m * N + k)] = y_cot.value[(size_t)(m * N + k)] * (sc ? sc->value[(size_t)(sl * N + k)] : 1.0);
+        }
+        std::vector<uint16_t> hi, lo, bb;
+        split_bf16(dys, hi, lo);
+        to_bf16(lb.value.data() + sl * N * R, (size_t)(N * R), bb);
+        const uint16_t* d_hi = upload(c, "dy_hi", hi);
+        const uint16_t* d_lo = upload(c, "dy_lo", lo);
+        const uint16_t* d_b = upload(c, "b_s", bb);
+        float* d_db = call.grads ? zeros(c, "db", (size_t)(N * R)) : nullptr;
+        r97q_ok(r97q_lora_expand_bwd(M, N, d_hi, d_b, (int32_t)R, 1.0f, d_t, d_tc, d_db, d_ws, wsb, s), "lora_expand adjoint");
+        r97q_ok(r97q_lora_expand_bwd(M, N, d_lo, d_b, (int32_t)R, 1.0f, d_t, d_tc, d_db, d_ws, wsb, s), "lora_expand adjoint");
+        if (call.grads) {
+            const std::vector<float> db = download(c, d_db, (size_t)(N * R));
+            const int64_t cols = call.fused_slots ? S * R : R;
+            const std::vector<int64_t> shape = {N, cols};
+            Param& leaf = grad_entry(call.grads, factor_grad_name(call, "lora_B", sl), shape);
+            const int64_t col0 = call.fused_slots ? sl * R : 0;
+            for (int64_t k = 0; k < N; ++k)
+                for (int64_t j = 0; j < R; ++j) leaf.value[(size_t)(k * cols + col0 + j)] += db[(size_t)(k * R + j)];
+        }
+    }
+    if (!any) return;
+    const std::vector<float> h = download(c, d_tc, (size_t)(M * R));
+    for (size_t i = 0; i < h.size(); ++i) t_cot.value[i] += (double)h[i];
+}
+
+}  // namespace
+
+// The frozen positions are the reference's (the weight for gemm_nt; slot, factor and scale for
+// the adapter's ops); the float shrink's device row is new here (the reference serves the float
+// shrink on the host only).
+R97_REGISTER_ADJOINT_IF_F("gemm_nt", device, gemm_nt_device, serves_bf16, 1)
+R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_device, float_act, 1, 2, 3)
+R97_REGISTER_ADJOINT_F("lora_expand", device, lora_expand_device, 1, 2, 3)
+
+R97_REGISTER_ADJOINT_FAMILY(Linear, "gemm_nt");
+R97_REGISTER_ADJOINT_FAMILY(Lora, "lora_shrink", "lora_expand");
+
+}  // namespace r97

@@ -1,0 +1,268 @@
+// rows_hook.cpp -- TEST INFRASTRUCTURE ONLY: a C entry for each device row of libr97rows.so, so the
+// Python tests can hand it numpy arrays. Each entry builds the record and the call the way the
+// reference's backward walk builds them (schema-ordered operands, f64 forward values, the stored
+// weight as raw + enc, dc pre-sized), looks the row up through the registry (adjoint_find on the
+// device side) and runs it. Also a self-test of the registry's lookup rules.
+#include <cstdint>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "r97/adjoint.h"
+#include "r97/adjoint_family.h"
+#include "r97/stored_weight.h"
+
+using namespace r97;
+
+namespace {
+
+thread_local std::string g_err;
+
+Operand opd(const char* name, const char* dtype, std::vector<int64_t> shape, bool written = false,
+            bool in_place = false) {
+    Operand o;
+    o.buffer = name;
+    o.dtype = dtype;
+    o.shape = std::move(shape);
+    o.written = written;
+    o.in_place = in_place;
+    return o;
+}
+
+AdValue val(const char* dtype, std::vector<int64_t> shape, const double* v) {
+    AdValue a;
+    a.dtype = dtype;
+    a.shape = std::move(shape);
+    int64_t n = 1;
+    for (int64_t d : a.shape) n *= d;
+    if (v) a.value.assign(v, v + n);
+    else a.value.assign((size_t)n, 0.0);
+    return a;
+}
+
+// the stored-weight encodings handed out, one stable object per plane pointer
+std::map<const void*, IqrStoredEnc>& encs() {
+    static std::map<const void*, IqrStoredEnc> m;
+    return m;
+}
+
+AdjointFn row(const char* op, const std::vector<OpParam>& params) {
+    std::string err;
+    AdjointFn fn = adjoint_find(op, Side::device, params, &err);
+    if (!fn) throw std::runtime_error(err);
+    return fn;
+}
+
+// registry self-test rows
+void fa(const AdjointCall&) {}
+void fb(const AdjointCall&) {}
+void fc(const AdjointCall&) {}
+void twin_a(const OpRecord&, const std::vector<AdValue>&, std::vector<AdValue>*) {}
+void twin_b(const OpRecord&, const std::vector<AdValue>&, std::vector<AdValue>*) {}
+bool is_x(const std::vector<OpParam>& p) {
+    for (const auto& kv : p)
+        if (kv.first == "dtype") {
+            const std::string* s = std::get_if<std::string>(&kv.second);
+            return s && *s == "x";
+        }
+    return false;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rh_last_error() { return g_err.c_str(); }
+
+// 0, or the line of the first failed check
+int rh_registry_selftest() {
+#define CHECK(c) \
+    do {         \
+        if (!(c)) return __LINE__; \
+    } while (0)
+    const std::vector<OpParam> px = {{"dtype", std::string("x")}}, py = {{"dtype", std::string("y")}};
+    // a catch-all registered before a predicated row still loses to it when the predicate accepts
+    adjoint_register("rh_op", Side::host, fa, {}, nullptr);
+    adjoint_register("rh_op", Side::host, fb, {1}, is_x);
+    adjoint_register("rh_op", Side::device, fc, {2}, nullptr);
+    CHECK(adjoint_find("rh_op", Side::host, px, nullptr) == fb);
+    CHECK(adjoint_find("rh_op", Side::host, py, nullptr) == fa);
+    CHECK(adjoint_frozen("rh_op", Side::host, px) == std::vector<int>{1});
+    CHECK(adjoint_frozen("rh_op", Side::host, py).empty());
+    CHECK(adjoint_find("rh_op", Side::device, py, nullptr) == fc);
+    CHECK(adjoint_frozen("rh_op", Side::device, px) == std::vector<int>{2});
+    std::string err;
+    CHECK(adjoint_find("rh_missing", Side::device, px, &err) == nullptr);
+    CHECK(err.find("rh_missing") != std::string::npos && err.find("dtype=x") != std::string::npos);
+    const OpRows rows = op_rows("rh_op");
+    CHECK(rows.host_adjoint && rows.device_adjoint && rows.device_frozen == std::vector<int>{2});
+    CHECK(!rows.twin);
+    twin_register("rh_op", twin_a, nullptr);
+    twin_register("rh_op", twin_b, is_x);
+    CHECK(twin_find("rh_op", px, nullptr) == twin_b && twin_find("rh_op", py, nullptr) == twin_a);
+    CHECK(op_rows("rh_op").twin);
+    bool seen = false;
+    for (const std::string& op : ops_registered()) seen = seen || op == "rh_op";
+    CHECK(seen);
+    // families: the same family twice is fine, a second family is a hard error
+    family_register(AdjointFamily::Lora, {"rh_fam"});
+    family_register(AdjointFamily::Lora, {"rh_fam"});
+    CHECK(family_find("rh_fam") == AdjointFamily::Lora);
+    bool threw = false;
+    try {
+        family_register(AdjointFamily::Linear, {"rh_fam"});
+    } catch (const std::logic_error&) {
+        threw = true;
+    }
+    CHECK(threw);
+    CHECK(family_find("rh_unclaimed") == AdjointFamily::None);
+    CHECK(std::strcmp(adjoint_family_name(AdjointFamily::Lora), "lora") == 0);
+    // this build's device rows
+    const std::vector<OpParam> bf16 = {{"dtype", std::string("bf16")}}, f32 = {{"dtype", std::string("f32")}},
+                               i8 = {{"dtype", std::string("i8")}};
+    CHECK(adjoint_find("gemm_nt", Side::device, bf16, nullptr) != nullptr);
+    CHECK(adjoint_frozen("gemm_nt", Side::device, bf16) == std::vector<int>{1});
+    CHECK(adjoint_find("gemm_nt", Side::device, f32, nullptr) == nullptr);
+    CHECK(adjoint_find("lora_shrink", Side::device, bf16, nullptr) != nullptr);
+    CHECK(adjoint_frozen("lora_shrink", Side::device, bf16) == (std::vector<int>{1, 2, 3}));
+    CHECK(adjoint_find("lora_shrink", Side::device, i8, nullptr) == nullptr);
+    CHECK(adjoint_find("lora_expand", Side::device, bf16, nullptr) != nullptr);
+    CHECK(adjoint_frozen("lora_expand", Side::device, f32) == (std::vector<int>{1, 2, 3}));
+    CHECK(family_find("gemm_nt") == AdjointFamily::Linear);
+    CHECK(family_find("lora_shrink") == AdjointFamily::Lora && family_find("lora_expand") == AdjointFamily::Lora);
+#undef CHECK
+    return 0;
+}
+
+// dx[M, K] += dy[M, N] . W: W the stored IQR weight `desc` (device planes; scale_col device or
+// null) when w_dense is null, else the dense bf16-valued W[N, K].
+int rh_gemm_nt(int64_t M, int64_t N, int64_t K, const double* dy, const R97IqrDecodeDesc* desc,
+               const float* scale_col, const double* w_dense, double* dx) {
+    try {
+        OpRecord rec;
+        rec.op = "gemm_nt";
+        rec.params = {{"dtype", std::string("bf16")}, {"M", M}, {"N", N}, {"K", K}};
+        rec.operands = {opd("a", "bf16", {M, K}), opd("b", w_dense ? "bf16" : "iqr", {N, K}),
+                        opd("y", "bf16", {M, N}, true)};
+        std::vector<AdValue> fwd = {val("bf16", {M, K}, nullptr), AdValue{}, AdValue{}};
+        fwd[1].dtype = rec.operands[1].dtype;
+        fwd[1].shape = {N, K};
+        if (w_dense) {
+            fwd[1].value.assign(w_dense, w_dense + N * K);
+        } else {
+            IqrStoredEnc& e = encs()[desc->codes];
+            e.desc = *desc;
+            e.scale_col = scale_col;
+            fwd[1].raw = desc->codes;
+            fwd[1].enc = &e;
+            rec.operands[1].enc = &e;
+        }
+        fwd[2].dtype = "bf16";
+        fwd[2].shape = {M, N};
+        const std::vector<AdValue> cot = {val("bf16", {M, N}, dy)};
+        std::vector<AdValue> dc = {val("bf16", {M, K}, dx), AdValue{}, AdValue{}};
+        const AdjointCall call{rec, fwd, cot, &dc, nullptr, "", {}, false, nullptr, nullptr};
+        row("gemm_nt", rec.params)(call);
+        std::memcpy(dx, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// the float shrink's row: dx[M, K] += ..., dA: the lora_A leaves, written as [S, R, K] (one slot's
+// leaf after another; with `fused` the one [S*R, K] leaf)
+int rh_lora_shrink(int64_t M, int64_t K, int64_t R, int64_t S, const double* x, const double* slot, const double* la,
+                   const double* t_cot, double* dx, float* dA, int fused) {
+    try {
+        OpRecord rec;
+        rec.op = "lora_shrink";
+        rec.params = {{"dtype", std::string("bf16")}};
+        rec.operands = {opd("a", "bf16", {M, K}), opd("none:1", "invalid", {}), opd("slot", "i32", {M}),
+                        opd("lora_a", "bf16", {S, R, K}), opd("t", "f32", {M, R}, true)};
+        AdValue held;
+        held.dtype = "invalid";
+        const std::vector<AdValue> fwd = {val("bf16", {M, K}, x), held, val("i32", {M}, slot),
+                                          val("bf16", {S, R, K}, la), val("f32", {M, R}, nullptr)};
+        const std::vector<AdValue> cot = {val("f32", {M, R}, t_cot)};
+        std::vector<AdValue> dc = {val("bf16", {M, K}, dx), AdValue{}, AdValue{}, AdValue{}, AdValue{}};
+        ParamSet grads;
+        AdjointCall call{rec, fwd, cot, &dc, dA ? &grads : nullptr, "layers.0.q", {}, fused != 0, nullptr, nullptr};
+        if (!fused) call.slot_prefix = [](int64_t s) { return "adapter" + std::to_string(s); };
+        row("lora_shrink", rec.params)(call);
+        std::memcpy(dx, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
+        if (dA) {
+            std::memset(dA, 0, sizeof(float) * (size_t)(S * R * K));
+            for (const Param& p : grads) {
+                if (fused) {
+                    if (p.name != "layers.0.q.lora_A") throw std::runtime_error("unexpected leaf " + p.name);
+                    std::memcpy(dA, p.value.data(), sizeof(float) * (size_t)(S * R * K));
+                } else {
+                    const std::string pre = "adapter";
+                    if (p.name.rfind(pre, 0) != 0) throw std::runtime_error("unexpected leaf " + p.name);
+                    const int64_t s = std::stoll(p.name.substr(pre.size()));
+                    std::memcpy(dA + s * R * K, p.value.data(), sizeof(float) * (size_t)(R * K));
+                }
+            }
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// the expand's row: t_cot[M, R] += ..., dB: the lora_B leaves written as [S, N, R] (fused: the one
+// [N, S*R] leaf, copied as is), scale [S, N] or null (a 4-operand record), in_place: y is an
+// in-place write whose own slot gets y_cot (returned in d_base[M, N])
+int rh_lora_expand(int64_t M, int64_t N, int64_t R, int64_t S, const double* t, const double* slot, const double* lb,
+                   const double* scale, const double* y_cot, double* t_cot, float* dB, int fused, int in_place,
+                   double* d_base) {
+    try {
+        OpRecord rec;
+        rec.op = "lora_expand";
+        rec.params = {{"dtype", std::string("bf16")}};
+        rec.operands = {opd("t", "f32", {M, R}), opd("slot", "i32", {M}), opd("lora_b", "bf16", {S, N, R})};
+        std::vector<AdValue> fwd = {val("f32", {M, R}, t), val("i32", {M}, slot), val("bf16", {S, N, R}, lb)};
+        if (scale) {
+            rec.operands.push_back(opd("scale", "f32", {S, N}));
+            fwd.push_back(val("f32", {S, N}, scale));
+        }
+        rec.operands.push_back(opd("y", "bf16", {M, N}, true, in_place != 0));
+        fwd.push_back(val("bf16", {M, N}, nullptr));  // y's value (an in-place write: the old one it reads)
+        const std::vector<AdValue> cot = {val("bf16", {M, N}, y_cot)};
+        std::vector<AdValue> dc(rec.operands.size());
+        dc[0] = val("f32", {M, R}, t_cot);
+        if (in_place) dc.back() = val("bf16", {M, N}, nullptr);
+        ParamSet grads;
+        AdjointCall call{rec, fwd, cot, &dc, dB ? &grads : nullptr, "layers.0.q", {}, fused != 0, nullptr, nullptr};
+        if (!fused) call.slot_prefix = [](int64_t s) { return "adapter" + std::to_string(s); };
+        row("lora_expand", rec.params)(call);
+        std::memcpy(t_cot, dc[0].value.data(), sizeof(double) * (size_t)(M * R));
+        if (in_place && d_base) std::memcpy(d_base, dc.back().value.data(), sizeof(double) * (size_t)(M * N));
+        if (dB) {
+            std::memset(dB, 0, sizeof(float) * (size_t)(S * N * R));
+            for (const Param& p : grads) {
+                if (fused) {
+                    if (p.name != "layers.0.q.lora_B") throw std::runtime_error("unexpected leaf " + p.name);
+                    std::memcpy(dB, p.value.data(), sizeof(float) * (size_t)(S * N * R));
+                } else {
+                    const int64_t s = std::stoll(p.name.substr(7));
+                    std::memcpy(dB + s * N * R, p.value.data(), sizeof(float) * (size_t)(N * R));
+                }
+            }
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+int64_t rh_weights_prepared() { return device_weight_count(); }
+void rh_weights_clear() { device_weight_clear(); }
+
+}  // extern "C"
