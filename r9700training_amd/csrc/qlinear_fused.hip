@@ -24,11 +24,11 @@
 // One barrier a step orders the decode of step s+1 against the reads of step s.
 //
 // Decode of one value (6 VALU ops): the 16-bit state is a bit-field (v_bfe_u32, or v_alignbit +
-// mask when it straddles a dword); the codebook hash is v_mad_u32_u24 + mask; v_dot4_u32_u8 sums
-// its bytes with 1024 in the accumulator, which makes the low half an f16 of 1024 + byte-sum; one
-// v_fma_mix_f32 with the exact constant -1150 * scale gives (byte-sum - 126) * scale exactly (19
-// significant bits at most, so no rounding), and v_cvt_pk_bf16_f32 rounds once to bf16: the
-// decoded tile is bf16(code * scale), bit for bit.
+// mask when it straddles a dword); the codebook hash is v_mad_u32_u24 + mask; v_sad_u8 against
+// zero sums its bytes with 1024 in the accumulator, which makes the low half an f16 of
+// 1024 + byte-sum; one v_fma_mix_f32 with the exact constant -1150 * scale gives
+// (byte-sum - 126) * scale exactly (19 significant bits at most, so no rounding), and
+// v_cvt_pk_bf16_f32 rounds once to bf16: the decoded tile is bf16(code * scale), bit for bit.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -51,8 +51,25 @@ typedef float f32x16 __attribute__((__vector_size__(64)));
 constexpr int kWaves = kThreads / 64;               // 8
 constexpr int kTileBytes = 128 * 128;               // one decoded bf16 tile (128 rows x 64 values)
 constexpr int kActBytes = kBM * 128;                // one token tile (512 rows x 64 values)
-constexpr int kLdsBytes = 2 * kActBytes + 2 * kTileBytes;  // 160 KiB: the whole LDS
 static_assert(kWaves * 64 == kBM, "one wave per 64 tokens");
+static_assert(2 * kActBytes + 2 * kTileBytes == 160 * 1024, "the buffers fill a gfx950 CU's LDS");
+
+// The double-buffered LDS tiles, declared as four separate arrays: the compiler then sees that the
+// direct global -> LDS loads into a token buffer do not alias the weight tile a wave reads, and
+// does not wait for those loads before every LDS read.
+struct Lds {
+    uint8_t* w[2];  // decoded weight tiles [128 rows][128 bytes]
+    uint8_t* x[2];  // token tiles [512 rows][128 bytes]
+};
+
+// The end of a main-loop step: this wave's global loads (token rows into LDS, stream words into
+// registers) have landed and its LDS writes are done, then the workgroup barrier. (__syncthreads
+// would do the same, written out so the wait is exactly vmcnt(0) lgkmcnt(0) and visible to the
+// compiler's own wait insertion.)
+__device__ __forceinline__ void step_barrier() {
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) expcnt(7: no wait) lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+}
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -137,7 +154,7 @@ __device__ __forceinline__ float slice_value(const Words<BITS, ROWS, COLS, SLICE
     if (sh + 16 <= 32) st = (wd.w[w].at(c) >> sh) & 0xFFFFu;
     else st = __builtin_amdgcn_alignbit(wd.w[w + 1].at(c), wd.w[w].at(c), sh) & 0xFFFFu;
     const uint32_t h = (st * (a24 & 0xFFFFFFu) + b) & 0x3F3F3F3Fu;
-    const uint32_t d = __builtin_amdgcn_udot4(h, 0x01010101u, 0x6400u, false);  // f16(1024 + sum)
+    const uint32_t d = __builtin_amdgcn_sad_u8(h, 0u, 0x6400u);  // f16(1024 + sum)
     const _Float16 hv = __builtin_bit_cast(_Float16, (uint16_t)d);
     return __builtin_fmaf((float)hv, sc, off);  // (sum - 126) * scale, exact
 }
@@ -191,7 +208,7 @@ struct Loop {
     int64_t T;
     int lane;
 
-    __device__ __forceinline__ void run(uint8_t* lds, f32x16 (&acc)[2][4]) {
+    __device__ __forceinline__ void run(const Lds& lds, f32x16 (&acc)[2][4]) {
         const int seg = FWD ? lane >> 4 : WAVE >> 2;
         const int cg = FWD ? lane & 15 : lane;
         const int nsteps = (int)(red / kStep);
@@ -251,22 +268,22 @@ struct Loop {
             if (row > T - 1) row = T - 1;
             gr[q] = act + row * red + 8 * (pc ^ swz(64 * WAVE + r));
         }
-        uint8_t* xw = lds + 2 * kTileBytes + (64 * WAVE) * 128;  // this wave's rows, buffer 0
+        uint8_t* x0 = lds.x[0] + (64 * WAVE) * 128;  // this wave's rows of the two token buffers
+        uint8_t* x1 = lds.x[1] + (64 * WAVE) * 128;
 
         W wa, wb;
         words_for(0, wa);
-        load_act(gr, xw, 0);
-        decode(wa, lds);
+        load_act(gr, x0, 0);
+        decode(wa, lds.w[0]);
         words_for(nsteps > 1 ? 1 : 0, wa);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        step_barrier();
 
         // step s: the words of step s+2 and the token tile of step s+1 are fetched first, the
         // MFMAs run on buffers s%2, tile s+1 is decoded from the words fetched a step ago, and
         // the step ends when this wave's token loads have landed and every wave has decoded.
         for (int s = 0; s < nsteps; s += 2) {
-            step(s, nsteps, gr, xw, xw + kActBytes, acc, lds, lds + kTileBytes, wa, wb, words_for, decode);
-            step(s + 1, nsteps, gr, xw + kActBytes, xw, acc, lds + kTileBytes, lds, wb, wa, words_for, decode);
+            step(s, nsteps, gr, x0, x1, acc, lds.w[0], lds.w[1], wa, wb, words_for, decode);
+            step(s + 1, nsteps, gr, x1, x0, acc, lds.w[1], lds.w[0], wb, wa, words_for, decode);
         }
     }
 
@@ -286,8 +303,11 @@ struct Loop {
         const int half = lane >> 5, l32 = lane & 31;
         words_for(s + 2 < nsteps ? s + 2 : nsteps - 1, fetch);
         load_act(gr, xn, (int64_t)(s + 1 < nsteps ? s + 1 : nsteps - 1) * kStep);
-        // The MFMAs of this step go first, the decode of the next tile after them: the matrix core
-        // runs while the two waves that share each SIMD issue their decode VALU beside it.
+        // The two waves that share a SIMD (w and w+4) work in opposite phases: wave w+4 decodes
+        // the next tile before this step's MFMAs, wave w after them, so each one's decode VALU
+        // issues while the other one's MFMAs keep the matrix core busy. (The next tile's buffer
+        // was last read in step s-1, which the barrier that ended it closed.)
+        if (WAVE >= 4) decode(dec, nxt);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             bf16x8 af[2], bf[4];
@@ -306,9 +326,8 @@ struct Loop {
 #pragma unroll
                 for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32(af[mi], bf[ni], acc[mi][ni]);
         }
-        decode(dec, nxt);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        if (WAVE < 4) decode(dec, nxt);
+        step_barrier();
     }
 };
 
@@ -365,7 +384,7 @@ __device__ __forceinline__ void store(const f32x16 (&acc)[2][4], void* out, int6
 }
 
 template <int BITS, int SLICE>
-__device__ __forceinline__ void fwd_wave(const FwdParams& p, uint8_t* lds, int lane, int mt, int nt) {
+__device__ __forceinline__ void fwd_wave(const FwdParams& p, const Lds& lds, int lane, int mt, int nt) {
     f32x16 acc[2][4];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
@@ -379,7 +398,7 @@ __device__ __forceinline__ void fwd_wave(const FwdParams& p, uint8_t* lds, int l
 }
 
 template <int BITS, int SLICE>
-__device__ __forceinline__ void dx_wave(const DxParams& p, uint8_t* lds, int lane, int mt, int kt) {
+__device__ __forceinline__ void dx_wave(const DxParams& p, const Lds& lds, int lane, int mt, int kt) {
     f32x16 acc[2][4];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
@@ -405,7 +424,8 @@ __device__ __forceinline__ void dx_wave(const DxParams& p, uint8_t* lds, int lan
     }
 
 __global__ __launch_bounds__(kThreads, 1) void qlinear_fwd_kernel(const FwdParams p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t w0[kTileBytes], w1[kTileBytes], x0[kActBytes], x1[kActBytes];
+    const Lds lds{{w0, w1}, {x0, x1}};
     const int tile = xcd_tile(blockIdx.x, p.mtiles * p.ntiles);
     const int mt = tile / p.ntiles, nt = tile % p.ntiles;
     const int lane = threadIdx.x & 63;
@@ -413,7 +433,8 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_fwd_kernel(const FwdParam
 }
 
 __global__ __launch_bounds__(kThreads, 1) void qlinear_dx_kernel(const DxParams p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t w0[kTileBytes], w1[kTileBytes], x0[kActBytes], x1[kActBytes];
+    const Lds lds{{w0, w1}, {x0, x1}};
     const int tile = xcd_tile(blockIdx.x, p.mtiles * p.ktiles);
     const int mt = tile / p.ktiles, kt = tile % p.ktiles;
     const int lane = threadIdx.x & 63;

@@ -120,19 +120,26 @@ class Planes:
 
 
 def trellis(rows, cols, bits, state_bits=16, run_rows=256, rb=1, mad=1, scale_dtype=F32,
-            rowf=False, second=False, seed=0, scale_col=None) -> Planes:
+            rowf=False, second=False, seed=0, scale_col=None, packed=False) -> Planes:
     """A trellis weight as tests/host/iqr_decode.cpp's Synth builds one (:100-211).
 
     rowf: one f32 scale a row plus a scale.col plane (ones unless `scale_col` given);
-    otherwise one scale a 128-column block in `scale_dtype`. second: a scale.1 of 0.625."""
+    otherwise one scale a 128-column block in `scale_dtype`. second: a scale.1 of 0.625.
+    packed: draw the packed code bytes themselves (uniform bytes are uniform codes; fast at full
+    layer sizes) and leave raw_codes unset."""
     rng = np.random.default_rng(seed)
     nkb = cols // 128
-    raw = rng.integers(0, 1 << bits, size=(rows, cols), dtype=np.uint32)
+    raw = None if packed else rng.integers(0, 1 << bits, size=(rows, cols), dtype=np.uint32)
     p = Planes(rows=rows, cols=cols, bits=bits, state_bits=state_bits, run_rows=run_rows, rb=rb,
                mad=mad, round_mad=int(bool(mad or rowf)), scale_dtype=scale_dtype,
                scale_block_cols=0 if rowf else 128)
     p.raw_codes = raw
-    p.codes = pack_rows(raw, bits)
+    if packed:
+        p.codes = rng.integers(0, 256, size=(rows, (cols * bits + 7) // 8), dtype=np.uint8)
+        if (cols * bits) % 8:  # the last byte's unused high bits stay clear, as pack_rows leaves them
+            p.codes[:, -1] &= (1 << ((cols * bits) % 8)) - 1
+    else:
+        p.codes = pack_rows(raw, bits)
     A = (int(rng.integers(0, 1 << 32)) & 0xFFFFFF) | 1
     B = int(rng.integers(0, 1 << 32))
     p.mad_a, p.mad_b = A, B
