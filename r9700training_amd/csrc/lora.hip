@@ -84,22 +84,39 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
     f32x4 acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = (f32x4){};
-    int64_t k = 0;
-    for (; k + 128 <= kq; k += 128) {
-        uint4 av[4], bv[4][NB];
+    // Chunks of U 32-deep slices (U loads of the token rows and U*NB of the factor a lane, 32
+    // registers a set), two register sets: the loads of chunk c+1 are in flight while chunk c
+    // multiplies, so a wave's whole share (two chunks at the common sizes) is requested at once
+    // instead of one memory latency per 128 values.
+    constexpr int U = 8 / NB;
+    constexpr int CH = 32 * U;
+    const int64_t nch = kq / CH;
+    uint4 xv[2][U], fv[2][U][NB];
+    auto load = [&](int64_t k, uint4 (&x)[U], uint4 (&f)[U][NB]) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            av[u] = *reinterpret_cast<const uint4*>(ap + k + 32 * u);
+        for (int u = 0; u < U; ++u) {
+            x[u] = *reinterpret_cast<const uint4*>(ap + k + 32 * u);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
-                bv[u][nb] = *reinterpret_cast<const uint4*>(wp + (int64_t)16 * nb * a.Kin + k + 32 * u);
+                f[u][nb] = *reinterpret_cast<const uint4*>(wp + (int64_t)16 * nb * a.Kin + k + 32 * u);
         }
+    };
+    auto mult = [&](const uint4 (&x)[U], const uint4 (&f)[U][NB]) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16(as_bf16x8(av[u]), as_bf16x8(bv[u][nb]), acc[nb]);
+            for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16(as_bf16x8(x[u]), as_bf16x8(f[u][nb]), acc[nb]);
+    };
+    int64_t c = 0;
+    if (nch > 0) load(0, xv[0], fv[0]);
+    for (; c + 2 <= nch; c += 2) {
+        load((c + 1) * CH, xv[1], fv[1]);
+        mult(xv[0], fv[0]);
+        if (c + 2 < nch) load((c + 2) * CH, xv[0], fv[0]);
+        mult(xv[1], fv[1]);
     }
-    for (; k < kq; k += 32) {
+    if (c < nch) mult(xv[0], fv[0]);  // an odd chunk count: the last one sits in set 0
+    for (int64_t k = nch * CH; k < kq; k += 32) {
         const bf16x8 av = as_bf16x8(*reinterpret_cast<const uint4*>(ap + k));
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
