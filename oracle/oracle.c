@@ -17,6 +17,16 @@
  *                                  brute-force numpy f64 matmul; <dy, twin(x)> == <adj(dy), x>.
  *   orc_lora_*                     golden vectors from the reference rows; numpy f64 closed forms;
  *                                  central finite differences of the twins; B = 0 => dA = 0, dt = 0.
+ *   orc_group_width                the reference's own cases (K 300 over 3 groups -> 128, one group
+ *                                  -> K) and the defining property over a sweep (the width divides
+ *                                  K into exactly `groups` groups).
+ *   orc_gemm_nt_q_* , orc_lora_shrink_q_*
+ *                                  the reference's own rows (oracle/_ref) on the reference tests'
+ *                                  shapes (golden vectors); numpy f64 closed forms; the adjoint is
+ *                                  the twin's transpose in the code basis (<dy, twin(a + e)> -
+ *                                  <dy, twin(a)> == <adj(dy), e> for code perturbations e, scale
+ *                                  held), and the a_scale cotangent is the derivative of the twin in
+ *                                  the scale.
  */
 #include "oracle.h"
 
@@ -550,4 +560,138 @@ void orc_lora_expand_adjoint(int64_t M, int64_t N, int64_t R, int64_t S, const d
     lora_ctx c = {M, 0, N, R, S, NULL, slot, NULL, lora_b, scale, cy, t, dt, db, fused, 0};
     parallel_for(M, 2, expand_dt_row, &c);
     if (db) parallel_for(N * R, 2, expand_db_pair, &c);
+}
+
+/* ------------------------------------------------------------------ the coded (i8a8h) trunk */
+/* src/adjoint/host/lora.cpp:70-77 */
+int64_t orc_group_width(int64_t k, int64_t groups) {
+    if (k <= 0) return 1;
+    if (groups <= 1) return k;
+    const int64_t lo = (k + groups - 1) / groups;
+    int64_t b = 1;
+    while (b < lo) b <<= 1;
+    return (k + b - 1) / b == groups ? b : lo;
+}
+
+typedef struct {
+    int64_t M, N, K, groups;
+    const double *a, *as;
+    const int8_t* codes;
+    const uint16_t* scale;
+    double* out;
+} qgemm_ctx;
+
+static void q_twin_row(void* p, int64_t m) {
+    const qgemm_ctx* g = (const qgemm_ctx*)p;
+    for (int64_t n = 0; n < g->N; ++n) {
+        double acc = 0.0;
+        for (int64_t gi = 0; gi < g->groups; ++gi) {
+            const int64_t k0 = gi * 128, k1 = k0 + 128 < g->K ? k0 + 128 : g->K;
+            double sub = 0.0;
+            for (int64_t k = k0; k < k1; ++k) sub += g->a[m * g->K + k] * (double)g->codes[n * g->K + k];
+            acc += sub * g->as[m * g->groups + gi] * (double)orc_bf16_to_f32(g->scale[n * g->groups + gi]);
+        }
+        g->out[m * g->N + n] = acc;
+    }
+}
+
+/* src/adjoint/host/linear.cpp:245-282 (parallel_for(M, 2)), group 128 over a stored weight */
+void orc_gemm_nt_q_twin(int64_t M, int64_t N, int64_t K, const double* a, const double* a_scale,
+                        const int8_t* codes, const uint16_t* scale, double* y) {
+    qgemm_ctx g = {M, N, K, (K + 127) / 128, a, a_scale, codes, scale, y};
+    parallel_for(M, 2, q_twin_row, &g);
+}
+
+static void q_adjoint_row(void* p, int64_t m) {
+    const qgemm_ctx* g = (const qgemm_ctx*)p;
+    for (int64_t k = 0; k < g->K; ++k) {
+        const int64_t gi = k / 128;
+        double acc = 0.0;
+        for (int64_t n = 0; n < g->N; ++n)
+            acc += g->a[m * g->N + n] * (double)g->codes[n * g->K + k] *
+                   (double)orc_bf16_to_f32(g->scale[n * g->groups + gi]);
+        g->out[m * g->K + k] += acc * g->as[m * g->groups + gi];
+    }
+}
+
+/* src/adjoint/host/linear.cpp:284-317 (parallel_for(M, 2)) */
+void orc_gemm_nt_q_adjoint(int64_t M, int64_t N, int64_t K, const double* dy, const int8_t* codes,
+                           const uint16_t* scale, const double* a_scale, double* da) {
+    qgemm_ctx g = {M, N, K, (K + 127) / 128, dy, a_scale, codes, scale, da};
+    parallel_for(M, 2, q_adjoint_row, &g);
+}
+
+typedef struct {
+    int64_t M, K, R, S, groups, group;
+    const double *a, *as, *slot, *la, *ct;
+    double *t, *da, *ds;
+    float* dA;
+    int fused;
+} qshrink_ctx;
+
+/* src/adjoint/host/lora.cpp:204-209: the code times its group's scale, one product */
+static inline double q_x_at(const qshrink_ctx* c, int64_t m, int64_t k) {
+    return c->a[m * c->K + k] * c->as[m * c->groups + k / c->group];
+}
+
+static void q_shrink_twin_row(void* p, int64_t m) {
+    const qshrink_ctx* c = (const qshrink_ctx*)p;
+    const int64_t s = row_slot(c->slot, c->S, m);
+    if (s < 0) return;
+    for (int64_t j = 0; j < c->R; ++j) {
+        double acc = 0.0;
+        for (int64_t k = 0; k < c->K; ++k) acc += q_x_at(c, m, k) * c->la[(s * c->R + j) * c->K + k];
+        c->t[m * c->R + j] = acc;
+    }
+}
+
+/* src/adjoint/host/lora.cpp:226-244 */
+void orc_lora_shrink_q_twin(int64_t M, int64_t K, int64_t R, int64_t S, int64_t groups,
+                            const double* a, const double* a_scale, const double* slot,
+                            const double* lora_a, double* t) {
+    qshrink_ctx c = {M, K, R, S, groups, orc_group_width(K, groups), a, a_scale, slot, lora_a, NULL,
+                     t, NULL, NULL, NULL, 0};
+    parallel_for(M, 2, q_shrink_twin_row, &c);
+}
+
+static void q_shrink_cot_row(void* p, int64_t m) {
+    const qshrink_ctx* c = (const qshrink_ctx*)p;
+    const int64_t s = row_slot(c->slot, c->S, m);
+    if (s < 0) return;
+    double* g = (double*)calloc((size_t)c->K, sizeof(double));
+    for (int64_t j = 0; j < c->R; ++j) {
+        const double ct = c->ct[m * c->R + j];
+        if (ct == 0.0) continue;
+        for (int64_t k = 0; k < c->K; ++k) g[k] += ct * c->la[(s * c->R + j) * c->K + k];
+    }
+    for (int64_t k = 0; k < c->K; ++k) {
+        const int64_t e = m * c->K + k, ge = m * c->groups + k / c->group;
+        c->da[e] += g[k] * c->as[ge];
+        if (c->ds) c->ds[ge] += g[k] * c->a[e];
+    }
+    free(g);
+}
+
+static void q_shrink_dA_pair(void* p, int64_t u) {
+    const qshrink_ctx* c = (const qshrink_ctx*)p;
+    const int64_t j = u / c->K, k = u % c->K;
+    for (int64_t m = 0; m < c->M; ++m) {
+        const int64_t s = row_slot(c->slot, c->S, m);
+        if (s < 0) continue;
+        const double ct = c->ct[m * c->R + j];
+        if (ct == 0.0) continue;
+        const int64_t row0 = c->fused ? s * c->R : 0;
+        c->dA[(row0 + j) * c->K + k] += (float)(ct * q_x_at(c, m, k));
+    }
+}
+
+/* src/adjoint/host/lora.cpp:260-328 (the coded activation) */
+void orc_lora_shrink_q_adjoint(int64_t M, int64_t K, int64_t R, int64_t S, int64_t groups,
+                               const double* a, const double* a_scale, const double* slot,
+                               const double* lora_a, const double* ct, double* da, double* ds,
+                               float* dA, int fused) {
+    qshrink_ctx c = {M, K, R, S, groups, orc_group_width(K, groups), a, a_scale, slot, lora_a, ct,
+                     NULL, da, ds, dA, fused};
+    parallel_for(M, 2, q_shrink_cot_row, &c);
+    if (dA) parallel_for(R * K, 2, q_shrink_dA_pair, &c);
 }

@@ -77,6 +77,34 @@ void orc_lora_expand_adjoint(int64_t M, int64_t N, int64_t R, int64_t S, const d
 /* bf16 rounding the _mm twin applies (src/adjoint/host/lora.cpp:127-135): no NaN quieting */
 double orc_rounded_bf16(double v);
 
+/* ---- the coded (i8a8h) trunk: int8 activation codes with an f32 scale per (row, group) ---- */
+
+/* the width of one scale group over k columns from the stream's `groups` columns
+ * (src/adjoint/host/lora.cpp:70-77): the power of two whose ceiling division gives `groups`
+ * (300 over 3 -> 128), else ceil(k / groups); one group spans the row */
+int64_t orc_group_width(int64_t k, int64_t groups);
+/* gemm_nt_q twin over a stored weight (src/adjoint/host/linear.cpp:245-282), group 128:
+ * y[m,n] = sum_g (sum_{k in g} a[m,k] code[n,k]) * a_scale[m,g] * bf16(scale[n,g]), f64 */
+void orc_gemm_nt_q_twin(int64_t M, int64_t N, int64_t K, const double* a, const double* a_scale,
+                        const int8_t* codes, const uint16_t* scale, double* y);
+/* gemm_nt_q adjoint (src/adjoint/host/linear.cpp:284-317), the code basis:
+ * da[m,k] += (sum_n dy[m,n] code[n,k] bf16(scale[n,g])) * a_scale[m,g], g = k/128 */
+void orc_gemm_nt_q_adjoint(int64_t M, int64_t N, int64_t K, const double* dy, const int8_t* codes,
+                           const uint16_t* scale, const double* a_scale, double* da);
+/* coded lora_shrink twin (src/adjoint/host/lora.cpp:204-244): x[m,k] = a[m,k] * a_scale[m,
+ * k/group], group = orc_group_width(K, groups); t[m,j] = sum_k x[m,k] A[s,j,k] */
+void orc_lora_shrink_q_twin(int64_t M, int64_t K, int64_t R, int64_t S, int64_t groups,
+                            const double* a, const double* a_scale, const double* slot,
+                            const double* lora_a, double* t);
+/* coded lora_shrink adjoint (src/adjoint/host/lora.cpp:246-328), with g = ct . A_s:
+ * da[m,k] += g[m,k] a_scale[m,g(k)];  ds[m,g(k)] += g[m,k] a[m,k] (k ascending);
+ * dA[(fused? s*R : 0)+j, k] += (float)(ct[m,j] x[m,k]), f32 per term, rows serial.
+ * `ds` and `dA` may be NULL. */
+void orc_lora_shrink_q_adjoint(int64_t M, int64_t K, int64_t R, int64_t S, int64_t groups,
+                               const double* a, const double* a_scale, const double* slot,
+                               const double* lora_a, const double* ct, double* da, double* ds,
+                               float* dA, int fused);
+
 #ifdef __cplusplus
 }
 #endif

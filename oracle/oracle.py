@@ -71,6 +71,12 @@ def lib():
         L.orc_lora_shrink_adjoint.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, C.c_int]
         L.orc_lora_expand_twin.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, C.c_int, _P]
         L.orc_lora_expand_adjoint.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, C.c_int]
+        L.orc_group_width.restype = C.c_int64
+        L.orc_group_width.argtypes = [_I, _I]
+        L.orc_gemm_nt_q_twin.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P]
+        L.orc_gemm_nt_q_adjoint.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P]
+        L.orc_lora_shrink_q_twin.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P]
+        L.orc_lora_shrink_q_adjoint.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int]
         L.orc_rounded_bf16.restype = C.c_double
         L.orc_rounded_bf16.argtypes = [C.c_double]
         L.orc_thread_count.restype = C.c_int
@@ -93,6 +99,10 @@ def ref():
         R.ref_lora_shrink_adjoint.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, C.c_int]
         R.ref_lora_expand_twin.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, C.c_int, _P]
         R.ref_lora_expand_adjoint.argtypes = [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, C.c_int]
+        R.ref_gemm_nt_q_twin.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P]
+        R.ref_gemm_nt_q_adjoint.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P]
+        R.ref_lora_shrink_q_twin.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P]
+        R.ref_lora_shrink_q_adjoint.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int]
         _ref = R
     return _ref
 
@@ -291,3 +301,80 @@ def qlinear_lora_reference(x, codes, scale, A, B, s, dy, rows=None):
     dx, dA = lora_shrink_adjoint(x, slot, la, dt)
     dx = gemm_nt_adjoint(dy, codes, scale, dx=dx)
     return dict(y=y, t=t, dx=dx, dA=dA, dB=dB)
+
+
+# ------------------------------------------------------------------ the coded (i8a8h) trunk
+def group_width(k: int, groups: int) -> int:
+    return int(lib().orc_group_width(int(k), int(groups)))
+
+
+def _check_ref(rc):
+    if rc:
+        raise RuntimeError(ref().ref_last_error().decode())
+
+
+def gemm_nt_q_twin(a, a_scale, codes, scale, use_ref=False):
+    """a [M,K] codes (f64 of integers), a_scale [M, K/128], the stored weight (codes, bf16 scale)
+    -> y [M,N] = sum_g (a . code over group g) * a_scale[m,g] * scale[n,g]."""
+    a, a_scale = _f64(a), _f64(a_scale)
+    M, K = a.shape
+    N = codes.shape[0]
+    codes = np.ascontiguousarray(codes, np.int8)
+    scale = np.ascontiguousarray(scale, np.uint16)
+    y = np.zeros((M, N), np.float64)
+    if use_ref:
+        _check_ref(ref().ref_gemm_nt_q_twin(M, N, K, _ptr(a), _ptr(a_scale), _ptr(codes), _ptr(scale), _ptr(y)))
+        return y
+    lib().orc_gemm_nt_q_twin(M, N, K, _ptr(a), _ptr(a_scale), _ptr(codes), _ptr(scale), _ptr(y))
+    return y
+
+
+def gemm_nt_q_adjoint(dy, codes, scale, a_scale, da=None, use_ref=False):
+    """da [M,K] += (dy . W)[m,k] * a_scale[m, k/128] (the code basis)."""
+    dy, a_scale = _f64(dy), _f64(a_scale)
+    M, N = dy.shape
+    K = codes.shape[1]
+    codes = np.ascontiguousarray(codes, np.int8)
+    scale = np.ascontiguousarray(scale, np.uint16)
+    da = np.zeros((M, K), np.float64) if da is None else _f64(da).copy()
+    if use_ref:
+        _check_ref(ref().ref_gemm_nt_q_adjoint(M, N, K, _ptr(dy), _ptr(codes), _ptr(scale), _ptr(a_scale), _ptr(da)))
+        return da
+    lib().orc_gemm_nt_q_adjoint(M, N, K, _ptr(dy), _ptr(codes), _ptr(scale), _ptr(a_scale), _ptr(da))
+    return da
+
+
+def lora_shrink_q_twin(a, a_scale, slot, lora_a, use_ref=False):
+    """The coded shrink: x = a * a_scale[m, k / group_width(K, groups)]; t = x . A_s^T."""
+    a, a_scale, slot, la = _f64(a), _f64(a_scale), _f64(slot), _f64(lora_a)
+    M, K = a.shape
+    groups = a_scale.shape[1]
+    S, R, _ = la.shape
+    t = np.zeros((M, R), np.float64)
+    if use_ref:
+        _check_ref(ref().ref_lora_shrink_q_twin(M, K, R, S, group_width(K, groups), _ptr(a), _ptr(a_scale),
+                                                _ptr(slot), _ptr(la), _ptr(t)))
+        return t
+    lib().orc_lora_shrink_q_twin(M, K, R, S, groups, _ptr(a), _ptr(a_scale), _ptr(slot), _ptr(la), _ptr(t))
+    return t
+
+
+def lora_shrink_q_adjoint(a, a_scale, slot, lora_a, ct, da=None, ds=None, dA=None, fused=False, use_ref=False):
+    """-> (da [M,K] code cotangent, ds [M,groups] scale cotangent, dA f32 leaf), each added into
+    what is passed."""
+    a, a_scale, slot, la, ct = _f64(a), _f64(a_scale), _f64(slot), _f64(lora_a), _f64(ct)
+    M, K = a.shape
+    groups = a_scale.shape[1]
+    S, R, _ = la.shape
+    da = np.zeros((M, K), np.float64) if da is None else _f64(da).copy()
+    ds = np.zeros((M, groups), np.float64) if ds is None else _f64(ds).copy()
+    rows = S * R if fused else R
+    dA = np.zeros((rows, K), np.float32) if dA is None else np.ascontiguousarray(dA, np.float32).copy()
+    if use_ref:
+        _check_ref(ref().ref_lora_shrink_q_adjoint(M, K, R, S, group_width(K, groups), _ptr(a), _ptr(a_scale),
+                                                   _ptr(slot), _ptr(la), _ptr(ct), _ptr(da), _ptr(ds), _ptr(dA),
+                                                   int(fused)))
+        return da, ds, dA
+    lib().orc_lora_shrink_q_adjoint(M, K, R, S, groups, _ptr(a), _ptr(a_scale), _ptr(slot), _ptr(la), _ptr(ct),
+                                    _ptr(da), _ptr(ds), _ptr(dA), int(fused))
+    return da, ds, dA

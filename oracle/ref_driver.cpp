@@ -91,6 +91,34 @@ OpRecord expand_rec(int64_t M, int64_t N, int64_t R, int64_t S, bool mm) {
     return rec;
 }
 
+// tests/host/adjoint_linear.cpp:108-120, the weight stored
+OpRecord gemm_nt_q_rec(int64_t M, int64_t N, int64_t K) {
+    OpRecord rec;
+    rec.op = "gemm_nt_q";
+    rec.params = {{"M", M}, {"N", N}, {"K", K}, {"group", 128}, {"dtype", "i8a8h"}};
+    rec.operands = {
+        {"a", "i8", {M, K}, 0, M, false},
+        {"a_scale", "f32", {M, K / 128}, 0, M, false},
+        {"b", "i8", {N, K}, 0, N, false},
+        {"b_scale", "bf16", {N, K / 128}, 0, N, false},
+        {"y", "f32", {M, N}, 0, M, true},
+    };
+    return rec;
+}
+
+// tests/host/adjoint_lora.cpp:89-106, the coded form
+OpRecord shrink_q_rec(int64_t M, int64_t K, int64_t R, int64_t S, int64_t group) {
+    OpRecord rec;
+    rec.op = "lora_shrink";
+    rec.params = {{"M", M}, {"K", K}, {"R", R}, {"S", S}, {"group", group}, {"dtype", "i8"}};
+    rec.operands = {{"a", "i8", {M, K}, 0, M, false},
+                    {"a_scale", "f32", {M, (K + group - 1) / group}, 0, M, false},
+                    {"slot", "i32", {M}, 0, M, false},
+                    {"lora_a", "bf16", {S, R, K}, 0, S, false},
+                    {"t", "f32", {M, R}, 0, M, true}};
+    return rec;
+}
+
 thread_local std::string g_err;
 
 }  // namespace
@@ -243,6 +271,107 @@ int ref_lora_expand_adjoint(int64_t M, int64_t N, int64_t R, int64_t S, const do
         fn(call);
         std::memcpy(dt, dc[0].value.data(), sizeof(double) * (size_t)(M * R));
         std::memcpy(db, grads[0].value.data(), sizeof(float) * (size_t)nb);
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+int ref_gemm_nt_q_twin(int64_t M, int64_t N, int64_t K, const double* a, const double* a_scale,
+                       const int8_t* codes, const uint16_t* scale, double* y) {
+    try {
+        put_weight(N, K, codes, scale);
+        OpRecord rec = gemm_nt_q_rec(M, N, K);
+        AdValue b = stored_operand(N, K);
+        b.dtype = "i8";
+        std::vector<AdValue> reads = {values("i8", {M, K}, a), values("f32", {M, K / 128}, a_scale), b,
+                                      values("bf16", {N, K / 128}, nullptr)};
+        std::vector<AdValue> out;
+        TwinFn fn = twin_find(rec.op, rec.params, &g_err);
+        if (!fn) return 1;
+        fn(rec, reads, &out);
+        stored_weight_clear();
+        if (out.size() != 1 || (int64_t)out[0].value.size() != M * N) return 2;
+        std::memcpy(y, out[0].value.data(), sizeof(double) * (size_t)(M * N));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+int ref_gemm_nt_q_adjoint(int64_t M, int64_t N, int64_t K, const double* dy, const int8_t* codes,
+                          const uint16_t* scale, const double* a_scale, double* da) {
+    try {
+        put_weight(N, K, codes, scale);
+        OpRecord rec = gemm_nt_q_rec(M, N, K);
+        AdValue b = stored_operand(N, K);
+        b.dtype = "i8";
+        std::vector<AdValue> fwd = {values("i8", {M, K}, nullptr), values("f32", {M, K / 128}, a_scale), b,
+                                    values("bf16", {N, K / 128}, nullptr), values("f32", {M, N}, nullptr)};
+        std::vector<AdValue> cot = {values("f32", {M, N}, dy)};
+        std::vector<AdValue> dc = {values("i8", {M, K}, da), AdValue{}, AdValue{}, AdValue{}, AdValue{}};
+        AdjointFn fn = adjoint_find(rec.op, Side::host, rec.params, &g_err);
+        if (!fn) return 1;
+        AdjointCall call{rec, fwd, cot, &dc, nullptr, ""};
+        fn(call);
+        stored_weight_clear();
+        std::memcpy(da, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+int ref_lora_shrink_q_twin(int64_t M, int64_t K, int64_t R, int64_t S, int64_t group, const double* a,
+                           const double* a_scale, const double* slot, const double* la, double* t) {
+    try {
+        OpRecord rec = shrink_q_rec(M, K, R, S, group);
+        const int64_t groups = (K + group - 1) / group;
+        std::vector<AdValue> reads = {values("i8", {M, K}, a), values("f32", {M, groups}, a_scale),
+                                      values("i32", {M}, slot), values("bf16", {S, R, K}, la)};
+        std::vector<AdValue> out;
+        TwinFn fn = twin_find(rec.op, rec.params, &g_err);
+        if (!fn) return 1;
+        fn(rec, reads, &out);
+        if (out.size() != 1) return 2;
+        std::memcpy(t, out[0].value.data(), sizeof(double) * (size_t)(M * R));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+int ref_lora_shrink_q_adjoint(int64_t M, int64_t K, int64_t R, int64_t S, int64_t group, const double* a,
+                              const double* a_scale, const double* slot, const double* la, const double* ct,
+                              double* da, double* ds, float* dA, int fused) {
+    try {
+        OpRecord rec = shrink_q_rec(M, K, R, S, group);
+        const int64_t groups = (K + group - 1) / group;
+        std::vector<AdValue> fwd = {values("i8", {M, K}, a), values("f32", {M, groups}, a_scale),
+                                    values("i32", {M}, slot), values("bf16", {S, R, K}, la),
+                                    values("f32", {M, R}, nullptr)};
+        std::vector<AdValue> cot = {values("f32", {M, R}, ct)};
+        std::vector<AdValue> dc = {values("i8", {M, K}, da), values("f32", {M, groups}, ds), AdValue{},
+                                   AdValue{}, AdValue{}};
+        ParamSet grads;
+        Param p;
+        p.name = "site.lora_A";
+        p.shape = fused ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
+        const int64_t na = (fused ? S * R : R) * K;
+        p.value.assign(dA, dA + na);
+        grads.push_back(std::move(p));
+        AdjointFn fn = adjoint_find(rec.op, Side::host, rec.params, &g_err);
+        if (!fn) return 1;
+        AdjointCall call{rec, fwd, cot, &dc, &grads, "site"};
+        call.fused_slots = fused != 0;
+        fn(call);
+        std::memcpy(da, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
+        std::memcpy(ds, dc[1].value.data(), sizeof(double) * (size_t)(M * groups));
+        std::memcpy(dA, grads[0].value.data(), sizeof(float) * (size_t)na);
         return 0;
     } catch (const std::exception& e) {
         g_err = e.what();

@@ -2,8 +2,9 @@
 
 Run in the build container, where oracle/_ref/libr97ref.so was compiled from the reference's host
 sources (oracle/Makefile): every expected output below is what the reference's r97_iqr_decode_host
-(src/iqr_decode.h:353-376), gemm_nt twin/adjoint (src/adjoint/host/linear.cpp:193-243) and float
-lora_shrink / lora_expand twins and adjoints (src/adjoint/host/lora.cpp:226-521) return for the
+(src/iqr_decode.h:353-376), gemm_nt / gemm_nt_q twins and adjoints (src/adjoint/host/linear.cpp:
+193-317) and float / coded lora_shrink and lora_expand twins and adjoints
+(src/adjoint/host/lora.cpp:204-521) return for the
 seeded inputs stored beside them. The fixtures are data only (inputs and expected outputs); the
 reference's source never enters the repository.
 
@@ -147,6 +148,55 @@ def lora_fixtures():
         print("lora", name)
 
 
+# The coded trunk (i8a8h). gemm_nt_q over a stored weight at the reference test's shapes
+# (tests/host/adjoint_linear.cpp:180-182: M, N, K) and the coded LoRA sites
+# (tests/host/adjoint_lora.cpp:66-68: name, M, K, N, R, S, group), with the test's value rules:
+# integer codes in [-60, 60], one positive f32 scale a (row, group).
+LINEAR_Q_SITES = [("q_small", 4, 256, 128, 601), ("q_one", 1, 128, 256, 602), ("q_odd", 7, 320, 384, 603)]
+LORA_Q_SITES = [("coded_q_proj", 3, 128, 4, 2, 128), ("coded_down_proj", 4, 256, 4, 1, 128),
+                ("coded_up_proj", 5, 300, 4, 2, 128)]
+
+
+def codes_and_scales(rng, M, K, groups):
+    a = np.rint(rng.uniform(-1.0, 1.0, (M, K)) * 60.0)
+    i = np.arange(M * groups).reshape(M, groups)
+    a_scale = (0.02 + 0.01 * (i % 7) + 0.004 * np.abs(rng.uniform(-1.0, 1.0, (M, groups)))).astype(np.float32)
+    return a, a_scale.astype(np.float64)
+
+
+def linear_q_fixtures():
+    rng = np.random.default_rng(17)
+    for name, M, N, K, seed in LINEAR_Q_SITES:
+        factor = (0.75 + 0.5 * rng.random(K // 128)).astype(np.float32)
+        codes, scale = stored_weight(N, K, seed=seed, scale_col=factor)
+        a, a_scale = codes_and_scales(rng, M, K, K // 128)
+        dy = rng.standard_normal((M, N))
+        da0 = rng.standard_normal((M, K))
+        y = O.gemm_nt_q_twin(a, a_scale, codes, scale, use_ref=True)
+        da = O.gemm_nt_q_adjoint(dy, codes, scale, a_scale, da=da0, use_ref=True)
+        np.savez_compressed(os.path.join(OUT, f"linear_{name}.npz"), a=a, a_scale=a_scale, dy=dy, da0=da0,
+                            codes=codes, scale=scale, y=y, da=da)
+        print("linear", name)
+
+
+def lora_q_fixtures():
+    rng = np.random.default_rng(19)
+    for name, M, K, R, S_, group in LORA_Q_SITES:
+        groups = (K + group - 1) // group
+        slot = slots_of(M, S_)
+        a, a_scale = codes_and_scales(rng, M, K, groups)
+        la = bf16r(rng.uniform(-1.0, 1.0, (S_, R, K)))
+        ct = rng.standard_normal((M, R))
+        t = O.lora_shrink_q_twin(a, a_scale, slot, la, use_ref=True)
+        out = {}
+        for fused in (0, 1):
+            da, ds, dA = O.lora_shrink_q_adjoint(a, a_scale, slot, la, ct, fused=bool(fused), use_ref=True)
+            out.update({f"da_f{fused}": da, f"ds_f{fused}": ds, f"dA_f{fused}": dA})
+        np.savez_compressed(os.path.join(OUT, f"lora_{name}.npz"), a=a, a_scale=a_scale, slot=slot, la=la,
+                            ct=ct, t=t, **out)
+        print("lora", name)
+
+
 def c1_fixture():
     """Config 1 composed from the reference rows: W 1024x1024 from
     N(0, 0.02) through this repo's quantizer is not available to the reference, so the stored
@@ -183,4 +233,6 @@ if __name__ == "__main__":
     decode_fixtures()
     linear_fixtures()
     lora_fixtures()
+    linear_q_fixtures()
+    lora_q_fixtures()
     c1_fixture()

@@ -384,3 +384,109 @@ def test_c1_reference_composition():
     assert np.array_equal(out["dx"][[0, 1, 63, 127]], z["dx_rows"])
     assert hashlib.sha256(out["y"].tobytes()).hexdigest() == str(z["y_sha"])
     assert hashlib.sha256(out["dx"].tobytes()).hexdigest() == str(z["dx_sha"])
+
+
+# ------------------------------------------------------------------ the coded (i8a8h) trunk
+def test_group_width_reference_cases_and_property():
+    # lora.cpp:64-69: 300 over three columns is groups of 128, 128, 44; one column spans the row
+    assert O.group_width(300, 3) == 128 and O.group_width(300, 1) == 300 and O.group_width(256, 2) == 128
+    assert O.group_width(0, 3) == 1
+    for k in range(1, 700, 7):
+        for groups in range(1, 9):
+            w = O.group_width(k, groups)
+            # every column's group index k // w stays inside the stream's `groups` columns
+            assert -(-k // w) <= groups and w >= -(-k // groups), (k, groups, w)
+    # a power-of-two width that splits k into exactly `groups` groups is the one read back
+    for p2 in (16, 64, 128, 256):
+        for groups in (2, 3, 5, 8):
+            for tail in (0, 1, p2 // 2, p2 - 1):
+                k = (groups - 1) * p2 + (tail if tail else p2)
+                assert O.group_width(k, groups) == p2, (k, groups)
+
+
+@pytest.mark.parametrize("name", ["q_small", "q_one", "q_odd"])
+def test_gemm_nt_q_golden_and_closed_form(name):
+    z = np.load(os.path.join(G, f"linear_{name}.npz"))
+    a, a_scale, dy, da0, codes, scale = (z[k] for k in ("a", "a_scale", "dy", "da0", "codes", "scale"))
+    y = O.gemm_nt_q_twin(a, a_scale, codes, scale)
+    da = O.gemm_nt_q_adjoint(dy, codes, scale, a_scale, da=da0)
+    assert np.array_equal(y, z["y"])
+    assert np.array_equal(da, z["da"])
+    # closed forms: x = a * a_scale (per row, group), W = code * scale
+    K = a.shape[1]
+    x = a * np.repeat(a_scale, 128, axis=1)[:, :K]
+    W = w_of(codes, scale)
+    np.testing.assert_allclose(y, x @ W.T, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(da, da0 + (dy @ W) * np.repeat(a_scale, 128, axis=1)[:, :K], rtol=1e-12, atol=1e-12)
+    # the code basis: <dy, twin(a + e)> - <dy, twin(a)> == <adj(dy), e> with the scale held
+    e = np.random.default_rng(3).standard_normal(a.shape)
+    lhs = np.sum(dy * O.gemm_nt_q_twin(a + e, a_scale, codes, scale)) - np.sum(dy * y)
+    rhs = np.sum(O.gemm_nt_q_adjoint(dy, codes, scale, a_scale) * e)
+    assert abs(lhs - rhs) <= 1e-9 * (abs(lhs) + 1.0)
+    # a wrong basis (the value-space cotangent, no a_scale) fails the identity
+    bad = np.sum((dy @ W) * e)
+    assert abs(lhs - bad) > 1e-3 * abs(lhs)
+
+
+@pytest.mark.parametrize("name", ["coded_q_proj", "coded_down_proj", "coded_up_proj"])
+def test_lora_shrink_q_golden_and_closed_forms(name):
+    z = np.load(os.path.join(G, f"lora_{name}.npz"))
+    a, a_scale, slot, la, ct = (z[k] for k in ("a", "a_scale", "slot", "la", "ct"))
+    t = O.lora_shrink_q_twin(a, a_scale, slot, la)
+    assert np.array_equal(t, z["t"])
+    for fused in (0, 1):
+        da, ds, dA = O.lora_shrink_q_adjoint(a, a_scale, slot, la, ct, fused=bool(fused))
+        assert np.array_equal(da, z[f"da_f{fused}"])
+        assert np.array_equal(ds, z[f"ds_f{fused}"])
+        assert np.array_equal(dA, z[f"dA_f{fused}"])
+    S_, R, K = la.shape
+    groups = a_scale.shape[1]
+    gw = O.group_width(K, groups)
+    gidx = np.arange(K) // gw
+    x = a * a_scale[:, gidx]
+    s = slot_matrix(slot, S_)
+    da, ds, dA = O.lora_shrink_q_adjoint(a, a_scale, slot, la, ct, fused=True)
+    for m in range(a.shape[0]):
+        if s[m] < 0:
+            assert not t[m].any() and not da[m].any() and not ds[m].any()
+            continue
+        g = ct[m] @ la[s[m]]
+        np.testing.assert_allclose(t[m], la[s[m]] @ x[m], rtol=1e-12)
+        np.testing.assert_allclose(da[m], g * a_scale[m, gidx], rtol=1e-12, atol=1e-15)
+        np.testing.assert_allclose(ds[m], np.bincount(gidx, weights=g * a[m], minlength=groups), rtol=1e-10,
+                                   atol=1e-12)
+        # the scale cotangent is the twin's derivative in the scale: d<ct, t>/d a_scale[m, q]
+        for q in range(groups):
+            hsc = a_scale.copy()
+            h = 1e-6 * a_scale[m, q]
+            hsc[m, q] += h
+            tp = O.lora_shrink_q_twin(a, hsc, slot, la)
+            hsc[m, q] -= 2 * h
+            tm = O.lora_shrink_q_twin(a, hsc, slot, la)
+            fd = (np.sum(ct * tp) - np.sum(ct * tm)) / (2 * h)
+            assert abs(fd - ds[m, q]) <= 1e-6 * (abs(ds[m, q]) + 1e-3)
+    for q in range(S_):
+        rows = s == q
+        np.testing.assert_allclose(dA[q * R:(q + 1) * R], ct[rows].T @ x[rows], rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built")
+def test_coded_rows_match_reference_fresh():
+    rng = np.random.default_rng(77)
+    M, N, K = 5, 128, 256
+    codes = rng.integers(-126, 127, size=(N, K)).astype(np.int8)
+    scale = S.f32_to_bf16_bits((1e-3 * (0.5 + rng.random((N, K // 128)))).astype(np.float32))
+    a = np.rint(rng.uniform(-60, 60, (M, K)))
+    a_scale = (0.01 + 0.05 * rng.random((M, K // 128))).astype(np.float32).astype(np.float64)
+    dy = rng.standard_normal((M, N))
+    assert np.array_equal(O.gemm_nt_q_twin(a, a_scale, codes, scale),
+                          O.gemm_nt_q_twin(a, a_scale, codes, scale, use_ref=True))
+    assert np.array_equal(O.gemm_nt_q_adjoint(dy, codes, scale, a_scale),
+                          O.gemm_nt_q_adjoint(dy, codes, scale, a_scale, use_ref=True))
+    slot = np.array([0, -1, 2, 1, 0], np.float64)
+    la = S.bf16_bits_to_f32(S.f32_to_bf16_bits(rng.standard_normal((2, 8, K)).astype(np.float32))).astype(np.float64)
+    ct = rng.standard_normal((M, 8))
+    got = O.lora_shrink_q_adjoint(a, a_scale, slot, la, ct)
+    want = O.lora_shrink_q_adjoint(a, a_scale, slot, la, ct, use_ref=True)
+    for g_, w_ in zip(got, want):
+        assert np.array_equal(g_, w_)
