@@ -249,6 +249,31 @@ int r97q_lora_expand_bwd(int64_t T, int64_t N, const uint16_t* dY, const uint16_
                          const float* t, float* t_cot, float* dB, void* workspace, int64_t workspace_bytes,
                          R97IqrStream stream);
 
+/* ------------------------------------------------------------------ the coded (i8a8h) trunk
+ *
+ * The activation arrives as int8 codes a [T, K] with one f32 scale a_scale [T, groups] per (row,
+ * group); its value is x = a * a_scale[m, k / group_width(K, groups)] (the reference's width rule,
+ * src/adjoint/host/lora.cpp:70-77). The rows differentiate in the code basis.
+ *
+ * gemm_nt_q's adjoint (the reference's device row gemm_nt_q_device, src/adjoint/device/linear.hip:
+ * 744-760, registered for dtype i8a8h with group 128; host form src/adjoint/host/linear.cpp:
+ * 284-317): dA[m, k] (+)= a_scale[m, k/128] . sum_n dY[m, n] W(n, k), the fused decode + MFMA dX
+ * kernel with the scale in its epilogue (each of its 128-column output tiles is one group).
+ * a_scale f32 [T, K/128]; dA f32 or bf16 [T, K], added into when accumulate. No workspace. */
+int r97q_gemm_nt_q_dx(const R97qWeight* w, const uint16_t* dY, int64_t T, const float* a_scale, void* dA,
+                      int32_t da_dtype, int32_t accumulate, R97IqrStream stream);
+/* The coded lora_shrink's adjoint (the reference's device row for the coded trunk,
+ * src/adjoint/device/lora.hip:437-577, registered for a coded activation; host form
+ * src/adjoint/host/lora.cpp:246-328), one adapter slot, with g = t_cot . A (f32 [T, K]):
+ *   da [T, K]      += g * a_scale        (the code's cotangent)
+ *   ds [T, groups] += sum over each group of g * a   (the scale's cotangent)
+ *   dA [r, K]      += t_cot^T . x
+ * t_cot f32 [T, r]; any output may be NULL; K a multiple of 128. */
+int64_t r97q_lora_shrink_q_bwd_workspace_bytes(int64_t T, int64_t K, int32_t rank);
+int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const int8_t* a, const float* a_scale, int64_t groups,
+                           const uint16_t* A, int32_t rank, const float* t_cot, float* da, float* ds, float* dA,
+                           void* workspace, int64_t workspace_bytes, R97IqrStream stream);
+
 #ifdef __cplusplus
 }
 #endif

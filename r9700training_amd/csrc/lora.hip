@@ -25,6 +25,10 @@
 //                      dX kernel carries it in its epilogue when the base product runs too).
 //   transpose2_kernel  B [N, r] -> B^T [rd, N] (zero rows up to the 16-wide rank) and
 //                      A [r, K] -> A^T [K, r], in one launch.
+//   coded_cot_kernel   the coded shrink's two cotangents from the value-space one g = t_cot . A:
+//                      the code's g * scale and the scale's sum over its group of g * code.
+//   coded_x_kernel     the coded activation's values x = code * scale as a [hi | lo] bf16 pair (the
+//                      token operand of its dA).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -412,6 +416,48 @@ __global__ __launch_bounds__(256) void lora_up_kernel(const uint16_t* __restrict
         }
 }
 
+// ---------------------------------------------------------------- the coded activation
+// One workgroup a (row m, scale group q), group width gw (the last group may be short):
+//   da[m, k] += g[m, k] * s[m, q];   ds[m, q] += sum_{k in q} g[m, k] * code[m, k]
+// the sum reduced in a fixed tree order (the same bits on every call).
+__global__ __launch_bounds__(256) void coded_cot_kernel(const float* __restrict__ g, const int8_t* __restrict__ code,
+                                                        const float* __restrict__ s, int64_t K, int64_t groups,
+                                                        int64_t gw, float* __restrict__ da, float* __restrict__ ds) {
+    __shared__ float red[256];
+    const int64_t m = blockIdx.x, q = blockIdx.y;
+    const float sc = s[m * groups + q];
+    const int64_t k0 = q * gw, k1 = k0 + gw < K ? k0 + gw : K;
+    float part = 0.0f;
+    for (int64_t k = k0 + threadIdx.x; k < k1; k += blockDim.x) {
+        const float gv = g[m * K + k];
+        if (da) da[m * K + k] += gv * sc;
+        part += gv * (float)code[m * K + k];
+    }
+    if (!ds) return;
+    red[threadIdx.x] = part;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) ds[m * groups + q] += red[0];
+}
+
+// x[m, k] = code[m, k] * s[m, k / gw] (exact in f32: an 8-bit code times an f32 scale rounds once),
+// as hi = bf16(x), lo = bf16(x - hi)
+__global__ __launch_bounds__(256) void coded_x_kernel(const int8_t* __restrict__ code, const float* __restrict__ s,
+                                                      int64_t T, int64_t K, int64_t groups, int64_t gw,
+                                                      uint16_t* __restrict__ xhi, uint16_t* __restrict__ xlo) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= T * K) return;
+    const int64_t m = i / K, k = i % K;
+    const float x = (float)code[i] * s[m * groups + k / gw];
+    uint16_t hi, lo;
+    split(x, hi, lo);
+    xhi[i] = hi;
+    xlo[i] = lo;
+}
+
 // ---------------------------------------------------------------- transposes
 // y 0: Bt[q][n] = B[n][q] for q < r, 0 for r <= q < rd;  y 1: At[k][j] = A[j][k]
 __global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* __restrict__ B,
@@ -511,6 +557,20 @@ int launch_lora_up(const uint16_t* P, const uint16_t* Q, int64_t T, int64_t C, i
     hipLaunchKernelGGL(lora_up_kernel, dim3((unsigned)((C + 255) / 256), (unsigned)((T + 31) / 32)), dim3(256), 0, s,
                        P, Q, T, C, r, out, accumulate);
     return launch_status("lora_up_kernel");
+}
+
+int launch_coded_cot(const float* g, const int8_t* code, const float* a_scale, int64_t T, int64_t K, int64_t groups,
+                     int64_t gw, float* da, float* ds, hipStream_t s) {
+    hipLaunchKernelGGL(coded_cot_kernel, dim3((unsigned)T, (unsigned)groups), dim3(gw >= 256 ? 256 : 128), 0, s, g,
+                       code, a_scale, K, groups, gw, da, ds);
+    return launch_status("coded_cot_kernel");
+}
+
+int launch_coded_x(const int8_t* code, const float* a_scale, int64_t T, int64_t K, int64_t groups, int64_t gw,
+                   uint16_t* xhi, uint16_t* xlo, hipStream_t s) {
+    hipLaunchKernelGGL(coded_x_kernel, dim3((unsigned)((T * K + 255) / 256)), dim3(256), 0, s, code, a_scale, T, K,
+                       groups, gw, xhi, xlo);
+    return launch_status("coded_x_kernel");
 }
 
 int launch_transpose2(const uint16_t* B, uint16_t* Bt, int64_t N, const uint16_t* A, uint16_t* At,

@@ -99,6 +99,38 @@ ExpandWs expand_ws(int64_t T, int64_t N, int r) {
     return w;
 }
 
+// The coded shrink's adjoint: P [T, 2r] | Pt [2r, ldt] | At [K, r] | g [T, K] f32 | xhi, xlo [T, K]
+// bf16 | part [chunks, r, K] f32.
+struct ShrinkQWs {
+    int64_t P, Pt, At, g, xhi, xlo, part, total;
+};
+ShrinkQWs shrink_q_ws(int64_t T, int64_t K, int r) {
+    ShrinkQWs w{};
+    if (r == 0) return w;
+    const int64_t ldt = grad_ld(T);
+    w.P = 0;
+    w.Pt = w.P + align256(T * 2 * r * 2);
+    w.At = w.Pt + align256(2 * r * ldt * 2);
+    w.g = w.At + align256(K * r * 2);
+    w.xhi = w.g + align256(T * K * 4);
+    w.xlo = w.xhi + align256(T * K * 2);
+    w.part = w.xlo + align256(T * K * 2);
+    w.total = w.part + align256(grad_chunks(T, K, 0) * r * K * 4);
+    return w;
+}
+
+// the width of one activation-scale group over k columns, read back from `groups` scale columns
+// (src/adjoint/host/lora.cpp:70-77): the power of two whose ceiling division gives `groups`, else
+// ceil(k / groups); one group spans the row
+int64_t group_width(int64_t k, int64_t groups) {
+    if (k <= 0) return 1;
+    if (groups <= 1) return k;
+    const int64_t lo = (k + groups - 1) / groups;
+    int64_t b = 1;
+    while (b < lo) b <<= 1;
+    return (k + b - 1) / b == groups ? b : lo;
+}
+
 // zero-fill + copy of a [r, cols] bf16 matrix into [rd, cols] (rows r..rd-1 zero)
 __global__ __launch_bounds__(256) void pad_rows16(const uint16_t* __restrict__ in, int r, int rd,
                                                   int64_t cols, uint16_t* __restrict__ out) {
@@ -248,9 +280,11 @@ int bwd_grads(const Shape& sh, const uint16_t* X, const uint16_t* dY, float* dA,
 }
 
 int dx_base(const R97qWeight* w, const Shape& sh, const uint16_t* dY, void* dX, int32_t dx_dtype,
-            int32_t accumulate, uint8_t* wsb, hipStream_t s) {
+            int32_t accumulate, uint8_t* wsb, hipStream_t s, const float* a_scale = nullptr) {
     const BwdWs ws = bwd_ws(sh);
     DxParams p{};
+    p.a_scale = a_scale;
+    p.a_scale_ld = sh.K / kBN;
     p.dY = dY;
     p.T = sh.T;
     p.N = sh.N;
@@ -433,6 +467,73 @@ int r97q_qlinear_lora_bwd(const R97qWeight* w, const uint16_t* X, const uint16_t
         if (int e = bwd_grads(sh, X, dY, dA, dB, wsb, s)) return e;
     }
     return dx_base(w, sh, dY, dX, dx_dtype, dx_accumulate, wsb, s);
+}
+
+int r97q_gemm_nt_q_dx(const R97qWeight* w, const uint16_t* dY, int64_t T, const float* a_scale, void* dA,
+                      int32_t da_dtype, int32_t accumulate, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_gemm_nt_q_dx";
+    if (int e = check_weight(w)) return e;
+    if (!dY || !dA || !a_scale || T <= 0) {
+        set_error("%s: null dY / dA / a_scale or T <= 0", who);
+        return R97Q_EINVAL;
+    }
+    const Shape sh{T, w->rows, w->cols, 0};
+    return dx_base(w, sh, dY, dA, da_dtype, accumulate, nullptr, (hipStream_t)stream, a_scale);
+}
+
+int64_t r97q_lora_shrink_q_bwd_workspace_bytes(int64_t T, int64_t K, int32_t rank) {
+    return rank_ok(rank) && T > 0 && K > 0 ? shrink_q_ws(T, K, rank).total : -1;
+}
+
+int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const int8_t* a, const float* a_scale, int64_t groups,
+                           const uint16_t* A, int32_t rank, const float* t_cot, float* da, float* ds, float* dA,
+                           void* workspace, int64_t workspace_bytes, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_lora_shrink_q_bwd";
+    if (T <= 0 || K <= 0 || K % kBN || groups <= 0 || groups > K) {
+        set_error("%s: T %lld K %lld groups %lld (T > 0, K a multiple of 128, 0 < groups <= K)", who, (long long)T,
+                  (long long)K, (long long)groups);
+        return R97Q_EINVAL;
+    }
+    if (int e = check_rank(rank, who)) return e;
+    if (rank == 0 || (!da && !ds && !dA)) return R97Q_OK;
+    if (!a || !a_scale || !A || !t_cot) {
+        set_error("%s: null a, a_scale, A or t_cot", who);
+        return R97Q_EINVAL;
+    }
+    const ShrinkQWs ws = shrink_q_ws(T, K, rank);
+    if (int e = check_ws(workspace_bytes, ws.total, workspace, who)) return e;
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    const hipStream_t s = (hipStream_t)stream;
+    const int64_t ldt = grad_ld(T);
+    const int64_t gw = group_width(K, groups);
+    uint16_t* P = reinterpret_cast<uint16_t*>(wsb + ws.P);
+    uint16_t* Pt = reinterpret_cast<uint16_t*>(wsb + ws.Pt);
+    if (int e = launch_split(t_cot, T, rank, ldt, 1.0f, P, dA ? Pt : nullptr, s)) return e;
+    if (da || ds) {
+        // g = t_cot . A, then its two code-basis cotangents
+        uint16_t* At = reinterpret_cast<uint16_t*>(wsb + ws.At);
+        float* g = reinterpret_cast<float*>(wsb + ws.g);
+        if (int e = launch_transpose2(nullptr, nullptr, 0, A, At, K, rank, s)) return e;
+        if (int e = launch_lora_up(P, At, T, K, rank, g, 0, s)) return e;
+        if (int e = launch_coded_cot(g, a, a_scale, T, K, groups, gw, da, ds, s)) return e;
+    }
+    if (dA) {
+        // dA += t_cot^T . x with x = [hi | lo](a * a_scale): two gradient passes, one a half
+        uint16_t* xhi = reinterpret_cast<uint16_t*>(wsb + ws.xhi);
+        uint16_t* xlo = reinterpret_cast<uint16_t*>(wsb + ws.xlo);
+        if (int e = launch_coded_x(a, a_scale, T, K, groups, gw, xhi, xlo, s)) return e;
+        for (const uint16_t* x : {xhi, xlo}) {
+            GradArgs g{};
+            g.T = T;
+            g.ldt = ldt;
+            g.chunk = grad_chunk_rows(T, K, 0);
+            g.one[0] = GradOne{Pt, x, K, dA, 1.0f, 0, reinterpret_cast<float*>(wsb + ws.part)};
+            if (int e = launch_lora_grads(rank, g, 1, s)) return e;
+        }
+    }
+    return R97Q_OK;
 }
 
 int64_t r97q_lora_shrink_bwd_workspace_bytes(int64_t T, int64_t K, int32_t rank) {

@@ -41,6 +41,8 @@ struct DxParams {
     void* dX;
     int dx_f32;
     int accumulate;
+    const float* a_scale;  // null, or f32 [T, a_scale_ld]: dX[m, k] is multiplied by a_scale[m, k/128]
+    int64_t a_scale_ld;
     int mtiles, ktiles;
 };
 

@@ -367,9 +367,11 @@ __device__ __forceinline__ void adapter(const uint16_t* P, const uint16_t* Q, in
     }
 }
 
-// accumulator element e of tile (mi, ni) is row 32*mi + 8*(e/4) + 4*half + e%4, column 32*ni + l32
+// accumulator element e of tile (mi, ni) is row 32*mi + 8*(e/4) + 4*half + e%4, column 32*ni + l32;
+// rs (optional): a factor a row, rs[row * rs_ld], applied before the write
 __device__ __forceinline__ void store(const f32x16 (&acc)[2][4], void* out, int64_t ld, int64_t m0,
-                                      int64_t o0, int64_t T, int lane, int f32, int accumulate) {
+                                      int64_t o0, int64_t T, int lane, int f32, int accumulate,
+                                      const float* rs = nullptr, int64_t rs_ld = 0) {
     const int half = lane >> 5, l32 = lane & 31;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
@@ -377,10 +379,11 @@ __device__ __forceinline__ void store(const f32x16 (&acc)[2][4], void* out, int6
         for (int e = 0; e < 16; ++e) {
             const int64_t row = m0 + 32 * mi + 8 * (e >> 2) + 4 * half + (e & 3);
             if (row >= T) continue;
+            const float f = rs ? rs[row * rs_ld] : 1.0f;
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni) {
                 const int64_t col = o0 + 32 * ni + l32;
-                float v = acc[mi][ni][e];
+                float v = rs ? acc[mi][ni][e] * f : acc[mi][ni][e];
                 if (f32) {
                     float* d = reinterpret_cast<float*>(out) + row * ld + col;
                     *d = accumulate ? *d + v : v;
@@ -418,7 +421,9 @@ __device__ __forceinline__ void dx_wave(const DxParams& p, const Lds& lds, int l
                                (int64_t)mt * kBM + 64 * SLICE, (int64_t)kt * kBN, p.T, lane};
     L.run(lds, acc);
     if (p.rank > 0) adapter<false>(p.P, p.At, p.rank, L.m0, L.o0, p.T, lane, acc);
-    store(acc, p.dX, p.K, L.m0, L.o0, p.T, lane, p.dx_f32, p.accumulate);
+    // the coded trunk's code basis: the tile's 128 columns are one activation-scale group
+    const float* rs = p.a_scale ? p.a_scale + kt : nullptr;
+    store(acc, p.dX, p.K, L.m0, L.o0, p.T, lane, p.dx_f32, p.accumulate, rs, p.a_scale_ld);
 }
 
 #define R97Q_WAVE_SWITCH(fn, ...)                  \

@@ -152,3 +152,41 @@ def lora_expand_bwd(dY, B, scale, t=None, t_cot=None, dB=None, want_dB=True, wor
                                     _ptr(dB if want_dB else None), _ptr(workspace), workspace.numel(), _stream(stream))
     check(rc, "r97q_lora_expand_bwd")
     return t_cot, dB
+
+
+# ------------------------------------------------------------------ the coded (i8a8h) trunk
+def gemm_nt_q_dx(w: QWeight, dY, a_scale, dA=None, accumulate=False, da_dtype=torch.float32, stream=None):
+    """gemm_nt_q's adjoint in the code basis: dA[m, k] (+)= a_scale[m, k/128] . (dY . W)[m, k].
+    dY bf16 [T, N], a_scale f32 [T, K/128]. Returns dA."""
+    T = dY.shape[0]
+    if dA is None:
+        dA = torch.zeros((T, w.K), dtype=da_dtype, device=dY.device)
+    rc = lib().r97q_gemm_nt_q_dx(C.byref(w.w), _ptr(dY), T, _ptr(a_scale), _ptr(dA),
+                                 R97Q_F32 if dA.dtype == torch.float32 else R97Q_BF16, int(bool(accumulate)),
+                                 _stream(stream))
+    check(rc, "r97q_gemm_nt_q_dx")
+    return dA
+
+
+def lora_shrink_q_bwd(a, a_scale, A, t_cot, da=None, ds=None, dA=None, want=("da", "ds", "dA"), workspace=None,
+                      stream=None):
+    """The coded shrink's adjoint: a int8 [T, K] codes, a_scale f32 [T, groups], A bf16 [r, K],
+    t_cot f32 [T, r]. Adds into (and returns) da f32 [T, K], ds f32 [T, groups], dA f32 [r, K]."""
+    T, K = a.shape
+    groups = a_scale.shape[1]
+    rank = A.shape[0]
+    dev = t_cot.device
+    if "da" in want and da is None:
+        da = torch.zeros((T, K), dtype=torch.float32, device=dev)
+    if "ds" in want and ds is None:
+        ds = torch.zeros((T, groups), dtype=torch.float32, device=dev)
+    if "dA" in want and dA is None:
+        dA = torch.zeros((rank, K), dtype=torch.float32, device=dev)
+    if workspace is None:
+        workspace = _workspace(lib().r97q_lora_shrink_q_bwd_workspace_bytes(T, K, rank), dev, "lora_shrink_q_bwd")
+    rc = lib().r97q_lora_shrink_q_bwd(T, K, _ptr(a), _ptr(a_scale), groups, _ptr(A), rank, _ptr(t_cot),
+                                      _ptr(da if "da" in want else None), _ptr(ds if "ds" in want else None),
+                                      _ptr(dA if "dA" in want else None), _ptr(workspace), workspace.numel(),
+                                      _stream(stream))
+    check(rc, "r97q_lora_shrink_q_bwd")
+    return da, ds, dA

@@ -10,6 +10,11 @@
 //   lora_expand  device, frozen {1, 2, 3}
 //                  dc[t] += (y_cot * scale_s) . B_s, leaf lora_B += (y_cot * scale_s)^T . t
 //                  and, for an in-place write, the write's own slot passes y_cot through
+//   gemm_nt_q    device, dtype i8a8h with group 128, frozen {1, 2, 3} (the coded trunk)
+//                  dc[a][m, k] += a_scale[m, k/128] . (dy . W)[m, k]   (the code basis)
+//   lora_shrink  device, a coded (int8) activation, frozen {2, 3}
+//                  with g = t_cot . A_s: dc[a] += g * a_scale, dc[a_scale] += the group sums of
+//                  g * a, leaf lora_A += t_cot^T . (a * a_scale)
 //
 // Every row follows the contract's ownership rules: it adds into `dc` and the leaves, never
 // overwrites, never writes a frozen slot, and returns with its results host-visible (one
@@ -25,6 +30,7 @@
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -74,6 +80,39 @@ bool serves_bf16(const std::vector<OpParam>& params) { return param_is(params, "
 bool float_act(const std::vector<OpParam>& params) {
     return !(param_is(params, "dtype", "i8") || param_is(params, "dtype", "fp8_e4m3") ||
              param_is(params, "dtype", "fp8_e5m2"));
+}
+
+// the coded trunk's gemm_nt_q: the i8a8h dtype with 128-wide groups (the stored weight's own)
+bool serves_i8a8h(const std::vector<OpParam>& params) {
+    const OpParam* g = find_param(params, "group");
+    const int64_t* gv = g ? std::get_if<int64_t>(&g->second) : nullptr;
+    return param_is(params, "dtype", "i8a8h") && gv && *gv == 128;
+}
+
+// the shrink's activation is int8 codes with a group scale (the fp8 code dtypes are not served)
+bool coded_i8_act(const std::vector<OpParam>& params) { return param_is(params, "dtype", "i8"); }
+
+// a scale operand's value for (row, group), the reference's layout rule for a grouped scale
+// (src/adjoint/host/linear.cpp:99-112): [rows, groups], one value, [groups] or [rows]
+double scale_at(const AdValue& sc, int64_t row, int64_t group, int64_t rows, int64_t groups) {
+    const int64_t n = (int64_t)sc.value.size();
+    if (n == 0) return 1.0;
+    if (n == 1) return sc.value[0];
+    if (n == rows * groups) return sc.value[(size_t)(row * groups + group)];
+    if (n == groups) return sc.value[(size_t)group];
+    if (n == rows) return sc.value[(size_t)row];
+    const int64_t at = std::min<int64_t>(row * groups + group, n - 1);
+    return sc.value[(size_t)at];
+}
+
+// src/adjoint/host/lora.cpp:70-77: the width of one scale group over k from `groups` columns
+int64_t group_width(int64_t k, int64_t groups) {
+    if (k <= 0) return 1;
+    if (groups <= 1) return k;
+    const int64_t lo = (k + groups - 1) / groups;
+    int64_t b = 1;
+    while (b < lo) b <<= 1;
+    return (k + b - 1) / b == groups ? b : lo;
 }
 
 bool rank_served(int64_t r) { return r == 8 || r == 16 || r == 32 || r == 64; }
@@ -415,6 +454,161 @@ void lora_expand_device(const AdjointCall& call) {
     for (size_t i = 0; i < h.size(); ++i) t_cot.value[i] += (double)h[i];
 }
 
+// ---------------------------------------------------------------- gemm_nt_q
+// gemm_nt_q's adjoint (src/adjoint/host/linear.cpp:284-317, device row
+// src/adjoint/device/linear.hip:744-760): schema a [M, K] codes, a_scale, b [N, K], b_scale, y;
+//   dc[a][m, k] += a_scale[m, k/128] . sum_n dy[m, n] code[n, k] b_scale[n, k/128]
+// the cotangent of the int8 codes (not a code itself: f64, added in unrounded).
+void gemm_nt_q_device(const AdjointCall& call) {
+    const OpRecord& rec = call.rec;
+    const int ia = operand_pos(rec, "a"), ias = operand_pos(rec, "a_scale"), ib = operand_pos(rec, "b"),
+              ibs = operand_pos(rec, "b_scale");
+    if (ia < 0 || ib < 0 || ias < 0 || call.cot.empty() || !call.dc ||
+        (size_t)std::max(std::max(ia, ib), std::max(ias, ibs)) >= call.fwd.size())
+        return;
+    const AdValue& a = call.fwd[(size_t)ia];
+    const AdValue& as = call.fwd[(size_t)ias];
+    const AdValue& b = call.fwd[(size_t)ib];
+    const AdValue& dy = call.cot[0];
+    const int64_t K = param_int(rec, "K", a.shape.size() >= 2 ? a.shape[1] : 0);
+    const int64_t N = param_int(rec, "N", b.shape.size() >= 2 ? b.shape[0] : 0);
+    const int64_t M = param_int(rec, "M", a.shape.empty() ? 0 : a.shape[0]);
+    AdValue& da = (*call.dc)[(size_t)ia];
+    if (M <= 0 || N <= 0 || K <= 0 || (int64_t)dy.value.size() != M * N || (int64_t)da.value.size() != M * K) return;
+    const bool stored = b.raw != nullptr || b.enc != nullptr;
+    if (!stored && ((int64_t)b.value.size() != N * K || ibs < 0)) return;
+    if (K % 128 || N % 128) refuse(rec.op, "weight " + dims({N, K}) + ": N and K must be multiples of 128");
+    const int64_t groups = K / 128;
+    std::vector<float> sa((size_t)(M * groups));
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t g = 0; g < groups; ++g) sa[(size_t)(m * groups + g)] = (float)scale_at(as, m, g, M, groups);
+
+    Card& c = card();
+    std::lock_guard<std::mutex> lock(c.mu);
+    const hipStream_t s = stream_of(c);
+    std::vector<uint16_t> hi, lo;
+    split_bf16(dy.value, hi, lo);
+    const uint16_t* d_hi = upload(c, "dy_hi", hi);
+    const uint16_t* d_lo = upload(c, "dy_lo", lo);
+    float* d_da = static_cast<float*>(buffer(c, "dx", (size_t)(M * K) * 4));
+    std::vector<float> h;
+    if (stored) {
+        if (!b.enc) refuse(rec.op, "a stored weight operand carries no encoding");
+        const R97qWeight* w = device_weight_get(static_cast<const IqrStoredEnc*>(b.enc), N, K, s);
+        const float* d_sa = upload(c, "a_scale", sa);
+        r97q_ok(r97q_gemm_nt_q_dx(w, d_hi, M, d_sa, d_da, R97Q_F32, 0, s), "gemm_nt_q dA");
+        r97q_ok(r97q_gemm_nt_q_dx(w, d_lo, M, d_sa, d_da, R97Q_F32, 1, s), "gemm_nt_q dA");
+        h = download(c, d_da, (size_t)(M * K));
+    } else {
+        // a weight carried as codes and their scale: W = bf16(code . scale), one rocBLAS product,
+        // then the activation's group scale on the way out
+        const AdValue& bs = call.fwd[(size_t)ibs];
+        std::vector<uint16_t> wb((size_t)(N * K));
+        for (int64_t n = 0; n < N; ++n)
+            for (int64_t k = 0; k < K; ++k)
+                wb[(size_t)(n * K + k)] = to_bf16((float)(b.value[(size_t)(n * K + k)] * scale_at(bs, n, k / 128, N, groups)));
+        const uint16_t* d_w = upload(c, "w", wb);
+        if (!c.blas) {
+            if (rocblas_create_handle(&c.blas) != rocblas_status_success) refuse(rec.op, "rocblas_create_handle failed");
+        }
+        rocblas_set_stream(c.blas, s);
+        const float one = 1.0f, zero = 0.0f;
+        for (int half = 0; half < 2; ++half) {
+            const rocblas_status st = rocblas_gemm_ex(
+                c.blas, rocblas_operation_none, rocblas_operation_none, (rocblas_int)K, (rocblas_int)M, (rocblas_int)N,
+                &one, d_w, rocblas_datatype_bf16_r, (rocblas_int)K, half ? d_lo : d_hi, rocblas_datatype_bf16_r,
+                (rocblas_int)N, half ? &one : &zero, d_da, rocblas_datatype_f32_r, (rocblas_int)K, d_da,
+                rocblas_datatype_f32_r, (rocblas_int)K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+            if (st != rocblas_status_success) refuse(rec.op, std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(st));
+        }
+        h = download(c, d_da, (size_t)(M * K));
+        for (int64_t m = 0; m < M; ++m)
+            for (int64_t k = 0; k < K; ++k) h[(size_t)(m * K + k)] *= sa[(size_t)(m * groups + k / 128)];
+    }
+    for (size_t i = 0; i < h.size(); ++i) da.value[i] += (double)h[i];
+}
+
+// ---------------------------------------------------------------- the coded lora_shrink
+// The coded shrink's adjoint (src/adjoint/host/lora.cpp:246-328, device row
+// src/adjoint/device/lora.hip:437-577): schema a [M, K] int8 codes, a_scale [M, groups] f32, slot,
+// lora_a [S, R, K], t. With x = a * a_scale[m, k / group_width(K, groups)] and, per slot s over its
+// rows, g = t_cot . A_s:
+//   dc[a] += g * a_scale;  dc[a_scale][m, q] += sum_{k in q} g[m, k] a[m, k];
+//   lora_A(s) += t_cot^T . x
+void lora_shrink_q_device(const AdjointCall& call) {
+    const std::vector<AdValue>& v = call.fwd;
+    if ((v.size() != 4 && v.size() != 5) || call.cot.empty() || !call.dc || call.dc->size() < 2) return;
+    const AdValue &a = v[0], &held = v[1], &slot = v[2], &la = v[3];
+    if (held.dtype == "invalid") return;  // a float activation: the float row's record
+    if (a.shape.size() != 2 || slot.shape.size() != 1 || la.shape.size() != 3 || held.shape.size() != 2) return;
+    const int64_t M = a.shape[0], K = a.shape[1], S = la.shape[0], R = la.shape[1];
+    if (M <= 0 || K <= 0 || R <= 0 || S <= 0 || la.shape[2] != K || slot.shape[0] != M) return;
+    const int64_t groups = held.shape[1];
+    if (held.shape[0] != M || groups <= 0 || (int64_t)held.value.size() != M * groups) return;
+    if ((int64_t)a.value.size() != M * K || (int64_t)slot.value.size() != M || (int64_t)la.value.size() != S * R * K)
+        return;
+    // the record's `group` states the same grid the scale's columns give (lora.cpp:183-191)
+    const int64_t gw = group_width(K, groups);
+    const int64_t stated = param_int(call.rec, "group", 0);
+    if (stated > 0 && (K + stated - 1) / stated != (K + gw - 1) / gw) return;
+    const AdValue& t_cot = call.cot[0];
+    AdValue& a_cot = call.dc->at(0);
+    AdValue& s_cot = call.dc->at(1);
+    if ((int64_t)t_cot.value.size() != M * R || (int64_t)a_cot.value.size() != M * K ||
+        (int64_t)s_cot.value.size() != M * groups)
+        return;
+    if (!rank_served(R) || K % 128)
+        refuse(call.rec.op, "rank " + std::to_string(R) + ", K " + std::to_string(K) +
+                                " not served (ranks 8, 16, 32, 64; K a multiple of 128)");
+    std::vector<char> used((size_t)S, 0);
+    for (int64_t m = 0; m < M; ++m) {
+        const int64_t sl = row_slot(slot, m, S);
+        if (sl >= 0) used[(size_t)sl] = 1;
+    }
+    bool any = false;
+    for (char u : used) any = any || u;
+    if (!any) return;  // every row a base row
+
+    Card& c = card();
+    std::lock_guard<std::mutex> lock(c.mu);
+    const hipStream_t s = stream_of(c);
+    std::vector<int8_t> codes((size_t)(M * K));
+    for (size_t i = 0; i < codes.size(); ++i) codes[i] = (int8_t)std::lrint(a.value[i]);
+    std::vector<float> sc(held.value.begin(), held.value.end());
+    const int8_t* d_a = upload(c, "codes", codes);
+    const float* d_s = upload(c, "a_scale", sc);
+    float* d_da = zeros(c, "dx", (size_t)(M * K));
+    float* d_ds = zeros(c, "ds", (size_t)(M * groups));
+    const int64_t wsb = r97q_lora_shrink_q_bwd_workspace_bytes(M, K, (int32_t)R);
+    void* d_ws = buffer(c, "ws", (size_t)wsb);
+    for (int64_t sl = 0; sl < S; ++sl) {
+        if (!used[(size_t)sl]) continue;
+        std::vector<uint16_t> ab;
+        to_bf16(la.value.data() + sl * R * K, (size_t)(R * K), ab);
+        const uint16_t* d_A = upload(c, "a_s", ab);
+        std::vector<float> tc((size_t)(M * R), 0.0f);
+        for (int64_t m = 0; m < M; ++m)
+            if (row_slot(slot, m, S) == sl)
+                for (int64_t j = 0; j < R; ++j) tc[(size_t)(m * R + j)] = (float)t_cot.value[(size_t)(m * R + j)];
+        const float* d_tc = upload(c, "t_cot", tc);
+        float* d_dA = call.grads ? zeros(c, "da", (size_t)(R * K)) : nullptr;
+        r97q_ok(r97q_lora_shrink_q_bwd(M, K, d_a, d_s, groups, d_A, (int32_t)R, d_tc, d_da, d_ds, d_dA, d_ws, wsb, s),
+                "lora_shrink (coded) adjoint");
+        if (call.grads) {
+            const std::vector<float> dA = download(c, d_dA, (size_t)(R * K));
+            const std::vector<int64_t> shape = call.fused_slots ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
+            Param& leaf = grad_entry(call.grads, factor_grad_name(call, "lora_A", sl), shape);
+            const int64_t row0 = call.fused_slots ? sl * R : 0;
+            for (int64_t j = 0; j < R; ++j)
+                for (int64_t k = 0; k < K; ++k) leaf.value[(size_t)((row0 + j) * K + k)] += dA[(size_t)(j * K + k)];
+        }
+    }
+    const std::vector<float> h = download(c, d_da, (size_t)(M * K));
+    for (size_t i = 0; i < h.size(); ++i) a_cot.value[i] += (double)h[i];
+    const std::vector<float> hs = download(c, d_ds, (size_t)(M * groups));
+    for (size_t i = 0; i < hs.size(); ++i) s_cot.value[i] += (double)hs[i];
+}
+
 }  // namespace
 
 // The frozen positions are the reference's (the weight for gemm_nt; slot, factor and scale for
@@ -423,8 +617,10 @@ void lora_expand_device(const AdjointCall& call) {
 R97_REGISTER_ADJOINT_IF_F("gemm_nt", device, gemm_nt_device, serves_bf16, 1)
 R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_device, float_act, 1, 2, 3)
 R97_REGISTER_ADJOINT_F("lora_expand", device, lora_expand_device, 1, 2, 3)
+R97_REGISTER_ADJOINT_IF_F("gemm_nt_q", device, gemm_nt_q_device, serves_i8a8h, 1, 2, 3)
+R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_q_device, coded_i8_act, 2, 3)
 
-R97_REGISTER_ADJOINT_FAMILY(Linear, "gemm_nt");
+R97_REGISTER_ADJOINT_FAMILY(Linear, "gemm_nt", "gemm_nt_q");
 R97_REGISTER_ADJOINT_FAMILY(Lora, "lora_shrink", "lora_expand");
 
 }  // namespace r97

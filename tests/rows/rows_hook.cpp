@@ -127,7 +127,19 @@ int rh_registry_selftest() {
     CHECK(adjoint_find("gemm_nt", Side::device, f32, nullptr) == nullptr);
     CHECK(adjoint_find("lora_shrink", Side::device, bf16, nullptr) != nullptr);
     CHECK(adjoint_frozen("lora_shrink", Side::device, bf16) == (std::vector<int>{1, 2, 3}));
-    CHECK(adjoint_find("lora_shrink", Side::device, i8, nullptr) == nullptr);
+    // the coded trunk: the i8 shrink and gemm_nt_q (i8a8h, group 128) have device rows; fp8 codes and
+    // another group width do not
+    CHECK(adjoint_find("lora_shrink", Side::device, i8, nullptr) != nullptr);
+    CHECK(adjoint_find("lora_shrink", Side::device, i8, nullptr) != adjoint_find("lora_shrink", Side::device, bf16, nullptr));
+    CHECK(adjoint_frozen("lora_shrink", Side::device, i8) == (std::vector<int>{2, 3}));
+    const std::vector<OpParam> fp8 = {{"dtype", std::string("fp8_e4m3")}};
+    CHECK(adjoint_find("lora_shrink", Side::device, fp8, nullptr) == nullptr);
+    const std::vector<OpParam> q128 = {{"dtype", std::string("i8a8h")}, {"group", int64_t(128)}},
+                               q64 = {{"dtype", std::string("i8a8h")}, {"group", int64_t(64)}};
+    CHECK(adjoint_find("gemm_nt_q", Side::device, q128, nullptr) != nullptr);
+    CHECK(adjoint_frozen("gemm_nt_q", Side::device, q128) == (std::vector<int>{1, 2, 3}));
+    CHECK(adjoint_find("gemm_nt_q", Side::device, q64, nullptr) == nullptr);
+    CHECK(family_find("gemm_nt_q") == AdjointFamily::Linear);
     CHECK(adjoint_find("lora_expand", Side::device, bf16, nullptr) != nullptr);
     CHECK(adjoint_frozen("lora_expand", Side::device, f32) == (std::vector<int>{1, 2, 3}));
     CHECK(family_find("gemm_nt") == AdjointFamily::Linear);
@@ -252,6 +264,85 @@ int rh_lora_expand(int64_t M, int64_t N, int64_t R, int64_t S, const double* t, 
                 } else {
                     const int64_t s = std::stoll(p.name.substr(7));
                     std::memcpy(dB + s * N * R, p.value.data(), sizeof(float) * (size_t)(N * R));
+                }
+            }
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// gemm_nt_q's row (the coded trunk): da[M, K] += ..., a codes (values unused by the adjoint),
+// a_scale [M, K/128], the weight stored (desc) or, when w_codes is given, carried as codes
+// [N, K] with b_scale [N, K/128]
+int rh_gemm_nt_q(int64_t M, int64_t N, int64_t K, const double* dy, const double* a_scale,
+                 const R97IqrDecodeDesc* desc, const float* scale_col, const double* w_codes, const double* b_scale,
+                 double* da) {
+    try {
+        const int64_t G = K / 128;
+        OpRecord rec;
+        rec.op = "gemm_nt_q";
+        rec.params = {{"M", M}, {"N", N}, {"K", K}, {"group", int64_t(128)}, {"dtype", std::string("i8a8h")}};
+        rec.operands = {opd("a", "i8", {M, K}), opd("a_scale", "f32", {M, G}), opd("b", w_codes ? "i8" : "iqr", {N, K}),
+                        opd("b_scale", "bf16", {N, G}), opd("y", "f32", {M, N}, true)};
+        std::vector<AdValue> fwd = {val("i8", {M, K}, nullptr), val("f32", {M, G}, a_scale), AdValue{},
+                                    val("bf16", {N, G}, b_scale), val("f32", {M, N}, nullptr)};
+        fwd[2].dtype = rec.operands[2].dtype;
+        fwd[2].shape = {N, K};
+        if (w_codes) {
+            fwd[2].value.assign(w_codes, w_codes + N * K);
+        } else {
+            IqrStoredEnc& e = encs()[desc->codes];
+            e.desc = *desc;
+            e.scale_col = scale_col;
+            fwd[2].raw = desc->codes;
+            fwd[2].enc = &e;
+            rec.operands[2].enc = &e;
+        }
+        const std::vector<AdValue> cot = {val("f32", {M, N}, dy)};
+        std::vector<AdValue> dc = {val("i8", {M, K}, da), AdValue{}, AdValue{}, AdValue{}, AdValue{}};
+        const AdjointCall call{rec, fwd, cot, &dc, nullptr, "", {}, false, nullptr, nullptr};
+        row("gemm_nt_q", rec.params)(call);
+        std::memcpy(da, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// the coded shrink's row: da[M, K] and ds[M, groups] += ..., dA: the lora_A leaves as [S, R, K]
+// (fused: the one [S*R, K] leaf)
+int rh_lora_shrink_q(int64_t M, int64_t K, int64_t R, int64_t S, int64_t groups, int64_t group, const double* a,
+                     const double* a_scale, const double* slot, const double* la, const double* t_cot, double* da,
+                     double* ds, float* dA, int fused) {
+    try {
+        OpRecord rec;
+        rec.op = "lora_shrink";
+        rec.params = {{"M", M}, {"K", K}, {"R", R}, {"S", S}, {"group", group}, {"dtype", std::string("i8")}};
+        rec.operands = {opd("a", "i8", {M, K}), opd("a_scale", "f32", {M, groups}), opd("slot", "i32", {M}),
+                        opd("lora_a", "bf16", {S, R, K}), opd("t", "f32", {M, R}, true)};
+        const std::vector<AdValue> fwd = {val("i8", {M, K}, a), val("f32", {M, groups}, a_scale), val("i32", {M}, slot),
+                                          val("bf16", {S, R, K}, la), val("f32", {M, R}, nullptr)};
+        const std::vector<AdValue> cot = {val("f32", {M, R}, t_cot)};
+        std::vector<AdValue> dc = {val("i8", {M, K}, da), val("f32", {M, groups}, ds), AdValue{}, AdValue{}, AdValue{}};
+        ParamSet grads;
+        AdjointCall call{rec, fwd, cot, &dc, dA ? &grads : nullptr, "layers.1.q", {}, fused != 0, nullptr, nullptr};
+        if (!fused) call.slot_prefix = [](int64_t s) { return "adapter" + std::to_string(s); };
+        row("lora_shrink", rec.params)(call);
+        std::memcpy(da, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
+        std::memcpy(ds, dc[1].value.data(), sizeof(double) * (size_t)(M * groups));
+        if (dA) {
+            std::memset(dA, 0, sizeof(float) * (size_t)(S * R * K));
+            for (const Param& p : grads) {
+                if (fused) {
+                    if (p.name != "layers.1.q.lora_A") throw std::runtime_error("unexpected leaf " + p.name);
+                    std::memcpy(dA, p.value.data(), sizeof(float) * (size_t)(S * R * K));
+                } else {
+                    const int64_t s = std::stoll(p.name.substr(7));
+                    std::memcpy(dA + s * R * K, p.value.data(), sizeof(float) * (size_t)(R * K));
                 }
             }
         }
