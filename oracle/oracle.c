@@ -27,6 +27,12 @@
  *                                  <dy, twin(a)> == <adj(dy), e> for code perturbations e, scale
  *                                  held), and the a_scale cotangent is the derivative of the twin in
  *                                  the scale.
+ *   orc_scheduled_lr, orc_clip_global_norm, orc_adamw_step
+ *                                  the reference's own Optimiser (oracle/_ref, src/optim.cpp) over
+ *                                  seeded multi-step runs, bit for bit (golden vectors); the
+ *                                  reference tests' known answers (tests/host/optim.cpp: the
+ *                                  schedule's values, the 3-4-5 clip); an f64 restatement of the
+ *                                  update to 1e-6.
  */
 #include "oracle.h"
 
@@ -694,4 +700,91 @@ void orc_lora_shrink_q_adjoint(int64_t M, int64_t K, int64_t R, int64_t S, int64
                      NULL, da, ds, dA, fused};
     parallel_for(M, 2, q_shrink_cot_row, &c);
     if (dA) parallel_for(R * K, 2, q_shrink_dA_pair, &c);
+}
+
+/* ------------------------------------------------------------------ AdamW */
+/* src/optim.cpp:113-126 */
+float orc_scheduled_lr(const OrcAdamWConfig* cfg, int32_t step) {
+    if (step <= 0) return 0.0f;
+    const double base = cfg->lr > 0.0f ? (double)cfg->lr : 0.0;
+    if (cfg->warmup_steps > 0 && step <= cfg->warmup_steps) {
+        const double r = (double)step / (double)cfg->warmup_steps;
+        return (float)(base * r);
+    }
+    if (cfg->total_steps <= 0 || cfg->total_steps <= cfg->warmup_steps) return cfg->lr;
+    const double floor_v = base * (cfg->lr_floor_frac >= 0.0f ? (double)cfg->lr_floor_frac : 0.0);
+    const double horizon = (double)(cfg->total_steps - cfg->warmup_steps);
+    const double tt = (double)(step - cfg->warmup_steps);
+    const double t = tt < horizon ? tt : horizon;
+    const double angle = 3.14159265358979323846 * t / horizon;
+    return (float)(floor_v + (base - floor_v) * 0.5 * (1.0 + cos(angle)));
+}
+
+/* element e of the concatenation: (array, offset) */
+static float* elem(float* const* x, const int64_t* n, int32_t count, int64_t e) {
+    for (int32_t i = 0; i < count; ++i) {
+        if (e < n[i]) return x[i] + e;
+        e -= n[i];
+    }
+    return NULL;
+}
+
+/* src/optim.cpp:131-184 (serially: the partials are per fixed chunk and summed in chunk order, so
+ * the thread count does not change the bits) */
+float orc_clip_global_norm(float* const* x, const int64_t* n, int32_t count, float max_norm) {
+    int64_t total = 0;
+    for (int32_t i = 0; i < count; ++i) total += n[i];
+    if (total == 0) return 0.0f;
+    const int64_t chunk = 4096, nchunks = (total + chunk - 1) / chunk;
+    double sq = 0.0;
+    for (int64_t c = 0; c < nchunks; ++c) {
+        const int64_t lo = c * chunk, hi = lo + chunk < total ? lo + chunk : total;
+        double part = 0.0;
+        for (int64_t e = lo; e < hi; ++e) {
+            const float v = *elem(x, n, count, e);
+            part += (double)v * (double)v;
+        }
+        sq += part;
+    }
+    const float norm = (float)sqrt(sq);
+    if (max_norm > 0.0f && norm > max_norm && norm > 0.0f) {
+        const float s = max_norm / norm;
+        for (int64_t e = 0; e < total; ++e) *elem(x, n, count, e) *= s;
+    }
+    return norm;
+}
+
+/* src/optim.cpp:213-296 */
+int32_t orc_adamw_step(const OrcAdamWConfig* cfg, float* const* w, float* const* m, float* const* v,
+                       float* const* acc, const int64_t* n, const int32_t* decay, int32_t count,
+                       const float* const* g, int32_t* step, int32_t* pending) {
+    for (int32_t i = 0; i < count; ++i)
+        for (int64_t k = 0; k < n[i]; ++k) acc[i][k] += g[i][k];
+    ++*pending;
+    if (*pending < cfg->accum_steps) return 0;
+    const float inv_k = 1.0f / (float)*pending;
+    for (int32_t i = 0; i < count; ++i)
+        for (int64_t k = 0; k < n[i]; ++k) acc[i][k] *= inv_k;
+    if (cfg->clip_norm > 0.0f) orc_clip_global_norm(acc, n, count, cfg->clip_norm);
+    const int32_t t = *step + 1;
+    const float lr = orc_scheduled_lr(cfg, t);
+    const float b1 = cfg->beta1, b2 = cfg->beta2, eps = cfg->eps;
+    const float bc1 = 1.0f - powf(b1, (float)t);
+    const float bc2 = 1.0f - powf(b2, (float)t);
+    for (int32_t i = 0; i < count; ++i) {
+        const float wd = decay[i] && cfg->weight_decay != 0.0f ? cfg->weight_decay : 0.0f;
+        for (int64_t k = 0; k < n[i]; ++k) {
+            const float gk = acc[i][k];
+            const float mk = m[i][k] = b1 * m[i][k] + (1.0f - b1) * gk;
+            const float vk = v[i][k] = b2 * v[i][k] + (1.0f - b2) * gk * gk;
+            const float mh = mk / bc1;
+            const float vh = vk / bc2;
+            w[i][k] -= lr * (mh / (sqrtf(vh) + eps) + wd * w[i][k]);
+        }
+    }
+    for (int32_t i = 0; i < count; ++i)
+        for (int64_t k = 0; k < n[i]; ++k) acc[i][k] = 0.0f;
+    ++*step;
+    *pending = 0;
+    return 1;
 }

@@ -105,6 +105,25 @@ void orc_lora_shrink_q_adjoint(int64_t M, int64_t K, int64_t R, int64_t S, int64
                                const double* lora_a, const double* ct, double* da, double* ds,
                                float* dA, int fused);
 
+/* ---- AdamW (include/r97/optim.h, src/optim.cpp) ---- */
+typedef struct {
+    float lr, beta1, beta2, eps, weight_decay, clip_norm, lr_floor_frac;
+    int32_t warmup_steps, total_steps, accum_steps;
+} OrcAdamWConfig;
+/* scheduled_lr (src/optim.cpp:113-126): linear warm-up, cosine to lr*floor_frac, flat beyond */
+float orc_scheduled_lr(const OrcAdamWConfig* cfg, int32_t step);
+/* clip_global_norm (src/optim.cpp:131-184): the norm over the concatenation of `count` arrays,
+ * one double partial per fixed 4096-element chunk summed in chunk order; rescaled in place when
+ * max_norm > 0 and the norm exceeds it. Returns the norm before clipping. */
+float orc_clip_global_norm(float* const* x, const int64_t* n, int32_t count, float max_norm);
+/* Optimiser::step (src/optim.cpp:213-296) over `count` parameters: acc += g; every accum_steps-th
+ * call the mean, the clip, the AdamW update (f32, in the reference's operation order), the buffer
+ * cleared. *step is the updates done so far, *pending the calls accumulated; both advance. Returns
+ * 1 when this call applied an update. decay[i] == 0 excludes parameter i from weight decay. */
+int32_t orc_adamw_step(const OrcAdamWConfig* cfg, float* const* w, float* const* m, float* const* v,
+                       float* const* acc, const int64_t* n, const int32_t* decay, int32_t count,
+                       const float* const* g, int32_t* step, int32_t* pending);
+
 #ifdef __cplusplus
 }
 #endif

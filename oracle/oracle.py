@@ -40,6 +40,20 @@ _P = C.c_void_p
 _I = C.c_int64
 
 
+class AdamWConfig(C.Structure):
+    """AdamWConfig (include/r97/optim.h:27-40) without no_decay (a per-parameter flag here) and threads."""
+
+    _fields_ = [("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
+                ("weight_decay", C.c_float), ("clip_norm", C.c_float), ("lr_floor_frac", C.c_float),
+                ("warmup_steps", C.c_int32), ("total_steps", C.c_int32), ("accum_steps", C.c_int32)]
+
+    @staticmethod
+    def make(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, clip_norm=0.0, lr_floor_frac=0.1,
+             warmup_steps=0, total_steps=0, accum_steps=1):
+        return AdamWConfig(lr, beta1, beta2, eps, weight_decay, clip_norm, lr_floor_frac, warmup_steps, total_steps,
+                           accum_steps)
+
+
 def _ptr(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
 
@@ -77,6 +91,12 @@ def lib():
         L.orc_gemm_nt_q_adjoint.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P]
         L.orc_lora_shrink_q_twin.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P]
         L.orc_lora_shrink_q_adjoint.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int]
+        L.orc_scheduled_lr.restype = C.c_float
+        L.orc_scheduled_lr.argtypes = [C.POINTER(AdamWConfig), C.c_int32]
+        L.orc_clip_global_norm.restype = C.c_float
+        L.orc_clip_global_norm.argtypes = [_P, _P, C.c_int32, C.c_float]
+        L.orc_adamw_step.restype = C.c_int32
+        L.orc_adamw_step.argtypes = [C.POINTER(AdamWConfig), _P, _P, _P, _P, _P, _P, C.c_int32, _P, _P, _P]
         L.orc_rounded_bf16.restype = C.c_double
         L.orc_rounded_bf16.argtypes = [C.c_double]
         L.orc_thread_count.restype = C.c_int
@@ -103,6 +123,11 @@ def ref():
         R.ref_gemm_nt_q_adjoint.argtypes = [_I, _I, _I, _P, _P, _P, _P, _P]
         R.ref_lora_shrink_q_twin.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P]
         R.ref_lora_shrink_q_adjoint.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, C.c_int]
+        R.ref_scheduled_lr.restype = C.c_float
+        R.ref_scheduled_lr.argtypes = [C.POINTER(AdamWConfig), C.c_int32]
+        R.ref_clip_global_norm.restype = C.c_float
+        R.ref_clip_global_norm.argtypes = [_P, _I, C.c_float]
+        R.ref_adamw_run.argtypes = [C.POINTER(AdamWConfig), _P, _P, C.c_int32, _P, _P, C.c_int32, _P, _P, _P, _P, _P]
         _ref = R
     return _ref
 
@@ -378,3 +403,62 @@ def lora_shrink_q_adjoint(a, a_scale, slot, lora_a, ct, da=None, ds=None, dA=Non
     lib().orc_lora_shrink_q_adjoint(M, K, R, S, groups, _ptr(a), _ptr(a_scale), _ptr(slot), _ptr(la), _ptr(ct),
                                     _ptr(da), _ptr(ds), _ptr(dA), int(fused))
     return da, ds, dA
+
+
+# ------------------------------------------------------------------ AdamW
+def _ptrs(arrays):
+    return (C.c_void_p * len(arrays))(*[a.ctypes.data for a in arrays])
+
+
+def scheduled_lr(cfg: AdamWConfig, step: int, use_ref=False) -> float:
+    if use_ref:
+        return float(ref().ref_scheduled_lr(C.byref(cfg), int(step)))
+    return float(lib().orc_scheduled_lr(C.byref(cfg), int(step)))
+
+
+def clip_global_norm(arrays, max_norm: float, use_ref=False):
+    """-> norm; the float32 arrays are rescaled in place (the reference takes one array here)."""
+    if use_ref:
+        assert len(arrays) == 1
+        return float(ref().ref_clip_global_norm(arrays[0].ctypes.data, arrays[0].size, float(max_norm)))
+    n = np.array([a.size for a in arrays], np.int64)
+    return float(lib().orc_clip_global_norm(_ptrs(arrays), _ptr(n), len(arrays), float(max_norm)))
+
+
+class AdamW:
+    """The oracle's Optimiser over host float32 arrays (parameters updated in place)."""
+
+    def __init__(self, cfg: AdamWConfig, params, decay=None):
+        self.cfg = cfg
+        self.w = params
+        self.m = [np.zeros_like(p) for p in params]
+        self.v = [np.zeros_like(p) for p in params]
+        self.acc = [np.zeros_like(p) for p in params]
+        self.n = np.array([p.size for p in params], np.int64)
+        self.decay = np.array([1] * len(params) if decay is None else decay, np.int32)
+        self.step_count = C.c_int32(0)
+        self.pending = C.c_int32(0)
+
+    def step(self, grads) -> bool:
+        grads = [np.ascontiguousarray(g, np.float32) for g in grads]
+        return bool(lib().orc_adamw_step(C.byref(self.cfg), _ptrs(self.w), _ptrs(self.m), _ptrs(self.v),
+                                         _ptrs(self.acc), _ptr(self.n), _ptr(self.decay), len(self.w), _ptrs(grads),
+                                         C.byref(self.step_count), C.byref(self.pending)))
+
+
+def adamw_run_ref(cfg: AdamWConfig, params, grads_per_step, decay=None):
+    """The reference's Optimiser over `params` (float32 arrays, not modified) for each gradient set;
+    -> (w, m, v, acc) lists and (updates, pending)."""
+    n = np.array([p.size for p in params], np.int64)
+    decay = np.array([1] * len(params) if decay is None else decay, np.int32)
+    w = np.concatenate([p.ravel() for p in params]).astype(np.float32)
+    g = np.concatenate([np.concatenate([x.ravel() for x in gs]) for gs in grads_per_step]).astype(np.float32)
+    m, v, acc = np.zeros_like(w), np.zeros_like(w), np.zeros_like(w)
+    upd, pend = C.c_int32(0), C.c_int32(0)
+    _check_ref(ref().ref_adamw_run(C.byref(cfg), _ptr(n), _ptr(decay), len(params), _ptr(w), _ptr(g),
+                                   len(grads_per_step), _ptr(m), _ptr(v), _ptr(acc), C.byref(upd), C.byref(pend)))
+    split = np.cumsum(n)[:-1]
+    return ([a.reshape(p.shape) for a, p in zip(np.split(w, split), params)],
+            [a.reshape(p.shape) for a, p in zip(np.split(m, split), params)],
+            [a.reshape(p.shape) for a, p in zip(np.split(v, split), params)],
+            [a.reshape(p.shape) for a, p in zip(np.split(acc, split), params)], (upd.value, pend.value))

@@ -12,6 +12,7 @@
 #include "r97/adjoint.h"
 
 #include "iqr_decode.h"
+#include "r97/optim.h"
 #include "stored_weight.h"
 
 #include <cstring>
@@ -372,6 +373,95 @@ int ref_lora_shrink_q_adjoint(int64_t M, int64_t K, int64_t R, int64_t S, int64_
         std::memcpy(da, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
         std::memcpy(ds, dc[1].value.data(), sizeof(double) * (size_t)(M * groups));
         std::memcpy(dA, grads[0].value.data(), sizeof(float) * (size_t)na);
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 3;
+    }
+}
+
+// ---- AdamW: the reference's Optimiser (src/optim.cpp) ----
+struct RefAdamWConfig {
+    float lr, beta1, beta2, eps, weight_decay, clip_norm, lr_floor_frac;
+    int32_t warmup_steps, total_steps, accum_steps;
+};
+
+static AdamWConfig adamw_cfg(const RefAdamWConfig* c) {
+    AdamWConfig a;
+    a.lr = c->lr;
+    a.beta1 = c->beta1;
+    a.beta2 = c->beta2;
+    a.eps = c->eps;
+    a.weight_decay = c->weight_decay;
+    a.clip_norm = c->clip_norm;
+    a.lr_floor_frac = c->lr_floor_frac;
+    a.warmup_steps = c->warmup_steps;
+    a.total_steps = c->total_steps;
+    a.accum_steps = c->accum_steps;
+    a.threads = 1;
+    return a;
+}
+
+float ref_scheduled_lr(const RefAdamWConfig* c, int32_t step) { return scheduled_lr(adamw_cfg(c), step); }
+
+float ref_clip_global_norm(float* x, int64_t n, float max_norm) {
+    ParamSet g(1);
+    g[0].name = "g";
+    g[0].shape = {n};
+    g[0].value.assign(x, x + n);
+    const float norm = clip_global_norm(g, max_norm, 1);
+    std::memcpy(x, g[0].value.data(), sizeof(float) * (size_t)n);
+    return norm;
+}
+
+// `count` parameters named p0, p1, ... (decay[i] == 0: the name carries the no_decay marker), initial
+// values w (concatenated), `nsteps` gradient sets g (nsteps x the concatenation); returns the final
+// w, m, v and accumulation buffer (each the concatenation), the updates done and the pending count,
+// read back through the optimiser's own serialise().
+int ref_adamw_run(const RefAdamWConfig* c, const int64_t* n, const int32_t* decay, int32_t count, float* w,
+                  const float* g, int32_t nsteps, float* m_out, float* v_out, float* acc_out, int32_t* updates,
+                  int32_t* pending) {
+    try {
+        ParamSet params((size_t)count);
+        int64_t total = 0;
+        for (int32_t i = 0; i < count; ++i) {
+            params[i].name = std::string("p") + std::to_string(i) + (decay[i] ? "" : ".nodecay");
+            params[i].shape = {n[i]};
+            params[i].value.assign(w + total, w + total + n[i]);
+            total += n[i];
+        }
+        AdamWConfig cfg = adamw_cfg(c);
+        cfg.no_decay = {".nodecay"};
+        Optimiser opt(params, cfg);
+        for (int32_t s = 0; s < nsteps; ++s) {
+            ParamSet grads = params;
+            int64_t off = 0;
+            for (int32_t i = 0; i < count; ++i) {
+                grads[i].value.assign(g + s * total + off, g + s * total + off + n[i]);
+                off += n[i];
+            }
+            opt.step(grads);
+        }
+        const std::vector<uint8_t> b = opt.serialise();
+        // "R97OPT" u16 version, u16 0, i64 step, i32 pending, i32 count, then per parameter u64 n and
+        // n floats each of w, m, v, acc
+        size_t at = 6 + 2 + 2;
+        int64_t step = 0;
+        std::memcpy(&step, b.data() + at, 8);
+        at += 8;
+        std::memcpy(pending, b.data() + at, 4);
+        at += 4 + 4;
+        int64_t off = 0;
+        for (int32_t i = 0; i < count; ++i) {
+            at += 8;
+            float* dst[4] = {w + off, m_out + off, v_out + off, acc_out + off};
+            for (int a = 0; a < 4; ++a) {
+                std::memcpy(dst[a], b.data() + at, sizeof(float) * (size_t)n[i]);
+                at += sizeof(float) * (size_t)n[i];
+            }
+            off += n[i];
+        }
+        *updates = (int32_t)step;
         return 0;
     } catch (const std::exception& e) {
         g_err = e.what();

@@ -3,8 +3,8 @@
 Run in the build container, where oracle/_ref/libr97ref.so was compiled from the reference's host
 sources (oracle/Makefile): every expected output below is what the reference's r97_iqr_decode_host
 (src/iqr_decode.h:353-376), gemm_nt / gemm_nt_q twins and adjoints (src/adjoint/host/linear.cpp:
-193-317) and float / coded lora_shrink and lora_expand twins and adjoints
-(src/adjoint/host/lora.cpp:204-521) return for the
+193-317), float / coded lora_shrink and lora_expand twins and adjoints
+(src/adjoint/host/lora.cpp:204-521) and the AdamW Optimiser (src/optim.cpp) return for the
 seeded inputs stored beside them. The fixtures are data only (inputs and expected outputs); the
 reference's source never enters the repository.
 
@@ -197,6 +197,40 @@ def lora_q_fixtures():
         print("lora", name)
 
 
+# AdamW (src/optim.cpp): the reference's Optimiser over LoRA-shaped parameters (an A [16, 256], a
+# B [384, 16] and a short vector excluded from weight decay; 10501 elements, so the clip's 4096-element
+# chunks span parameters), six gradient sets, under three configurations: the defaults; warm-up +
+# cosine with weight decay and a clip that bites; and accumulation over two calls with a clip that
+# does not.
+ADAMW_CONFIGS = {
+    "plain": dict(),
+    "schedule_clip_decay": dict(lr=1e-2, warmup_steps=2, total_steps=5, lr_floor_frac=0.1, weight_decay=0.05,
+                                clip_norm=1.0),
+    "accumulate": dict(lr=3e-3, accum_steps=2, clip_norm=1e3),
+}
+
+
+def adamw_fixture():
+    rng = np.random.default_rng(23)
+    params = [(0.05 * rng.standard_normal((16, 256))).astype(np.float32),
+              (0.05 * rng.standard_normal((384, 16))).astype(np.float32),
+              rng.standard_normal(5).astype(np.float32)]
+    decay = [1, 1, 0]
+    grads = [[(0.1 * rng.standard_normal(p.shape)).astype(np.float32) for p in params] for _ in range(6)]
+    out = {f"w{i}": p for i, p in enumerate(params)}
+    for s_ in range(6):
+        for i in range(3):
+            out[f"g{s_}_{i}"] = grads[s_][i]
+    for name, kw in ADAMW_CONFIGS.items():
+        cfg = O.AdamWConfig.make(**kw)
+        w, m, v, acc, (upd, pend) = O.adamw_run_ref(cfg, params, grads, decay=decay)
+        for i in range(3):
+            out[f"{name}_w{i}"], out[f"{name}_m{i}"], out[f"{name}_v{i}"], out[f"{name}_acc{i}"] = w[i], m[i], v[i], acc[i]
+        out[f"{name}_updates"], out[f"{name}_pending"] = upd, pend
+    np.savez_compressed(os.path.join(OUT, "adamw_runs.npz"), decay=np.array(decay), **out)
+    print("adamw")
+
+
 def c1_fixture():
     """Config 1 composed from the reference rows: W 1024x1024 from
     N(0, 0.02) through this repo's quantizer is not available to the reference, so the stored
@@ -235,4 +269,5 @@ if __name__ == "__main__":
     lora_fixtures()
     linear_q_fixtures()
     lora_q_fixtures()
+    adamw_fixture()
     c1_fixture()

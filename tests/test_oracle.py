@@ -490,3 +490,53 @@ def test_coded_rows_match_reference_fresh():
     want = O.lora_shrink_q_adjoint(a, a_scale, slot, la, ct, use_ref=True)
     for g_, w_ in zip(got, want):
         assert np.array_equal(g_, w_)
+
+
+# ------------------------------------------------------------------ AdamW
+def test_adamw_schedule_and_clip_known_answers():
+    """tests/host/optim.cpp:134-164: the schedule's values and the 3-4-5 clip."""
+    cfg = O.AdamWConfig.make(lr=2e-3, warmup_steps=10, total_steps=100, lr_floor_frac=0.1)
+    floor = 2e-3 * 0.1
+    assert O.scheduled_lr(cfg, 0) == 0.0
+    assert abs(O.scheduled_lr(cfg, 1) - 2e-3 * 0.1) < 1e-6 and abs(O.scheduled_lr(cfg, 5) - 2e-3 * 0.5) < 1e-6
+    assert abs(O.scheduled_lr(cfg, 10) - 2e-3) < 1e-6
+    assert abs(O.scheduled_lr(cfg, 55) - 0.5 * (floor + 2e-3)) < 1e-6
+    assert abs(O.scheduled_lr(cfg, 100) - floor) < 1e-6 and abs(O.scheduled_lr(cfg, 500) - floor) < 1e-6
+    nocos = O.AdamWConfig.make(lr=3e-3)
+    assert O.scheduled_lr(nocos, 1) == np.float32(3e-3) and O.scheduled_lr(nocos, 77) == np.float32(3e-3)
+    g = [np.array([3.0, 4.0], np.float32)]
+    assert abs(O.clip_global_norm(g, 2.5) - 5.0) < 1e-5
+    assert abs(g[0][0] - 1.5) < 1e-5 and abs(g[0][1] - 2.0) < 1e-5
+    O.clip_global_norm(g, 100.0)
+    assert abs(g[0][0] - 1.5) < 1e-5
+
+
+def test_adamw_golden_and_f64_restatement():
+    z = np.load(os.path.join(G, "adamw_runs.npz"))
+    params0 = [z[f"w{i}"] for i in range(3)]
+    grads = [[z[f"g{s}_{i}"] for i in range(3)] for s in range(6)]
+    for name in ("plain", "schedule_clip_decay", "accumulate"):
+        kw = {"plain": {}, "schedule_clip_decay": dict(lr=1e-2, warmup_steps=2, total_steps=5, lr_floor_frac=0.1,
+                                                       weight_decay=0.05, clip_norm=1.0),
+              "accumulate": dict(lr=3e-3, accum_steps=2, clip_norm=1e3)}[name]
+        cfg = O.AdamWConfig.make(**kw)
+        opt = O.AdamW(cfg, [p.copy() for p in params0], decay=list(z["decay"]))
+        for g in grads:
+            opt.step(g)
+        for i in range(3):
+            for k, arr in (("w", opt.w), ("m", opt.m), ("v", opt.v), ("acc", opt.acc)):
+                assert np.array_equal(arr[i], z[f"{name}_{k}{i}"]), (name, k, i)
+        assert opt.step_count.value == z[f"{name}_updates"] and opt.pending.value == z[f"{name}_pending"]
+    # an f64 restatement of the plain run (tests/host/optim.cpp:35-46), to 1e-6
+    cfg = O.AdamWConfig.make()
+    w = [p.astype(np.float64) for p in params0]
+    m = [np.zeros_like(x) for x in w]
+    v = [np.zeros_like(x) for x in w]
+    for t, g in enumerate(grads, start=1):
+        for i in range(3):
+            m[i] = 0.9 * m[i] + 0.1 * g[i]
+            v[i] = 0.999 * v[i] + 0.001 * g[i].astype(np.float64) ** 2
+            mh, vh = m[i] / (1 - 0.9 ** t), v[i] / (1 - 0.999 ** t)
+            w[i] = w[i] - 1e-3 * (mh / (np.sqrt(vh) + 1e-8))
+    for i in range(3):
+        assert np.max(np.abs(w[i] - z[f"plain_w{i}"])) < 1e-6
