@@ -274,6 +274,41 @@ int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const int8_t* a, const float* a
                            const uint16_t* A, int32_t rank, const float* t_cot, float* da, float* ds, float* dA,
                            void* workspace, int64_t workspace_bytes, R97IqrStream stream);
 
+/* ------------------------------------------------------------------ the step's far side: AdamW
+ *
+ * The reference's Optimiser::step (src/optim.cpp:213-296; its config include/r97/optim.h:27-40) on
+ * the card, over device f32 master weights, moments and accumulation buffers: each call adds the
+ * gradients into the buffers; every accum_steps-th call takes the mean, clips it to clip_norm by
+ * the global norm (when clip_norm > 0), applies the AdamW update at scheduled_lr(t), and clears the
+ * buffers. The results are the reference host optimiser's bits: the same f32 operations in the
+ * same order, the norm's double partials over the same 4096-element chunks added in chunk order.
+ * No_decay names become decay = 0 on their parameters; the thread count has no counterpart. */
+typedef struct {
+    float lr, beta1, beta2, eps, weight_decay, clip_norm, lr_floor_frac;
+    int32_t warmup_steps, total_steps, accum_steps;
+} R97qAdamWConfig;
+typedef struct {
+    float* w;    /* master weights, f32 [n] */
+    float* m;    /* first moment */
+    float* v;    /* second moment */
+    float* acc;  /* the accumulation buffer (zero between updates) */
+    int64_t n;
+    int32_t decay; /* 0: excluded from weight decay */
+} R97qAdamWParam;
+/* scheduled_lr (src/optim.cpp:113-126): the learning rate of the step-th update (1-based) */
+float r97q_scheduled_lr(const R97qAdamWConfig* cfg, int32_t step);
+/* the clip's partials: one double a 4096 elements of the parameters (-1: no parameters) */
+int64_t r97q_adamw_workspace_bytes(const R97qAdamWParam* params, int32_t count);
+/* One optimiser call. grads[i]: f32 [params[i].n] on the card. *updates (updates applied so far)
+ * and *pending (calls accumulated) are the optimiser's counters, kept by the caller; *applied
+ * (may be NULL) is set to 1 when this call updated. With clipping, the call reads the norm's
+ * partials back and so synchronises the stream. */
+int r97q_adamw_step(const R97qAdamWConfig* cfg, const R97qAdamWParam* params, const float* const* grads,
+                    int32_t count, int32_t* updates, int32_t* pending, int32_t* applied, void* workspace,
+                    int64_t workspace_bytes, R97IqrStream stream);
+/* y = bf16(x) (RNE, NaN quieted), n elements: the kernels' bf16 operands from the f32 master weights */
+int r97q_f32_to_bf16(const float* x, uint16_t* y, int64_t n, R97IqrStream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,21 @@ class Weight(C.Structure):
     ]
 
 
+class AdamWConfig(C.Structure):
+    """R97qAdamWConfig (include/r97q.h): the reference's AdamWConfig (include/r97/optim.h:27-40)."""
+
+    _fields_ = [("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
+                ("weight_decay", C.c_float), ("clip_norm", C.c_float), ("lr_floor_frac", C.c_float),
+                ("warmup_steps", C.c_int32), ("total_steps", C.c_int32), ("accum_steps", C.c_int32)]
+
+
+class AdamWParam(C.Structure):
+    """R97qAdamWParam (include/r97q.h): one parameter's device buffers."""
+
+    _fields_ = [("w", C.c_void_p), ("m", C.c_void_p), ("v", C.c_void_p), ("acc", C.c_void_p), ("n", C.c_int64),
+                ("decay", C.c_int32)]
+
+
 # every symbol include/r97q.h declares, with its ctypes signature
 _P, _I, _i = C.c_void_p, C.c_int64, C.c_int32
 SIGNATURES = {
@@ -75,6 +90,11 @@ SIGNATURES = {
     "r97q_gemm_nt_q_dx": (C.c_int, [C.POINTER(Weight), _P, _I, _P, _P, _i, _i, _P]),
     "r97q_lora_shrink_q_bwd_workspace_bytes": (_I, [_I, _I, _i]),
     "r97q_lora_shrink_q_bwd": (C.c_int, [_I, _I, _P, _P, _I, _P, _i, _P, _P, _P, _P, _P, _I, _P]),
+    "r97q_scheduled_lr": (C.c_float, [C.POINTER(AdamWConfig), _i]),
+    "r97q_adamw_workspace_bytes": (_I, [C.POINTER(AdamWParam), _i]),
+    "r97q_adamw_step": (C.c_int, [C.POINTER(AdamWConfig), C.POINTER(AdamWParam), C.POINTER(C.c_void_p), _i,
+                                  C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.POINTER(C.c_int32), _P, _I, _P]),
+    "r97q_f32_to_bf16": (C.c_int, [_P, _P, _I, _P]),
 }
 
 _lib = None
