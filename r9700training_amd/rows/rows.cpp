@@ -18,7 +18,9 @@
 //
 // Every row follows the contract's ownership rules: it adds into `dc` and the leaves, never
 // overwrites, never writes a frozen slot, and returns with its results host-visible (one
-// process-wide stream, synchronised before return). A record whose layout is malformed is left
+// process-wide stream, synchronised before return). The factor gradients (lora_A, lora_B) are
+// added into the step's f32 accumulators on the card (r97/grad_stage.h), named and shaped as the
+// leaves, as the reference's device rows do; the walk's grad_stage_flush puts them in `grads`. A record whose layout is malformed is left
 // untouched, as the reference's rows do; a well-formed record this build's kernels cannot serve
 // (a rank outside 8/16/32/64, a K or N not a multiple of 128, a stored form the fused kernels do not
 // decode) throws std::runtime_error naming the op and the shape, instead of dropping a gradient.
@@ -41,6 +43,7 @@
 
 #include "r97/adjoint.h"
 #include "r97/adjoint_family.h"
+#include "r97/grad_stage.h"
 #include "r97/stored_weight.h"
 #include "r97q.h"
 
@@ -128,19 +131,6 @@ std::string dims(std::initializer_list<int64_t> d) {
 }
 
 // ---------------------------------------------------------------- leaves
-Param& grad_entry(ParamSet* grads, const std::string& name, const std::vector<int64_t>& shape) {
-    for (Param& p : *grads)
-        if (p.name == name) return p;
-    Param p;
-    p.name = name;
-    p.shape = shape;
-    int64_t n = 1;
-    for (int64_t d : shape) n *= d;
-    p.value.assign((size_t)n, 0.0f);
-    grads->push_back(std::move(p));
-    return grads->back();
-}
-
 std::string grad_name(const char* prefix, const char* leaf) {
     if (!prefix || !*prefix) return leaf;
     return std::string(prefix) + "." + leaf;
@@ -151,6 +141,47 @@ std::string factor_grad_name(const AdjointCall& call, const char* leaf, int64_t 
     if (call.fused_slots) return grad_name(call.prefix, leaf);
     if (call.slot_prefix) return grad_name(call.slot_prefix(slot).c_str(), leaf);
     return grad_name(call.prefix, leaf);
+}
+
+// The step's accumulator each pool row's factor gradient lands in (the reference's grad_dest,
+// src/adjoint/device/lora.hip:125-152): the row's block of the fused factor (`stride` elements
+// apart), the row's own leaf (slot_prefix), or the one leaf every row sums into. Pool rows the
+// record never names get none; a leaf the stage refuses comes out nullptr.
+std::vector<float*> stage_dest(const AdjointCall& call, const char* leaf, int64_t S, const std::vector<char>& used,
+                               const std::vector<int64_t>& shape, int64_t stride) {
+    std::vector<float*> dest((size_t)S, nullptr);
+    if (!call.grads) return dest;
+    if (call.fused_slots) {
+        float* base = device::grad_stage_slot(factor_grad_name(call, leaf, 0), shape);
+        for (int64_t s = 0; base && s < S; ++s)
+            if (used[(size_t)s]) dest[(size_t)s] = base + s * stride;
+        return dest;
+    }
+    if (call.slot_prefix) {
+        for (int64_t s = 0; s < S; ++s)
+            if (used[(size_t)s]) dest[(size_t)s] = device::grad_stage_slot(factor_grad_name(call, leaf, s), shape);
+        return dest;
+    }
+    float* base = device::grad_stage_slot(factor_grad_name(call, leaf, 0), shape);
+    for (int64_t s = 0; base && s < S; ++s)
+        if (used[(size_t)s]) dest[(size_t)s] = base;
+    return dest;
+}
+
+bool stage_refused(const std::vector<float*>& dest, const std::vector<char>& used, bool want) {
+    if (!want) return false;
+    for (size_t s = 0; s < used.size(); ++s)
+        if (used[s] && !dest[s]) return true;
+    return false;
+}
+
+// dst[r * ld + c] += src[r * cols + c]: a slot's [N, R] factor gradient into its columns of a fused
+// [N, S*R] accumulator
+__global__ void add_columns_kernel(float* dst, int64_t ld, const float* src, int64_t rows, int64_t cols) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * cols) return;
+    const int64_t r = i / cols, c = i % cols;
+    dst[r * ld + c] += src[i];
 }
 
 // row m's adapter slot, or -1 for a base row (negative, NaN or past the pool)
@@ -333,6 +364,10 @@ void lora_shrink_device(const AdjointCall& call) {
         const int64_t sl = row_slot(slot, m, S);
         if (sl >= 0) used[(size_t)sl] = 1;
     }
+    // dA waits in the step's staging on the card (r97/grad_stage.h)
+    const std::vector<int64_t> a_shape = call.fused_slots ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
+    const std::vector<float*> d_dA = stage_dest(call, "lora_A", S, used, a_shape, R * K);
+    if (stage_refused(d_dA, used, call.grads != nullptr)) return;
 
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
@@ -354,18 +389,10 @@ void lora_shrink_device(const AdjointCall& call) {
             if (row_slot(slot, m, S) == sl)
                 for (int64_t j = 0; j < R; ++j) tc[(size_t)(m * R + j)] = (float)t_cot.value[(size_t)(m * R + j)];
         const float* d_tc = upload(c, "t_cot", tc);
-        float* d_da = call.grads ? zeros(c, "da", (size_t)(R * K)) : nullptr;
-        r97q_ok(r97q_lora_shrink_bwd(M, K, d_x, d_a, (int32_t)R, d_tc, d_dx, first ? 0 : 1, d_da, d_ws, wsb, s),
+        r97q_ok(r97q_lora_shrink_bwd(M, K, d_x, d_a, (int32_t)R, d_tc, d_dx, first ? 0 : 1,
+                                     call.grads ? d_dA[(size_t)sl] : nullptr, d_ws, wsb, s),
                 "lora_shrink adjoint");
         first = false;
-        if (call.grads) {
-            const std::vector<float> da = download(c, d_da, (size_t)(R * K));
-            const std::vector<int64_t> shape = call.fused_slots ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
-            Param& leaf = grad_entry(call.grads, factor_grad_name(call, "lora_A", sl), shape);
-            const int64_t row0 = call.fused_slots ? sl * R : 0;
-            for (int64_t j = 0; j < R; ++j)
-                for (int64_t k = 0; k < K; ++k) leaf.value[(size_t)((row0 + j) * K + k)] += da[(size_t)(j * K + k)];
-        }
     }
     if (first) return;  // every row a base row
     const std::vector<float> h = download(c, d_dx, (size_t)(M * K));
@@ -411,6 +438,11 @@ void lora_expand_device(const AdjointCall& call) {
         const int64_t sl = row_slot(slot, m, S);
         if (sl >= 0) used[(size_t)sl] = 1;
     }
+    // dB waits in the step's staging on the card: a slot's [N, R] leaf, or its R columns of the
+    // fused [N, S*R] one
+    const std::vector<int64_t> b_shape = call.fused_slots ? std::vector<int64_t>{N, S * R} : std::vector<int64_t>{N, R};
+    const std::vector<float*> d_dB = stage_dest(call, "lora_B", S, used, b_shape, R);
+    if (stage_refused(d_dB, used, call.grads != nullptr)) return;
 
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
@@ -436,17 +468,14 @@ void lora_expand_device(const AdjointCall& call) {
         const uint16_t* d_hi = upload(c, "dy_hi", hi);
         const uint16_t* d_lo = upload(c, "dy_lo", lo);
         const uint16_t* d_b = upload(c, "b_s", bb);
-        float* d_db = call.grads ? zeros(c, "db", (size_t)(N * R)) : nullptr;
+        // a fused leaf's columns are strided: the slot's [N, R] sum goes through a buffer
+        float* d_db = !call.grads ? nullptr : call.fused_slots ? zeros(c, "db", (size_t)(N * R)) : d_dB[(size_t)sl];
         r97q_ok(r97q_lora_expand_bwd(M, N, d_hi, d_b, (int32_t)R, 1.0f, d_t, d_tc, d_db, d_ws, wsb, s), "lora_expand adjoint");
         r97q_ok(r97q_lora_expand_bwd(M, N, d_lo, d_b, (int32_t)R, 1.0f, d_t, d_tc, d_db, d_ws, wsb, s), "lora_expand adjoint");
-        if (call.grads) {
-            const std::vector<float> db = download(c, d_db, (size_t)(N * R));
-            const int64_t cols = call.fused_slots ? S * R : R;
-            const std::vector<int64_t> shape = {N, cols};
-            Param& leaf = grad_entry(call.grads, factor_grad_name(call, "lora_B", sl), shape);
-            const int64_t col0 = call.fused_slots ? sl * R : 0;
-            for (int64_t k = 0; k < N; ++k)
-                for (int64_t j = 0; j < R; ++j) leaf.value[(size_t)(k * cols + col0 + j)] += db[(size_t)(k * R + j)];
+        if (call.grads && call.fused_slots) {
+            hipLaunchKernelGGL(add_columns_kernel, dim3((unsigned)((N * R + 255) / 256)), dim3(256), 0, s, d_dB[(size_t)sl],
+                               S * R, d_db, N, R);
+            hip_ok(hipGetLastError(), "add_columns_kernel");
         }
     }
     if (!any) return;
@@ -568,6 +597,9 @@ void lora_shrink_q_device(const AdjointCall& call) {
     bool any = false;
     for (char u : used) any = any || u;
     if (!any) return;  // every row a base row
+    const std::vector<int64_t> a_shape = call.fused_slots ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
+    const std::vector<float*> d_dA = stage_dest(call, "lora_A", S, used, a_shape, R * K);
+    if (stage_refused(d_dA, used, call.grads != nullptr)) return;
 
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
@@ -591,17 +623,9 @@ void lora_shrink_q_device(const AdjointCall& call) {
             if (row_slot(slot, m, S) == sl)
                 for (int64_t j = 0; j < R; ++j) tc[(size_t)(m * R + j)] = (float)t_cot.value[(size_t)(m * R + j)];
         const float* d_tc = upload(c, "t_cot", tc);
-        float* d_dA = call.grads ? zeros(c, "da", (size_t)(R * K)) : nullptr;
-        r97q_ok(r97q_lora_shrink_q_bwd(M, K, d_a, d_s, groups, d_A, (int32_t)R, d_tc, d_da, d_ds, d_dA, d_ws, wsb, s),
+        r97q_ok(r97q_lora_shrink_q_bwd(M, K, d_a, d_s, groups, d_A, (int32_t)R, d_tc, d_da, d_ds,
+                                       call.grads ? d_dA[(size_t)sl] : nullptr, d_ws, wsb, s),
                 "lora_shrink (coded) adjoint");
-        if (call.grads) {
-            const std::vector<float> dA = download(c, d_dA, (size_t)(R * K));
-            const std::vector<int64_t> shape = call.fused_slots ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
-            Param& leaf = grad_entry(call.grads, factor_grad_name(call, "lora_A", sl), shape);
-            const int64_t row0 = call.fused_slots ? sl * R : 0;
-            for (int64_t j = 0; j < R; ++j)
-                for (int64_t k = 0; k < K; ++k) leaf.value[(size_t)((row0 + j) * K + k)] += dA[(size_t)(j * K + k)];
-        }
     }
     const std::vector<float> h = download(c, d_da, (size_t)(M * K));
     for (size_t i = 0; i < h.size(); ++i) a_cot.value[i] += (double)h[i];

@@ -10,8 +10,11 @@
 #include <string>
 #include <vector>
 
+#include <hip/hip_runtime_api.h>
+
 #include "r97/adjoint.h"
 #include "r97/adjoint_family.h"
+#include "r97/grad_stage.h"
 #include "r97/stored_weight.h"
 
 using namespace r97;
@@ -53,6 +56,14 @@ AdjointFn row(const char* op, const std::vector<OpParam>& params) {
     AdjointFn fn = adjoint_find(op, Side::device, params, &err);
     if (!fn) throw std::runtime_error(err);
     return fn;
+}
+
+// a staged leaf's f32 accumulator copied out (the step's staging on the card), n floats
+void staged(const std::string& name, const std::vector<int64_t>& shape, float* out, size_t n) {
+    float* d = device::grad_stage_slot(name, shape);
+    if (!d) throw std::runtime_error("no staged leaf " + name);
+    if (hipMemcpy(out, d, n * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess)
+        throw std::runtime_error("staged leaf copy failed");
 }
 
 // registry self-test rows
@@ -207,18 +218,19 @@ int rh_lora_shrink(int64_t M, int64_t K, int64_t R, int64_t S, const double* x, 
         row("lora_shrink", rec.params)(call);
         std::memcpy(dx, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
         if (dA) {
+            // the leaves wait in the step's staging; nothing reached `grads`
+            if (!grads.empty()) throw std::runtime_error("a leaf reached grads before the flush");
             std::memset(dA, 0, sizeof(float) * (size_t)(S * R * K));
-            for (const Param& p : grads) {
-                if (fused) {
-                    if (p.name != "layers.0.q.lora_A") throw std::runtime_error("unexpected leaf " + p.name);
-                    std::memcpy(dA, p.value.data(), sizeof(float) * (size_t)(S * R * K));
-                } else {
-                    const std::string pre = "adapter";
-                    if (p.name.rfind(pre, 0) != 0) throw std::runtime_error("unexpected leaf " + p.name);
-                    const int64_t s = std::stoll(p.name.substr(pre.size()));
-                    std::memcpy(dA + s * R * K, p.value.data(), sizeof(float) * (size_t)(R * K));
+            if (fused) {
+                staged("layers.0.q.lora_A", {S * R, K}, dA, (size_t)(S * R * K));
+            } else {
+                for (int64_t s = 0; s < S; ++s) {
+                    bool used = false;
+                    for (int64_t m = 0; m < M; ++m) used = used || (slot[m] >= 0 && (int64_t)slot[m] == s);
+                    if (used) staged("adapter" + std::to_string(s) + ".lora_A", {R, K}, dA + s * R * K, (size_t)(R * K));
                 }
             }
+            device::grad_stage_discard();
         }
         return 0;
     } catch (const std::exception& e) {
@@ -256,16 +268,18 @@ int rh_lora_expand(int64_t M, int64_t N, int64_t R, int64_t S, const double* t, 
         std::memcpy(t_cot, dc[0].value.data(), sizeof(double) * (size_t)(M * R));
         if (in_place && d_base) std::memcpy(d_base, dc.back().value.data(), sizeof(double) * (size_t)(M * N));
         if (dB) {
+            if (!grads.empty()) throw std::runtime_error("a leaf reached grads before the flush");
             std::memset(dB, 0, sizeof(float) * (size_t)(S * N * R));
-            for (const Param& p : grads) {
-                if (fused) {
-                    if (p.name != "layers.0.q.lora_B") throw std::runtime_error("unexpected leaf " + p.name);
-                    std::memcpy(dB, p.value.data(), sizeof(float) * (size_t)(S * N * R));
-                } else {
-                    const int64_t s = std::stoll(p.name.substr(7));
-                    std::memcpy(dB + s * N * R, p.value.data(), sizeof(float) * (size_t)(N * R));
+            if (fused) {
+                staged("layers.0.q.lora_B", {N, S * R}, dB, (size_t)(S * N * R));
+            } else {
+                for (int64_t s = 0; s < S; ++s) {
+                    bool used = false;
+                    for (int64_t m = 0; m < M; ++m) used = used || (slot[m] >= 0 && (int64_t)slot[m] == s);
+                    if (used) staged("adapter" + std::to_string(s) + ".lora_B", {N, R}, dB + s * N * R, (size_t)(N * R));
                 }
             }
+            device::grad_stage_discard();
         }
         return 0;
     } catch (const std::exception& e) {
@@ -335,22 +349,53 @@ int rh_lora_shrink_q(int64_t M, int64_t K, int64_t R, int64_t S, int64_t groups,
         std::memcpy(da, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
         std::memcpy(ds, dc[1].value.data(), sizeof(double) * (size_t)(M * groups));
         if (dA) {
+            if (!grads.empty()) throw std::runtime_error("a leaf reached grads before the flush");
             std::memset(dA, 0, sizeof(float) * (size_t)(S * R * K));
-            for (const Param& p : grads) {
-                if (fused) {
-                    if (p.name != "layers.1.q.lora_A") throw std::runtime_error("unexpected leaf " + p.name);
-                    std::memcpy(dA, p.value.data(), sizeof(float) * (size_t)(S * R * K));
-                } else {
-                    const int64_t s = std::stoll(p.name.substr(7));
-                    std::memcpy(dA + s * R * K, p.value.data(), sizeof(float) * (size_t)(R * K));
+            if (fused) {
+                staged("layers.1.q.lora_A", {S * R, K}, dA, (size_t)(S * R * K));
+            } else {
+                for (int64_t s = 0; s < S; ++s) {
+                    bool used = false;
+                    for (int64_t m = 0; m < M; ++m) used = used || (slot[m] >= 0 && (int64_t)slot[m] == s);
+                    if (used) staged("adapter" + std::to_string(s) + ".lora_A", {R, K}, dA + s * R * K, (size_t)(R * K));
                 }
             }
+            device::grad_stage_discard();
         }
         return 0;
     } catch (const std::exception& e) {
         g_err = e.what();
         return -1;
     }
+}
+
+// The staging's own rules: `n` floats staged under "stage.x" (twice, adding, the same block both
+// times), a second name asked with another shape refused; then flushed into a ParamSet holding
+// "stage.x" = base (n) -- out = base + bf16(total) -- and a fresh leaf "stage.y" (zeros + bf16 of its
+// total) returned in out_y; the staging is empty after. Returns 0, or the failing check's line.
+int rh_stage_flush(const float* a, const float* b, const float* base, int64_t n, float* out, float* out_y) {
+    const std::vector<int64_t> shape = {n};
+    float* d = device::grad_stage_slot("stage.x", shape);
+    if (!d || device::grad_stage_slot("stage.x", shape) != d) return __LINE__;
+    if (device::grad_stage_slot("stage.x", {n + 1}) != nullptr) return __LINE__;
+    if (device::grad_stage_bytes() != n * (int64_t)sizeof(float)) return __LINE__;
+    std::vector<float> zero((size_t)n);
+    if (hipMemcpy(zero.data(), d, n * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess) return __LINE__;
+    for (float z : zero)
+        if (z != 0.0f) return __LINE__;  // a fresh block is zeroed
+    if (hipMemcpy(d, a, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) return __LINE__;
+    float* e = device::grad_stage_slot("stage.y", shape);
+    if (!e || hipMemcpy(e, b, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess) return __LINE__;
+    ParamSet grads(1);
+    grads[0].name = "stage.x";
+    grads[0].shape = shape;
+    grads[0].value.assign(base, base + n);
+    if (!device::grad_stage_flush(&grads)) return __LINE__;
+    if (grads.size() != 2 || grads[1].name != "stage.y" || grads[1].shape != shape) return __LINE__;
+    std::memcpy(out, grads[0].value.data(), n * sizeof(float));
+    std::memcpy(out_y, grads[1].value.data(), n * sizeof(float));
+    if (device::grad_stage_bytes() != 0) return __LINE__;
+    return 0;
 }
 
 int64_t rh_weights_prepared() { return device_weight_count(); }

@@ -165,3 +165,24 @@ def test_unserved_rank_is_refused():
     dx = np.zeros((M, K))
     assert L.rh_lora_shrink(M, K, R, 1, p(x), p(slot), p(la), p(ct), p(dx), None, 0) != 0
     assert b"rank 12" in L.rh_last_error()
+
+
+@pytest.mark.gpu
+def test_grad_stage_flush_rounds_once():
+    """The step's staging (r97/grad_stage.h, the reference's src/adjoint/device/grad_stage.cpp): a
+    block is zeroed on the first ask and the same buffer after; a second shape under the name is
+    refused; the flush adds bf16(total) (RNE) into an existing leaf and makes a missing one."""
+    L = hook()
+    L.rh_stage_flush.argtypes = [_P, _P, _P, C.c_int64, _P, _P]
+    rng = np.random.default_rng(9)
+    n = 5000
+    a = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    a[:3] = [1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8)]  # ties: to the even bf16 significand
+    b = rng.standard_normal(n).astype(np.float32)
+    base = rng.standard_normal(n).astype(np.float32)
+    out, out_y = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    line = L.rh_stage_flush(p(a), p(b), p(base), n, p(out), p(out_y))
+    assert line == 0, f"stage check failed at rows_hook.cpp:{line}"
+    rb = lambda x: S.bf16_bits_to_f32(S.f32_to_bf16_bits(x))
+    assert np.array_equal(out, base + rb(a)) and np.array_equal(out_y, rb(b))
+    assert out[0] - base[0] == np.float32(1.0) and out[1] - base[1] != np.float32(1.0 + 3 * 2 ** -8)
