@@ -259,20 +259,21 @@ def main():
     ms_step_ev = (time.perf_counter() - t0) * 1e3 / args.steps
     fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
     dx_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
-    # The whole LoRA step: the same steps plus the factors' AdamW on the card (f32 master weights,
-    # the reference Optimiser's update) and the bf16 copies the next step's kernels read.
-    from r9700training_amd.optim import DeviceAdamW, bf16_copies, config
+    # The whole LoRA step: the same steps, then the factors' AdamW on the card (f32 master weights,
+    # the reference Optimiser's update) taking dA, dB as the step's staged gradients (the grad-stage
+    # flush's bf16 rounding, the buffers cleared for the next step) and writing the bf16 copies the
+    # next step's kernels read: one launch.
+    from r9700training_amd.optim import DeviceAdamW, config
 
     masters = [inp["A"].float().contiguous(), inp["B"].float().contiguous()]
-    opt = DeviceAdamW(masters, config(lr=1e-4))
     A_next, B_next = torch.empty_like(inp["A"]), torch.empty_like(inp["B"])
+    opt = DeviceAdamW(masters, config(lr=1e-4), bf16_out=[A_next, B_next])
+    dA.zero_()
+    dB.zero_()
 
     def lora_step():
-        dA.zero_()
-        dB.zero_()
         step()
-        opt.step([dA, dB], stream=stream)
-        bf16_copies(masters, out=[A_next, B_next], stream=stream)
+        opt.step([dA, dB], stream=stream, staged=True)
 
     for _ in range(args.warmup // 5 + 1):
         lora_step()
@@ -311,7 +312,7 @@ def main():
                    "T": T, "N": N, "K": K, "rank": r, "alpha": alpha, "out_dtype": args.out_dtype},
         "tokens_per_s": round(T / (ms_step * 1e-3), 1),
         "lora_step": {"tokens_per_s": round(T / (ms_lora_step * 1e-3), 1), "ms": round(ms_lora_step, 4),
-                      "what": "fwd+bwd + dA/dB cleared + AdamW on A, B (device, f32 masters) + their bf16 copies"},
+                      "what": "fwd+bwd + the staged dA/dB flushed into AdamW on A, B (device, f32 masters) + their bf16 copies"},
         "flops_per_step": total_flops,
         "kernels_ms": {"qlinear_fwd_kernel": round(fwd_ms, 4), "qlinear_dx_kernel": round(dx_ms, 4),
                        "other": round(ms_step_ev - fwd_ms - dx_ms, 4), "ms_per_step_with_events": round(ms_step_ev, 4)},

@@ -276,13 +276,15 @@ int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const int8_t* a, const float* a
 
 /* ------------------------------------------------------------------ the step's far side: AdamW
  *
- * The reference's Optimiser::step (src/optim.cpp:213-296; its config include/r97/optim.h:27-40) on
+ * The reference's Optimiser::step (src/optim.cpp:223-307; its config include/r97/optim.h:27-40) on
  * the card, over device f32 master weights, moments and accumulation buffers: each call adds the
  * gradients into the buffers; every accum_steps-th call takes the mean, clips it to clip_norm by
  * the global norm (when clip_norm > 0), applies the AdamW update at scheduled_lr(t), and clears the
  * buffers. The results are the reference host optimiser's bits: the same f32 operations in the
  * same order, the norm's double partials over the same 4096-element chunks added in chunk order.
- * No_decay names become decay = 0 on their parameters; the thread count has no counterpart. */
+ * No_decay names become decay = 0 on their parameters; the thread count has no counterpart.
+ * An update is one elementwise launch over up to 16 parameters (two more with clipping); nothing
+ * is read back to the host. */
 typedef struct {
     float lr, beta1, beta2, eps, weight_decay, clip_norm, lr_floor_frac;
     int32_t warmup_steps, total_steps, accum_steps;
@@ -292,20 +294,26 @@ typedef struct {
     float* m;    /* first moment */
     float* v;    /* second moment */
     float* acc;  /* the accumulation buffer (zero between updates) */
+    uint16_t* w_bf16; /* NULL, or bf16 [n]: the updated weights' bf16 copy (RNE), written by the update */
     int64_t n;
     int32_t decay; /* 0: excluded from weight decay */
 } R97qAdamWParam;
 /* scheduled_lr (src/optim.cpp:113-126): the learning rate of the step-th update (1-based) */
 float r97q_scheduled_lr(const R97qAdamWConfig* cfg, int32_t step);
-/* the clip's partials: one double a 4096 elements of the parameters (-1: no parameters) */
+/* the clip's workspace: its factor, then one double a 4096 elements of the parameters (-1: no
+ * parameters); needed only with clip_norm > 0 */
 int64_t r97q_adamw_workspace_bytes(const R97qAdamWParam* params, int32_t count);
-/* One optimiser call. grads[i]: f32 [params[i].n] on the card. *updates (updates applied so far)
- * and *pending (calls accumulated) are the optimiser's counters, kept by the caller; *applied
- * (may be NULL) is set to 1 when this call updated. With clipping, the call reads the norm's
- * partials back and so synchronises the stream. */
-int r97q_adamw_step(const R97qAdamWConfig* cfg, const R97qAdamWParam* params, const float* const* grads,
-                    int32_t count, int32_t* updates, int32_t* pending, int32_t* applied, void* workspace,
-                    int64_t workspace_bytes, R97IqrStream stream);
+/* One optimiser call (Optimiser::step, src/optim.cpp:223-307). grads[i]: f32 [params[i].n] on the
+ * card, only read unless flags holds R97Q_ADAMW_GRADS_STAGED: then they are the device rows' f32
+ * staging buffers (include/r97/grad_stage.h), each value taken as grad_stage_flush leaves it in a
+ * zero-filled leaf (rounded once to bf16, src/adjoint/device/grad_stage.cpp:69-73) and the buffers
+ * cleared by the call -- the flush, the leaf fill and the step in one pass. *updates (updates
+ * applied so far) and *pending (calls accumulated) are the optimiser's counters, kept by the
+ * caller; *applied (may be NULL) is set to 1 when this call updated. */
+#define R97Q_ADAMW_GRADS_STAGED 1
+int r97q_adamw_step(const R97qAdamWConfig* cfg, const R97qAdamWParam* params, float* const* grads,
+                    int32_t count, int32_t flags, int32_t* updates, int32_t* pending, int32_t* applied,
+                    void* workspace, int64_t workspace_bytes, R97IqrStream stream);
 /* y = bf16(x) (RNE, NaN quieted), n elements: the kernels' bf16 operands from the f32 master weights */
 int r97q_f32_to_bf16(const float* x, uint16_t* y, int64_t n, R97IqrStream stream);
 

@@ -754,7 +754,7 @@ float orc_clip_global_norm(float* const* x, const int64_t* n, int32_t count, flo
     return norm;
 }
 
-/* src/optim.cpp:213-296 */
+/* src/optim.cpp:223-307 */
 int32_t orc_adamw_step(const OrcAdamWConfig* cfg, float* const* w, float* const* m, float* const* v,
                        float* const* acc, const int64_t* n, const int32_t* decay, int32_t count,
                        const float* const* g, int32_t* step, int32_t* pending) {

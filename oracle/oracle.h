@@ -116,7 +116,7 @@ float orc_scheduled_lr(const OrcAdamWConfig* cfg, int32_t step);
  * one double partial per fixed 4096-element chunk summed in chunk order; rescaled in place when
  * max_norm > 0 and the norm exceeds it. Returns the norm before clipping. */
 float orc_clip_global_norm(float* const* x, const int64_t* n, int32_t count, float max_norm);
-/* Optimiser::step (src/optim.cpp:213-296) over `count` parameters: acc += g; every accum_steps-th
+/* Optimiser::step (src/optim.cpp:223-307) over `count` parameters: acc += g; every accum_steps-th
  * call the mean, the clip, the AdamW update (f32, in the reference's operation order), the buffer
  * cleared. *step is the updates done so far, *pending the calls accumulated; both advance. Returns
  * 1 when this call applied an update. decay[i] == 0 excludes parameter i from weight decay. */

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(HERE, "libr97q.so")
 
 R97Q_F32 = 0
 R97Q_BF16 = 1
+R97Q_ADAMW_GRADS_STAGED = 1  # r97q_adamw_step flags: the gradients are staging buffers (include/r97q.h)
 
 
 class R97qError(RuntimeError):
@@ -59,8 +60,8 @@ class AdamWConfig(C.Structure):
 class AdamWParam(C.Structure):
     """R97qAdamWParam (include/r97q.h): one parameter's device buffers."""
 
-    _fields_ = [("w", C.c_void_p), ("m", C.c_void_p), ("v", C.c_void_p), ("acc", C.c_void_p), ("n", C.c_int64),
-                ("decay", C.c_int32)]
+    _fields_ = [("w", C.c_void_p), ("m", C.c_void_p), ("v", C.c_void_p), ("acc", C.c_void_p),
+                ("w_bf16", C.c_void_p), ("n", C.c_int64), ("decay", C.c_int32)]
 
 
 # every symbol include/r97q.h declares, with its ctypes signature
@@ -92,7 +93,7 @@ SIGNATURES = {
     "r97q_lora_shrink_q_bwd": (C.c_int, [_I, _I, _P, _P, _I, _P, _i, _P, _P, _P, _P, _P, _I, _P]),
     "r97q_scheduled_lr": (C.c_float, [C.POINTER(AdamWConfig), _i]),
     "r97q_adamw_workspace_bytes": (_I, [C.POINTER(AdamWParam), _i]),
-    "r97q_adamw_step": (C.c_int, [C.POINTER(AdamWConfig), C.POINTER(AdamWParam), C.POINTER(C.c_void_p), _i,
+    "r97q_adamw_step": (C.c_int, [C.POINTER(AdamWConfig), C.POINTER(AdamWParam), C.POINTER(C.c_void_p), _i, _i,
                                   C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.POINTER(C.c_int32), _P, _I, _P]),
     "r97q_f32_to_bf16": (C.c_int, [_P, _P, _I, _P]),
 }

@@ -368,7 +368,9 @@ __device__ __forceinline__ void adapter(const uint16_t* P, const uint16_t* Q, in
 }
 
 // accumulator element e of tile (mi, ni) is row 32*mi + 8*(e/4) + 4*half + e%4, column 32*ni + l32;
-// rs (optional): a factor a row, rs[row * rs_ld], applied before the write
+// SCALED: a factor a row, rs[row * rs_ld], applied before the write (a compile-time choice: the
+// plain kernels keep the register allocation and schedule they have without it)
+template <bool SCALED = false>
 __device__ __forceinline__ void store(const f32x16 (&acc)[2][4], void* out, int64_t ld, int64_t m0,
                                       int64_t o0, int64_t T, int lane, int f32, int accumulate,
                                       const float* rs = nullptr, int64_t rs_ld = 0) {
@@ -379,11 +381,11 @@ __device__ __forceinline__ void store(const f32x16 (&acc)[2][4], void* out, int6
         for (int e = 0; e < 16; ++e) {
             const int64_t row = m0 + 32 * mi + 8 * (e >> 2) + 4 * half + (e & 3);
             if (row >= T) continue;
-            const float f = rs ? rs[row * rs_ld] : 1.0f;
+            const float f = SCALED ? rs[row * rs_ld] : 1.0f;
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni) {
                 const int64_t col = o0 + 32 * ni + l32;
-                float v = rs ? acc[mi][ni][e] * f : acc[mi][ni][e];
+                float v = SCALED ? acc[mi][ni][e] * f : acc[mi][ni][e];
                 if (f32) {
                     float* d = reinterpret_cast<float*>(out) + row * ld + col;
                     *d = accumulate ? *d + v : v;
@@ -410,7 +412,7 @@ __device__ __forceinline__ void fwd_wave(const FwdParams& p, const Lds& lds, int
     store(acc, p.Y, p.N, L.m0, L.o0, p.T, lane, p.y_f32, 0);
 }
 
-template <int BITS, int SLICE>
+template <int BITS, int SLICE, bool SCALED>
 __device__ __forceinline__ void dx_wave(const DxParams& p, const Lds& lds, int lane, int mt, int kt) {
     f32x16 acc[2][4];
 #pragma unroll
@@ -422,21 +424,25 @@ __device__ __forceinline__ void dx_wave(const DxParams& p, const Lds& lds, int l
     L.run(lds, acc);
     if (p.rank > 0) adapter<false>(p.P, p.At, p.rank, L.m0, L.o0, p.T, lane, acc);
     // the coded trunk's code basis: the tile's 128 columns are one activation-scale group
-    const float* rs = p.a_scale ? p.a_scale + kt : nullptr;
-    store(acc, p.dX, p.K, L.m0, L.o0, p.T, lane, p.dx_f32, p.accumulate, rs, p.a_scale_ld);
+    if constexpr (SCALED)
+        store<true>(acc, p.dX, p.K, L.m0, L.o0, p.T, lane, p.dx_f32, p.accumulate, p.a_scale + kt, p.a_scale_ld);
+    else
+        store(acc, p.dX, p.K, L.m0, L.o0, p.T, lane, p.dx_f32, p.accumulate);
 }
 
-#define R97Q_WAVE_SWITCH(fn, ...)                  \
-    switch (threadIdx.x >> 6) {                    \
-        case 0: fn<R97Q_BITS, 0>(__VA_ARGS__); break; \
-        case 1: fn<R97Q_BITS, 1>(__VA_ARGS__); break; \
-        case 2: fn<R97Q_BITS, 2>(__VA_ARGS__); break; \
-        case 3: fn<R97Q_BITS, 3>(__VA_ARGS__); break; \
-        case 4: fn<R97Q_BITS, 4>(__VA_ARGS__); break; \
-        case 5: fn<R97Q_BITS, 5>(__VA_ARGS__); break; \
-        case 6: fn<R97Q_BITS, 6>(__VA_ARGS__); break; \
-        default: fn<R97Q_BITS, 7>(__VA_ARGS__); break; \
+// X: further template arguments after the slice (", SCALED"), or empty
+#define R97Q_WAVE_SWITCH(fn, X, ...)                    \
+    switch (threadIdx.x >> 6) {                         \
+        case 0: fn<R97Q_BITS, 0 X>(__VA_ARGS__); break;    \
+        case 1: fn<R97Q_BITS, 1 X>(__VA_ARGS__); break;    \
+        case 2: fn<R97Q_BITS, 2 X>(__VA_ARGS__); break;    \
+        case 3: fn<R97Q_BITS, 3 X>(__VA_ARGS__); break;    \
+        case 4: fn<R97Q_BITS, 4 X>(__VA_ARGS__); break;    \
+        case 5: fn<R97Q_BITS, 5 X>(__VA_ARGS__); break;    \
+        case 6: fn<R97Q_BITS, 6 X>(__VA_ARGS__); break;    \
+        default: fn<R97Q_BITS, 7 X>(__VA_ARGS__); break;   \
     }
+#define R97Q_COMMA_SCALED , SCALED
 
 __global__ __launch_bounds__(kThreads, 1) void qlinear_fwd_kernel(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t w0[kTileBytes], w1[kTileBytes], x0[kActBytes], x1[kActBytes];
@@ -444,16 +450,18 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_fwd_kernel(const FwdParam
     const int tile = xcd_tile(blockIdx.x, p.mtiles * p.ntiles);
     const int mt = tile / p.ntiles, nt = tile % p.ntiles;
     const int lane = threadIdx.x & 63;
-    R97Q_WAVE_SWITCH(fwd_wave, p, lds, lane, mt, nt)
+    R97Q_WAVE_SWITCH(fwd_wave, , p, lds, lane, mt, nt)
 }
 
+// SCALED: dX in the code basis of an i8a8h activation (p.a_scale set)
+template <bool SCALED>
 __global__ __launch_bounds__(kThreads, 1) void qlinear_dx_kernel(const DxParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t w0[kTileBytes], w1[kTileBytes], x0[kActBytes], x1[kActBytes];
     const Lds lds{{w0, w1}, {x0, x1}};
     const int tile = xcd_tile(blockIdx.x, p.mtiles * p.ktiles);
     const int mt = tile / p.ktiles, kt = tile % p.ktiles;
     const int lane = threadIdx.x & 63;
-    R97Q_WAVE_SWITCH(dx_wave, p, lds, lane, mt, kt)
+    R97Q_WAVE_SWITCH(dx_wave, R97Q_COMMA_SCALED, p, lds, lane, mt, kt)
 }
 
 }  // namespace
@@ -465,7 +473,11 @@ void launch_fwd<R97Q_BITS>(const FwdParams& p, hipStream_t s) {
 
 template <>
 void launch_dx<R97Q_BITS>(const DxParams& p, hipStream_t s) {
-    hipLaunchKernelGGL(qlinear_dx_kernel, dim3((unsigned)(p.mtiles * p.ktiles)), dim3(kThreads), 0, s, p);
+    const dim3 grid((unsigned)(p.mtiles * p.ktiles));
+    if (p.a_scale)
+        hipLaunchKernelGGL(qlinear_dx_kernel<true>, grid, dim3(kThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL(qlinear_dx_kernel<false>, grid, dim3(kThreads), 0, s, p);
 }
 
 }  // namespace r97q
