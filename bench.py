@@ -78,7 +78,9 @@ def profiled_traffic(kernel, config):
             return None
     if config != "c2" or h.hexdigest()[:16] != prof.get("sources_sha256_16"):
         return None
-    k = prof.get("kernels", {}).get(kernel)
+    kernels = prof.get("kernels", {})
+    # the profiler names a template instance with its arguments (qlinear_dx_kernel<false>)
+    k = kernels.get(kernel) or next((v for n, v in kernels.items() if n.split("<")[0] == kernel), None)
     return None if k is None else k["traffic_bytes"]
 
 
