@@ -113,10 +113,20 @@ int r97_iqr_decode(const R97IqrDecodeDesc* desc, R97IqrStream stream);
  *   scale_t : the effective bf16 scale of every (row, 128-column block), transposed to
  *             [cols/128][rows]: the block scale with scale.1 settled (src/iqr_decode.h:223-235) and
  *             the optional scale.col factor folded in with one rounding (src/iqr_form.h:203-216).
- * The fused path serves trellis forms with rb = 1, the computed `trellis.mad` codebook, bits 3..6,
- * state_bits 16, any scale dtype with optional scale.1 / scale.col, cols % 128 == 0,
- * rows % 32 == 0 and run_rows % 32 == 0; other forms are refused with R97Q_EUNSUPPORTED (the
- * standalone r97_iqr_decode serves every form). */
+ * The trellis decode runs inside the fused kernels for trellis forms with rb = 1, the computed
+ * `trellis.mad` codebook, bits 3..6, state_bits 16, any scale dtype with optional scale.1 /
+ * scale.col, cols % 128 == 0, rows % 32 == 0 and run_rows % 32 == 0.
+ *
+ * Every other form the decode reads (a stored-LUT codebook, rb > 1 row blocks, other code widths
+ * and state sizes, the affine grid) is decoded once into the int8-code form (bits =
+ * R97Q_CODES8): the reference's stored weight (src/stored_weight.h:24-33: int8 codes [rows, cols]
+ * and a bf16 scale a (row, 128 columns)) in the fused kernels' tiled layout, the GPU-resident
+ * counterpart of the reference's unit-major device form:
+ *   stream  : 32-byte units of 8 rows x 4 columns, k-major inside (byte 8*c + i is row i,
+ *             column c of the unit), ordered [rows/8][cols/4]; rows * cols bytes;
+ *   scale_t : as above.
+ * The fused kernels multiply code x scale, rounded once to bf16, in both forms. */
+#define R97Q_CODES8 8
 typedef struct R97qWeight {
     int64_t rows;          /* N */
     int64_t cols;          /* K */
@@ -131,16 +141,29 @@ typedef struct R97qWeight {
     const uint16_t* scale_t;  /* device, (cols/128) * rows bf16 */
 } R97qWeight;
 
-/* Bytes of the stream plane for the whole weight `desc` describes (row0 = 0, rows = rows_all);
- * -1 when the form is not one the fused path serves (r97q_last_error says why). */
+/* Bytes of the stream plane for the whole weight `desc` describes (row0 = 0, rows = rows_all): the
+ * trellis stream for the forms decoded inside the kernels, rows * cols for the int8-code form;
+ * -1 when the description is outside the decode's rules, rows is not a multiple of 8 or cols of
+ * 128 (r97q_last_error says why). */
 int64_t r97q_weight_stream_bytes(const R97IqrDecodeDesc* desc);
 
 /* Build the prepared weight from the canonical device planes `desc` points at (whole weight:
  * row0 = 0, rows = rows_all; the out_* fields are unused). `scale_col` is the optional
  * scale.col plane (cols/128 f32 on the device, NULL when the form has none). Writes `stream_out`
- * (r97q_weight_stream_bytes bytes) and `scale_t_out` ((cols/128)*rows bf16) and fills `w`. */
+ * (r97q_weight_stream_bytes bytes) and `scale_t_out` ((cols/128)*rows bf16) and fills `w`: the
+ * trellis stream when the kernels decode the form themselves, else the int8-code form. Replaces
+ * the stored-weight put of a decoded grid (src/stored_weight.cpp:38-75) on the card. */
 int r97q_weight_prepare(const R97IqrDecodeDesc* desc, const float* scale_col, uint32_t* stream_out,
                         uint16_t* scale_t_out, R97qWeight* w, R97IqrStream stream);
+/* The int8-code form of any form the decode reads (r97_iqr_decode's values, tiled; the scale.col
+ * fold of src/iqr_form.h:203-216 when `scale_col` is given): codes_out rows * cols bytes. */
+int r97q_weight_prepare_codes8(const R97IqrDecodeDesc* desc, const float* scale_col, int8_t* codes_out,
+                               uint16_t* scale_t_out, R97qWeight* w, R97IqrStream stream);
+/* The int8-code form from a weight already decoded (the reference's StoredWeight,
+ * src/stored_weight.h:24-33, on the card): codes int8 [rows, cols], scale bf16 [rows, cols/128];
+ * rows a multiple of 8, cols of 128. The counterpart of stored_weight_put (src/stored_weight.h:37) for the kernels. */
+int r97q_weight_from_decoded(const int8_t* codes, const uint16_t* scale, int64_t rows, int64_t cols,
+                             int8_t* codes_out, uint16_t* scale_t_out, R97qWeight* w, R97IqrStream stream);
 
 /* ------------------------------------------------------------------ fused forward / backward
  *

@@ -95,10 +95,28 @@ __device__ inline int32_t rb_round(int32_t v, float ratio, int32_t mad) {
     return (int32_t)__builtin_rintf((float)v * ratio);
 }
 
+// Where the decode writes. Canonical: out_codes [rows, cols] int8 row-major and out_scale
+// [rows, cols/128] bf16 (the reference's grids). TILED: the int8-code form the fused kernels read
+// (out_codes holds 32-byte units of 8 rows x 4 columns, k-major inside -- byte 8*c + i is row i,
+// column c -- ordered [rows/8][cols/4]) and the scale transposed to [cols/128][rows_all].
+template <bool TILED>
+struct DecodeOut {
+    __device__ static int64_t code(const R97IqrDecodeDesc& d, int64_t q, int64_t j) {
+        if (!TILED) return (q - d.row0) * d.cols + j;
+        return ((q >> 3) * (d.cols >> 2) + (j >> 2)) * 32 + 8 * (j & 3) + (q & 7);
+    }
+    __device__ static int64_t scale(const R97IqrDecodeDesc& d, int64_t q, int64_t kb) {
+        if (!TILED) return (q - d.row0) * (d.cols >> 7) + kb;
+        return kb * d.rows_all + q;
+    }
+};
+
 // One thread: column j, rows [r, r_end) of the run [run_start, run_end).
+template <bool TILED>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDecodeDesc d,
                                                                 int64_t chunk_rows,
                                                                 int64_t chunks) {
+    using O = DecodeOut<TILED>;
     const int64_t j = (int64_t)blockIdx.x * kDecodeThreads + threadIdx.x;
     const int64_t ch = blockIdx.y + (int64_t)blockIdx.z * gridDim.y;
     if (j >= d.cols || ch >= chunks) return;
@@ -110,7 +128,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
     if (r_end > run_end) r_end = run_end;
     if (r_end > d.row0 + d.rows) r_end = d.row0 + d.rows;
     const int64_t kb = j >> 7;
-    const int64_t nkb = d.cols >> 7;
     const bool first = (j & 127) == 0;
 
     if (d.affine) {
@@ -119,8 +136,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
             const int64_t bc = d.scale_block_cols > 0 ? d.scale_block_cols : d.cols;
             const int64_t gb = bc == d.cols ? 0 : (kb * 128) / bc;
             const uint32_t zero = load_bits(d.zero + (q - d.row0) * d.zero_row_bytes, d.zero_bits, gb);
-            d.out_codes[(q - d.row0) * d.cols + j] = (int8_t)((int32_t)code - (int32_t)zero);
-            if (first) d.out_scale[(q - d.row0) * nkb + kb] = f32_to_bf16(block_scale(d, q, kb));
+            d.out_codes[O::code(d, q, j)] = (int8_t)((int32_t)code - (int32_t)zero);
+            if (first) d.out_scale[O::scale(d, q, kb)] = f32_to_bf16(block_scale(d, q, kb));
         }
         return;
     }
@@ -154,8 +171,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
             sc = block_scale(d, q, kb);
             out = v;
         }
-        d.out_codes[(q - d.row0) * d.cols + j] = (int8_t)out;
-        if (first) d.out_scale[(q - d.row0) * nkb + kb] = f32_to_bf16(sc);
+        d.out_codes[O::code(d, q, j)] = (int8_t)out;
+        if (first) d.out_scale[O::scale(d, q, kb)] = f32_to_bf16(sc);
     }
 }
 
@@ -183,6 +200,41 @@ __global__ __launch_bounds__(256) void prepare_stream_kernel(const R97IqrDecodeD
     for (int q = 0; q < d.bits; ++q) stream[stream_index(g, d.bits, q, d.cols, col)] = w[q];
 }
 
+// One thread per 32-byte unit (8 rows x 4 columns) of a decoded int8 grid [rows, cols]: the unit in
+// the fused kernels' int8-code form (the TILED layout of decode_kernel).
+__global__ __launch_bounds__(256) void tile_codes_kernel(const int8_t* __restrict__ codes, int64_t rows,
+                                                         int64_t cols, int8_t* __restrict__ tiled) {
+    const int64_t k4 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t n8 = blockIdx.y;
+    if (k4 >= cols / 4) return;
+    uint32_t row[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) row[i] = *reinterpret_cast<const uint32_t*>(codes + (n8 * 8 + i) * cols + 4 * k4);
+    uint32_t out[8];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo |= ((row[i] >> (8 * c)) & 0xFFu) << (8 * i);
+            hi |= ((row[i + 4] >> (8 * c)) & 0xFFu) << (8 * i);
+        }
+        out[2 * c] = lo;
+        out[2 * c + 1] = hi;
+    }
+    uint4* dst = reinterpret_cast<uint4*>(tiled + (n8 * (cols / 4) + k4) * 32);
+    dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+    dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+}
+
+// [rows, nkb] bf16 -> [nkb, rows]
+__global__ __launch_bounds__(256) void transpose_scale_kernel(const uint16_t* __restrict__ scale, int64_t rows,
+                                                              int64_t nkb, uint16_t* __restrict__ scale_t) {
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t kb = blockIdx.y;
+    if (n < rows) scale_t[kb * rows + n] = scale[n * nkb + kb];
+}
+
 // One thread per (row, 128-column block): the effective bf16 scale, transposed to [cols/128][rows].
 __global__ __launch_bounds__(256) void prepare_scale_kernel(const R97IqrDecodeDesc d,
                                                             const float* __restrict__ scale_col,
@@ -202,6 +254,17 @@ __global__ __launch_bounds__(256) void prepare_scale_kernel(const R97IqrDecodeDe
 }
 
 }  // namespace
+
+template <bool TILED>
+void launch_decode(const R97IqrDecodeDesc& d, hipStream_t s) {
+    const int64_t chunk_rows = (d.run_rows % 8 == 0) ? 8 : 1;
+    // chunks never straddle a run: runs start at multiples of run_rows and chunk_rows divides it
+    const int64_t chunks = (d.rows + chunk_rows - 1) / chunk_rows;
+    const int64_t gy = chunks < 65535 ? chunks : 65535;
+    const int64_t gz = (chunks + gy - 1) / gy;
+    dim3 grid((unsigned)((d.cols + kDecodeThreads - 1) / kDecodeThreads), (unsigned)gy, (unsigned)gz);
+    hipLaunchKernelGGL(decode_kernel<TILED>, grid, dim3(kDecodeThreads), 0, s, d, chunk_rows, chunks);
+}
 
 // Whether `d` is a form the fused kernels serve; the reason goes to the error message.
 bool fused_form(const R97IqrDecodeDesc& d, const float* scale_col) {
@@ -234,6 +297,21 @@ bool fused_form(const R97IqrDecodeDesc& d, const float* scale_col) {
     return true;
 }
 
+// Whether `d` (valid) can take the int8-code form: every form the decode reads, with whole 8-row
+// units and 128-column blocks.
+bool codes8_form(const R97IqrDecodeDesc& d, const float* scale_col) {
+    if (d.rows_all % 8 != 0 || d.cols % 128 != 0) {
+        set_error("int8-code form: rows %lld must be a multiple of 8, cols %lld of 128", (long long)d.rows_all,
+                  (long long)d.cols);
+        return false;
+    }
+    if (scale_col && (d.scale_dtype != R97_IQR_F32 || d.scale_block_cols > 0)) {
+        set_error("int8-code form: scale.col needs one f32 scale a row (src/iqr_form.h:209)");
+        return false;
+    }
+    return true;
+}
+
 }  // namespace r97q
 
 using namespace r97q;
@@ -251,14 +329,7 @@ int r97_iqr_decode(const R97IqrDecodeDesc* desc, R97IqrStream stream) {
         return 1;
     }
     const R97IqrDecodeDesc& d = *desc;
-    const int64_t chunk_rows = (d.run_rows % 8 == 0) ? 8 : 1;
-    // chunks never straddle a run: runs start at multiples of run_rows and chunk_rows divides it
-    const int64_t chunks = (d.rows + chunk_rows - 1) / chunk_rows;
-    const int64_t gy = chunks < 65535 ? chunks : 65535;
-    const int64_t gz = (chunks + gy - 1) / gy;
-    dim3 grid((unsigned)((d.cols + kDecodeThreads - 1) / kDecodeThreads), (unsigned)gy, (unsigned)gz);
-    hipLaunchKernelGGL(decode_kernel, grid, dim3(kDecodeThreads), 0, (hipStream_t)stream, d,
-                       chunk_rows, chunks);
+    launch_decode<false>(d, (hipStream_t)stream);
     return launch_status("r97_iqr_decode") == R97Q_OK ? 0 : 1;
 }
 
@@ -268,8 +339,20 @@ int64_t r97q_weight_stream_bytes(const R97IqrDecodeDesc* desc) {
         set_error("r97q_weight_stream_bytes: null description");
         return -1;
     }
-    if (!fused_form(*desc, nullptr)) return -1;
-    return desc->rows_all / 32 * desc->bits * desc->cols * 4;
+    if (fused_form(*desc, nullptr)) return desc->rows_all / 32 * desc->bits * desc->cols * 4;
+    // the other forms: the int8-code form (the description's own rules still apply)
+    R97IqrDecodeDesc d = *desc;
+    int8_t probe_codes = 0;
+    uint16_t probe_scale = 0;
+    d.out_codes = &probe_codes;
+    d.out_scale = &probe_scale;
+    if (validate(d)) {
+        set_error("r97q_weight_stream_bytes: the description is outside the decode's rules");
+        return -1;
+    }
+    if (!codes8_form(d, nullptr)) return -1;
+    clear_error();
+    return d.rows_all * d.cols;
 }
 
 int r97q_weight_prepare(const R97IqrDecodeDesc* desc, const float* scale_col,
@@ -292,7 +375,12 @@ int r97q_weight_prepare(const R97IqrDecodeDesc* desc, const float* scale_col,
         set_error("r97q_weight_prepare: the description is outside the decode's rules");
         return R97Q_EINVAL;
     }
-    if (!fused_form(d, scale_col)) return R97Q_EUNSUPPORTED;
+    if (!fused_form(d, scale_col)) {
+        // every other form the decode reads: decoded once into the int8-code form
+        clear_error();
+        return r97q_weight_prepare_codes8(desc, scale_col, reinterpret_cast<int8_t*>(stream_out), scale_t_out, w,
+                                          stream);
+    }
     const hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(prepare_stream_kernel,
                        dim3((unsigned)((d.cols + 255) / 256), (unsigned)(d.rows_all / 32)), dim3(256),
@@ -313,6 +401,81 @@ int r97q_weight_prepare(const R97IqrDecodeDesc* desc, const float* scale_col,
     out.mad_b = d.mad_b;
     out.lut = d.lut;
     out.stream = stream_out;
+    out.scale_t = scale_t_out;
+    *w = out;
+    return R97Q_OK;
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int r97q_weight_prepare_codes8(const R97IqrDecodeDesc* desc, const float* scale_col, int8_t* codes_out,
+                               uint16_t* scale_t_out, R97qWeight* w, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_weight_prepare_codes8";
+    if (!desc || !codes_out || !scale_t_out || !w) {
+        set_error("%s: null argument", who);
+        return R97Q_EINVAL;
+    }
+    R97IqrDecodeDesc d = *desc;
+    if (d.row0 != 0 || d.rows != d.rows_all) {
+        set_error("%s: the whole weight is prepared at once (row0 0, rows = rows_all)", who);
+        return R97Q_EINVAL;
+    }
+    d.out_codes = codes_out;
+    d.out_scale = scale_t_out;
+    if (validate(d)) {
+        set_error("%s: the description is outside the decode's rules", who);
+        return R97Q_EINVAL;
+    }
+    if (!codes8_form(d, scale_col)) return R97Q_EUNSUPPORTED;
+    const hipStream_t s = (hipStream_t)stream;
+    // the decode writes the codes in the tiled form and the scale transposed
+    launch_decode<true>(d, s);
+    if (int e = launch_status("decode_kernel (int8-code form)")) return e;
+    if (scale_col) {
+        // src/iqr_form.h:203-216: the scale.col fold replaces the decoded scale
+        hipLaunchKernelGGL(prepare_scale_kernel,
+                           dim3((unsigned)((d.rows_all + 255) / 256), (unsigned)(d.cols / 128)), dim3(256), 0, s, d,
+                           scale_col, scale_t_out);
+        if (int e = launch_status("prepare_scale_kernel")) return e;
+    }
+    R97qWeight out{};
+    out.rows = d.rows_all;
+    out.cols = d.cols;
+    out.bits = R97Q_CODES8;
+    out.stream = reinterpret_cast<const uint32_t*>(codes_out);
+    out.scale_t = scale_t_out;
+    *w = out;
+    return R97Q_OK;
+}
+
+int r97q_weight_from_decoded(const int8_t* codes, const uint16_t* scale, int64_t rows, int64_t cols,
+                             int8_t* codes_out, uint16_t* scale_t_out, R97qWeight* w, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_weight_from_decoded";
+    if (!codes || !scale || !codes_out || !scale_t_out || !w) {
+        set_error("%s: null argument", who);
+        return R97Q_EINVAL;
+    }
+    if (rows <= 0 || cols <= 0 || rows % 8 != 0 || cols % 128 != 0) {
+        set_error("%s: rows %lld must be a positive multiple of 8, cols %lld of 128", who, (long long)rows,
+                  (long long)cols);
+        return R97Q_EINVAL;
+    }
+    const hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(tile_codes_kernel, dim3((unsigned)((cols / 4 + 255) / 256), (unsigned)(rows / 8)), dim3(256),
+                       0, s, codes, rows, cols, codes_out);
+    if (int e = launch_status("tile_codes_kernel")) return e;
+    hipLaunchKernelGGL(transpose_scale_kernel, dim3((unsigned)((rows + 255) / 256), (unsigned)(cols / 128)),
+                       dim3(256), 0, s, scale, rows, cols / 128, scale_t_out);
+    if (int e = launch_status("transpose_scale_kernel")) return e;
+    R97qWeight out{};
+    out.rows = rows;
+    out.cols = cols;
+    out.bits = R97Q_CODES8;
+    out.stream = reinterpret_cast<const uint32_t*>(codes_out);
     out.scale_t = scale_t_out;
     *w = out;
     return R97Q_OK;

@@ -145,11 +145,12 @@ int check_weight(const R97qWeight* w) {
         set_error("qlinear: null weight");
         return R97Q_EINVAL;
     }
-    if (!w->mad || w->state_bits != 16 || w->bits < 3 || w->bits > 6) {
-        set_error("qlinear: weight form not served (trellis.mad, L 16, bits 3..6)");
+    const bool codes8 = w->bits == R97Q_CODES8;
+    if (!codes8 && (!w->mad || w->state_bits != 16 || w->bits < 3 || w->bits > 6)) {
+        set_error("qlinear: weight form not served (trellis.mad, L 16, bits 3..6, or the int8-code form)");
         return R97Q_EUNSUPPORTED;
     }
-    if (w->rows % kBN != 0 || w->cols % kBN != 0 || w->run_rows % 32 != 0) {
+    if (w->rows % kBN != 0 || w->cols % kBN != 0 || (!codes8 && w->run_rows % 32 != 0)) {
         set_error("qlinear: N %lld and K %lld must be multiples of 128, run %d of 32",
                   (long long)w->rows, (long long)w->cols, (int)w->run_rows);
         return R97Q_EUNSUPPORTED;
@@ -228,7 +229,8 @@ int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* X, const uint
         case 3: launch_fwd<3>(p, s); break;
         case 4: launch_fwd<4>(p, s); break;
         case 5: launch_fwd<5>(p, s); break;
-        default: launch_fwd<6>(p, s); break;
+        case 6: launch_fwd<6>(p, s); break;
+        default: launch_fwd<R97Q_CODES8>(p, s); break;
     }
     return launch_status("qlinear_fwd_kernel");
 }
@@ -306,7 +308,8 @@ int dx_base(const R97qWeight* w, const Shape& sh, const uint16_t* dY, void* dX, 
         case 3: launch_dx<3>(p, s); break;
         case 4: launch_dx<4>(p, s); break;
         case 5: launch_dx<5>(p, s); break;
-        default: launch_dx<6>(p, s); break;
+        case 6: launch_dx<6>(p, s); break;
+        default: launch_dx<R97Q_CODES8>(p, s); break;
     }
     return launch_status("qlinear_dx_kernel");
 }

@@ -164,12 +164,28 @@ __device__ __forceinline__ void scales_of(uint32_t w, float& a, float& b) {
     b = __builtin_bit_cast(float, w & 0xFFFF0000u);
 }
 
+// off: the exact product that turns the decoded unsigned value into (value - bias) * scale in one
+// fma (trellis: f16(1024 + byte sum), bias 1150; int8 codes: code ^ 0x80, bias 128)
 template <int N>
-__device__ __forceinline__ void slice_scales(const uint32_t* w, float (&sc)[N], float (&off)[N]) {
+__device__ __forceinline__ void slice_scales(const uint32_t* w, float (&sc)[N], float (&off)[N], float bias) {
 #pragma unroll
     for (int i = 0; i < N / 2; ++i) scales_of(w[i], sc[2 * i], sc[2 * i + 1]);
 #pragma unroll
-    for (int i = 0; i < N; ++i) off[i] = -1150.0f * sc[i];
+    for (int i = 0; i < N; ++i) off[i] = -bias * sc[i];
+}
+
+// The int8-code form's words of one lane: the 32-byte unit (8 rows x 4 columns, byte 8*c + i is
+// row i of column c) of a forward lane, or the 16-byte half of one (columns 2h, 2h+1) of a dX lane,
+// and the rows' bf16 scales.
+template <bool FWD>
+struct Codes8 {
+    uint4 c[FWD ? 2 : 1];
+    typename std::conditional<FWD, uint2, uint4>::type s;
+};
+
+// byte `b` of `w` (code ^ 0x80) as code * sc, exactly: (u - 128) * sc has at most 16 significant bits
+[[maybe_unused]] __device__ __forceinline__ float code8_value(uint32_t w, int b, float sc, float off) {
+    return __builtin_fmaf((float)((w >> (8 * b)) & 0xFFu), sc, off);
 }
 
 // XCD-aware tile order: consecutive workgroup ids are dealt round-robin over the 8 XCDs;
@@ -194,7 +210,8 @@ struct Loop {
     static constexpr int ROWS = FWD ? 4 : 8;
     static constexpr int COLS = FWD ? 4 : 2;
     static constexpr int SLICE = FWD ? WAVE : (WAVE & 3);
-    using W = Words<BITS, ROWS, COLS, SLICE>;
+    static constexpr bool kCodes8 = BITS == R97Q_CODES8;
+    using W = typename std::conditional<kCodes8, Codes8<FWD>, Words<BITS, ROWS, COLS, SLICE>>::type;
 
     const uint16_t* act;       // X (fwd) or dY (dx): [T, red]
     int64_t red;               // reduction length: K (fwd) or N (dx)
@@ -215,29 +232,63 @@ struct Loop {
 
         // where step s's weight tile comes from
         auto words_for = [&](int s, W& wd) {
-            int64_t g, col, kb;
-            if (FWD) {
-                g = (o0 >> 5) + seg;
-                col = (int64_t)s * kStep + 4 * cg;
-                kb = ((int64_t)s * kStep) >> 7;
+            if constexpr (kCodes8) {
+                // forward: rows o0 + 32*seg + 4*WAVE .. +4 (half WAVE&1 of unit row n8), columns
+                // 4*cg.. of the step; dX: rows 64*s + 32*seg + 8*SLICE .. +8 (unit row n8), columns
+                // o0 + 2*lane, +1 (half lane&1 of unit column k4)
+                const int8_t* units = reinterpret_cast<const int8_t*>(stream);
+                int64_t srow, k4, half, kb;
+                if (FWD) {
+                    srow = o0 + 32 * seg + 4 * WAVE;
+                    k4 = (int64_t)s * (kStep / 4) + cg;
+                    half = 0;
+                    kb = ((int64_t)s * kStep) >> 7;
+                } else {
+                    srow = (int64_t)s * kStep + 32 * seg + 8 * SLICE;
+                    k4 = (o0 >> 2) + (lane >> 1);
+                    half = lane & 1;
+                    kb = o0 >> 7;
+                }
+                const uint4* src = reinterpret_cast<const uint4*>(units + ((srow >> 3) * (K >> 2) + k4) * 32) + half;
+                wd.c[0] = src[0];
+                if constexpr (FWD) wd.c[1] = src[1];
+                wd.s = *reinterpret_cast<const decltype(wd.s)*>(scale_t + kb * N + srow);
             } else {
-                g = (((int64_t)s * kStep) >> 5) + seg;
-                col = o0 + 2 * cg;
-                kb = o0 >> 7;
+                int64_t g, col, kb;
+                if (FWD) {
+                    g = (o0 >> 5) + seg;
+                    col = (int64_t)s * kStep + 4 * cg;
+                    kb = ((int64_t)s * kStep) >> 7;
+                } else {
+                    g = (((int64_t)s * kStep) >> 5) + seg;
+                    col = o0 + 2 * cg;
+                    kb = o0 >> 7;
+                }
+                load_words<BITS, ROWS, COLS, SLICE>(stream, scale_t, N, g, halo_segment(g, run_rows, N), K, col,
+                                                    kb, wd);
             }
-            load_words<BITS, ROWS, COLS, SLICE>(stream, scale_t, N, g, halo_segment(g, run_rows, N), K, col,
-                                                kb, wd);
         };
         auto decode = [&](const W& wd, uint8_t* tile) {
             float sc[ROWS], off[ROWS];
-            slice_scales<ROWS>(reinterpret_cast<const uint32_t*>(&wd.s), sc, off);
+            slice_scales<ROWS>(reinterpret_cast<const uint32_t*>(&wd.s), sc, off, kCodes8 ? 128.0f : 1150.0f);
+            // the value of the lane's row i, column c
+            auto value = [&](int c, int i) -> float {
+                if constexpr (kCodes8) {
+                    // forward: dword 2c + (WAVE&1) of the unit; dX: dword 2c + i/4 of the half
+                    const int q = FWD ? 2 * c + (WAVE & 1) : 2 * c + (i >> 2);
+                    const uint32_t w = comp(wd.c[q >> 2], q & 3) ^ 0x80808080u;
+                    return code8_value(w, i & 3, sc[i], off[i]);
+                } else {
+                    return slice_value<BITS, ROWS, COLS, SLICE>(wd, c, i, a24, b, sc[i], off[i]);
+                }
+            };
             if (FWD) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float v0 = slice_value<BITS, ROWS, COLS, SLICE>(wd, 0, i, a24, b, sc[i], off[i]);
-                    const float v1 = slice_value<BITS, ROWS, COLS, SLICE>(wd, 1, i, a24, b, sc[i], off[i]);
-                    const float v2 = slice_value<BITS, ROWS, COLS, SLICE>(wd, 2, i, a24, b, sc[i], off[i]);
-                    const float v3 = slice_value<BITS, ROWS, COLS, SLICE>(wd, 3, i, a24, b, sc[i], off[i]);
+                    const float v0 = value(0, i);
+                    const float v1 = value(1, i);
+                    const float v2 = value(2, i);
+                    const float v3 = value(3, i);
                     const int row = 32 * seg + 4 * SLICE + i;
                     const uint2 o = {pack_bf16(v0, v1), pack_bf16(v2, v3)};
                     *reinterpret_cast<uint2*>(chunk_at(tile, row, cg >> 1) + ((cg & 1) << 3)) = o;
@@ -247,7 +298,7 @@ struct Loop {
                 for (int c = 0; c < 2; ++c) {
                     float v[8];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) v[i] = slice_value<BITS, ROWS, COLS, SLICE>(wd, c, i, a24, b, sc[i], off[i]);
+                    for (int i = 0; i < 8; ++i) v[i] = value(c, i);
                     const uint4 o = {pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
                                      pack_bf16(v[6], v[7])};
                     // rows n = 32*seg + 8*SLICE .. +8 of column 2*cg + c: chunk 4*seg + SLICE

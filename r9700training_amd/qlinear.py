@@ -37,23 +37,50 @@ def iqr_decode(desc: Desc, out_codes: torch.Tensor, out_scale: torch.Tensor, str
 
 
 class QWeight:
-    """A prepared IQR weight on the device: the column streams and the transposed effective scale
-    (made once: the base weight is frozen)."""
+    """A prepared IQR weight on the device (made once: the base weight is frozen): the column
+    streams for the forms the kernels decode themselves, else the int8-code form (codes8=True asks
+    for the int8-code form whatever the form), and the transposed effective scale."""
 
-    def __init__(self, desc: Desc, scale_col: torch.Tensor | None = None, device="cuda", stream=None):
+    def __init__(self, desc: Desc, scale_col: torch.Tensor | None = None, device="cuda", stream=None,
+                 codes8=False):
         L = lib()
         d = Desc.from_buffer_copy(desc)
-        nbytes = L.r97q_weight_stream_bytes(C.byref(d))
+        self.rows, self.cols = int(d.rows_all), int(d.cols)
+        nbytes = self.rows * self.cols if codes8 else L.r97q_weight_stream_bytes(C.byref(d))
         if nbytes < 0:
             check(2, "r97q_weight_stream_bytes")
-        self.rows, self.cols = int(d.rows_all), int(d.cols)
-        self.stream_plane = torch.empty(nbytes // 4, dtype=torch.int32, device=device)
+        self.stream_plane = torch.empty((nbytes + 3) // 4, dtype=torch.int32, device=device)
         self.scale_t = torch.empty((self.cols // 128) * self.rows, dtype=torch.int16, device=device)
         self.w = Weight()
         self._scale_col = scale_col
-        rc = L.r97q_weight_prepare(C.byref(d), _ptr(scale_col), _ptr(self.stream_plane),
-                                   _ptr(self.scale_t), C.byref(self.w), _stream(stream))
-        check(rc, "r97q_weight_prepare")
+        entry = "r97q_weight_prepare_codes8" if codes8 else "r97q_weight_prepare"
+        rc = getattr(L, entry)(C.byref(d), _ptr(scale_col), _ptr(self.stream_plane), _ptr(self.scale_t),
+                               C.byref(self.w), _stream(stream))
+        check(rc, entry)
+
+    @classmethod
+    def from_decoded(cls, codes: torch.Tensor, scale: torch.Tensor, stream=None) -> "QWeight":
+        """The int8-code form of a decoded weight: codes int8 [N, K], scale bf16 bits (int16 or
+        uint16 storage) [N, K/128], both on the device (the reference's StoredWeight)."""
+        if codes.dtype != torch.int8 or codes.dim() != 2 or not codes.is_contiguous():
+            raise ValueError("QWeight.from_decoded: codes are a contiguous int8 [N, K] tensor")
+        N, K = codes.shape
+        if scale.element_size() != 2 or scale.numel() != N * (K // 128) or not scale.is_contiguous():
+            raise ValueError("QWeight.from_decoded: scale holds N * K/128 bf16 values")
+        self = cls.__new__(cls)
+        self.rows, self.cols = int(N), int(K)
+        self.stream_plane = torch.empty((N * K + 3) // 4, dtype=torch.int32, device=codes.device)
+        self.scale_t = torch.empty((K // 128) * N, dtype=torch.int16, device=codes.device)
+        self.w = Weight()
+        self._scale_col = None
+        check(lib().r97q_weight_from_decoded(_ptr(codes), _ptr(scale), N, K, _ptr(self.stream_plane),
+                                             _ptr(self.scale_t), C.byref(self.w), _stream(stream)),
+              "r97q_weight_from_decoded")
+        return self
+
+    @property
+    def codes8(self) -> bool:
+        return self.w.bits == 8
 
     @property
     def N(self):

@@ -166,12 +166,14 @@ def test_refusals():
     from gpu_util import device_desc
 
     keep = []
+    # forms the kernels do not decode themselves take the int8-code form (tests/test_gpu_codes8.py)
     lut = S.trellis(rows=128, cols=256, bits=5, run_rows=64, mad=0, scale_dtype=S.BF16, seed=2)
-    with pytest.raises(R97qError, match="LUT"):
-        QWeight(device_desc(lut, keep))
+    assert QWeight(device_desc(lut, keep)).codes8
     rb = S.trellis(rows=128, cols=256, bits=4, run_rows=64, rb=8, mad=1, rowf=True, seed=2)
-    with pytest.raises(R97qError, match="rb"):
-        QWeight(device_desc(rb, keep))
+    assert QWeight(device_desc(rb, keep), scale_col=torch.ones(2, device="cuda")).codes8
+    odd = S.trellis(rows=100, cols=256, bits=4, run_rows=100, mad=1, seed=2)
+    with pytest.raises(R97qError, match="multiple of 8"):
+        QWeight(device_desc(odd, keep))
     p = weight_planes(256, 256, seed=3)
     w = prepared(p, keep)
     X = torch.zeros((64, 256), dtype=torch.bfloat16, device="cuda")
