@@ -50,6 +50,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="target CPU work for the cpu_baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=2001)
+    ap.add_argument("--weight-form", default="trellis", choices=["trellis", "codes8"],
+                    help="the prepared weight the kernels read: the trellis stream (decoded inside the "
+                         "kernels), or the same weight in the int8-code form")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (3 launches), the known-size "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
@@ -89,7 +92,7 @@ def flops(T, N, K, r):
     return 4 * T * N * K + 6 * T * r * (K + N)
 
 
-def make_inputs(T, N, K, r, seed, device):
+def make_inputs(T, N, K, r, seed, device, weight_form="trellis"):
     import numpy as np
     import torch
 
@@ -105,7 +108,7 @@ def make_inputs(T, N, K, r, seed, device):
     d = device_desc(dict(codes=codes, scale=scale), N, K, dict(
         bits=5, state_bits=16, run_rows=256, rb=1, mad=1, round_mad=1, mad_a=q["mad_a"], mad_b=q["mad_b"],
         codes_row_bytes=q["codes"].shape[1], scale_dtype=0, scale_block_cols=0, scale_row_bytes=4))
-    w = QWeight(d, scale_col=col)
+    w = QWeight(d, scale_col=col, codes8=weight_form == "codes8")
     g = torch.Generator(device="cpu").manual_seed(seed + 1)
     X = torch.randn((T, K), generator=g).to(torch.bfloat16).to(device)
     dY = torch.randn((T, N), generator=g).to(torch.bfloat16).to(device)
@@ -212,7 +215,7 @@ def main():
     torch.cuda.set_device(dev)
     T, N, K, r, alpha = CONFIGS[args.config]
     s = alpha / r
-    inp = make_inputs(T, N, K, r, args.seed, dev)
+    inp = make_inputs(T, N, K, r, args.seed, dev, args.weight_form)
     w = inp["w"]
     out_dt = torch.float32 if args.out_dtype == "f32" else torch.bfloat16
     code = R97Q_F32 if args.out_dtype == "f32" else R97Q_BF16
@@ -293,7 +296,7 @@ def main():
     name = max(kern, key=lambda k: kern[k][0])
     kms, kfl = kern[name]
     achieved = kfl / (kms * 1e-3) / 1e12
-    packed_bytes = N * K * 5 // 8
+    packed_bytes = N * K if args.weight_form == "codes8" else N * K * 5 // 8
     line = {
         "metric": "qlinear+LoRA fwd+bwd TFLOP/s, % MFMA/HBM roofline; LoRA-step tokens/s",
         "value": round(value, 3),
@@ -310,8 +313,10 @@ def main():
                 "A, B ~ N(0,0.01) bf16",
         "config": {"workload": f"{args.config.upper()}: IQR linear {N}x{K} (b5 trellis.mad L16, 256-row runs, "
                                f"f32 row scale + scale.col) + LoRA r{r} alpha {alpha:g}, T={T}, fwd+bwd, "
-                               f"Y/dX {args.out_dtype}",
-                   "T": T, "N": N, "K": K, "rank": r, "alpha": alpha, "out_dtype": args.out_dtype},
+                               f"Y/dX {args.out_dtype}"
+                               + (", weight in the int8-code form" if args.weight_form == "codes8" else ""),
+                   "T": T, "N": N, "K": K, "rank": r, "alpha": alpha, "out_dtype": args.out_dtype,
+                   "weight_form": args.weight_form},
         "tokens_per_s": round(T / (ms_step * 1e-3), 1),
         "lora_step": {"tokens_per_s": round(T / (ms_lora_step * 1e-3), 1), "ms": round(ms_lora_step, 4),
                       "what": "fwd+bwd + the staged dA/dB flushed into AdamW on A, B (device, f32 masters) + their bf16 copies"},
@@ -320,7 +325,7 @@ def main():
                        "other": round(ms_step_ev - fwd_ms - dx_ms, 4), "ms_per_step_with_events": round(ms_step_ev, 4)},
         "roofline": {"bound": "mfma", "kernel": name, "achieved": round(achieved, 3),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": profiled_traffic(name, args.config),
+                     "traffic": profiled_traffic(name, args.config) if args.weight_form == "trellis" else None,
                      "packed_weight_GBs": round(packed_bytes / (kms * 1e-3) / 1e9, 2)},
         "quantizer_rel_err": round(inp["q"]["rel_err"], 4),
     }

@@ -122,7 +122,7 @@ int r97_iqr_decode(const R97IqrDecodeDesc* desc, R97IqrStream stream);
  * R97Q_CODES8): the reference's stored weight (src/stored_weight.h:24-33: int8 codes [rows, cols]
  * and a bf16 scale a (row, 128 columns)) in the fused kernels' tiled layout, the GPU-resident
  * counterpart of the reference's unit-major device form:
- *   stream  : 32-byte units of 8 rows x 4 columns, k-major inside (byte 8*c + i is row i,
+ *   stream  : 32-byte units of 8 rows x 4 columns (byte 16*(c>>1) + 2*i + (c&1) is row i,
  *             column c of the unit), ordered [rows/8][cols/4]; rows * cols bytes;
  *   scale_t : as above.
  * The fused kernels multiply code x scale, rounded once to bf16, in both forms. */

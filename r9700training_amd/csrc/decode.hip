@@ -97,13 +97,13 @@ __device__ inline int32_t rb_round(int32_t v, float ratio, int32_t mad) {
 
 // Where the decode writes. Canonical: out_codes [rows, cols] int8 row-major and out_scale
 // [rows, cols/128] bf16 (the reference's grids). TILED: the int8-code form the fused kernels read
-// (out_codes holds 32-byte units of 8 rows x 4 columns, k-major inside -- byte 8*c + i is row i,
+// (out_codes holds 32-byte units of 8 rows x 4 columns -- byte 16*(c>>1) + 2*i + (c&1) is row i,
 // column c -- ordered [rows/8][cols/4]) and the scale transposed to [cols/128][rows_all].
 template <bool TILED>
 struct DecodeOut {
     __device__ static int64_t code(const R97IqrDecodeDesc& d, int64_t q, int64_t j) {
         if (!TILED) return (q - d.row0) * d.cols + j;
-        return ((q >> 3) * (d.cols >> 2) + (j >> 2)) * 32 + 8 * (j & 3) + (q & 7);
+        return ((q >> 3) * (d.cols >> 2) + (j >> 2)) * 32 + 16 * ((j >> 1) & 1) + 2 * (q & 7) + (j & 1);
     }
     __device__ static int64_t scale(const R97IqrDecodeDesc& d, int64_t q, int64_t kb) {
         if (!TILED) return (q - d.row0) * (d.cols >> 7) + kb;
@@ -210,17 +210,18 @@ __global__ __launch_bounds__(256) void tile_codes_kernel(const int8_t* __restric
     uint32_t row[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) row[i] = *reinterpret_cast<const uint32_t*>(codes + (n8 * 8 + i) * cols + 4 * k4);
+    // byte b of the unit: column 2*(b>>4) + (b&1), row (b&15)>>1
     uint32_t out[8];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        uint32_t lo = 0, hi = 0;
+    for (int q = 0; q < 8; ++q) {
+        uint32_t v = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lo |= ((row[i] >> (8 * c)) & 0xFFu) << (8 * i);
-            hi |= ((row[i + 4] >> (8 * c)) & 0xFFu) << (8 * i);
+        for (int t = 0; t < 4; ++t) {
+            const int b = 4 * q + t;
+            const int c = 2 * (b >> 4) + (b & 1), i = (b & 15) >> 1;
+            v |= ((row[i] >> (8 * c)) & 0xFFu) << (8 * t);
         }
-        out[2 * c] = lo;
-        out[2 * c + 1] = hi;
+        out[q] = v;
     }
     uint4* dst = reinterpret_cast<uint4*>(tiled + (n8 * (cols / 4) + k4) * 32);
     dst[0] = make_uint4(out[0], out[1], out[2], out[3]);

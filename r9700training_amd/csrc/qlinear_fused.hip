@@ -174,12 +174,12 @@ __device__ __forceinline__ void slice_scales(const uint32_t* w, float (&sc)[N], 
     for (int i = 0; i < N; ++i) off[i] = -bias * sc[i];
 }
 
-// The int8-code form's words of one lane: the 32-byte unit (8 rows x 4 columns, byte 8*c + i is
-// row i of column c) of a forward lane, or the 16-byte half of one (columns 2h, 2h+1) of a dX lane,
-// and the rows' bf16 scales.
+// The int8-code form's words of one lane, 16 bytes of a 32-byte unit (8 rows x 4 columns; byte
+// 16*(c>>1) + 2*i + (c&1) is row i, column c): a forward lane's 4 rows x 4 columns (two 8-byte
+// pieces, one a column pair), a dX lane's 8 rows x one column pair; and the rows' bf16 scales.
 template <bool FWD>
 struct Codes8 {
-    uint4 c[FWD ? 2 : 1];
+    uint4 c;
     typename std::conditional<FWD, uint2, uint4>::type s;
 };
 
@@ -233,25 +233,28 @@ struct Loop {
         // where step s's weight tile comes from
         auto words_for = [&](int s, W& wd) {
             if constexpr (kCodes8) {
-                // forward: rows o0 + 32*seg + 4*WAVE .. +4 (half WAVE&1 of unit row n8), columns
-                // 4*cg.. of the step; dX: rows 64*s + 32*seg + 8*SLICE .. +8 (unit row n8), columns
-                // o0 + 2*lane, +1 (half lane&1 of unit column k4)
+                // forward: rows o0 + 32*seg + 4*WAVE .. +4 (row half WAVE&1 of the unit), columns
+                // 4*cg.. of the step; dX: rows 64*s + 32*seg + 8*SLICE .. +8, columns o0 + 2*lane,
+                // +1 (column pair lane&1 of the unit)
                 const int8_t* units = reinterpret_cast<const int8_t*>(stream);
-                int64_t srow, k4, half, kb;
+                int64_t srow, k4, kb;
                 if (FWD) {
                     srow = o0 + 32 * seg + 4 * WAVE;
                     k4 = (int64_t)s * (kStep / 4) + cg;
-                    half = 0;
                     kb = ((int64_t)s * kStep) >> 7;
                 } else {
                     srow = (int64_t)s * kStep + 32 * seg + 8 * SLICE;
                     k4 = (o0 >> 2) + (lane >> 1);
-                    half = lane & 1;
                     kb = o0 >> 7;
                 }
-                const uint4* src = reinterpret_cast<const uint4*>(units + ((srow >> 3) * (K >> 2) + k4) * 32) + half;
-                wd.c[0] = src[0];
-                if constexpr (FWD) wd.c[1] = src[1];
+                const int8_t* unit = units + ((srow >> 3) * (K >> 2) + k4) * 32;
+                if constexpr (FWD) {
+                    const uint2 p0 = *reinterpret_cast<const uint2*>(unit + 8 * (WAVE & 1));
+                    const uint2 p1 = *reinterpret_cast<const uint2*>(unit + 16 + 8 * (WAVE & 1));
+                    wd.c = make_uint4(p0.x, p0.y, p1.x, p1.y);
+                } else {
+                    wd.c = *reinterpret_cast<const uint4*>(unit + 16 * (lane & 1));
+                }
                 wd.s = *reinterpret_cast<const decltype(wd.s)*>(scale_t + kb * N + srow);
             } else {
                 int64_t g, col, kb;
@@ -274,10 +277,11 @@ struct Loop {
             // the value of the lane's row i, column c
             auto value = [&](int c, int i) -> float {
                 if constexpr (kCodes8) {
-                    // forward: dword 2c + (WAVE&1) of the unit; dX: dword 2c + i/4 of the half
-                    const int q = FWD ? 2 * c + (WAVE & 1) : 2 * c + (i >> 2);
-                    const uint32_t w = comp(wd.c[q >> 2], q & 3) ^ 0x80808080u;
-                    return code8_value(w, i & 3, sc[i], off[i]);
+                    // forward: column c, row i of the row half: byte 8*(c>>1) + 2*i + (c&1) of the
+                    // two pieces; dX: column c of the pair, row i: byte 2*i + c
+                    const int byte = FWD ? 8 * (c >> 1) + 2 * i + (c & 1) : 2 * i + c;
+                    const uint32_t w = comp(wd.c, byte >> 2) ^ 0x80808080u;
+                    return code8_value(w, byte & 3, sc[i], off[i]);
                 } else {
                     return slice_value<BITS, ROWS, COLS, SLICE>(wd, c, i, a24, b, sc[i], off[i]);
                 }

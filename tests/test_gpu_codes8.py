@@ -51,8 +51,9 @@ def prepare(p, keep, codes8=False):
 def untile(w):
     """The prepared int8-code form back in the reference's grids: codes [N, K], scale bits [N, K/128]."""
     N, K = w.rows, w.cols
-    units = w.stream_plane.cpu().numpy().view(np.int8)[: N * K].reshape(N // 8, K // 4, 4, 8)
-    codes = units.transpose(0, 3, 1, 2).reshape(N, K)
+    # unit byte 16*(c>>1) + 2*i + (c&1): [n8][k4][c>>1][i][c&1]
+    units = w.stream_plane.cpu().numpy().view(np.int8)[: N * K].reshape(N // 8, K // 4, 2, 8, 2)
+    codes = units.transpose(0, 3, 1, 2, 4).reshape(N, K)
     scale = w.scale_t.cpu().numpy().view(np.uint16).reshape(K // 128, N).T
     return codes, scale
 
