@@ -340,6 +340,43 @@ int r97q_adamw_step(const R97qAdamWConfig* cfg, const R97qAdamWParam* params, fl
 /* y = bf16(x) (RNE, NaN quieted), n elements: the kernels' bf16 operands from the f32 master weights */
 int r97q_f32_to_bf16(const float* x, uint16_t* y, int64_t n, R97IqrStream stream);
 
+/* ------------------------------------------------------------------ the vocabulary head
+ *
+ * The vocabulary head's transposed product (src/vocab_head.h:27-99, its kernels
+ * src/adjoint/device/vocab_head.hip:82-238): for classes of IQR-coded rows, each with the
+ * vocabulary ids of its rows and a per-128-column factor,
+ *   d_x[rows, n_embd] += H . sum over classes c of (dy[:, ids_c] . W_c) * scale.col_c
+ * with W_c the class's decoded int8 grid times its settled bf16 scale, H the unnormalised 128-wide
+ * Hadamard per 128 columns when transform == 128 (applied to the whole of d_x once the classes are
+ * added, as the reference does), and ids outside [vocab_offset, vocab_offset + vocab) contributing
+ * zero. The same structs as the reference's VocabHeadClass / VocabHeadPlan. */
+typedef struct {
+    int64_t rows;
+    R97IqrDecodeDesc decode;  /* the class's planes on the card; out_* unused, rows_all == rows */
+    const void* ids;          /* device int32 [rows]: each row's vocabulary id */
+    const void* scale_col;    /* device [n_embd/128] of scale_col_dtype (required, as the reference) */
+    int32_t scale_col_dtype;  /* R97IqrScaleType */
+    int64_t scale_col_row_bytes;
+} R97qVocabClass;
+typedef struct {
+    int64_t n_embd;
+    int64_t vocab;
+    int64_t vocab_offset;
+    int64_t transform; /* 128: fwht128, 0: none */
+    int32_t classes;
+    R97qVocabClass cls[4];
+} R97qVocabPlan;
+/* Workspace for a call over `rows` token rows (-1 when the plan is outside the rules). */
+int64_t r97q_vocab_head_workspace_bytes(const R97qVocabPlan* plan, int64_t rows);
+/* d_x f32 [rows, n_embd] (added to) from dy bf16 [rows, vocab]. Unlike the reference's entry it
+ * does not drain the stream: its scratch is the caller's workspace. The class weights are decoded
+ * into the workspace as the call goes (the int8-code form, a range of rows at a time), then each
+ * range runs through the fused dX kernel with the class's scale.col in its epilogue. */
+int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int64_t rows, float* d_x,
+                              void* workspace, int64_t workspace_bytes, R97IqrStream stream);
+/* dst bf16 <- src f32 (RNE, src/adjoint/device/vocab_head.hip:80-86) */
+int r97q_vocab_head_cast(uint16_t* dst, const float* src, int64_t values, R97IqrStream stream);
+
 #ifdef __cplusplus
 }
 #endif

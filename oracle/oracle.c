@@ -27,6 +27,12 @@
  *                                  <dy, twin(a)> == <adj(dy), e> for code perturbations e, scale
  *                                  held), and the a_scale cotangent is the derivative of the twin in
  *                                  the scale.
+ *   orc_vocab_class_product, orc_fwht128
+ *                                  the reference test's own known answer (tests/gpu/vocab_head.cpp:
+ *                                  a one-hot cotangent row selects one weight row, scaled by its
+ *                                  row scale and scale.col); numpy's f64 matmul over the gathered
+ *                                  columns; scipy's Sylvester Hadamard for the transform and
+ *                                  H . H = 128 I; ids outside the vocabulary contribute nothing.
  *   orc_scheduled_lr, orc_clip_global_norm, orc_adamw_step
  *                                  the reference's own Optimiser (oracle/_ref, src/optim.cpp) over
  *                                  seeded multi-step runs, bit for bit (golden vectors); the
@@ -787,4 +793,44 @@ int32_t orc_adamw_step(const OrcAdamWConfig* cfg, float* const* w, float* const*
     ++*step;
     *pending = 0;
     return 1;
+}
+
+/* ------------------------------------------------------------------ the vocabulary head */
+
+/* src/adjoint/device/vocab_head.hip:88-143 */
+void orc_vocab_class_product(int64_t rows, int64_t K, int64_t ns, int64_t vocab, int64_t vocab_offset,
+                             const uint16_t* dy, const int32_t* ids, const int8_t* codes, const uint16_t* gscale,
+                             const float* cf, double* d_x) {
+    const int64_t nkb = K / 128;
+    double* acc = (double*)calloc((size_t)K, sizeof(double));
+    for (int64_t m = 0; m < rows; ++m) {
+        memset(acc, 0, (size_t)K * sizeof(double));
+        for (int64_t n = 0; n < ns; ++n) {
+            const int64_t id = ids[n];
+            if (id < vocab_offset || id >= vocab_offset + vocab) continue;
+            const double a = (double)orc_bf16_to_f32(dy[m * vocab + (id - vocab_offset)]);
+            if (a == 0.0) continue;
+            for (int64_t kb = 0; kb < nkb; ++kb) {
+                const double ag = a * (double)orc_bf16_to_f32(gscale[n * nkb + kb]);
+                const int8_t* c = codes + n * K + kb * 128;
+                for (int j = 0; j < 128; ++j) acc[kb * 128 + j] += ag * (double)c[j];
+            }
+        }
+        for (int64_t k = 0; k < K; ++k) d_x[m * K + k] += (double)cf[k / 128] * acc[k];
+    }
+    free(acc);
+}
+
+/* src/adjoint/device/vocab_head.hip:145-163 */
+void orc_fwht128(int64_t rows, int64_t K, double* d_x) {
+    for (int64_t b = 0; b < rows * K; b += 128) {
+        double* v = d_x + b;
+        for (int h = 1; h < 128; h <<= 1)
+            for (int i = 0; i < 64; ++i) {
+                const int j = (i / h) * 2 * h + i % h;
+                const double x = v[j], y = v[j + h];
+                v[j] = x + y;
+                v[j + h] = x - y;
+            }
+    }
 }

@@ -124,6 +124,18 @@ int32_t orc_adamw_step(const OrcAdamWConfig* cfg, float* const* w, float* const*
                        float* const* acc, const int64_t* n, const int32_t* decay, int32_t count,
                        const float* const* g, int32_t* step, int32_t* pending);
 
+/* The vocabulary head's transposed product for one class (src/adjoint/device/vocab_head.hip:88-143,
+ * the gather and the GEMV; f64 here): for every token row m and column k,
+ *   d_x[m, k] += cf[k/128] * sum_n dy[m, ids[n] - vocab_offset] * gscale[n, k/128] * codes[n, k]
+ * with dy bf16 [rows, vocab], codes int8 [ns, K], gscale bf16 [ns, K/128], cf [K/128]; an id outside
+ * [vocab_offset, vocab_offset + vocab) contributes zero. */
+void orc_vocab_class_product(int64_t rows, int64_t K, int64_t ns, int64_t vocab, int64_t vocab_offset,
+                             const uint16_t* dy, const int32_t* ids, const int8_t* codes, const uint16_t* gscale,
+                             const float* cf, double* d_x);
+/* The unnormalised 128-wide Hadamard over each 128 columns of d_x [rows, K], in place
+ * (src/adjoint/device/vocab_head.hip:145-163: the seven butterfly stages, no factor). */
+void orc_fwht128(int64_t rows, int64_t K, double* d_x);
+
 #ifdef __cplusplus
 }
 #endif

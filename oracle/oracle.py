@@ -97,6 +97,8 @@ def lib():
         L.orc_clip_global_norm.argtypes = [_P, _P, C.c_int32, C.c_float]
         L.orc_adamw_step.restype = C.c_int32
         L.orc_adamw_step.argtypes = [C.POINTER(AdamWConfig), _P, _P, _P, _P, _P, _P, C.c_int32, _P, _P, _P]
+        L.orc_vocab_class_product.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]
+        L.orc_fwht128.argtypes = [_I, _I, _P]
         L.orc_rounded_bf16.restype = C.c_double
         L.orc_rounded_bf16.argtypes = [C.c_double]
         L.orc_thread_count.restype = C.c_int
@@ -462,3 +464,30 @@ def adamw_run_ref(cfg: AdamWConfig, params, grads_per_step, decay=None):
             [a.reshape(p.shape) for a, p in zip(np.split(m, split), params)],
             [a.reshape(p.shape) for a, p in zip(np.split(v, split), params)],
             [a.reshape(p.shape) for a, p in zip(np.split(acc, split), params)], (upd.value, pend.value))
+
+
+def vocab_head_transpose(dy_bits, classes, vocab_offset=0, transform=0, d_x=None):
+    """The vocabulary head's transposed product (src/adjoint/device/vocab_head.hip:169-238) in f64:
+    dy_bits uint16 bf16 bits [rows, vocab]; classes: (codes int8 [ns, K], gscale uint16 [ns, K/128],
+    ids int32 [ns], cf f32 [K/128]) each; d_x f64 [rows, K] added to (zeros when None), then the
+    unnormalised Hadamard over the whole of d_x when transform == 128."""
+    dy_bits = np.ascontiguousarray(dy_bits, np.uint16)
+    rows, vocab = dy_bits.shape
+    K = classes[0][0].shape[1]
+    out = np.zeros((rows, K)) if d_x is None else np.array(d_x, np.float64, copy=True, order="C")
+    for codes, gscale, ids, cf in classes:
+        codes = np.ascontiguousarray(codes, np.int8)
+        lib().orc_vocab_class_product(rows, K, codes.shape[0], vocab, vocab_offset, _ptr(dy_bits),
+                                      _ptr(np.ascontiguousarray(ids, np.int32)), _ptr(codes),
+                                      _ptr(np.ascontiguousarray(gscale, np.uint16)),
+                                      _ptr(np.ascontiguousarray(cf, np.float32)), _ptr(out))
+    if transform == 128:
+        lib().orc_fwht128(rows, K, _ptr(out))
+    return out
+
+
+def fwht128(x):
+    """The unnormalised 128-wide Hadamard over each 128 values of the rows of x (f64 copy)."""
+    out = np.array(x, np.float64, copy=True, order="C")
+    lib().orc_fwht128(out.shape[0], out.shape[1], _ptr(out))
+    return out

@@ -65,6 +65,20 @@ class AdamWParam(C.Structure):
                 ("w_bf16", C.c_void_p), ("n", C.c_int64), ("decay", C.c_int32)]
 
 
+class VocabClass(C.Structure):
+    """R97qVocabClass (include/r97q.h): the reference's VocabHeadClass (src/vocab_head.h:27-40)."""
+
+    _fields_ = [("rows", C.c_int64), ("decode", Desc), ("ids", C.c_void_p), ("scale_col", C.c_void_p),
+                ("scale_col_dtype", C.c_int32), ("scale_col_row_bytes", C.c_int64)]
+
+
+class VocabPlan(C.Structure):
+    """R97qVocabPlan (include/r97q.h): the reference's VocabHeadPlan (src/vocab_head.h:42-50)."""
+
+    _fields_ = [("n_embd", C.c_int64), ("vocab", C.c_int64), ("vocab_offset", C.c_int64),
+                ("transform", C.c_int64), ("classes", C.c_int32), ("cls", VocabClass * 4)]
+
+
 # every symbol include/r97q.h declares, with its ctypes signature
 _P, _I, _i = C.c_void_p, C.c_int64, C.c_int32
 SIGNATURES = {
@@ -99,6 +113,9 @@ SIGNATURES = {
     "r97q_adamw_step": (C.c_int, [C.POINTER(AdamWConfig), C.POINTER(AdamWParam), C.POINTER(C.c_void_p), _i, _i,
                                   C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.POINTER(C.c_int32), _P, _I, _P]),
     "r97q_f32_to_bf16": (C.c_int, [_P, _P, _I, _P]),
+    "r97q_vocab_head_workspace_bytes": (_I, [C.POINTER(VocabPlan), _I]),
+    "r97q_vocab_head_transpose": (C.c_int, [C.POINTER(VocabPlan), _P, _I, _P, _P, _I, _P]),
+    "r97q_vocab_head_cast": (C.c_int, [_P, _P, _I, _P]),
 }
 
 _lib = None

@@ -95,19 +95,22 @@ __device__ inline int32_t rb_round(int32_t v, float ratio, int32_t mad) {
     return (int32_t)__builtin_rintf((float)v * ratio);
 }
 
-// Where the decode writes. Canonical: out_codes [rows, cols] int8 row-major and out_scale
-// [rows, cols/128] bf16 (the reference's grids). TILED: the int8-code form the fused kernels read
-// (out_codes holds 32-byte units of 8 rows x 4 columns -- byte 16*(c>>1) + 2*i + (c&1) is row i,
-// column c -- ordered [rows/8][cols/4]) and the scale transposed to [cols/128][rows_all].
+// Where the decode writes (rows counted from the description's row0). Canonical: out_codes
+// [rows, cols] int8 row-major and out_scale [rows, cols/128] bf16 (the reference's grids). TILED:
+// the int8-code form the fused kernels read (out_codes holds 32-byte units of 8 rows x 4 columns
+// -- byte 16*(c>>1) + 2*i + (c&1) is row i, column c -- ordered [rows/8][cols/4]) and the scale
+// transposed to [cols/128][ld] (ld >= rows).
 template <bool TILED>
 struct DecodeOut {
     __device__ static int64_t code(const R97IqrDecodeDesc& d, int64_t q, int64_t j) {
-        if (!TILED) return (q - d.row0) * d.cols + j;
+        q -= d.row0;
+        if (!TILED) return q * d.cols + j;
         return ((q >> 3) * (d.cols >> 2) + (j >> 2)) * 32 + 16 * ((j >> 1) & 1) + 2 * (q & 7) + (j & 1);
     }
-    __device__ static int64_t scale(const R97IqrDecodeDesc& d, int64_t q, int64_t kb) {
-        if (!TILED) return (q - d.row0) * (d.cols >> 7) + kb;
-        return kb * d.rows_all + q;
+    __device__ static int64_t scale(const R97IqrDecodeDesc& d, int64_t q, int64_t kb, int64_t ld) {
+        q -= d.row0;
+        if (!TILED) return q * (d.cols >> 7) + kb;
+        return kb * ld + q;
     }
 };
 
@@ -115,7 +118,7 @@ struct DecodeOut {
 template <bool TILED>
 __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDecodeDesc d,
                                                                 int64_t chunk_rows,
-                                                                int64_t chunks) {
+                                                                int64_t chunks, int64_t scale_ld) {
     using O = DecodeOut<TILED>;
     const int64_t j = (int64_t)blockIdx.x * kDecodeThreads + threadIdx.x;
     const int64_t ch = blockIdx.y + (int64_t)blockIdx.z * gridDim.y;
@@ -137,7 +140,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
             const int64_t gb = bc == d.cols ? 0 : (kb * 128) / bc;
             const uint32_t zero = load_bits(d.zero + (q - d.row0) * d.zero_row_bytes, d.zero_bits, gb);
             d.out_codes[O::code(d, q, j)] = (int8_t)((int32_t)code - (int32_t)zero);
-            if (first) d.out_scale[O::scale(d, q, kb)] = f32_to_bf16(block_scale(d, q, kb));
+            if (first) d.out_scale[O::scale(d, q, kb, scale_ld)] = f32_to_bf16(block_scale(d, q, kb));
         }
         return;
     }
@@ -172,7 +175,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
             out = v;
         }
         d.out_codes[O::code(d, q, j)] = (int8_t)out;
-        if (first) d.out_scale[O::scale(d, q, kb)] = f32_to_bf16(sc);
+        if (first) d.out_scale[O::scale(d, q, kb, scale_ld)] = f32_to_bf16(sc);
     }
 }
 
@@ -257,14 +260,21 @@ __global__ __launch_bounds__(256) void prepare_scale_kernel(const R97IqrDecodeDe
 }  // namespace
 
 template <bool TILED>
-void launch_decode(const R97IqrDecodeDesc& d, hipStream_t s) {
+void launch_decode(const R97IqrDecodeDesc& d, hipStream_t s, int64_t scale_ld = 0) {
     const int64_t chunk_rows = (d.run_rows % 8 == 0) ? 8 : 1;
     // chunks never straddle a run: runs start at multiples of run_rows and chunk_rows divides it
     const int64_t chunks = (d.rows + chunk_rows - 1) / chunk_rows;
     const int64_t gy = chunks < 65535 ? chunks : 65535;
     const int64_t gz = (chunks + gy - 1) / gy;
     dim3 grid((unsigned)((d.cols + kDecodeThreads - 1) / kDecodeThreads), (unsigned)gy, (unsigned)gz);
-    hipLaunchKernelGGL(decode_kernel<TILED>, grid, dim3(kDecodeThreads), 0, s, d, chunk_rows, chunks);
+    hipLaunchKernelGGL(decode_kernel<TILED>, grid, dim3(kDecodeThreads), 0, s, d, chunk_rows, chunks, scale_ld);
+}
+
+// The rows [row0, row0 + rows) of a valid description, decoded into the int8-code form at
+// d.out_codes / d.out_scale (row row0 first; the scale with leading dimension scale_ld).
+int decode_tiled(const R97IqrDecodeDesc& d, int64_t scale_ld, hipStream_t s) {
+    launch_decode<true>(d, s, scale_ld);
+    return launch_status("decode_kernel (int8-code form)");
 }
 
 // Whether `d` is a form the fused kernels serve; the reason goes to the error message.
@@ -433,7 +443,7 @@ int r97q_weight_prepare_codes8(const R97IqrDecodeDesc* desc, const float* scale_
     if (!codes8_form(d, scale_col)) return R97Q_EUNSUPPORTED;
     const hipStream_t s = (hipStream_t)stream;
     // the decode writes the codes in the tiled form and the scale transposed
-    launch_decode<true>(d, s);
+    launch_decode<true>(d, s, d.rows_all);
     if (int e = launch_status("decode_kernel (int8-code form)")) return e;
     if (scale_col) {
         // src/iqr_form.h:203-216: the scale.col fold replaces the decoded scale

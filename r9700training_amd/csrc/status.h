@@ -23,4 +23,11 @@ inline int hip_status(hipError_t e, const char* what) {
 // The launch just issued on this thread: hipGetLastError after a <<<>>> launch.
 inline int launch_status(const char* kernel) { return hip_status(hipGetLastError(), kernel); }
 
+// The description's rules (src/iqr_decode.h:321-349): 0 when valid.
+int32_t validate(const R97IqrDecodeDesc& d);
+
+// Rows [d.row0, d.row0 + d.rows) of a valid description decoded into the int8-code form at
+// d.out_codes (units from row row0) and d.out_scale ([cols/128][scale_ld]) (decode.hip).
+int decode_tiled(const R97IqrDecodeDesc& d, int64_t scale_ld, hipStream_t s);
+
 }  // namespace r97q

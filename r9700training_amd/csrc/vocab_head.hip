@@ -1,0 +1,249 @@
+// vocab_head.hip -- the vocabulary head's transposed product on gfx950 (the reference's
+// src/vocab_head.h:27-99 contract, its kernels src/adjoint/device/vocab_head.hip:82-238):
+//
+//   d_x[rows, n_embd] += H . sum over classes c of (dy[:, ids_c] . W_c) * scale.col_c
+//
+// The reference runs it as a gather, a per-token-row GEMV over the decoded int8 grid with f32
+// fmas, and the un-rotation. Here it is the fused dX kernel's product: per class, a range of its
+// rows is decoded into the int8-code form in the workspace (the standalone decode's kernel writing
+// tiled), the cotangent's columns for those rows are gathered into a bf16 [rows, range] operand,
+// and qlinear_dx_kernel<R97Q_CODES8> adds (gathered . W) * scale.col into d_x with bf16 MFMA,
+// the class's scale.col applied in its epilogue (one factor a 128-column tile). Ranges are padded
+// to 128 rows with zero codes, zero scales and zero cotangent columns. Once every class is in,
+// the unnormalised 128-wide Hadamard runs over each 128 columns of d_x.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/r97q.h"
+#include "iqr_device.h"
+#include "qlinear_fused.h"
+#include "status.h"
+
+namespace r97q {
+namespace {
+
+constexpr int64_t kRangeRows = 16384;  // rows of a class decoded at once (whole trellis runs)
+
+int64_t round_up(int64_t n, int64_t m) { return (n + m - 1) / m * m; }
+
+// the rows one range takes: whole runs (the decode's rule for a row range), about kRangeRows
+int64_t range_rows(const R97qVocabClass& c) {
+    const int64_t run = c.decode.affine ? 1 : (c.decode.run_rows > 0 ? c.decode.run_rows : 1);
+    int64_t r = kRangeRows / run * run;
+    if (r < run) r = run;
+    return r < c.rows ? r : c.rows;
+}
+
+struct VocabWs {
+    int64_t codes, scale, gather, cf, total;
+};
+
+VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
+    int64_t S = 0;
+    for (int c = 0; c < plan.classes; ++c) {
+        const int64_t s = round_up(range_rows(plan.cls[c]), 128);
+        S = s > S ? s : S;
+    }
+    const int64_t nkb = plan.n_embd / 128;
+    VocabWs w{};
+    int64_t off = 0;
+    auto take = [&](int64_t bytes) {
+        const int64_t at = off;
+        off += round_up(bytes, 256);
+        return at;
+    };
+    w.codes = take(S * plan.n_embd);
+    w.scale = take(nkb * S * 2);
+    w.gather = take(rows * S * 2);
+    w.cf = take(nkb * 4);
+    w.total = off;
+    return w;
+}
+
+// the padding rows [ns, ns_pad) of a range: zero codes (from the unit row that holds row ns on) and
+// zero scales
+__global__ __launch_bounds__(256) void vocab_pad_kernel(int8_t* __restrict__ codes, uint16_t* __restrict__ scale_t,
+                                                        int64_t ns, int64_t ns_pad, int64_t K) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t c0 = (ns / 8) * (K / 4) * 32 / 4, c1 = ns_pad * K / 4;  // in dwords
+    if (c0 + i < c1) reinterpret_cast<uint32_t*>(codes)[c0 + i] = 0u;
+    const int64_t pad = ns_pad - ns, nkb = K / 128;
+    if (i < pad * nkb) scale_t[(i / pad) * ns_pad + ns + i % pad] = 0;
+}
+
+// a[m, n] = dy[m, ids[n] - vocab_offset] for n < ns and an id inside this vocabulary, else 0
+__global__ __launch_bounds__(256) void vocab_gather_kernel(const uint16_t* __restrict__ dy,
+                                                           const int32_t* __restrict__ ids,
+                                                           uint16_t* __restrict__ a, int64_t rows, int64_t vocab,
+                                                           int64_t vocab_offset, int64_t ns, int64_t ns_pad) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * ns_pad) return;
+    const int64_t m = i / ns_pad, n = i - m * ns_pad;
+    uint16_t v = 0;
+    if (n < ns) {
+        const int64_t id = ids[n];
+        if (id >= vocab_offset && id < vocab_offset + vocab) v = dy[m * vocab + (id - vocab_offset)];
+    }
+    a[i] = v;
+}
+
+__global__ __launch_bounds__(64) void vocab_cf_kernel(const uint8_t* __restrict__ cf, int32_t dtype, int64_t nkb,
+                                                      float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (i < nkb) out[i] = load_scalar(cf, dtype, i);
+}
+
+// The unnormalised Hadamard of one 128-column block of one row, in place: the seven butterfly
+// stages (pairs j, j + h for h = 1, 2, .., 64; sum in j, difference in j + h) -- the natural-order
+// Sylvester matrix, as src/adjoint/device/vocab_head.hip:145-163 applies it.
+__global__ __launch_bounds__(128) void vocab_unrotate_kernel(float* __restrict__ d_x, int64_t K) {
+    __shared__ float v[128];
+    const int t = threadIdx.x;
+    float* p = d_x + (int64_t)blockIdx.x * K + (int64_t)blockIdx.y * 128;
+    v[t] = p[t];
+    __syncthreads();
+    for (int h = 1; h < 128; h <<= 1) {
+        if (t < 64) {
+            const int j = (t / h) * 2 * h + t % h;
+            const float a = v[j], b = v[j + h];
+            v[j] = a + b;
+            v[j + h] = a - b;
+        }
+        __syncthreads();
+    }
+    p[t] = v[t];
+}
+
+__global__ __launch_bounds__(256) void vocab_cast_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
+                                                         int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = f32_to_bf16(src[i]);
+}
+
+unsigned blocks(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+// the reference's rules for the plan and the buffers (src/adjoint/device/vocab_head.hip:170-211)
+bool plan_ok(const R97qVocabPlan* plan, int64_t rows, const char* who) {
+    if (!plan || rows <= 0 || plan->classes <= 0 || plan->classes > 4 || plan->n_embd <= 0 ||
+        plan->n_embd % 128 != 0 || plan->vocab <= 0 || plan->vocab_offset < 0 ||
+        (plan->transform != 0 && plan->transform != 128)) {
+        set_error("%s: the plan or the buffers are outside the kernel's rules", who);
+        return false;
+    }
+    for (int c = 0; c < plan->classes; ++c) {
+        const R97qVocabClass& k = plan->cls[c];
+        if (k.rows <= 0 || !k.ids || !k.scale_col || k.decode.rows_all != k.rows || k.decode.cols != plan->n_embd) {
+            set_error("%s: the plan's class %d is incomplete", who, c);
+            return false;
+        }
+    }
+    return true;
+}
+
+}  // namespace
+}  // namespace r97q
+
+using namespace r97q;
+
+extern "C" {
+
+int64_t r97q_vocab_head_workspace_bytes(const R97qVocabPlan* plan, int64_t rows) {
+    clear_error();
+    if (!plan_ok(plan, rows, "r97q_vocab_head_workspace_bytes")) return -1;
+    return vocab_ws(*plan, rows).total;
+}
+
+int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int64_t rows, float* d_x,
+                              void* workspace, int64_t workspace_bytes, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_vocab_head_transpose";
+    if (!dy || !d_x) {
+        set_error("%s: the plan or the buffers are outside the kernel's rules", who);
+        return R97Q_EINVAL;
+    }
+    if (!plan_ok(plan, rows, who)) return R97Q_EINVAL;
+    const VocabWs ws = vocab_ws(*plan, rows);
+    if (!workspace || workspace_bytes < ws.total) {
+        set_error("%s: workspace %lld bytes, needs %lld", who, (long long)workspace_bytes, (long long)ws.total);
+        return R97Q_EWORKSPACE;
+    }
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    int8_t* codes = reinterpret_cast<int8_t*>(wsb + ws.codes);
+    uint16_t* scale_t = reinterpret_cast<uint16_t*>(wsb + ws.scale);
+    uint16_t* gathered = reinterpret_cast<uint16_t*>(wsb + ws.gather);
+    float* cf = reinterpret_cast<float*>(wsb + ws.cf);
+    const hipStream_t s = (hipStream_t)stream;
+    const int64_t K = plan->n_embd, nkb = K / 128;
+
+    for (int c = 0; c < plan->classes; ++c) {
+        const R97qVocabClass& cls = plan->cls[c];
+        hipLaunchKernelGGL(vocab_cf_kernel, dim3(blocks(nkb, 64)), dim3(64), 0, s,
+                           static_cast<const uint8_t*>(cls.scale_col), cls.scale_col_dtype, nkb, cf);
+        if (int e = launch_status("vocab_cf_kernel")) return e;
+        const int64_t R = range_rows(cls);
+        for (int64_t r0 = 0; r0 < cls.rows; r0 += R) {
+            const int64_t ns = R < cls.rows - r0 ? R : cls.rows - r0;
+            const int64_t ns_pad = round_up(ns, 128);
+            R97IqrDecodeDesc d = cls.decode;
+            d.row0 = r0;
+            d.rows = ns;
+            d.codes = d.codes + r0 * d.codes_row_bytes;
+            d.scale = d.scale + r0 * d.scale_row_bytes;
+            d.zero = d.zero ? d.zero + r0 * d.zero_row_bytes : nullptr;
+            d.out_codes = codes;
+            d.out_scale = scale_t;
+            if (validate(d)) {
+                set_error("%s: the plan's class %d decode is outside the kernel's rules", who, c);
+                return R97Q_EINVAL;
+            }
+            if (ns_pad != ns) {
+                const int64_t n = ns_pad * K / 4 - (ns / 8) * (K / 4) * 8;
+                const int64_t m = (ns_pad - ns) * nkb;
+                hipLaunchKernelGGL(vocab_pad_kernel, dim3(blocks(n > m ? n : m, 256)), dim3(256), 0, s, codes,
+                                   scale_t, ns, ns_pad, K);
+                if (int e = launch_status("vocab_pad_kernel")) return e;
+            }
+            if (int e = decode_tiled(d, ns_pad, s)) return e;
+            hipLaunchKernelGGL(vocab_gather_kernel, dim3(blocks(rows * ns_pad, 256)), dim3(256), 0, s, dy,
+                               static_cast<const int32_t*>(cls.ids) + r0, gathered, rows, plan->vocab,
+                               plan->vocab_offset, ns, ns_pad);
+            if (int e = launch_status("vocab_gather_kernel")) return e;
+            DxParams p{};
+            p.dY = gathered;
+            p.T = rows;
+            p.N = ns_pad;
+            p.K = K;
+            p.stream = reinterpret_cast<const uint32_t*>(codes);
+            p.scale_t = scale_t;
+            p.rank = 0;
+            p.dX = d_x;
+            p.dx_f32 = 1;
+            p.accumulate = 1;
+            p.a_scale = cf;  // one factor a 128-column tile: every row reads cf[kt]
+            p.a_scale_ld = 0;
+            p.mtiles = (int)((rows + kBM - 1) / kBM);
+            p.ktiles = (int)(K / kBN);
+            launch_dx<R97Q_CODES8>(p, s);
+            if (int e = launch_status("qlinear_dx_kernel (vocab head)")) return e;
+        }
+    }
+    if (plan->transform == 128) {
+        hipLaunchKernelGGL(vocab_unrotate_kernel, dim3((unsigned)rows, (unsigned)nkb), dim3(128), 0, s, d_x, K);
+        if (int e = launch_status("vocab_unrotate_kernel")) return e;
+    }
+    return R97Q_OK;
+}
+
+int r97q_vocab_head_cast(uint16_t* dst, const float* src, int64_t values, R97IqrStream stream) {
+    clear_error();
+    if (!dst || !src || values <= 0) {
+        set_error("r97q_vocab_head_cast: null buffer or no values");
+        return R97Q_EINVAL;
+    }
+    hipLaunchKernelGGL(vocab_cast_kernel, dim3(blocks(values, 256)), dim3(256), 0, (hipStream_t)stream, src, dst,
+                       values);
+    return launch_status("vocab_cast_kernel");
+}
+
+}  // extern "C"

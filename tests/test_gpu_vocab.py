@@ -1,0 +1,161 @@
+"""The vocabulary head's transposed product on the card (r97q_vocab_head_transpose) against the
+oracle's restatement of the reference's kernels (src/adjoint/device/vocab_head.hip:88-163, pinned in
+tests/test_oracle.py), with the reference test's own checks (tests/gpu/vocab_head.cpp): a one-hot
+cotangent row per class selects one weight row; chunking the token rows is additive; the cast
+rounds like f32 -> bf16.
+
+Bar: d_x within relative L2 2e-3 of the f64 restatement (the class weight enters the MFMA as
+bf16(code * scale), one rounding of each weight, as in the base products)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import iqr_synth as S
+from gpu_util import device_desc, dev, rel_l2
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+FORMS = {
+    "trunk-b5": dict(bits=5, state_bits=16, run_rows=256, rb=1, mad=1, scale_dtype=S.F32, rowf=True),
+    "stored-u4": dict(bits=4, state_bits=16, run_rows=128, rb=1, mad=0, scale_dtype=S.BF16, rowf=False),
+    "embedding": dict(bits=4, state_bits=12, run_rows=256, rb=1, mad=0, scale_dtype=S.E4M3, rowf=False, second=True),
+}
+
+
+def make_class(rng, form, rows, K, ids, keep, seed):
+    """A class: its planes on the card (the decode description), ids, scale.col; and the oracle's
+    view of it (decoded codes, the settled bf16 scale, ids, scale.col)."""
+    cf = (0.5 + rng.random(K // 128)).astype(np.float32)
+    p = S.trellis(rows=rows, cols=K, seed=seed, **FORMS[form])
+    p.scale_col = None  # the head multiplies its scale.col after the product; the decode does not fold it
+    d = device_desc(p, keep)
+    codes, gscale = O.decode(p.desc())
+    ids_d, cf_d = dev(ids.astype(np.int32)), dev(cf)
+    keep += [ids_d, cf_d]
+    return (d, ids_d, cf_d), (codes, gscale.astype(np.uint16), ids.astype(np.int32), cf)
+
+
+def head_and_oracle(rng, K, sizes, forms, vocab_offset=0, stray=0, transform=128):
+    from r9700training_amd.vocab_head import VocabHead
+
+    vocab = sum(sizes)
+    perm = rng.permutation(vocab) + vocab_offset
+    keep, dev_cls, orc_cls, at = [], [], [], 0
+    for i, (n, form) in enumerate(zip(sizes, forms)):
+        ids = perm[at:at + n].copy()
+        at += n
+        if stray:
+            ids[:stray] = vocab_offset + vocab + rng.integers(0, 9, stray)
+        dc, oc = make_class(rng, form, n, K, ids, keep, seed=100 + i)
+        dev_cls.append(dc)
+        orc_cls.append(oc)
+    head = VocabHead(K, vocab, dev_cls, vocab_offset=vocab_offset, transform=transform)
+    head._keep += keep
+    return head, orc_cls, vocab
+
+
+@pytest.mark.parametrize("rows,K,sizes,forms,offset,transform", [
+    (37, 256, [1000, 700], ["trunk-b5", "stored-u4"], 0, 128),
+    (300, 512, [1500, 333, 900], ["trunk-b5", "embedding", "trunk-b5"], 4096, 128),
+    (600, 384, [2048], ["trunk-b5"], 0, 0),
+])
+def test_vocab_head_matches_oracle(rows, K, sizes, forms, offset, transform):
+    print(f"case vocab head rows={rows} K={K} sizes={sizes} forms={forms} offset={offset} transform={transform}",
+          flush=True)
+    rng = np.random.default_rng(rows + K)
+    head, orc_cls, vocab = head_and_oracle(rng, K, sizes, forms, offset, stray=5, transform=transform)
+    dy = S.f32_to_bf16_bits(rng.standard_normal((rows, vocab)).astype(np.float32))
+    d0 = rng.standard_normal((rows, K)).astype(np.float32)
+    d_x = torch.tensor(d0, device="cuda")
+    head.transpose(torch.from_numpy(dy.view(np.int16)).cuda().view(torch.bfloat16), d_x)
+    torch.cuda.synchronize()
+    want = O.vocab_head_transpose(dy, orc_cls, vocab_offset=offset, transform=transform, d_x=d0)
+    base = O.fwht128(d0) if transform else d0.astype(np.float64)
+    e = rel_l2(d_x.cpu().numpy() - base, want - base)
+    print(f"  rel L2 {e:.3e}", flush=True)
+    assert e <= TOL
+
+
+def test_vocab_head_ranges_and_padding():
+    """A class past one decode range (16384 rows) and a short last range padded to 128 rows."""
+    print("case vocab head ranges", flush=True)
+    rng = np.random.default_rng(4)
+    rows, K = 64, 128
+    head, orc_cls, vocab = head_and_oracle(rng, K, [20000 + 77], ["trunk-b5"], transform=0)
+    dy = S.f32_to_bf16_bits(rng.standard_normal((rows, vocab)).astype(np.float32))
+    d_x = torch.zeros((rows, K), device="cuda")
+    head.transpose(torch.from_numpy(dy.view(np.int16)).cuda().view(torch.bfloat16), d_x)
+    torch.cuda.synchronize()
+    want = O.vocab_head_transpose(dy, orc_cls)
+    e = rel_l2(d_x.cpu().numpy(), want)
+    print(f"  rel L2 {e:.3e}", flush=True)
+    assert e <= TOL
+
+
+def test_vocab_head_one_hot_and_chunking():
+    """The reference test's checks: one-hot rows against the class rows they select (row scale,
+    scale.col, then the transform); the same rows in two calls equal one call."""
+    print("case vocab head one-hot", flush=True)
+    rng = np.random.default_rng(8)
+    K, rows = 256, 8
+    head, orc_cls, vocab = head_and_oracle(rng, K, [768, 512], ["trunk-b5", "trunk-b5"], transform=128)
+    dy = np.zeros((rows, vocab), np.uint16)
+    want = np.zeros((rows, K))
+    for m in range(rows):
+        for c, (codes, gscale, ids, cf) in enumerate(orc_cls):
+            r = 32 * c + 8 * m + 1
+            dy[m, ids[r]] = 0x3F80
+            want[m] += (codes[r].astype(np.float64) * np.repeat(S.bf16_bits_to_f32(gscale[r]).astype(np.float64), 128)
+                        * np.repeat(cf.astype(np.float64), 128))
+    want = O.fwht128(want)
+    dyt = torch.from_numpy(dy.view(np.int16)).cuda().view(torch.bfloat16)
+    one = torch.zeros((rows, K), device="cuda")
+    head.transpose(dyt, one)
+    two = torch.zeros((rows, K), device="cuda")
+    head.transpose(dyt[:3].contiguous(), two[:3])
+    rest = torch.zeros((rows - 3, K), device="cuda")
+    head.transpose(dyt[3:].contiguous(), rest)
+    torch.cuda.synchronize()
+    two[3:] = rest
+    got = one.cpu().numpy()
+    e = rel_l2(got, want)
+    print(f"  one-hot rel L2 {e:.3e}", flush=True)
+    assert e <= TOL
+    assert torch.equal(one, two)
+    assert rel_l2(got, 2 * want) > 0.3  # teeth: a doubled transform misses
+
+
+def test_vocab_head_cast():
+    from r9700training_amd.vocab_head import cast
+
+    x = torch.randn(5000, device="cuda") * 100
+    x[:4] = torch.tensor([0.0, -0.0, 1.0 / 16384.0, float("nan")], device="cuda")
+    y = cast(x)
+    torch.cuda.synchronize()
+    want = x.cpu().to(torch.bfloat16)
+    assert torch.equal(y.cpu()[4:].view(torch.int16), want[4:].view(torch.int16))
+    assert torch.equal(y.cpu()[:3].view(torch.int16), want[:3].view(torch.int16)) and torch.isnan(y.cpu()[3])
+
+
+def test_vocab_head_refusals():
+    from r9700training_amd import R97qError, VocabPlan, lib
+
+    rng = np.random.default_rng(1)
+    head, _, vocab = head_and_oracle(rng, 128, [256], ["trunk-b5"])
+    L = lib()
+    bad = VocabPlan.from_buffer_copy(head.plan)
+    bad.cls[0].scale_col = None
+    assert L.r97q_vocab_head_workspace_bytes(C.byref(bad), 4) == -1
+    assert b"incomplete" in L.r97q_last_error()
+    bad = VocabPlan.from_buffer_copy(head.plan)
+    bad.transform = 64
+    assert L.r97q_vocab_head_workspace_bytes(C.byref(bad), 4) == -1
+    dy = torch.zeros((4, vocab), dtype=torch.bfloat16, device="cuda")
+    d_x = torch.zeros((4, 128), device="cuda")
+    with pytest.raises(R97qError, match="workspace"):
+        head.transpose(dy, d_x, workspace=torch.empty(16, dtype=torch.uint8, device="cuda"))

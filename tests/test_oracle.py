@@ -540,3 +540,83 @@ def test_adamw_golden_and_f64_restatement():
             w[i] = w[i] - 1e-3 * (mh / (np.sqrt(vh) + 1e-8))
     for i in range(3):
         assert np.max(np.abs(w[i] - z[f"plain_w{i}"])) < 1e-6
+
+
+# ---------------------------------------------------------------- the vocabulary head
+def _vocab_classes(rng, K, sizes, vocab, offset, stray=0):
+    """Classes of random int8 rows with bf16 row scales, ids a shuffle of this rank's vocabulary
+    (plus `stray` ids outside it), and a scale.col each."""
+    ids_all = rng.permutation(vocab) + offset
+    out, at = [], 0
+    for n in sizes:
+        ids = ids_all[at:at + n].astype(np.int32)
+        at += n
+        if stray:
+            ids[:stray] = offset + vocab + rng.integers(0, 50, stray)  # past the vocabulary
+            ids[stray:2 * stray] = offset - 1 - rng.integers(0, max(offset, 1), stray)  # before it
+        codes = rng.integers(-127, 128, (n, K)).astype(np.int8)
+        gscale = S.f32_to_bf16_bits((0.001 + 0.01 * rng.random((n, 1))).astype(np.float32)).repeat(K // 128, 1)
+        cf = (0.5 + rng.random(K // 128)).astype(np.float32)
+        out.append((codes, gscale.astype(np.uint16), ids, cf))
+    return out
+
+
+def test_fwht128_is_the_sylvester_hadamard():
+    import scipy.linalg
+
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 384))
+    H = scipy.linalg.hadamard(128).astype(np.float64)
+    want = np.concatenate([x[:, b:b + 128] @ H.T for b in range(0, 384, 128)], axis=1)
+    assert np.allclose(O.fwht128(x), want, rtol=0, atol=1e-12)
+    assert np.allclose(O.fwht128(O.fwht128(x)), 128 * x, rtol=0, atol=1e-10)
+
+
+def test_vocab_head_one_hot_known_answer():
+    """The reference test's check (tests/gpu/vocab_head.cpp): a one-hot cotangent row per class
+    selects that class's weight row, scaled by its row scale and the class's scale.col; the transform
+    follows."""
+    rng = np.random.default_rng(5)
+    K, vocab, rows = 256, 900, 4
+    cls = _vocab_classes(rng, K, [300, 400, 200], vocab, 0)
+    dy = np.zeros((rows, vocab), np.uint16)
+    picks = []
+    for m in range(rows):
+        for c, (codes, gscale, ids, cf) in enumerate(cls):
+            r = 17 * m + 5 * c + 3
+            dy[m, ids[r]] = 0x3F80  # 1.0
+            picks.append((m, c, r))
+    want = np.zeros((rows, K))
+    for m, c, r in picks:
+        codes, gscale, ids, cf = cls[c]
+        want[m] += (codes[r].astype(np.float64) * S.bf16_bits_to_f32(gscale[r]).astype(np.float64).repeat(128)
+                    * np.repeat(cf.astype(np.float64), 128))
+    for transform in (0, 128):
+        got = O.vocab_head_transpose(dy, cls, transform=transform)
+        ref = want if transform == 0 else O.fwht128(want)
+        assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    # teeth: the scale.col dropped, the transform doubled
+    no_cf = [(c, g, i, np.ones_like(f)) for c, g, i, f in cls]
+    assert not np.allclose(O.vocab_head_transpose(dy, no_cf, transform=128), O.fwht128(want))
+    assert not np.allclose(O.vocab_head_transpose(dy, cls, transform=128), 2 * O.fwht128(want))
+
+
+def test_vocab_head_matches_matmul_and_ignores_stray_ids():
+    rng = np.random.default_rng(9)
+    K, vocab, offset, rows = 384, 1500, 700, 9
+    cls = _vocab_classes(rng, K, [500, 600, 300], vocab, offset, stray=6)
+    dy = S.f32_to_bf16_bits(rng.standard_normal((rows, vocab)).astype(np.float32))
+    d0 = rng.standard_normal((rows, K))
+    want = d0.copy()
+    dyf = S.bf16_bits_to_f32(dy).astype(np.float64)
+    for codes, gscale, ids, cf in cls:
+        inside = (ids >= offset) & (ids < offset + vocab)
+        g = np.zeros((rows, len(ids)))
+        g[:, inside] = dyf[:, ids[inside] - offset]
+        W = codes.astype(np.float64) * np.repeat(S.bf16_bits_to_f32(gscale).astype(np.float64), 128, axis=1)
+        want += (g @ W) * np.repeat(cf.astype(np.float64), 128)
+    got = O.vocab_head_transpose(dy, cls, vocab_offset=offset, d_x=d0)
+    assert np.allclose(got, want, rtol=1e-10, atol=1e-9)
+    # the transform runs over the whole of d_x once the classes are in
+    got_t = O.vocab_head_transpose(dy, cls, vocab_offset=offset, transform=128, d_x=d0)
+    assert np.allclose(got_t, O.fwht128(want), rtol=1e-10, atol=1e-8)
