@@ -53,6 +53,10 @@ def parse():
     ap.add_argument("--weight-form", default="trellis", choices=["trellis", "codes8"],
                     help="the prepared weight the kernels read: the trellis stream (decoded inside the "
                          "kernels), or the same weight in the int8-code form")
+    ap.add_argument("--workload", default="qlinear", choices=["qlinear", "vocab_head"],
+                    help="qlinear: the C2 fwd+bwd step (the headline); vocab_head: the vocabulary head's "
+                         "transposed product at a 248320-row head, n_embd 2048, --vocab-rows token rows")
+    ap.add_argument("--vocab-rows", type=int, default=4096)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (3 launches), the known-size "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
@@ -187,6 +191,67 @@ def cpu_baseline(inp, T, N, K, r, s, target_s):
     }
 
 
+VOCAB_CLASSES = [32768, 65536, 98304, 51712]  # rows a class (one trellis width each): 248320 in all
+VOCAB_EMBD = 2048
+
+
+def vocab_head_bench(args):
+    """The vocabulary head's transposed product (r97q_vocab_head_transpose) on a synthetic head the
+    size of the reference container's (four b5 trellis.mad classes, f32 row scale + scale.col, the
+    fwht128 transform), d_x += H . sum_c (dy[:, ids_c] . W_c) * scale.col_c over --vocab-rows rows.
+    Each call decodes the classes into its workspace, as the reference's does."""
+    import numpy as np
+    import torch
+
+    from r9700training_amd.qlinear import device_desc
+    from r9700training_amd.vocab_head import VocabHead
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rows, K = args.vocab_rows, VOCAB_EMBD
+    vocab = sum(VOCAB_CLASSES)
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    perm = torch.randperm(vocab, device="cuda", generator=g).to(torch.int32)
+    rng = np.random.default_rng(args.seed)
+    classes, keep, at = [], [], 0
+    for n in VOCAB_CLASSES:
+        codes = torch.randint(0, 256, (n, K * 5 // 8), dtype=torch.uint8, device="cuda", generator=g)
+        scale = torch.from_numpy((0.0005 + 0.01 * rng.random(n)).astype(np.float32).view(np.uint8)).to(dev)
+        cf = torch.from_numpy((0.5 + rng.random(K // 128)).astype(np.float32)).to(dev)
+        d = device_desc(dict(codes=codes, scale=scale), n, K, dict(
+            bits=5, state_bits=16, run_rows=256, rb=1, mad=1, round_mad=1, mad_a=0x2F1E3D | 1, mad_b=0x9E3779B9,
+            codes_row_bytes=K * 5 // 8, scale_dtype=0, scale_block_cols=0, scale_row_bytes=4))
+        ids = perm[at:at + n].sort().values.contiguous()  # a class's ids ascend, as a partition of the vocabulary
+        at += n
+        classes.append((d, ids, cf))
+        keep += [codes, scale, cf, ids]
+    head = VocabHead(K, vocab, classes, transform=128)
+    dy = torch.randn((rows, vocab), dtype=torch.bfloat16, device=dev, generator=g)
+    d_x = torch.zeros((rows, K), device=dev)
+    ws = torch.empty(head.workspace_bytes(rows), dtype=torch.uint8, device=dev)
+    steps, warmup = max(1, min(args.steps, 20)), max(1, min(args.warmup, 5))
+    for _ in range(warmup):
+        head.transpose(dy, d_x, ws)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        head.transpose(dy, d_x, ws)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    flops = 2.0 * rows * vocab * K
+    tf = flops / (ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "vocab head transposed product TFLOP/s (decode + gather + MFMA + transform per call)",
+        "value": round(tf, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_call": round(ms, 4), "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"vocab head: {len(VOCAB_CLASSES)} b5 trellis.mad classes, {vocab} rows in all, "
+                               f"n_embd {K}, fwht128, {rows} token rows", "classes": VOCAB_CLASSES,
+                   "n_embd": K, "rows": rows},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -207,6 +272,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_mib": args.calibrate_copy_mib, "launches": 3}), flush=True)
         return
+
+    if args.workload == "vocab_head":
+        return vocab_head_bench(args)
 
     from r9700training_amd import R97Q_BF16, R97Q_F32, _ptr, _stream, check, lib
     from r9700training_amd.qlinear import bwd_workspace, fwd_workspace

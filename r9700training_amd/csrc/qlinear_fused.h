@@ -44,6 +44,10 @@ struct DxParams {
     const float* a_scale;  // null, or f32 [T, a_scale_ld]: dX[m, k] is multiplied by a_scale[m, k/128]
     int64_t a_scale_ld;
     int mtiles, ktiles;
+    // batch > 1 (the int8-code form only): gridDim.z independent products, slice z at dY + z*z_dy,
+    // stream + z*z_w (uint32 units), scale_t + z*z_scale, dX + z*z_out (elements of dX's dtype)
+    int batch;
+    int64_t z_dy, z_w, z_scale, z_out;
 };
 
 template <int BITS>

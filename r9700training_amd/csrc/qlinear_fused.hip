@@ -508,11 +508,21 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_fwd_kernel(const FwdParam
     R97Q_WAVE_SWITCH(fwd_wave, , p, lds, lane, mt, nt)
 }
 
-// SCALED: dX in the code basis of an i8a8h activation (p.a_scale set)
-template <bool SCALED>
-__global__ __launch_bounds__(kThreads, 1) void qlinear_dx_kernel(const DxParams p) {
+// SCALED: dX in the code basis of an i8a8h activation (p.a_scale set); BATCHED: slice blockIdx.z of
+// a batch of independent products (the slices' pointers p.z_* apart)
+template <bool SCALED, bool BATCHED = false>
+__global__ __launch_bounds__(kThreads, 1) void qlinear_dx_kernel(const DxParams pb) {
     __shared__ __attribute__((aligned(16))) uint8_t w0[kTileBytes], w1[kTileBytes], x0[kActBytes], x1[kActBytes];
     const Lds lds{{w0, w1}, {x0, x1}};
+    DxParams p = pb;
+    if constexpr (BATCHED) {
+        const int64_t z = blockIdx.z;
+        p.dY += z * pb.z_dy;
+        p.stream += z * pb.z_w;
+        p.scale_t += z * pb.z_scale;
+        p.dX = p.dx_f32 ? static_cast<void*>(static_cast<float*>(pb.dX) + z * pb.z_out)
+                        : static_cast<void*>(static_cast<uint16_t*>(pb.dX) + z * pb.z_out);
+    }
     const int tile = xcd_tile(blockIdx.x, p.mtiles * p.ktiles);
     const int mt = tile / p.ktiles, kt = tile % p.ktiles;
     const int lane = threadIdx.x & 63;
@@ -528,6 +538,16 @@ void launch_fwd<R97Q_BITS>(const FwdParams& p, hipStream_t s) {
 
 template <>
 void launch_dx<R97Q_BITS>(const DxParams& p, hipStream_t s) {
+    if constexpr (R97Q_BITS == R97Q_CODES8) {
+        if (p.batch > 1) {
+            const dim3 grid((unsigned)(p.mtiles * p.ktiles), 1, (unsigned)p.batch);
+            if (p.a_scale)
+                hipLaunchKernelGGL((qlinear_dx_kernel<true, true>), grid, dim3(kThreads), 0, s, p);
+            else
+                hipLaunchKernelGGL((qlinear_dx_kernel<false, true>), grid, dim3(kThreads), 0, s, p);
+            return;
+        }
+    }
     const dim3 grid((unsigned)(p.mtiles * p.ktiles));
     if (p.a_scale)
         hipLaunchKernelGGL(qlinear_dx_kernel<true>, grid, dim3(kThreads), 0, s, p);

@@ -4,13 +4,16 @@
 //   d_x[rows, n_embd] += H . sum over classes c of (dy[:, ids_c] . W_c) * scale.col_c
 //
 // The reference runs it as a gather, a per-token-row GEMV over the decoded int8 grid with f32
-// fmas, and the un-rotation. Here it is the fused dX kernel's product: per class, a range of its
-// rows is decoded into the int8-code form in the workspace (the standalone decode's kernel writing
-// tiled), the cotangent's columns for those rows are gathered into a bf16 [rows, range] operand,
-// and qlinear_dx_kernel<R97Q_CODES8> adds (gathered . W) * scale.col into d_x with bf16 MFMA,
-// the class's scale.col applied in its epilogue (one factor a 128-column tile). Ranges are padded
-// to 128 rows with zero codes, zero scales and zero cotangent columns. Once every class is in,
-// the unnormalised 128-wide Hadamard runs over each 128 columns of d_x.
+// fmas, and the un-rotation. Here it is the fused dX kernel's product. A class's rows go in ranges
+// of about 4096 (whole trellis runs), a batch of up to kBatch ranges at a time: each range is
+// decoded into the int8-code form in the workspace (the standalone decode's kernel writing tiled),
+// the cotangent's columns for the batch's rows are gathered into bf16 [range][rows][Np] operands,
+// and one batched qlinear_dx_kernel<R97Q_CODES8> launch (a grid slice a range, so a head with few
+// token rows or a narrow n_embd still fills the chip) writes each range's (gathered . W) *
+// scale.col -- the class's scale.col in its epilogue, one factor a 128-column tile -- into its own
+// f32 partial; the partials are then added into d_x in range order (deterministic). Ranges are
+// padded to Np (a multiple of 128) rows with zero codes, zero scales and zero cotangent columns.
+// Once every class is in, the unnormalised 128-wide Hadamard runs over each 128 columns of d_x.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -23,7 +26,9 @@
 namespace r97q {
 namespace {
 
-constexpr int64_t kRangeRows = 16384;  // rows of a class decoded at once (whole trellis runs)
+constexpr int64_t kRangeRows = 4096;  // rows of a range (whole trellis runs)
+constexpr int kBatch = 8;             // ranges a batched launch
+constexpr int kFillWorkgroups = 512;  // a batch large enough for this many workgroups (256 CUs)
 
 int64_t round_up(int64_t n, int64_t m) { return (n + m - 1) / m * m; }
 
@@ -35,17 +40,24 @@ int64_t range_rows(const R97qVocabClass& c) {
     return r < c.rows ? r : c.rows;
 }
 
+// ranges a batch takes: enough for kFillWorkgroups workgroups, at most kBatch
+int batch_of(int64_t rows, int64_t K) {
+    const int64_t wgs = (rows + kBM - 1) / kBM * (K / kBN);
+    const int64_t b = (kFillWorkgroups + wgs - 1) / wgs;
+    return (int)(b < 1 ? 1 : b > kBatch ? kBatch : b);
+}
+
 struct VocabWs {
-    int64_t codes, scale, gather, cf, total;
+    int64_t codes, scale, gather, part, cf, total;
 };
 
 VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
-    int64_t S = 0;
+    int64_t Np = 0;
     for (int c = 0; c < plan.classes; ++c) {
         const int64_t s = round_up(range_rows(plan.cls[c]), 128);
-        S = s > S ? s : S;
+        Np = s > Np ? s : Np;
     }
-    const int64_t nkb = plan.n_embd / 128;
+    const int64_t K = plan.n_embd, nkb = K / 128, Z = batch_of(rows, K);
     VocabWs w{};
     int64_t off = 0;
     auto take = [&](int64_t bytes) {
@@ -53,9 +65,10 @@ VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
         off += round_up(bytes, 256);
         return at;
     };
-    w.codes = take(S * plan.n_embd);
-    w.scale = take(nkb * S * 2);
-    w.gather = take(rows * S * 2);
+    w.codes = take(Z * Np * K);
+    w.scale = take(Z * nkb * Np * 2);
+    w.gather = take(Z * rows * Np * 2);
+    w.part = take(Z * rows * K * 4);
     w.cf = take(nkb * 4);
     w.total = off;
     return w;
@@ -72,20 +85,35 @@ __global__ __launch_bounds__(256) void vocab_pad_kernel(int8_t* __restrict__ cod
     if (i < pad * nkb) scale_t[(i / pad) * ns_pad + ns + i % pad] = 0;
 }
 
-// a[m, n] = dy[m, ids[n] - vocab_offset] for n < ns and an id inside this vocabulary, else 0
+// a[z][m][n] = dy[m, ids[z*R + n] - vocab_offset] for class rows inside the batch's rows [0, ns)
+// and an id inside this vocabulary, else 0: grid (Np/256, token rows from m0, Z), a column a
+// thread (measured: 8 columns a thread with one 16-byte store is 40% slower -- fewer loads in
+// flight)
 __global__ __launch_bounds__(256) void vocab_gather_kernel(const uint16_t* __restrict__ dy,
                                                            const int32_t* __restrict__ ids,
                                                            uint16_t* __restrict__ a, int64_t rows, int64_t vocab,
-                                                           int64_t vocab_offset, int64_t ns, int64_t ns_pad) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * ns_pad) return;
-    const int64_t m = i / ns_pad, n = i - m * ns_pad;
+                                                           int64_t vocab_offset, int64_t R, int64_t ns, int64_t Np,
+                                                           int64_t m0) {
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t m = m0 + blockIdx.y, z = blockIdx.z;
+    if (n >= Np) return;
+    const int64_t r = z * R + n;
     uint16_t v = 0;
-    if (n < ns) {
-        const int64_t id = ids[n];
+    if (n < R && r < ns) {
+        const int64_t id = ids[r];
         if (id >= vocab_offset && id < vocab_offset + vocab) v = dy[m * vocab + (id - vocab_offset)];
     }
-    a[i] = v;
+    a[(z * rows + m) * Np + n] = v;
+}
+
+// d_x[i] += part[0][i] + part[1][i] + ... (the ranges in order)
+__global__ __launch_bounds__(256) void vocab_reduce_kernel(float* __restrict__ d_x, const float* __restrict__ part,
+                                                           int64_t n, int Z) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float v = d_x[i];
+    for (int z = 0; z < Z; ++z) v += part[z * n + i];
+    d_x[i] = v;
 }
 
 __global__ __launch_bounds__(64) void vocab_cf_kernel(const uint8_t* __restrict__ cf, int32_t dtype, int64_t nkb,
@@ -172,6 +200,7 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
     int8_t* codes = reinterpret_cast<int8_t*>(wsb + ws.codes);
     uint16_t* scale_t = reinterpret_cast<uint16_t*>(wsb + ws.scale);
     uint16_t* gathered = reinterpret_cast<uint16_t*>(wsb + ws.gather);
+    float* part = reinterpret_cast<float*>(wsb + ws.part);
     float* cf = reinterpret_cast<float*>(wsb + ws.cf);
     const hipStream_t s = (hipStream_t)stream;
     const int64_t K = plan->n_embd, nkb = K / 128;
@@ -181,51 +210,69 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
         hipLaunchKernelGGL(vocab_cf_kernel, dim3(blocks(nkb, 64)), dim3(64), 0, s,
                            static_cast<const uint8_t*>(cls.scale_col), cls.scale_col_dtype, nkb, cf);
         if (int e = launch_status("vocab_cf_kernel")) return e;
-        const int64_t R = range_rows(cls);
-        for (int64_t r0 = 0; r0 < cls.rows; r0 += R) {
-            const int64_t ns = R < cls.rows - r0 ? R : cls.rows - r0;
-            const int64_t ns_pad = round_up(ns, 128);
-            R97IqrDecodeDesc d = cls.decode;
-            d.row0 = r0;
-            d.rows = ns;
-            d.codes = d.codes + r0 * d.codes_row_bytes;
-            d.scale = d.scale + r0 * d.scale_row_bytes;
-            d.zero = d.zero ? d.zero + r0 * d.zero_row_bytes : nullptr;
-            d.out_codes = codes;
-            d.out_scale = scale_t;
-            if (validate(d)) {
-                set_error("%s: the plan's class %d decode is outside the kernel's rules", who, c);
-                return R97Q_EINVAL;
+        const int64_t R = range_rows(cls), Np = round_up(R, 128);
+        const int Zmax = batch_of(rows, K);
+        for (int64_t b0 = 0; b0 < cls.rows; b0 += Zmax * R) {
+            const int64_t nb = Zmax * R < cls.rows - b0 ? Zmax * R : cls.rows - b0;  // the batch's class rows
+            const int Z = (int)((nb + R - 1) / R);
+            for (int z = 0; z < Z; ++z) {
+                const int64_t r0 = b0 + z * R;
+                const int64_t ns = R < cls.rows - r0 ? R : cls.rows - r0;
+                int8_t* zc = codes + z * Np * K;
+                uint16_t* zs = scale_t + z * nkb * Np;
+                R97IqrDecodeDesc d = cls.decode;
+                d.row0 = r0;
+                d.rows = ns;
+                d.codes = d.codes + r0 * d.codes_row_bytes;
+                d.scale = d.scale + r0 * d.scale_row_bytes;
+                d.zero = d.zero ? d.zero + r0 * d.zero_row_bytes : nullptr;
+                d.out_codes = zc;
+                d.out_scale = zs;
+                if (validate(d)) {
+                    set_error("%s: the plan's class %d decode is outside the kernel's rules", who, c);
+                    return R97Q_EINVAL;
+                }
+                if (Np != ns) {
+                    const int64_t n = Np * K / 4 - (ns / 8) * (K / 4) * 8;
+                    const int64_t m = (Np - ns) * nkb;
+                    hipLaunchKernelGGL(vocab_pad_kernel, dim3(blocks(n > m ? n : m, 256)), dim3(256), 0, s, zc, zs,
+                                       ns, Np, K);
+                    if (int e = launch_status("vocab_pad_kernel")) return e;
+                }
+                if (int e = decode_tiled(d, Np, s)) return e;
             }
-            if (ns_pad != ns) {
-                const int64_t n = ns_pad * K / 4 - (ns / 8) * (K / 4) * 8;
-                const int64_t m = (ns_pad - ns) * nkb;
-                hipLaunchKernelGGL(vocab_pad_kernel, dim3(blocks(n > m ? n : m, 256)), dim3(256), 0, s, codes,
-                                   scale_t, ns, ns_pad, K);
-                if (int e = launch_status("vocab_pad_kernel")) return e;
+            for (int64_t m0 = 0; m0 < rows; m0 += 65535) {  // gridDim.y's limit
+                const int64_t mr = rows - m0 < 65535 ? rows - m0 : 65535;
+                hipLaunchKernelGGL(vocab_gather_kernel, dim3(blocks(Np, 256), (unsigned)mr, (unsigned)Z), dim3(256), 0,
+                                   s, dy, static_cast<const int32_t*>(cls.ids) + b0, gathered, rows, plan->vocab,
+                                   plan->vocab_offset, R, nb, Np, m0);
+                if (int e = launch_status("vocab_gather_kernel")) return e;
             }
-            if (int e = decode_tiled(d, ns_pad, s)) return e;
-            hipLaunchKernelGGL(vocab_gather_kernel, dim3(blocks(rows * ns_pad, 256)), dim3(256), 0, s, dy,
-                               static_cast<const int32_t*>(cls.ids) + r0, gathered, rows, plan->vocab,
-                               plan->vocab_offset, ns, ns_pad);
-            if (int e = launch_status("vocab_gather_kernel")) return e;
             DxParams p{};
             p.dY = gathered;
             p.T = rows;
-            p.N = ns_pad;
+            p.N = Np;
             p.K = K;
             p.stream = reinterpret_cast<const uint32_t*>(codes);
             p.scale_t = scale_t;
             p.rank = 0;
-            p.dX = d_x;
+            p.dX = part;
             p.dx_f32 = 1;
-            p.accumulate = 1;
+            p.accumulate = 0;
             p.a_scale = cf;  // one factor a 128-column tile: every row reads cf[kt]
             p.a_scale_ld = 0;
             p.mtiles = (int)((rows + kBM - 1) / kBM);
             p.ktiles = (int)(K / kBN);
+            p.batch = Z;
+            p.z_dy = rows * Np;
+            p.z_w = Np * K / 4;
+            p.z_scale = nkb * Np;
+            p.z_out = rows * K;
             launch_dx<R97Q_CODES8>(p, s);
             if (int e = launch_status("qlinear_dx_kernel (vocab head)")) return e;
+            hipLaunchKernelGGL(vocab_reduce_kernel, dim3(blocks(rows * K, 256)), dim3(256), 0, s, d_x, part, rows * K,
+                               Z);
+            if (int e = launch_status("vocab_reduce_kernel")) return e;
         }
     }
     if (plan->transform == 128) {
