@@ -340,6 +340,23 @@ int r97q_adamw_step(const R97qAdamWConfig* cfg, const R97qAdamWParam* params, fl
 /* y = bf16(x) (RNE, NaN quieted), n elements: the kernels' bf16 operands from the f32 master weights */
 int r97q_f32_to_bf16(const float* x, uint16_t* y, int64_t n, R97IqrStream stream);
 
+/* ------------------------------------------------------------------ the activation quantiser
+ *
+ * quant_act_i8g / had_quant_act_i8g, the coded trunk's activation codes (the reference's host rows
+ * src/adjoint/host/quant.cpp:179-236 and the geometry :150-177): per row of x [rows, n] (bf16 or
+ * f32) and per group of `group` columns (group <= 0 or > n: one group a row; a short last group
+ * when it does not divide n; rotated: the unnormalised Walsh-Hadamard transform of each group
+ * first, `group` a power of two dividing n, at most 4096 here), scale = amax / 127 (1 for an
+ * all-zero group), codes = clamp(rint(v / scale), -127, 127). codes int8 [rows, n], scale f32
+ * [rows, ceil(n / group)]. The host rows' f64 arithmetic, so the same codes and scales. */
+int r97q_quant_act_i8g(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t group, int32_t rotated,
+                       int8_t* codes, float* scale, R97IqrStream stream);
+/* The straight-through adjoint (src/adjoint/host/quant.cpp:318-372): dx f32 [rows, n] += W^T (live
+ * * g / scale), g the codes' cotangent f32 [rows, n], live 0 where the clamp engaged (|v / scale| >
+ * 127), scale the forward's (positive, as the forward writes it); the scale's cotangent is dropped. */
+int r97q_quant_act_i8g_bwd(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t group, int32_t rotated,
+                           const float* scale, const float* g, float* dx, R97IqrStream stream);
+
 /* ------------------------------------------------------------------ the vocabulary head
  *
  * The vocabulary head's transposed product (src/vocab_head.h:27-99, its kernels

@@ -27,6 +27,13 @@
  *                                  <dy, twin(a)> == <adj(dy), e> for code perturbations e, scale
  *                                  held), and the a_scale cotangent is the derivative of the twin in
  *                                  the scale.
+ *   orc_quant_act_i8g, orc_quant_act_i8g_adjoint
+ *                                  the reference test's known answers (tests/host/adjoint_quant.cpp:
+ *                                  326-430: the saturated group's clamped code, scale and masked
+ *                                  cotangents; the zero group's pass-through and W (1,..,1) = (t, 0..));
+ *                                  scipy's Sylvester Hadamard for the rotation; the codes against a
+ *                                  numpy rint/clip; ties to even on exact halves; the adjoint as the
+ *                                  transpose of the straight-through linearisation (dot products).
  *   orc_vocab_class_product, orc_fwht128
  *                                  the reference test's own known answer (tests/gpu/vocab_head.cpp:
  *                                  a one-hot cotangent row selects one weight row, scaled by its
@@ -833,4 +840,87 @@ void orc_fwht128(int64_t rows, int64_t K, double* d_x) {
                 v[j + h] = x - y;
             }
     }
+}
+
+/* ------------------------------------------------------------------ the activation quantiser */
+
+/* src/adjoint/host/quant.cpp:150-177 */
+static int64_t quant_group(int64_t n, int64_t group, int32_t rotated) {
+    if (n <= 0) return 0;
+    if (rotated) return (group <= 0 || (group & (group - 1)) != 0 || n % group != 0) ? 0 : group;
+    return (group <= 0 || group > n) ? n : group;
+}
+
+/* src/adjoint/host/quant.cpp:181-191 */
+static void quant_fwht(double* v, int64_t t) {
+    for (int64_t h = 1; h < t; h <<= 1)
+        for (int64_t i0 = 0; i0 < t; i0 += 2 * h)
+            for (int64_t j = i0; j < i0 + h; ++j) {
+                const double a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+}
+
+/* src/adjoint/host/quant.cpp:208-236 */
+int32_t orc_quant_act_i8g(const double* x, int64_t rows, int64_t n, int64_t group, int32_t rotated, double* codes,
+                          double* scale, uint8_t* live) {
+    const int64_t t = quant_group(n, group, rotated);
+    if (t == 0) return 1;
+    const int64_t ngrp = (n + t - 1) / t;
+    double* v = (double*)malloc((size_t)n * sizeof(double));
+    for (int64_t r = 0; r < rows; ++r) {
+        memcpy(v, x + r * n, (size_t)n * sizeof(double));
+        for (int64_t g = 0; g < ngrp; ++g) {
+            const int64_t k0 = g * t, w = t < n - k0 ? t : n - k0;
+            double* vg = v + k0;
+            if (rotated) quant_fwht(vg, t);
+            double amax = 0.0;
+            for (int64_t i = 0; i < w; ++i) amax = fabs(vg[i]) > amax ? fabs(vg[i]) : amax;
+            const double s = amax > 0.0 ? amax * (1.0 / 127.0) : 1.0;
+            scale[r * ngrp + g] = s;
+            for (int64_t i = 0; i < w; ++i) {
+                const double u = vg[i] * (1.0 / s);
+                const double c = nearbyint(u);
+                codes[r * n + k0 + i] = c > 127.0 ? 127.0 : (c < -127.0 ? -127.0 : c);
+                if (live) live[r * n + k0 + i] = fabs(u) <= 127.0 ? 1 : 0;
+            }
+        }
+    }
+    free(v);
+    return 0;
+}
+
+/* src/adjoint/host/quant.cpp:349-372 */
+int32_t orc_quant_act_i8g_adjoint(const double* x, int64_t rows, int64_t n, int64_t group, int32_t rotated,
+                                  const double* scale, const double* g, double* dx) {
+    const int64_t t = quant_group(n, group, rotated);
+    if (t == 0) return 1;
+    const int64_t ngrp = (n + t - 1) / t;
+    double* v = (double*)malloc((size_t)n * sizeof(double));
+    double* d = (double*)malloc((size_t)n * sizeof(double));
+    int32_t rc = 0;
+    for (int64_t r = 0; r < rows && rc == 0; ++r) {
+        memcpy(v, x + r * n, (size_t)n * sizeof(double));
+        memcpy(d, g + r * n, (size_t)n * sizeof(double));
+        for (int64_t gi = 0; gi < ngrp; ++gi) {
+            const int64_t k0 = gi * t, w = t < n - k0 ? t : n - k0;
+            if (rotated) quant_fwht(v + k0, t);
+            const double s = scale[r * ngrp + gi];
+            if (!(s > 0.0)) {
+                rc = 2;
+                break;
+            }
+            for (int64_t i = 0; i < w; ++i) {
+                const int64_t j = k0 + i;
+                d[j] = fabs(v[j] * (1.0 / s)) > 127.0 ? 0.0 : d[j] / s;
+            }
+            if (rotated) quant_fwht(d + k0, t);
+        }
+        if (rc == 0)
+            for (int64_t j = 0; j < n; ++j) dx[r * n + j] += d[j];
+    }
+    free(v);
+    free(d);
+    return rc;
 }

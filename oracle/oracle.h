@@ -124,6 +124,17 @@ int32_t orc_adamw_step(const OrcAdamWConfig* cfg, float* const* w, float* const*
                        float* const* acc, const int64_t* n, const int32_t* decay, int32_t count,
                        const float* const* g, int32_t* step, int32_t* pending);
 
+/* quant_act_i8g / had_quant_act_i8g (src/adjoint/host/quant.cpp:150-236): x f64 [rows, n] ->
+ * codes f64 [rows, n] (integers in [-127, 127]), scale f64 [rows, ngrp], live [rows, n] (1 where the
+ * clamp did not engage; may be NULL). group is the record's parameter (the effective group is
+ * derived as the reference does); returns 0, or 1 when the geometry is refused. */
+int32_t orc_quant_act_i8g(const double* x, int64_t rows, int64_t n, int64_t group, int32_t rotated, double* codes,
+                          double* scale, uint8_t* live);
+/* Its straight-through adjoint (src/adjoint/host/quant.cpp:318-372): dx += W^T(live * g / s). Returns
+ * 0, 1 for a refused geometry, 2 for a non-positive scale (the reference throws). */
+int32_t orc_quant_act_i8g_adjoint(const double* x, int64_t rows, int64_t n, int64_t group, int32_t rotated,
+                                  const double* scale, const double* g, double* dx);
+
 /* The vocabulary head's transposed product for one class (src/adjoint/device/vocab_head.hip:88-143,
  * the gather and the GEMV; f64 here): for every token row m and column k,
  *   d_x[m, k] += cf[k/128] * sum_n dy[m, ids[n] - vocab_offset] * gscale[n, k/128] * codes[n, k]

@@ -99,6 +99,10 @@ def lib():
         L.orc_adamw_step.argtypes = [C.POINTER(AdamWConfig), _P, _P, _P, _P, _P, _P, C.c_int32, _P, _P, _P]
         L.orc_vocab_class_product.argtypes = [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]
         L.orc_fwht128.argtypes = [_I, _I, _P]
+        L.orc_quant_act_i8g.restype = C.c_int32
+        L.orc_quant_act_i8g.argtypes = [_P, _I, _I, _I, C.c_int32, _P, _P, _P]
+        L.orc_quant_act_i8g_adjoint.restype = C.c_int32
+        L.orc_quant_act_i8g_adjoint.argtypes = [_P, _I, _I, _I, C.c_int32, _P, _P, _P]
         L.orc_rounded_bf16.restype = C.c_double
         L.orc_rounded_bf16.argtypes = [C.c_double]
         L.orc_thread_count.restype = C.c_int
@@ -490,4 +494,31 @@ def fwht128(x):
     """The unnormalised 128-wide Hadamard over each 128 values of the rows of x (f64 copy)."""
     out = np.array(x, np.float64, copy=True, order="C")
     lib().orc_fwht128(out.shape[0], out.shape[1], _ptr(out))
+    return out
+
+
+def quant_act_i8g(x, group, rotated=False):
+    """quant_act_i8g / had_quant_act_i8g (src/adjoint/host/quant.cpp:208-236) on x f64 [rows, n]
+    -> (codes f64, scale f64 [rows, ngrp], live uint8); None when the geometry is refused."""
+    x = np.ascontiguousarray(x, np.float64)
+    rows, n = x.shape
+    t = group if rotated else (n if group <= 0 or group > n else group)
+    ngrp = (n + t - 1) // max(t, 1)
+    codes, scale = np.zeros((rows, n)), np.zeros((rows, ngrp))
+    live = np.zeros((rows, n), np.uint8)
+    if lib().orc_quant_act_i8g(_ptr(x), rows, n, group, int(rotated), _ptr(codes), _ptr(scale), _ptr(live)):
+        return None
+    return codes, scale, live
+
+
+def quant_act_i8g_adjoint(x, scale, g, group, rotated=False, dx=None):
+    """The straight-through adjoint (src/adjoint/host/quant.cpp:318-372): dx + W^T(live g / s)."""
+    x = np.ascontiguousarray(x, np.float64)
+    rows, n = x.shape
+    out = np.zeros((rows, n)) if dx is None else np.array(dx, np.float64, copy=True, order="C")
+    rc = lib().orc_quant_act_i8g_adjoint(_ptr(x), rows, n, group, int(rotated),
+                                         _ptr(np.ascontiguousarray(scale, np.float64)),
+                                         _ptr(np.ascontiguousarray(g, np.float64)), _ptr(out))
+    if rc:
+        raise ValueError("quant adjoint: geometry refused" if rc == 1 else "quant adjoint: non-positive scale")
     return out

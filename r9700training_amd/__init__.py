@@ -113,6 +113,8 @@ SIGNATURES = {
     "r97q_adamw_step": (C.c_int, [C.POINTER(AdamWConfig), C.POINTER(AdamWParam), C.POINTER(C.c_void_p), _i, _i,
                                   C.POINTER(C.c_int32), C.POINTER(C.c_int32), C.POINTER(C.c_int32), _P, _I, _P]),
     "r97q_f32_to_bf16": (C.c_int, [_P, _P, _I, _P]),
+    "r97q_quant_act_i8g": (C.c_int, [_P, _i, _I, _I, _I, _i, _P, _P, _P]),
+    "r97q_quant_act_i8g_bwd": (C.c_int, [_P, _i, _I, _I, _I, _i, _P, _P, _P, _P]),
     "r97q_vocab_head_workspace_bytes": (_I, [C.POINTER(VocabPlan), _I]),
     "r97q_vocab_head_transpose": (C.c_int, [C.POINTER(VocabPlan), _P, _I, _P, _P, _I, _P]),
     "r97q_vocab_head_cast": (C.c_int, [_P, _P, _I, _P]),

@@ -620,3 +620,94 @@ def test_vocab_head_matches_matmul_and_ignores_stray_ids():
     # the transform runs over the whole of d_x once the classes are in
     got_t = O.vocab_head_transpose(dy, cls, vocab_offset=offset, transform=128, d_x=d0)
     assert np.allclose(got_t, O.fwht128(want), rtol=1e-10, atol=1e-8)
+
+
+# ---------------------------------------------------------------- the activation quantiser
+def _scanned_amax():
+    """tests/host/adjoint_quant.cpp:236-243: the first a = 1 + k/64 whose own scale clamps it."""
+    for k in range(64):
+        a = 1.0 + k / 64.0
+        s = a * (1.0 / 127.0)
+        if abs(a * (1.0 / s)) > 127.0:
+            return a
+    raise AssertionError("no clamping amax")
+
+
+@pytest.mark.parametrize("rotated", [False, True])
+def test_quant_saturated_group_known_answers(rotated):
+    """tests/host/adjoint_quant.cpp:332-370: the clamped code and its scale, the masked cotangent,
+    an inside code's cotangent divided by the scale and rotated back."""
+    a = _scanned_amax()
+    scale = a * (1.0 / 127.0)
+    x = np.array([[0.75 * a, 0.25 * a]]) if rotated else np.array([[a, 0.5 * a, -0.25 * a, 0.125 * a]])
+    n = x.shape[1]
+    codes, sc, live = O.quant_act_i8g(x, n, rotated)
+    assert codes[0, 0] == 127.0 and sc[0, 0] == scale
+    g = np.zeros((1, n))
+    g[0, 0] = 1.0
+    assert not O.quant_act_i8g_adjoint(x, sc, g, n, rotated).any()
+    g = np.zeros((1, n))
+    g[0, 1] = 1.0
+    dx = O.quant_act_i8g_adjoint(x, sc, g, n, rotated)
+    want = [1.0 / scale, -1.0 / scale] if rotated else [0.0, 1.0 / scale, 0.0, 0.0]
+    assert np.array_equal(dx[0], want)
+
+
+@pytest.mark.parametrize("rotated", [False, True])
+def test_quant_zero_group_passes_through(rotated):
+    """tests/host/adjoint_quant.cpp:378-430: the zero group's codes and scale, e0 back through the
+    adjoint, and W (1, .., 1) = (t, 0, .., 0) for the rotation's transpose."""
+    rows, n, group = (2, 8, 8) if rotated else (2, 6, 3)
+    x = np.zeros((rows, n))
+    codes, sc, _ = O.quant_act_i8g(x, group, rotated)
+    assert not codes.any() and (sc == 1.0).all()
+    first = np.zeros((rows, n))
+    first[:, ::group] = 1.0
+    dx = O.quant_act_i8g_adjoint(x, sc, first, group, rotated)
+    assert np.array_equal(dx, np.ones((rows, n)) if rotated else first)
+    dy = O.quant_act_i8g_adjoint(x, sc, np.ones((rows, n)), group, rotated)
+    want = np.zeros((rows, n))
+    want[:, ::group] = group
+    assert np.array_equal(dy, want if rotated else np.ones((rows, n)))
+
+
+@pytest.mark.parametrize("n,group,rotated", [(384, 128, False), (300, 128, False), (200, 0, False), (256, 64, True),
+                                             (512, 512, True)])
+def test_quant_against_numpy_and_the_transpose(n, group, rotated):
+    """The codes against numpy's rint/clip over scipy's Hadamard (ties to even on exact halves);
+    the adjoint is the transpose of the straight-through linearisation: <g, J e> == <J^T g, e>."""
+    import scipy.linalg
+
+    rng = np.random.default_rng(n + group)
+    rows = 5
+    x = S.bf16_bits_to_f32(S.f32_to_bf16_bits(rng.standard_normal((rows, n)).astype(np.float32))).astype(np.float64)
+    x[1, :] = 0.0  # a zero row
+    t = group if rotated else (n if group <= 0 or group > n else group)
+    v = x.copy()
+    if rotated:
+        H = scipy.linalg.hadamard(t).astype(np.float64)
+        v = np.concatenate([v[:, b:b + t] @ H.T for b in range(0, n, t)], axis=1)
+    # exact halves: place u = k + 0.5 at a known scale in row 2's first group
+    codes, sc, live = O.quant_act_i8g(x, group, rotated)
+    ngrp = sc.shape[1]
+    for r in range(rows):
+        for gi in range(ngrp):
+            seg = v[r, gi * t:(gi + 1) * t]
+            amax = np.abs(seg).max()
+            s = amax * (1.0 / 127.0) if amax > 0 else 1.0
+            assert sc[r, gi] == s
+            u = seg * (1.0 / s)
+            assert np.array_equal(codes[r, gi * t:gi * t + len(seg)], np.clip(np.rint(u), -127, 127))
+    # ties to even: a group whose values sit on halves of its own scale
+    hx = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5]])
+    hc, hs, _ = O.quant_act_i8g(hx, 0, False)
+    assert hs[0, 0] == 1.0 and np.array_equal(hc[0], [127, 0, 2, 2, 0, -2])
+    # transpose of the linearisation: J e = live * (W e) / s per group
+    g = rng.standard_normal((rows, n))
+    e = rng.standard_normal((rows, n))
+    We = e.copy()
+    if rotated:
+        We = np.concatenate([We[:, b:b + t] @ H.T for b in range(0, n, t)], axis=1)
+    Je = live * We / np.repeat(sc, t, axis=1)[:, :n]
+    JTg = O.quant_act_i8g_adjoint(x, sc, g, group, rotated)
+    assert abs((g * Je).sum() - (JTg * e).sum()) <= 1e-9 * (abs((g * Je).sum()) + 1)
