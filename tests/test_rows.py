@@ -62,6 +62,44 @@ def test_registry_rules_and_registrations():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("form", ["lut-bf16", "mad-rb", "e4m3-scale1"])
+def test_gemm_nt_row_other_forms(form):
+    """A stored weight in a form the kernels do not decode themselves (a stored LUT with bf16 block
+    scales, rb > 1 row blocks, e4m3 block scales with scale.1) reaches the row through the same
+    stored-weight store, prepared once into the int8-code form."""
+    from gpu_util import device_desc, dev, host_weight
+    from oracle import oracle as O
+
+    print(f"case gemm_nt stored form {form}", flush=True)
+    L = hook()
+    # the store is keyed by the encoding, as the reference's is; this test's planes may reuse an
+    # earlier case's device addresses (and so its encoding entry), so it starts from an empty store,
+    # as the reference's walk does at every step (stored_weight_clear)
+    L.rh_weights_clear()
+    M, N, K = 72, 256, 384
+    rng = np.random.default_rng(len(form))
+    kw = {"lut-bf16": dict(bits=4, state_bits=16, run_rows=128, rb=1, mad=0, scale_dtype=S.BF16),
+          "mad-rb": dict(bits=4, state_bits=16, run_rows=128, rb=8, mad=1, scale_dtype=S.F32, rowf=True),
+          "e4m3-scale1": dict(bits=5, state_bits=12, run_rows=128, rb=1, mad=0, scale_dtype=S.E4M3, second=True)}[form]
+    planes = S.trellis(rows=N, cols=K, seed=7, **kw)
+    keep = []
+    d = device_desc(planes, keep)
+    sc = None
+    if planes.scale_col is not None:
+        sc = dev(planes.scale_col)
+        keep.append(sc)
+    dy = rng.standard_normal((M, N))
+    dx0 = rng.standard_normal((M, K))
+    dx = dx0.copy()
+    check(L, L.rh_gemm_nt(M, N, K, p(dy), C.addressof(d), sc.data_ptr() if sc is not None else None, None, p(dx)))
+    codes, scale = host_weight(planes)
+    want = O.gemm_nt_adjoint(dy, codes, scale, dx=dx0)
+    e = rel_l2(dx - dx0, want - dx0)
+    print(f"  rel L2 dx {e:.3e}", flush=True)
+    assert e <= TOL_STORED
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K,dense", [(96, 256, 384, False), (200, 512, 256, False), (64, 384, 256, True)])
 def test_gemm_nt_row(M, N, K, dense):
     from gpu_util import device_desc, dev, host_weight
@@ -69,6 +107,7 @@ def test_gemm_nt_row(M, N, K, dense):
 
     print(f"case gemm_nt M={M} N={N} K={K} dense={dense}", flush=True)
     L = hook()
+    L.rh_weights_clear()  # an earlier case's encoding entry may sit at this case's device addresses
     rng = np.random.default_rng(M + N + K)
     dy = rng.standard_normal((M, N))
     dx0 = rng.standard_normal((M, K))
