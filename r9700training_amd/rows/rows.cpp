@@ -633,12 +633,64 @@ void lora_shrink_q_device(const AdjointCall& call) {
     for (size_t i = 0; i < hs.size(); ++i) s_cot.value[i] += (double)hs[i];
 }
 
+// ---------------------------------------------------------------- the activation quantiser
+// had_quant_act_i8g's straight-through adjoint on the card (the reference's device row
+// src/adjoint/device/quant.hip:951-958 with its predicate :129-137; the rule
+// src/adjoint/host/quant.cpp:318-372): schema x (read); codes, scale (written). dc[x] += W^T (live
+// * cot[codes] / scale); the scale's cotangent is dropped.
+bool serves_rotated(const std::vector<OpParam>& params) {
+    int64_t n = 0, group = 0;
+    for (const OpParam& p : params) {
+        if (const int64_t* v = std::get_if<int64_t>(&p.second)) {
+            if (p.first == "n") n = *v;
+            if (p.first == "group") group = *v;
+        }
+    }
+    return n > 0 && group > 0 && group <= 1024 && (group & (group - 1)) == 0 && n % group == 0;
+}
+
+void had_quant_device(const AdjointCall& call) {
+    const OpRecord& rec = call.rec;
+    size_t reads = 0;
+    for (const Operand& o : rec.operands)
+        if (!o.written) ++reads;
+    if (reads == 0 || call.fwd.size() < reads + 2)
+        refuse(rec.op, "the record must read the activation and write the codes and the scale");
+    if (call.cot.empty()) refuse(rec.op, "the walk handed no cotangent for the codes");
+    if (!call.dc || call.dc->empty()) refuse(rec.op, "the walk handed no room for the activation's cotangent");
+    const int64_t n = param_int(rec, "n", 0), group = param_int(rec, "group", 0);
+    const AdValue& x = call.fwd[0];
+    const AdValue& scale = call.fwd[reads + 1];
+    const AdValue& g = call.cot[0];
+    if (n <= 0 || x.value.size() % (size_t)n != 0) refuse(rec.op, "the activation is not a whole number of rows of 'n'");
+    const int64_t rows = (int64_t)x.value.size() / n;
+    if (g.value.size() != x.value.size()) refuse(rec.op, "the codes' cotangent has the activation's shape");
+    if ((int64_t)scale.value.size() != rows * (n / group)) refuse(rec.op, "the scale does not have one value per (row, group)");
+    for (double sv : scale.value)
+        if (!(sv > 0.0)) refuse(rec.op, "the scale of a group must be positive");
+    AdValue& dx = call.dc->at(0);
+    if (dx.value.size() != x.value.size()) refuse(rec.op, "the activation's cotangent has the activation's shape");
+    std::vector<float> xf(x.value.begin(), x.value.end()), sf(scale.value.begin(), scale.value.end()),
+        gf(g.value.begin(), g.value.end());
+    Card& c = card();
+    std::lock_guard<std::mutex> lock(c.mu);
+    const hipStream_t s = stream_of(c);
+    const float* d_x = upload(c, "q_x", xf);
+    const float* d_s = upload(c, "q_scale", sf);
+    const float* d_g = upload(c, "q_g", gf);
+    float* d_dx = zeros(c, "q_dx", xf.size());
+    r97q_ok(r97q_quant_act_i8g_bwd(d_x, R97Q_F32, rows, n, group, 1, d_s, d_g, d_dx, s), "had_quant_act_i8g adjoint");
+    const std::vector<float> h = download(c, d_dx, xf.size());
+    for (size_t i = 0; i < h.size(); ++i) dx.value[i] += (double)h[i];
+}
+
 }  // namespace
 
 // The frozen positions are the reference's (the weight for gemm_nt; slot, factor and scale for
 // the adapter's ops); the float shrink's device row is new here (the reference serves the float
 // shrink on the host only).
 R97_REGISTER_ADJOINT_IF_F("gemm_nt", device, gemm_nt_device, serves_bf16, 1)
+R97_REGISTER_ADJOINT_IF("had_quant_act_i8g", device, had_quant_device, serves_rotated)
 R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_device, float_act, 1, 2, 3)
 R97_REGISTER_ADJOINT_F("lora_expand", device, lora_expand_device, 1, 2, 3)
 R97_REGISTER_ADJOINT_IF_F("gemm_nt_q", device, gemm_nt_q_device, serves_i8a8h, 1, 2, 3)

@@ -398,6 +398,32 @@ int rh_stage_flush(const float* a, const float* b, const float* base, int64_t n,
     return 0;
 }
 
+// had_quant_act_i8g's device row: x [rows, n] f64, scale [rows, n/group] (the forward's), g the codes'
+// cotangent; dx [rows, n] added to. Returns -2 when no device row serves the parameters.
+int rh_had_quant(int64_t rows, int64_t n, int64_t group, const double* x, const double* scale, const double* g,
+                 double* dx) {
+    try {
+        OpRecord rec;
+        rec.op = "had_quant_act_i8g";
+        rec.params = {{"M", rows}, {"n", n}, {"group", group}, {"dtype", std::string("bf16")}};
+        rec.operands = {opd("x", "bf16", {rows, n}), opd("q", "i8", {rows, n}, true),
+                        opd("scale", "f32", {rows, n / group}, true)};
+        const std::vector<AdValue> fwd = {val("bf16", {rows, n}, x), val("i8", {rows, n}, nullptr),
+                                          val("f32", {rows, n / group}, scale)};
+        const std::vector<AdValue> cot = {val("f32", {rows, n}, g), val("f32", {rows, n / group}, nullptr)};
+        std::vector<AdValue> dc = {val("bf16", {rows, n}, dx), AdValue{}, AdValue{}};
+        AdjointFn fn = adjoint_find(rec.op, Side::device, rec.params, nullptr);
+        if (!fn) return -2;
+        AdjointCall call{rec, fwd, cot, &dc, nullptr, "", {}, false, nullptr, nullptr};
+        fn(call);
+        std::memcpy(dx, dc[0].value.data(), sizeof(double) * (size_t)(rows * n));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
 int64_t rh_weights_prepared() { return device_weight_count(); }
 void rh_weights_clear() { device_weight_clear(); }
 

@@ -85,3 +85,28 @@ def test_quant_refusals():
         quant_act_i8g(x, 48, rotated=True)
     with pytest.raises(R97qError, match="power of two"):
         quant_act_i8g(torch.zeros((4, 100), dtype=torch.bfloat16, device="cuda"), 64, rotated=True)
+
+
+@pytest.mark.parametrize("rows,n,group", [(12, 512, 128), (7, 1024, 1024)])
+def test_had_quant_device_row(rows, n, group):
+    """The had_quant_act_i8g device row (registered like the reference's, src/adjoint/device/
+    quant.hip:958) called through the registry against the oracle's adjoint."""
+    import ctypes as C
+
+    from test_rows import check, hook, p
+
+    print(f"case had_quant row rows={rows} n={n} group={group}", flush=True)
+    L = hook()
+    L.rh_had_quant.argtypes = [C.c_int64] * 3 + [C.c_void_p] * 4
+    rng = np.random.default_rng(rows + n)
+    x = S.bf16_bits_to_f32(S.f32_to_bf16_bits(rng.standard_normal((rows, n)).astype(np.float32))).astype(np.float64)
+    _, scale, _ = O.quant_act_i8g(x, group, True)
+    scale = scale.astype(np.float32).astype(np.float64)  # as the forward writes it
+    g = rng.standard_normal((rows, n)).astype(np.float32).astype(np.float64)
+    dx0 = rng.standard_normal((rows, n))
+    dx = dx0.copy()
+    check(L, L.rh_had_quant(rows, n, group, p(x), p(scale), p(g), p(dx)))
+    want = O.quant_act_i8g_adjoint(x, scale, g, group, True, dx=dx0)
+    assert np.allclose(dx, want, rtol=1e-6, atol=1e-6 * np.abs(want - dx0).max())
+    # a group wider than the device row serves finds no row (the host row takes it)
+    assert L.rh_had_quant(1, 2048, 2048, p(np.zeros(2048)), p(np.ones(1)), p(np.zeros(2048)), p(np.zeros(2048))) == -2
