@@ -53,9 +53,10 @@ def parse():
     ap.add_argument("--weight-form", default="trellis", choices=["trellis", "codes8"],
                     help="the prepared weight the kernels read: the trellis stream (decoded inside the "
                          "kernels), or the same weight in the int8-code form")
-    ap.add_argument("--workload", default="qlinear", choices=["qlinear", "vocab_head"],
+    ap.add_argument("--workload", default="qlinear", choices=["qlinear", "vocab_head", "c5_stack"],
                     help="qlinear: the C2 fwd+bwd step (the headline); vocab_head: the vocabulary head's "
-                         "transposed product at a 248320-row head, n_embd 2048, --vocab-rows token rows")
+                         "transposed product at a 248320-row head, n_embd 2048, --vocab-rows token rows; "
+                         "c5_stack: one whole LoRA step of the 24-layer stack (BASELINE config 5)")
     ap.add_argument("--vocab-rows", type=int, default=4096)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (3 launches), the known-size "
@@ -252,6 +253,107 @@ def vocab_head_bench(args):
     }), flush=True)
 
 
+# C5: per layer (hidden 2048) attn-in 2048->8192, attn-out 4096->2048, gate/up 2048->6144, down
+# 6144->2048; 24 layers; LoRA rank 16 alpha 32 on every projection; T = 32768 tokens
+C5_PROJ = [(8192, 2048), (2048, 4096), (6144, 2048), (2048, 6144)]  # (N, K)
+C5_LAYERS, C5_T, C5_R, C5_ALPHA = 24, 32768, 16, 32.0
+
+
+def c5_stack_bench(args):
+    """One complete LoRA step of the 24-layer stack on one GPU: the forward of every projection,
+    layer by layer, then the backward in reverse (dX, dA, dB, the adapters' gradients staged), then
+    AdamW on all 192 factors with their bf16 copies refreshed. Synthetic: the 96 weights are random
+    b5 trellis.mad codes (any bytes are valid codes) with an f32 row scale and scale.col, prepared
+    on the card; each projection's X and dY are shared random bf16 buffers of its shape (the
+    projections between them -- norms, attention, the gated product -- are not this path)."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    from r9700training_amd import R97Q_F32, _ptr, _stream, check, lib
+    from r9700training_amd.optim import DeviceAdamW, config
+    from r9700training_amd.qlinear import QWeight, bwd_workspace, device_desc, fwd_workspace
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    T, r, s = C5_T, C5_R, C5_ALPHA / C5_R
+    L = lib()
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    rng = np.random.default_rng(args.seed)
+    weights, keep = [], []
+    for _layer in range(C5_LAYERS):
+        for N, K in C5_PROJ:
+            codes = torch.randint(0, 256, (N, K * 5 // 8), dtype=torch.uint8, device=dev, generator=g)
+            scale = torch.from_numpy((0.0005 + 0.01 * rng.random(N)).astype(np.float32).view(np.uint8)).to(dev)
+            cf = torch.from_numpy((0.5 + rng.random(K // 128)).astype(np.float32)).to(dev)
+            d = device_desc(dict(codes=codes, scale=scale), N, K, dict(
+                bits=5, state_bits=16, run_rows=256, rb=1, mad=1, round_mad=1, mad_a=0x2F1E3D | 1,
+                mad_b=0x9E3779B9, codes_row_bytes=K * 5 // 8, scale_dtype=0, scale_block_cols=0, scale_row_bytes=4))
+            weights.append(QWeight(d, scale_col=cf))
+            keep += [codes, scale, cf]
+    X = {K: torch.randn((T, K), dtype=torch.bfloat16, device=dev, generator=g) for _, K in C5_PROJ}
+    dY = {N: torch.randn((T, N), dtype=torch.bfloat16, device=dev, generator=g) for N, _ in C5_PROJ}
+    Y = {N: torch.empty((T, N), dtype=torch.float32, device=dev) for N, _ in C5_PROJ}
+    dX = {K: torch.empty((T, K), dtype=torch.float32, device=dev) for _, K in C5_PROJ}
+    A = [(0.01 * torch.randn((r, K), generator=g, device=dev)).to(torch.bfloat16)
+         for _ in range(C5_LAYERS) for _, K in C5_PROJ]
+    B = [(0.01 * torch.randn((N, r), generator=g, device=dev)).to(torch.bfloat16)
+         for _ in range(C5_LAYERS) for N, _ in C5_PROJ]
+    tt = [torch.empty((T, r), dtype=torch.float32, device=dev) for _ in A]
+    dA = [torch.zeros((r, a.shape[1]), dtype=torch.float32, device=dev) for a in A]
+    dB = [torch.zeros((b.shape[0], r), dtype=torch.float32, device=dev) for b in B]
+    wsf = max((fwd_workspace(T, N, K, r, dev) for N, K in C5_PROJ), key=lambda x: x.numel())
+    wsb = max((bwd_workspace(T, N, K, r, dev) for N, K in C5_PROJ), key=lambda x: x.numel())
+    masters = [a.float().contiguous() for a in A] + [b.float().contiguous() for b in B]
+    copies = A + B
+    opt = DeviceAdamW(masters, config(lr=1e-4), bf16_out=copies)
+    stream = torch.cuda.current_stream()
+    st = _stream(stream)
+    P = _ptr
+
+    def lora_step():
+        for i, w in enumerate(weights):
+            N, K = C5_PROJ[i % 4]
+            check(L.r97q_lora_fwd_prep(T, N, K, P(X[K]), P(A[i]), r, s, P(tt[i]), P(wsf), wsf.numel(), st), "prep")
+            check(L.r97q_qlinear_fwd_base(C.byref(w.w), P(X[K]), T, P(B[i]), r, P(Y[N]), R97Q_F32, P(wsf),
+                                          wsf.numel(), st), "fwd")
+        for i in reversed(range(len(weights))):
+            N, K = C5_PROJ[i % 4]
+            w = weights[i]
+            check(L.r97q_lora_bwd_prep(T, N, K, P(dY[N]), P(A[i]), P(B[i]), P(tt[i]), r, s, P(wsb), wsb.numel(), st),
+                  "bwd_prep")
+            check(L.r97q_lora_bwd_grads(T, N, K, P(X[K]), P(dY[N]), r, P(dA[i]), P(dB[i]), P(wsb), wsb.numel(), st),
+                  "grads")
+            check(L.r97q_qlinear_dx_base(C.byref(w.w), P(dY[N]), T, r, P(dX[K]), R97Q_F32, 0, P(wsb), wsb.numel(), st),
+                  "dx")
+        opt.step(dA + dB, stream=stream, staged=True)
+
+    steps, warmup = max(1, min(args.steps, 5)), max(1, min(args.warmup, 2))
+    for _ in range(warmup):
+        lora_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        lora_step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    total = C5_LAYERS * sum(flops(T, N, K, r) for N, K in C5_PROJ)
+    tf = total / (ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "C5 LoRA-step tokens/s (24-layer stack, fwd + bwd + AdamW on the adapters)",
+        "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+        "tflops": round(tf, 3),
+        "config": {"workload": "C5: 24 layers x (2048->8192, 4096->2048, 2048->6144, 6144->2048) b5 trellis.mad, "
+                               "LoRA r16 alpha 32 on every projection, T=32768, Y/dX f32",
+                   "T": T, "layers": C5_LAYERS, "rank": r},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "memory_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 2),
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -275,6 +377,8 @@ def main():
 
     if args.workload == "vocab_head":
         return vocab_head_bench(args)
+    if args.workload == "c5_stack":
+        return c5_stack_bench(args)
 
     from r9700training_amd import R97Q_BF16, R97Q_F32, _ptr, _stream, check, lib
     from r9700training_amd.qlinear import bwd_workspace, fwd_workspace
