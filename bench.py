@@ -56,7 +56,7 @@ def parse():
     ap.add_argument("--workload", default="qlinear", choices=["qlinear", "vocab_head", "c5_stack"],
                     help="qlinear: the C2 fwd+bwd step (the headline); vocab_head: the vocabulary head's "
                          "transposed product at a 248320-row head, n_embd 2048, --vocab-rows token rows; "
-                         "c5_stack: one whole LoRA step of the 24-layer stack (BASELINE config 5)")
+                         "c5_stack: one whole LoRA step of the 24-layer stack (T=32768, rank 16 on every projection)")
     ap.add_argument("--vocab-rows", type=int, default=4096)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (3 launches), the known-size "
