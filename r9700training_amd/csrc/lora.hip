@@ -514,9 +514,10 @@ int launch_lora_down(const DownArgs& a, hipStream_t s) {
 }
 
 int64_t grad_chunks(int64_t T, int64_t K, int64_t N) {
-    // about 256 workgroups over dA's and dB's column blocks (one a CU)
+    // about 128 workgroups over dA's and dB's column blocks (measured at C2 against 256 and 512:
+    // fewer chunk partials for grad_reduce to add outweigh the idle half of the chip, 2 us a step)
     const int64_t cols = (K + kGradCols - 1) / kGradCols + (N + kGradCols - 1) / kGradCols;
-    int64_t chunks = (256 + cols - 1) / cols;
+    int64_t chunks = (128 + cols - 1) / cols;
     const int64_t tiles = grad_ld(T) / 64;  // no chunk smaller than one 64-token tile
     if (chunks > tiles) chunks = tiles;
     return chunks < 1 ? 1 : chunks;
