@@ -360,10 +360,9 @@ struct Loop {
         const int half = lane >> 5, l32 = lane & 31;
         const int64_t kn = (int64_t)(s + 1 < nsteps ? s + 1 : nsteps - 1) * kStep;
         words_for(s + 2 < nsteps ? s + 2 : nsteps - 1, fetch);
-        // The token tile of step s+1: the dX kernel issues its loads here; the forward issues
-        // them half in each of rounds 1 and 2 (measured: 12% faster for the forward, 2% slower
-        // for dX).
-        if constexpr (!FWD) load_act(gr, xn, kn);
+        // The token tile of step s+1 is issued inside the rounds: the forward half in each of
+        // rounds 1 and 2, dX all in round 0 after its fragment reads (measured against issuing it
+        // here at the step's start: 12% faster for the forward, 1% for dX).
         // The two waves that share a SIMD (w and w+4) work in opposite phases: wave w+4 decodes
         // the next tile before this step's MFMAs, wave w after them, so each one's decode VALU
         // issues while the other one's MFMAs keep the matrix core busy. (The next tile's buffer
@@ -385,6 +384,8 @@ struct Loop {
             if constexpr (FWD) {
                 if (j == 1) load_act<0, 4>(gr, xn, kn);
                 if (j == 2) load_act<4, 8>(gr, xn, kn);
+            } else {
+                if (j == 0) load_act(gr, xn, kn);
             }
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
