@@ -86,24 +86,30 @@ __global__ __launch_bounds__(256) void vocab_pad_kernel(int8_t* __restrict__ cod
 }
 
 // a[z][m][n] = dy[m, ids[z*R + n] - vocab_offset] for class rows inside the batch's rows [0, ns)
-// and an id inside this vocabulary, else 0: grid (Np/256, token rows from m0, Z), a column a
-// thread (measured: 8 columns a thread with one 16-byte store is 40% slower -- fewer loads in
-// flight)
+// and an id inside this vocabulary, else 0: grid (Np/256, token rows from m0 in groups of
+// kGatherRows, Z), a column and kGatherRows token rows a thread (the id read once for them;
+// measured: 8 columns a thread with one 16-byte store is 40% slower -- fewer loads in flight)
+constexpr int kGatherRows = 8;
 __global__ __launch_bounds__(256) void vocab_gather_kernel(const uint16_t* __restrict__ dy,
                                                            const int32_t* __restrict__ ids,
                                                            uint16_t* __restrict__ a, int64_t rows, int64_t vocab,
                                                            int64_t vocab_offset, int64_t R, int64_t ns, int64_t Np,
                                                            int64_t m0) {
     const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t m = m0 + blockIdx.y, z = blockIdx.z;
+    const int64_t mb = m0 + (int64_t)blockIdx.y * kGatherRows, z = blockIdx.z;
     if (n >= Np) return;
     const int64_t r = z * R + n;
-    uint16_t v = 0;
+    int64_t col = -1;
     if (n < R && r < ns) {
         const int64_t id = ids[r];
-        if (id >= vocab_offset && id < vocab_offset + vocab) v = dy[m * vocab + (id - vocab_offset)];
+        if (id >= vocab_offset && id < vocab_offset + vocab) col = id - vocab_offset;
     }
-    a[(z * rows + m) * Np + n] = v;
+#pragma unroll
+    for (int i = 0; i < kGatherRows; ++i) {
+        const int64_t m = mb + i;
+        if (m >= rows) break;
+        a[(z * rows + m) * Np + n] = col >= 0 ? dy[m * vocab + col] : (uint16_t)0;
+    }
 }
 
 // d_x[i] += part[0][i] + part[1][i] + ... (the ranges in order)
@@ -241,9 +247,12 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
                 }
                 if (int e = decode_tiled(d, Np, s)) return e;
             }
-            for (int64_t m0 = 0; m0 < rows; m0 += 65535) {  // gridDim.y's limit
-                const int64_t mr = rows - m0 < 65535 ? rows - m0 : 65535;
-                hipLaunchKernelGGL(vocab_gather_kernel, dim3(blocks(Np, 256), (unsigned)mr, (unsigned)Z), dim3(256), 0,
+            const int64_t span = 65535 * (int64_t)kGatherRows;  // gridDim.y's limit
+            for (int64_t m0 = 0; m0 < rows; m0 += span) {
+                const int64_t mr = rows - m0 < span ? rows - m0 : span;
+                hipLaunchKernelGGL(vocab_gather_kernel,
+                                   dim3(blocks(Np, 256), (unsigned)((mr + kGatherRows - 1) / kGatherRows), (unsigned)Z),
+                                   dim3(256), 0,
                                    s, dy, static_cast<const int32_t*>(cls.ids) + b0, gathered, rows, plan->vocab,
                                    plan->vocab_offset, R, nb, Np, m0);
                 if (int e = launch_status("vocab_gather_kernel")) return e;
