@@ -163,19 +163,22 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
     for (int64_t q = r; q < r_end; ++q) {
         st = ((st << d.bits) | load_bits(d.codes + (q - d.row0) * d.codes_row_bytes, d.bits, j)) & mask;
         const int32_t v = state_value(d, st);
-        int32_t out;
-        float sc;
+        int32_t out = v;
         if (d.rb > 1) {
             if (q % d.rb == 0) cur = block_max(d, q, kb);
             const float sr = block_scale(d, q, kb);
-            sc = cur;
             out = cur <= 0.0f ? 0 : rb_round(v, sr / cur, d.round_mad);
-        } else {
-            sc = block_scale(d, q, kb);
-            out = v;
+            if (first) d.out_scale[O::scale(d, q, kb, scale_ld)] = f32_to_bf16(cur);
         }
         d.out_codes[O::code(d, q, j)] = (int8_t)out;
-        if (first) d.out_scale[O::scale(d, q, kb, scale_ld)] = f32_to_bf16(sc);
+    }
+    // rb == 1: the chunk's scales of the 128-column block, one row a lane of the block's first
+    // lanes (a wave that ran the generic scale read for one lane on every row spent most of the
+    // launch there)
+    const int64_t i = j & 127;
+    if (d.rb == 1 && i < r_end - r) {
+        const int64_t q = r + i;
+        d.out_scale[O::scale(d, q, kb, scale_ld)] = f32_to_bf16(block_scale(d, q, kb));
     }
 }
 
