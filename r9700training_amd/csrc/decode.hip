@@ -160,8 +160,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
     // a block takes the block's value, which is what the serial walk carried there.
     float cur = 0.0f;
     if (d.rb > 1 && (r % d.rb) != 0) cur = block_max(d, (r / d.rb) * d.rb, kb);
-    for (int64_t q = r; q < r_end; ++q) {
-        st = ((st << d.bits) | load_bits(d.codes + (q - d.row0) * d.codes_row_bytes, d.bits, j)) & mask;
+    // the code row and the output byte advance by fixed steps down the chunk (a TILED chunk never
+    // leaves its 8-row unit: it is 8 rows from a multiple of 8, or 1 row)
+    const uint8_t* row = d.codes + (r - d.row0) * d.codes_row_bytes;
+    int8_t* dst = d.out_codes + O::code(d, r, j);
+    const int64_t dst_step = TILED ? 2 : d.cols;
+    for (int64_t q = r; q < r_end; ++q, row += d.codes_row_bytes, dst += dst_step) {
+        st = ((st << d.bits) | load_bits(row, d.bits, j)) & mask;
         const int32_t v = state_value(d, st);
         int32_t out = v;
         if (d.rb > 1) {
@@ -170,7 +175,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
             out = cur <= 0.0f ? 0 : rb_round(v, sr / cur, d.round_mad);
             if (first) d.out_scale[O::scale(d, q, kb, scale_ld)] = f32_to_bf16(cur);
         }
-        d.out_codes[O::code(d, q, j)] = (int8_t)out;
+        *dst = (int8_t)out;
     }
     // rb == 1: the chunk's scales of the 128-column block, one row a lane of the block's first
     // lanes (a wave that ran the generic scale read for one lane on every row spent most of the
