@@ -54,6 +54,8 @@ int64_t grad_chunk_rows(int64_t T, int64_t K, int64_t N);
 
 int launch_lora_down(const DownArgs& a, hipStream_t s);
 int launch_lora_grads(int r, const GradArgs& g, int nz, hipStream_t s);
+// dst = the fused kernels' tiled copy (act_tiles.h) of act [T, R] bf16 (R a multiple of 64)
+int launch_act_tile(const uint16_t* act, int64_t T, int64_t R, uint16_t* dst, hipStream_t s);
 int launch_transpose2(const uint16_t* B, uint16_t* Bt, int64_t N, const uint16_t* A, uint16_t* At,
                       int64_t K, int r, hipStream_t s);
 // P [T, 2r] / Pt [2r, ldt] = [hi | lo](scale * U), U f32 [T, r]; either output may be null

@@ -458,6 +458,21 @@ __global__ __launch_bounds__(256) void coded_x_kernel(const int8_t* __restrict__
     xlo[i] = lo;
 }
 
+// ---------------------------------------------------------------- the tiled token operand
+// dst = the fused kernels' tiled copy (act_tiles.h) of act [T, R] bf16. One workgroup a 32-row x
+// 64-value block: thread t reads row t/8's 16-byte chunk t%8 (128 contiguous bytes a row) and
+// writes it to lane 32*(chunk/4) + row of slice chunk%4 (128 contiguous bytes for eight rows);
+// rows past T are written as zero.
+__global__ __launch_bounds__(256) void act_tile_kernel(const uint16_t* __restrict__ act, int64_t T, int64_t R,
+                                                       uint16_t* __restrict__ dst) {
+    const int64_t s = blockIdx.x, rb = blockIdx.y;
+    const int i = threadIdx.x >> 3, c = threadIdx.x & 7;
+    const int64_t m = 32 * rb + i;
+    uint4 v = {0u, 0u, 0u, 0u};
+    if (m < T) v = *reinterpret_cast<const uint4*>(act + m * R + 64 * s + 8 * c);
+    *reinterpret_cast<uint4*>(dst + ((s * (int64_t)gridDim.y + rb) * 4 + (c & 3)) * 512 + (32 * (c >> 2) + i) * 8) = v;
+}
+
 // ---------------------------------------------------------------- transposes
 // y 0: Bt[q][n] = B[n][q] for q < r, 0 for r <= q < rd;  y 1: At[k][j] = A[j][k]
 __global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* __restrict__ B,
@@ -572,6 +587,16 @@ int launch_coded_x(const int8_t* code, const float* a_scale, int64_t T, int64_t 
     hipLaunchKernelGGL(coded_x_kernel, dim3((unsigned)((T * K + 255) / 256)), dim3(256), 0, s, code, a_scale, T, K,
                        groups, gw, xhi, xlo);
     return launch_status("coded_x_kernel");
+}
+
+int launch_act_tile(const uint16_t* act, int64_t T, int64_t R, uint16_t* dst, hipStream_t s) {
+    if (R % 64 != 0 || T <= 0) {
+        set_error("act tile: T %lld R %lld (R a multiple of 64)", (long long)T, (long long)R);
+        return R97Q_EINVAL;
+    }
+    hipLaunchKernelGGL(act_tile_kernel, dim3((unsigned)(R / 64), (unsigned)((T + 31) / 32)), dim3(256), 0, s, act, T,
+                       R, dst);
+    return launch_status("act_tile_kernel");
 }
 
 int launch_transpose2(const uint16_t* B, uint16_t* Bt, int64_t N, const uint16_t* A, uint16_t* At,

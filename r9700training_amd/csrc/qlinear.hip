@@ -6,18 +6,21 @@
 //   backward  dt = s.dY.B;  dX = dY.W + dt.A;          (linear.cpp:221-243, lora.cpp:260-328,
 //             dA += dt^T.X;  dB += s.dY^T.t            451-521)
 //
-// Kernels: the fused decode + MFMA base products (qlinear_fused.hip) carry the adapter's
-// up-projection in their epilogue; the adapter's down products and factor gradients are
-// lora.hip's. A step is 2 launches forward (down, fused) and 4 backward (transposes, down, grads,
-// fused).
+// Kernels: the fused decode + MFMA base products (qlinear_rt.hip, fed the token operand from
+// its tiled copy in the workspace) carry the adapter's up-projection in their epilogue; the
+// adapter's down products, factor gradients and the token operand's tiled copy are lora.hip's.
+// The coded trunk's dX (the activation's group scale in the epilogue) and the vocabulary head run
+// the LDS-staged kernels of qlinear_fused.hip on the row-major operand.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 #include <cstring>
 
+#include "act_tiles.h"
 #include "iqr_device.h"
 #include "lora.h"
 #include "qlinear_fused.h"
+#include "qlinear_rt.h"
 #include "status.h"
 
 using namespace r97q;
@@ -33,30 +36,39 @@ struct Shape {
     int r;
 };
 
-// Workspace layout. Forward: P [T, 2r] | Apad [rd, K] (when r is not a multiple of 16).
-// Backward: Bt [rd, N] | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt] | partA [chunks, r, K]
-// | partB [chunks, r, N] (f32 partial sums of the factor gradients).
+// Workspace layout. Forward: Xt (X's tiled copy, act_tiles.h) | P [T, 2r] | Apad [rd, K] (when r
+// is not a multiple of 16).
+// Backward: dYt (dY's tiled copy) | Bt [rd, N] | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt]
+// | partA [chunks, r, K] | partB [chunks, r, N] (f32 partial sums of the factor gradients).
 struct FwdWs {
-    int64_t P, Apad, total;
+    int64_t Xt, P, Apad, total;
 };
 FwdWs fwd_ws(const Shape& s) {
     FwdWs w{};
-    if (s.r == 0) return w;
+    w.Xt = 0;
+    w.P = w.Xt + align256(act_tile_bytes(s.T, s.K));
+    if (s.r == 0) {
+        w.total = w.P;
+        return w;
+    }
     const int rd = down_rank(s.r);
-    w.P = 0;
     w.Apad = w.P + align256(s.T * 2 * s.r * 2);
     w.total = w.Apad + (rd != s.r ? align256((int64_t)rd * s.K * 2) : 0);
     return w;
 }
 struct BwdWs {
-    int64_t Bt, At, P, PtA, PtB, partA, partB, total;
+    int64_t dYt, Bt, At, P, PtA, PtB, partA, partB, total;
 };
 BwdWs bwd_ws(const Shape& s) {
     BwdWs w{};
-    if (s.r == 0) return w;
+    w.dYt = 0;
+    w.Bt = w.dYt + align256(act_tile_bytes(s.T, s.N));
+    if (s.r == 0) {
+        w.total = w.Bt;
+        return w;
+    }
     const int rd = down_rank(s.r);
     const int64_t ldt = grad_ld(s.T);
-    w.Bt = 0;
     w.At = w.Bt + align256((int64_t)rd * s.N * 2);
     w.P = w.At + align256(s.K * s.r * 2);
     w.PtA = w.P + align256(s.T * 2 * s.r * 2);
@@ -183,6 +195,8 @@ int check_ws(int64_t have, int64_t need, const void* ws, const char* who) {
 int fwd_prep(const Shape& sh, const uint16_t* X, const uint16_t* A, float scale, float* t_out,
              uint8_t* wsb, hipStream_t s) {
     const FwdWs ws = fwd_ws(sh);
+    if (int e = launch_act_tile(X, sh.T, sh.K, reinterpret_cast<uint16_t*>(wsb + ws.Xt), s)) return e;
+    if (sh.r == 0) return R97Q_OK;
     const int rank = sh.r, rd = down_rank(rank);
     const uint16_t* Wd = A;
     if (rd != rank) {
@@ -206,10 +220,11 @@ int fwd_prep(const Shape& sh, const uint16_t* X, const uint16_t* A, float scale,
     return launch_lora_down(a, s);
 }
 
-int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* X, const uint16_t* B, void* Y,
-             int32_t y_dtype, uint8_t* wsb, hipStream_t s) {
-    FwdParams p{};
-    p.X = X;
+// the register-fed fused product over the token operand's tiled copy `act` (forward or dX)
+int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act, const uint16_t* P,
+            const uint16_t* Q, void* out, int32_t out_dtype, int32_t accumulate, hipStream_t s) {
+    rt::Params p{};
+    p.act = act;
     p.T = sh.T;
     p.N = sh.N;
     p.K = sh.K;
@@ -218,21 +233,30 @@ int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* X, const uint
     p.a24 = w->mad_a & 0xFFFFFFu;
     p.b = w->mad_b;
     p.run_rows = w->run_rows;
-    p.P = sh.r > 0 ? reinterpret_cast<const uint16_t*>(wsb + fwd_ws(sh).P) : nullptr;
-    p.B = B;
+    p.P = sh.r > 0 ? P : nullptr;
+    p.Q = sh.r > 0 ? Q : nullptr;
     p.rank = sh.r;
-    p.Y = Y;
-    p.y_f32 = y_dtype == R97Q_F32;
-    p.mtiles = (int)((sh.T + kBM - 1) / kBM);
-    p.ntiles = (int)(sh.N / kBN);
+    p.out = out;
+    p.out_f32 = out_dtype == R97Q_F32;
+    p.accumulate = accumulate != 0;
+    p.mtiles = (int)((sh.T + rt::kBM - 1) / rt::kBM);
+    p.otiles = (int)((fwd ? sh.N : sh.K) / rt::kBN);
+    auto go = [&](auto fwd_fn, auto dx_fn) { fwd ? fwd_fn(p, s) : dx_fn(p, s); };
     switch (w->bits) {
-        case 3: launch_fwd<3>(p, s); break;
-        case 4: launch_fwd<4>(p, s); break;
-        case 5: launch_fwd<5>(p, s); break;
-        case 6: launch_fwd<6>(p, s); break;
-        default: launch_fwd<R97Q_CODES8>(p, s); break;
+        case 3: go(rt::launch_fwd<3>, rt::launch_dx<3>); break;
+        case 4: go(rt::launch_fwd<4>, rt::launch_dx<4>); break;
+        case 5: go(rt::launch_fwd<5>, rt::launch_dx<5>); break;
+        case 6: go(rt::launch_fwd<6>, rt::launch_dx<6>); break;
+        default: go(rt::launch_fwd<R97Q_CODES8>, rt::launch_dx<R97Q_CODES8>); break;
     }
-    return launch_status("qlinear_fwd_kernel");
+    return launch_status(fwd ? "qlinear_rt_kernel<fwd>" : "qlinear_rt_kernel<dx>");
+}
+
+int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* B, void* Y, int32_t y_dtype, uint8_t* wsb,
+             hipStream_t s) {
+    const FwdWs ws = fwd_ws(sh);
+    return rt_base(w, true, sh, reinterpret_cast<const uint16_t*>(wsb + ws.Xt),
+                   reinterpret_cast<const uint16_t*>(wsb + ws.P), B, Y, y_dtype, 0, s);
 }
 
 // B^T [rd, N] (zero rows past r), A^T [K, r]; dt = s.dY.B as P = [hi | lo](dt) for the fused dX
@@ -240,6 +264,8 @@ int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* X, const uint
 int bwd_prep(const Shape& sh, const uint16_t* dY, const uint16_t* A, const uint16_t* B, const float* t,
              float scale, uint8_t* wsb, hipStream_t s) {
     const BwdWs ws = bwd_ws(sh);
+    if (int e = launch_act_tile(dY, sh.T, sh.N, reinterpret_cast<uint16_t*>(wsb + ws.dYt), s)) return e;
+    if (sh.r == 0) return R97Q_OK;
     uint16_t* Bt = reinterpret_cast<uint16_t*>(wsb + ws.Bt);
     uint16_t* At = reinterpret_cast<uint16_t*>(wsb + ws.At);
     if (int e = launch_transpose2(B, Bt, sh.N, A, At, sh.K, sh.r, s)) return e;
@@ -281,9 +307,18 @@ int bwd_grads(const Shape& sh, const uint16_t* X, const uint16_t* dY, float* dA,
     return launch_lora_grads(sh.r, g, nz, s);
 }
 
-int dx_base(const R97qWeight* w, const Shape& sh, const uint16_t* dY, void* dX, int32_t dx_dtype,
-            int32_t accumulate, uint8_t* wsb, hipStream_t s, const float* a_scale = nullptr) {
+int dx_base(const R97qWeight* w, const Shape& sh, void* dX, int32_t dx_dtype, int32_t accumulate, uint8_t* wsb,
+            hipStream_t s) {
     const BwdWs ws = bwd_ws(sh);
+    return rt_base(w, false, sh, reinterpret_cast<const uint16_t*>(wsb + ws.dYt),
+                   reinterpret_cast<const uint16_t*>(wsb + ws.P), reinterpret_cast<const uint16_t*>(wsb + ws.At), dX,
+                   dx_dtype, accumulate, s);
+}
+
+// the LDS-staged dX kernel over row-major dY with the coded trunk's activation scale in its
+// epilogue (no adapter, no workspace)
+int dx_scaled(const R97qWeight* w, const Shape& sh, const uint16_t* dY, void* dX, int32_t dx_dtype,
+              int32_t accumulate, hipStream_t s, const float* a_scale) {
     DxParams p{};
     p.a_scale = a_scale;
     p.a_scale_ld = sh.K / kBN;
@@ -296,9 +331,9 @@ int dx_base(const R97qWeight* w, const Shape& sh, const uint16_t* dY, void* dX, 
     p.a24 = w->mad_a & 0xFFFFFFu;
     p.b = w->mad_b;
     p.run_rows = w->run_rows;
-    p.P = sh.r > 0 ? reinterpret_cast<const uint16_t*>(wsb + ws.P) : nullptr;
-    p.At = sh.r > 0 ? reinterpret_cast<const uint16_t*>(wsb + ws.At) : nullptr;
-    p.rank = sh.r;
+    p.P = nullptr;
+    p.At = nullptr;
+    p.rank = 0;
     p.dX = dX;
     p.dx_f32 = dx_dtype == R97Q_F32;
     p.accumulate = accumulate != 0;
@@ -342,9 +377,8 @@ int r97q_lora_fwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* X, const
     const char* who = "r97q_lora_fwd_prep";
     if (int e = shape_ok(T, N, K, who)) return e;
     if (int e = check_rank(rank, who)) return e;
-    if (rank == 0) return R97Q_OK;
-    if (!X || !A || !t_out) {
-        set_error("%s: null X, A or t_out", who);
+    if (!X || (rank > 0 && (!A || !t_out))) {
+        set_error("%s: null X, or A or t_out with rank > 0", who);
         return R97Q_EINVAL;
     }
     const Shape sh{T, N, K, rank};
@@ -365,7 +399,7 @@ int r97q_qlinear_fwd_base(const R97qWeight* w, const uint16_t* X, int64_t T, con
     }
     const Shape sh{T, w->rows, w->cols, rank};
     if (int e = check_ws(workspace_bytes, fwd_ws(sh).total, workspace, who)) return e;
-    return fwd_base(w, sh, X, B, Y, y_dtype, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
+    return fwd_base(w, sh, B, Y, y_dtype, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
 }
 
 int r97q_qlinear_lora_fwd(const R97qWeight* w, const uint16_t* X, int64_t T, const uint16_t* A,
@@ -388,9 +422,8 @@ int r97q_qlinear_lora_fwd(const R97qWeight* w, const uint16_t* X, int64_t T, con
     if (int e = check_ws(workspace_bytes, fwd_ws(sh).total, workspace, who)) return e;
     uint8_t* wsb = static_cast<uint8_t*>(workspace);
     const hipStream_t s = (hipStream_t)stream;
-    if (rank > 0)
-        if (int e = fwd_prep(sh, X, A, scale, t_out, wsb, s)) return e;
-    return fwd_base(w, sh, X, B, Y, y_dtype, wsb, s);
+    if (int e = fwd_prep(sh, X, A, scale, t_out, wsb, s)) return e;
+    return fwd_base(w, sh, B, Y, y_dtype, wsb, s);
 }
 
 int r97q_lora_bwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* dY, const uint16_t* A,
@@ -400,9 +433,8 @@ int r97q_lora_bwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* dY, cons
     const char* who = "r97q_lora_bwd_prep";
     if (int e = shape_ok(T, N, K, who)) return e;
     if (int e = check_rank(rank, who)) return e;
-    if (rank == 0) return R97Q_OK;
-    if (!dY || !A || !B) {
-        set_error("%s: null dY, A or B", who);
+    if (!dY || (rank > 0 && (!A || !B))) {
+        set_error("%s: null dY, or A or B with rank > 0", who);
         return R97Q_EINVAL;
     }
     const Shape sh{T, N, K, rank};
@@ -440,8 +472,7 @@ int r97q_qlinear_dx_base(const R97qWeight* w, const uint16_t* dY, int64_t T, int
     }
     const Shape sh{T, w->rows, w->cols, rank};
     if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
-    return dx_base(w, sh, dY, dX, dx_dtype, dx_accumulate, static_cast<uint8_t*>(workspace),
-                   (hipStream_t)stream);
+    return dx_base(w, sh, dX, dx_dtype, dx_accumulate, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
 }
 
 int r97q_qlinear_lora_bwd(const R97qWeight* w, const uint16_t* X, const uint16_t* dY, int64_t T,
@@ -465,11 +496,10 @@ int r97q_qlinear_lora_bwd(const R97qWeight* w, const uint16_t* X, const uint16_t
     if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
     uint8_t* wsb = static_cast<uint8_t*>(workspace);
     const hipStream_t s = (hipStream_t)stream;
-    if (rank > 0) {
-        if (int e = bwd_prep(sh, dY, A, B, t, scale, wsb, s)) return e;
+    if (int e = bwd_prep(sh, dY, A, B, t, scale, wsb, s)) return e;
+    if (rank > 0)
         if (int e = bwd_grads(sh, X, dY, dA, dB, wsb, s)) return e;
-    }
-    return dx_base(w, sh, dY, dX, dx_dtype, dx_accumulate, wsb, s);
+    return dx_base(w, sh, dX, dx_dtype, dx_accumulate, wsb, s);
 }
 
 int r97q_gemm_nt_q_dx(const R97qWeight* w, const uint16_t* dY, int64_t T, const float* a_scale, void* dA,
@@ -482,7 +512,7 @@ int r97q_gemm_nt_q_dx(const R97qWeight* w, const uint16_t* dY, int64_t T, const 
         return R97Q_EINVAL;
     }
     const Shape sh{T, w->rows, w->cols, 0};
-    return dx_base(w, sh, dY, dA, da_dtype, accumulate, nullptr, (hipStream_t)stream, a_scale);
+    return dx_scaled(w, sh, dY, dA, da_dtype, accumulate, (hipStream_t)stream, a_scale);
 }
 
 int64_t r97q_lora_shrink_q_bwd_workspace_bytes(int64_t T, int64_t K, int32_t rank) {

@@ -1,0 +1,40 @@
+// qlinear_rt.h -- parameters and launchers of the register-fed fused IQR-decode + MFMA kernels
+// (qlinear_rt.hip, compiled once per code width with -DR97Q_BITS=3..6, 8).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace r97q {
+namespace rt {
+
+constexpr int kBM = 512;      // tokens per workgroup (four waves of 128)
+constexpr int kBN = 128;      // outputs per workgroup: features n (forward) or columns k (dX)
+constexpr int kStep = 64;     // reduction depth per main-loop step
+constexpr int kThreadsMax = 512; // at most 8 waves (two per SIMD)
+
+// One launch of either product. The token operand `act` is the tiled copy (act_tiles.h) of X
+// [T, K] (forward) or dY [T, N] (dX).
+struct Params {
+    const uint16_t* act;
+    int64_t T, N, K;           // the weight is [N, K]
+    const uint32_t* stream;
+    const uint16_t* scale_t;
+    uint32_t a24, b;
+    int64_t run_rows;
+    const uint16_t* P;         // [T, 2r] bf16: hi | lo of s.t (forward) or dt (dX); null when r = 0
+    const uint16_t* Q;         // [outputs, r] bf16: B (forward) or A^T (dX)
+    int rank;
+    void* out;                 // Y [T, N] or dX [T, K]
+    int out_f32;
+    int accumulate;            // dX only: add into `out`
+    int mtiles, otiles;
+};
+
+template <int BITS>
+void launch_fwd(const Params& p, hipStream_t s);
+template <int BITS>
+void launch_dx(const Params& p, hipStream_t s);
+
+}  // namespace rt
+}  // namespace r97q

@@ -1,0 +1,562 @@
+// qlinear_rt.hip -- the register-fed fused IQR-decode + bf16-MFMA base products of the quantized
+// linear, for CDNA4 (gfx950). Compiled once per code width (-DR97Q_BITS=3..6, or 8 for the
+// int8-code form).
+//
+//   qlinear_rt_kernel<true>    Y[T,N]  = X[T,K] . W^T   (+ the adapter's s.t.B^T in the epilogue)
+//   qlinear_rt_kernel<false>   dX[T,K] = dY[T,N] . W    (+ the adapter's dt.A in the epilogue)
+//
+// The reference's rows are gemm_nt_twin / gemm_nt_adjoint over a stored weight
+// (src/adjoint/host/linear.cpp:132-243): W(n,k) = code(n,k) * bf16 scale(n, k/128).
+//
+// Shape of a launch. A workgroup owns a 512-token x 128-output tile and has WAVES waves (4: one per
+// SIMD, each 128 tokens x 128 outputs, 256 accumulation registers; 8: two per SIMD, each 64 tokens
+// x 128 outputs, 128 registers, so one wave's stalls are covered by the other's MFMAs). Each wave
+// accumulates in v_mfma_f32_32x32x16_bf16 tiles. The reduction walks in 64-deep steps of four
+// rounds (one 16-deep slice each):
+//   * the token operand (X, or dY) is loaded straight into registers from its tiled copy
+//     (act_tiles.h: every fragment one coalesced 1 KiB load); a round's fragments are reloaded
+//     with the next step's once its MFMAs have issued. A wave's token rows are its own, so they
+//     never pass through LDS;
+//   * the weight tile of the next step (128 x 64 values) is decoded by every lane of the
+//     workgroup from the column streams (iqr_device.h) into one half of a double-buffered,
+//     XOR-swizzled bf16 LDS tile that all waves read (each decoded value feeds 512 tokens); the
+//     decode is spread over the step's first three rounds;
+//   * one barrier a step, after the third round: the next tile is complete and no wave still reads
+//     the tile it replaces, so the fourth round's MFMAs run while the next tile's first fragments
+//     are read.
+// LDS holds only the two decoded tiles (32 KiB); per step and CU it takes 16 KiB of decoded writes
+// and WAVES x 16 KiB of fragment reads against 256 MFMAs.
+//
+// Decode of one trellis value (6 VALU ops): the 16-bit state is a bit-field (v_bfe_u32, or
+// v_alignbit + mask when it straddles a dword); the codebook hash is v_mad_u32_u24 + mask;
+// v_sad_u8 against zero sums its bytes with 1024 in the accumulator, which makes the low half an
+// f16 of 1024 + byte-sum; one v_fma_mix_f32 with the exact constant -1150 * scale gives
+// (byte-sum - 126) * scale exactly, and v_cvt_pk_bf16_f32 rounds once to bf16: the decoded tile
+// is bf16(code * scale), bit for bit. The int8-code form reads (code ^ 0x80) as an unsigned byte
+// and applies -128 * scale the same way.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <type_traits>
+
+#include "act_tiles.h"
+#include "iqr_device.h"
+#include "qlinear_rt.h"
+
+#ifndef R97Q_BITS
+#error "compile with -DR97Q_BITS=<code width>"
+#endif
+
+namespace r97q {
+namespace rt {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((__vector_size__(16)));
+typedef __bf16 bf16x2 __attribute__((__vector_size__(4)));
+typedef float f32x16 __attribute__((__vector_size__(64)));
+
+constexpr int kNI = kBN / 32;               // 4 output blocks of 32
+constexpr int kTileBytes = kBN * kStep * 2; // one decoded bf16 tile: 128 rows x 128 bytes
+constexpr int kBlock = 32 * kStep;          // bf16 elements in one 32 x 64 block of the tiled operand
+
+// the geometry of a workgroup of W waves
+template <int W>
+struct Geo {
+    static constexpr int kWaveM = kBM / W;  // tokens a wave: 128 or 64
+    static constexpr int kMI = kWaveM / 32; // its token blocks of 32
+    static constexpr int kFRows = 32 / W;   // forward decode: rows a lane takes of each 32-row segment
+    static constexpr int kDRows = 64 / W;   // dX decode: rows a lane takes of the step's 64
+    static_assert(W == 4 || W == 8, "4 or 8 waves");
+};
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint32_t comp(const uint4& v, int c) {
+    return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
+}
+__device__ __forceinline__ uint32_t comp(const uint2& v, int c) { return c == 0 ? v.x : v.y; }
+
+// XOR swizzle of a 128-byte LDS row's eight 16-byte chunks: 16 consecutive rows reading one
+// logical chunk land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+__device__ __forceinline__ uint8_t* chunk_at(uint8_t* tile, int row, int chunk) {
+    return tile + row * 128 + ((chunk ^ swz(row)) << 4);
+}
+
+// The end of the decode of a tile: this wave's LDS writes (and fragment reads) are done, then the
+// workgroup barrier. Vector-memory loads (the wave's own token rows, the stream words) are not
+// waited for: nothing another wave reads depends on them.
+__device__ __forceinline__ void tile_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// XCD-aware tile order: consecutive workgroup ids are dealt round-robin over the 8 XCDs;
+// renumber so each XCD's workgroups take one contiguous run of tiles (tokens outer, outputs
+// inner), which keeps a token panel in that XCD's L2.
+__device__ __forceinline__ int xcd_tile(int bid, int nwg) {
+    const int xcd = bid & 7, local = bid >> 3;
+    const int base = nwg >> 3, rem = nwg & 7;
+    return xcd * base + (xcd < rem ? xcd : rem) + local;
+}
+
+// ---------------------------------------------------------------- one lane's slice of a tile
+// ROWS consecutive rows ROWS*SLICE.. of a 32-row segment. Their trellis states are the 16-bit
+// windows at bits BITS*(31-i) of the segment's stream; together they span dwords D0..D1 (D1 ==
+// BITS is the first dword of the next segment in the stream: the segment below, or the run's top
+// one at the seam).
+template <int BITS, int ROWS, int SLICE>
+struct Span {
+    static constexpr int kLo = BITS * (32 - ROWS * (SLICE + 1));
+    static constexpr int kHi = BITS * (31 - ROWS * SLICE) + 16;
+    static constexpr int D0 = kLo / 32;
+    static constexpr int D1 = (kHi - 1) / 32;
+    static constexpr int NW = D1 - D0 + 1;
+    static_assert(D1 <= BITS, "a window reaches past the next segment's first dword");
+};
+
+// The words a lane decodes one tile from: the trellis stream dwords of its COLS columns, or its
+// 2*ROWS bytes of int8 codes; and its rows' bf16 scales (two a dword).
+template <int BITS, int ROWS, int COLS, int SLICE, bool C8 = (BITS == R97Q_CODES8)>
+struct LaneWords {
+    using S = Span<BITS, ROWS, SLICE>;
+    typename std::conditional<COLS == 4, uint4, uint2>::type w[S::NW];
+    uint32_t s[ROWS / 2];
+};
+template <int BITS, int ROWS, int COLS, int SLICE>
+struct LaneWords<BITS, ROWS, COLS, SLICE, true> {
+    uint32_t c[ROWS];  // forward: 4 columns x ROWS rows; dX: 2 columns x ROWS rows (COLS * ROWS bytes)
+    uint32_t s[ROWS / 2];
+};
+
+// n bf16 scales (n = 4, 8 or 16) from 8-byte-aligned `src` into s[n / 2]
+template <int N>
+__device__ __forceinline__ void load_scales(const uint16_t* src, uint32_t (&s)[N / 2]) {
+    if constexpr (N == 4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        s[0] = v.x;
+        s[1] = v.y;
+    } else {
+#pragma unroll
+        for (int q = 0; q < N / 8; ++q) {
+            const uint4 v = *reinterpret_cast<const uint4*>(src + 8 * q);
+            s[4 * q] = v.x;
+            s[4 * q + 1] = v.y;
+            s[4 * q + 2] = v.z;
+            s[4 * q + 3] = v.w;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- one wave
+// FWD: decoded tile [128 n][64 k] (k contiguous). Wave w decodes rows FR*w..FR*w+FR-1 of each of
+//      the tile's four 32-row segments (FR = 32 / WAVES); lane = (segment lane>>4, 4 columns
+//      4*(lane&15)); each lane writes 8 bytes (4 k) a row.
+// DX:  decoded tile [128 k][64 n] (n contiguous). Wave w decodes DR = 64 / WAVES rows of the step's
+//      64, rows DR*(w % (WAVES/2)) .. of segment w / (WAVES/2); lane = 2 columns 2*lane; each lane
+//      writes DR/8 16-byte chunks (8 n each) a column.
+template <bool FWD, int WAVES, int WAVE>
+struct Wave {
+    using G = Geo<WAVES>;
+    static constexpr int kMI = G::kMI;
+    static constexpr int BITS = R97Q_BITS;
+    static constexpr bool C8 = BITS == R97Q_CODES8;
+    static constexpr int ROWS = FWD ? G::kFRows : G::kDRows;
+    static constexpr int COLS = FWD ? 4 : 2;
+    static constexpr int SLICE = FWD ? WAVE : WAVE % (WAVES / 2);
+    static constexpr int SEG = FWD ? 0 : WAVE / (WAVES / 2);  // dX: the wave's segment of the step's two
+    using LW = LaneWords<BITS, ROWS, COLS, SLICE>;
+    // the pieces of a decode, spread over rounds 0-2: forward rows, dX (column, 8-row chunk) pairs
+    static constexpr int kPieces = FWD ? ROWS : 2 * (ROWS / 8);
+
+    const Params& p;
+    int64_t red;     // reduction length: K (fwd) or N (dx)
+    int64_t m0;      // the wave's first token
+    int64_t o0;      // the tile's first output
+    int64_t sstride; // elements between consecutive steps of the tiled operand
+    int lane;
+    int nsteps;
+
+    // ------------------------------------------------ the weight words of step s
+    __device__ __forceinline__ void words(int s, LW& wd) const {
+        const int64_t N = p.N, K = p.K;
+        if constexpr (C8) {
+            const uint8_t* units = reinterpret_cast<const uint8_t*>(p.stream);
+            if constexpr (FWD) {
+                // rows ROWS*WAVE.. of each segment: one whole 8 x 4 unit (ROWS 8) or one row half
+                // of it (ROWS 4: bytes 8h..8h+7 and 16+8h..16+8h+7)
+                const int seg = lane >> 4, cg = lane & 15;
+                const int64_t srow = o0 + 32 * seg + ROWS * WAVE;
+                const uint8_t* u = units + (((srow >> 3) * (K >> 2) + (int64_t)s * (kStep / 4) + cg) * 32);
+                if constexpr (ROWS == 8) {
+                    const uint4 a = *reinterpret_cast<const uint4*>(u);
+                    const uint4 b = *reinterpret_cast<const uint4*>(u + 16);
+                    wd.c[0] = a.x; wd.c[1] = a.y; wd.c[2] = a.z; wd.c[3] = a.w;
+                    wd.c[4] = b.x; wd.c[5] = b.y; wd.c[6] = b.z; wd.c[7] = b.w;
+                } else {
+                    const int h = (int)(srow & 7) >> 2;
+                    const uint2 a = *reinterpret_cast<const uint2*>(u + 8 * h);
+                    const uint2 b = *reinterpret_cast<const uint2*>(u + 16 + 8 * h);
+                    wd.c[0] = a.x; wd.c[1] = a.y; wd.c[2] = b.x; wd.c[3] = b.y;
+                }
+                load_scales<ROWS>(p.scale_t + (((int64_t)s * kStep) >> 7) * N + srow, wd.s);
+            } else {
+                // the lane's column pair (half lane&1 of each unit) in ROWS/8 units down the rows
+                const int64_t srow = (int64_t)s * kStep + 32 * SEG + ROWS * SLICE;
+                const int64_t k4 = (o0 >> 2) + (lane >> 1);
+                const uint8_t* u = units + ((srow >> 3) * (K >> 2) + k4) * 32 + 16 * (lane & 1);
+#pragma unroll
+                for (int q = 0; q < ROWS / 8; ++q) {
+                    const uint4 a = *reinterpret_cast<const uint4*>(u + q * (K >> 2) * 32);
+                    wd.c[4 * q] = a.x; wd.c[4 * q + 1] = a.y; wd.c[4 * q + 2] = a.z; wd.c[4 * q + 3] = a.w;
+                }
+                load_scales<ROWS>(p.scale_t + (o0 >> 7) * N + srow, wd.s);
+            }
+        } else {
+            using S = Span<BITS, ROWS, SLICE>;
+            const int64_t rs = p.run_rows >> 5;  // segments a run
+            if constexpr (FWD) {
+                const int seg = lane >> 4, cg = lane & 15;
+                const int64_t g = (o0 >> 5) + seg;
+                const int64_t gh = g % rs != 0 ? g - 1 : (((g / rs + 1) * rs < (N >> 5) ? (g / rs + 1) * rs : (N >> 5)) - 1);
+                const int64_t col4 = (int64_t)s * (kStep / 4) + cg;  // 4-column group
+#pragma unroll
+                for (int t = 0; t < S::NW; ++t) {
+                    const int d = S::D0 + t;
+                    const int64_t idx = d < BITS ? ((g * BITS + d) * (K >> 2) + col4) * 4 : (gh * BITS * (K >> 2) + col4) * 4;
+                    wd.w[t] = *reinterpret_cast<const uint4*>(p.stream + idx);
+                }
+                load_scales<ROWS>(p.scale_t + (((int64_t)s * kStep) >> 7) * N + 32 * g + ROWS * SLICE, wd.s);
+            } else {
+                // the wave's segment is uniform: its halo is computed once, in scalar registers
+                const int64_t g = 2 * (int64_t)s + SEG;
+                const int gi = __builtin_amdgcn_readfirstlane((int)g);
+                const int rsi = (int)rs, ns = (int)(N >> 5);
+                int ghi = gi - 1;
+                if (gi % rsi == 0) {
+                    const int top = (gi / rsi + 1) * rsi;
+                    ghi = (top < ns ? top : ns) - 1;
+                }
+                const int64_t gh = ghi;
+                const int64_t col = o0 + 2 * lane;
+#pragma unroll
+                for (int t = 0; t < S::NW; ++t) {
+                    const int d = S::D0 + t;
+                    const int64_t idx = d < BITS ? (g * BITS + d) * K + col : gh * BITS * K + col;
+                    wd.w[t] = *reinterpret_cast<const uint2*>(p.stream + idx);
+                }
+                load_scales<ROWS>(p.scale_t + (o0 >> 7) * N + 32 * g + ROWS * SLICE, wd.s);
+            }
+        }
+    }
+
+    // ------------------------------------------------ the value of the lane's row i, column c
+    __device__ __forceinline__ float value(const LW& wd, int c, int i, float sc, float off) const {
+        if constexpr (C8) {
+            // forward: byte 2*ROWS*(c>>1) + 2*i + (c&1) of the lane's codes; dX: byte 2*(i&7) + c
+            // of its unit i>>3
+            const int byte = FWD ? 2 * ROWS * (c >> 1) + 2 * i + (c & 1) : 16 * (i >> 3) + 2 * (i & 7) + c;
+            const uint32_t w = wd.c[byte >> 2] ^ 0x80808080u;
+            return __builtin_fmaf((float)((w >> (8 * (byte & 3))) & 0xFFu), sc, off);
+        } else {
+            using S = Span<BITS, ROWS, SLICE>;
+            const int o = BITS * (31 - (ROWS * SLICE + i)) - 32 * S::D0;
+            const int w = o >> 5, sh = o & 31;
+            uint32_t st;
+            if (sh + 16 <= 32) st = (comp(wd.w[w], c) >> sh) & 0xFFFFu;
+            else st = __builtin_amdgcn_alignbit(comp(wd.w[w + 1], c), comp(wd.w[w], c), sh) & 0xFFFFu;
+            const uint32_t h = (st * (p.a24 & 0xFFFFFFu) + p.b) & 0x3F3F3F3Fu;
+            const uint32_t d = __builtin_amdgcn_sad_u8(h, 0u, 0x6400u);  // f16(1024 + sum)
+            const _Float16 hv = __builtin_bit_cast(_Float16, (uint16_t)d);
+            return __builtin_fmaf((float)hv, sc, off);  // (sum - 126) * scale, exact
+        }
+    }
+
+    __device__ __forceinline__ void scale_of(const LW& wd, int i, float& sc, float& off) const {
+        const uint32_t w = wd.s[i >> 1];
+        sc = __builtin_bit_cast(float, (i & 1) ? (w & 0xFFFF0000u) : (w << 16));
+        off = (C8 ? -128.0f : -1150.0f) * sc;
+    }
+
+    // ------------------------------------------------ part PART (0..2) of the decode into `tile`
+    template <int PART>
+    __device__ __forceinline__ void decode(const LW& wd, uint8_t* tile) const {
+        constexpr int q0 = PART * kPieces / 3, q1 = (PART + 1) * kPieces / 3;
+        if constexpr (FWD) {
+            const int seg = lane >> 4, cg = lane & 15;
+#pragma unroll
+            for (int i = q0; i < q1; ++i) {
+                float sc, off;
+                scale_of(wd, i, sc, off);
+                const float v0 = value(wd, 0, i, sc, off);
+                const float v1 = value(wd, 1, i, sc, off);
+                const float v2 = value(wd, 2, i, sc, off);
+                const float v3 = value(wd, 3, i, sc, off);
+                const int row = 32 * seg + ROWS * WAVE + i;
+                const uint2 o = {pack_bf16(v0, v1), pack_bf16(v2, v3)};
+                *reinterpret_cast<uint2*>(chunk_at(tile, row, cg >> 1) + ((cg & 1) << 3)) = o;
+            }
+        } else {
+#pragma unroll
+            for (int q = q0; q < q1; ++q) {
+                const int c = q / (ROWS / 8), hh = q % (ROWS / 8);
+                float v[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    float sc, off;
+                    scale_of(wd, 8 * hh + i, sc, off);
+                    v[i] = value(wd, c, 8 * hh + i, sc, off);
+                }
+                const uint4 o = {pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
+                                 pack_bf16(v[6], v[7])};
+                // rows n = 32*SEG + ROWS*SLICE + 8*hh .. +8 of column 2*lane + c
+                *reinterpret_cast<uint4*>(chunk_at(tile, 2 * lane + c, 4 * SEG + (ROWS / 8) * SLICE + hh)) = o;
+            }
+        }
+    }
+
+    // ------------------------------------------------ the token fragments of step s, round j
+    // blk[mi]: element offset of the wave's token block mi in step 0 (clamped to the operand's
+    // last block)
+    __device__ __forceinline__ void tokens(const uint16_t* act, const int64_t (&blk)[kMI], int s, int j,
+                                           uint4 (&t)[kMI][4]) const {
+#pragma unroll
+        for (int mi = 0; mi < kMI; ++mi)
+            t[mi][j] = *reinterpret_cast<const uint4*>(act + blk[mi] + (int64_t)s * sstride + 512 * j);
+    }
+
+    __device__ __forceinline__ void frags(const uint8_t* tile, int j, bf16x8 (&b)[kNI]) const {
+        const int half = lane >> 5, l32 = lane & 31;
+#pragma unroll
+        for (int ni = 0; ni < kNI; ++ni)
+            b[ni] = as_bf16x8(*reinterpret_cast<const uint4*>(
+                chunk_at(const_cast<uint8_t*>(tile), 32 * ni + l32, 4 * half + j)));
+    }
+
+    __device__ __forceinline__ void round(const uint4 (&t)[kMI][4], int j, const bf16x8 (&b)[kNI],
+                                          f32x16 (&acc)[kMI][kNI]) const {
+#pragma unroll
+        for (int mi = 0; mi < kMI; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = mfma32(as_bf16x8(t[mi][j]), b[ni], acc[mi][ni]);
+    }
+
+    // The issue order of one round: its MFMAs, each followed by a share of the round's other work --
+    // the next round's fragment reads first (they are needed a round later), then the
+    // vector-memory loads, NVALU decode operations spread evenly, the decode's LDS writes last.
+    template <int NDSR, int NVMEM, int NVALU, int NDSW>
+    __device__ __forceinline__ static void interleave() {
+        constexpr int M = kMI * kNI;
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            if (i < NDSR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+            if (i >= 1 && i - 1 < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+            if (NVALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, (NVALU + M - 1) / M, 0);  // VALU
+            if (i >= M - NDSW) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+        }
+    }
+
+    static constexpr int kWordLoads = C8 ? (FWD ? 2 : ROWS / 8) + (ROWS + 7) / 8
+                                         : Span<C8 ? 5 : BITS, ROWS, SLICE>::NW + (ROWS + 7) / 8;
+    static constexpr int kValuPart = (FWD ? 4 * ROWS : 2 * ROWS) * 7 / 3 + 8;  // decode operations of a part
+    static constexpr int kWrites(int part) { return (part + 1) * kPieces / 3 - part * kPieces / 3; }
+
+    // step s: MFMAs on tile s (LDS `cur`) with the token fragments `t`; each round's fragments are
+    // reloaded with the next step's one round after their MFMAs issued (round 3's at the start of
+    // the step: they are this step's); tile s+1 decoded from `dec` into `nxt` over rounds 0-2; the
+    // words of step s+2 into `fetch`. On entry b0 holds tile s's round-0 fragments; on exit tile
+    // s+1's. Each round is its own scheduling region.
+    __device__ __forceinline__ void step(int s, const uint16_t* act, const int64_t (&blk)[kMI], uint4 (&t)[kMI][4],
+                                         const uint8_t* cur, uint8_t* nxt, const LW& dec, LW& fetch,
+                                         bf16x8 (&b0)[kNI], bf16x8 (&b1)[kNI], f32x16 (&acc)[kMI][kNI]) const {
+        const int sn = s + 1 < nsteps ? s + 1 : nsteps - 1;
+        const int sf = s + 2 < nsteps ? s + 2 : nsteps - 1;
+        __builtin_amdgcn_sched_barrier(0);
+        tokens(act, blk, s, 3, t);
+        words(sf, fetch);
+        frags(cur, 1, b1);
+        round(t, 0, b0, acc);
+        decode<0>(dec, nxt);
+        interleave<4, kMI + kWordLoads, kValuPart, kWrites(0)>();
+        __builtin_amdgcn_sched_barrier(0);
+        tokens(act, blk, sn, 0, t);
+        frags(cur, 2, b0);
+        round(t, 1, b1, acc);
+        decode<1>(dec, nxt);
+        interleave<4, kMI, kValuPart, kWrites(1)>();
+        __builtin_amdgcn_sched_barrier(0);
+        tokens(act, blk, sn, 1, t);
+        frags(cur, 3, b1);
+        round(t, 2, b0, acc);
+        decode<2>(dec, nxt);
+        interleave<4, kMI, kValuPart, kWrites(2)>();
+        __builtin_amdgcn_sched_barrier(0);
+        tile_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        tokens(act, blk, sn, 2, t);
+        frags(nxt, 0, b0);
+        round(t, 3, b1, acc);
+        interleave<4, kMI, 0, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    __device__ __forceinline__ void run(const uint16_t* act, uint8_t* t0, uint8_t* t1, f32x16 (&acc)[kMI][kNI]) const {
+        // the wave's token blocks; rows past the operand's last block read that block again (their
+        // products land in rows that are never stored)
+        const int64_t nblk = act_tile_blocks(p.T);
+        int64_t blk[kMI];
+#pragma unroll
+        for (int mi = 0; mi < kMI; ++mi) {
+            int64_t rb = (m0 >> 5) + mi;
+            if (rb > nblk - 1) rb = nblk - 1;
+            blk[mi] = rb * kBlock + 8 * lane;
+        }
+        uint4 t[kMI][4];
+        LW wa, wb;
+        bf16x8 b0[kNI], b1[kNI];
+        // the loads outstanding at the loop's head are, in order, the words of step 1 and the
+        // token fragments of step 0's rounds 0-2: the order every later step leaves them in
+        words(0, wa);
+        decode<0>(wa, t0);
+        decode<1>(wa, t0);
+        decode<2>(wa, t0);
+        __builtin_amdgcn_sched_barrier(0);
+        words(nsteps > 1 ? 1 : 0, wb);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) tokens(act, blk, 0, j, t);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_barrier();
+        frags(t0, 0, b0);
+        // step s decodes tile s+1 from the words of step s+1 and fetches those of step s+2 into
+        // the set step s+1 decoded from; unrolled by two so the sets keep fixed names
+        for (int s = 0; s < nsteps; s += 2) {
+            step(s, act, blk, t, t0, t1, wb, wa, b0, b1, acc);
+            step(s + 1, act, blk, t, t1, t0, wa, wb, b0, b1, acc);
+        }
+    }
+};
+
+// ---------------------------------------------------------------- epilogue
+// acc += [hi | lo](P)[m, :] . [Q | Q][o, :]^T over 2r: P [T, 2r] bf16; Q [outputs, r] bf16
+template <int MI>
+__device__ __forceinline__ void adapter(const uint16_t* P, const uint16_t* Q, int r, int64_t m0, int64_t o0,
+                                        int64_t T, int lane, f32x16 (&acc)[MI][kNI]) {
+    const int half = lane >> 5, l32 = lane & 31;
+    for (int kk = 0; kk < 2 * r; kk += 16) {
+        const int kq = kk + 8 * half;
+        bf16x8 pa[MI], qb[kNI];
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) {
+            int64_t row = m0 + 32 * mi + l32;
+            if (row > T - 1) row = T - 1;
+            pa[mi] = as_bf16x8(*reinterpret_cast<const uint4*>(P + row * 2 * r + kq));
+        }
+#pragma unroll
+        for (int ni = 0; ni < kNI; ++ni)
+            qb[ni] = as_bf16x8(*reinterpret_cast<const uint4*>(Q + (o0 + 32 * ni + l32) * r + (kq % r)));
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = mfma32(pa[mi], qb[ni], acc[mi][ni]);
+    }
+}
+
+// accumulator element e of tile (mi, ni) is row 32*mi + 8*(e/4) + 4*half + e%4, column 32*ni + l32
+template <int MI>
+__device__ __forceinline__ void store(const f32x16 (&acc)[MI][kNI], void* out, int64_t ld, int64_t m0, int64_t o0,
+                                      int64_t T, int lane, int f32, int accumulate) {
+    const int half = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int64_t row = m0 + 32 * mi + 8 * (e >> 2) + 4 * half + (e & 3);
+            if (row >= T) continue;
+#pragma unroll
+            for (int ni = 0; ni < kNI; ++ni) {
+                const int64_t col = o0 + 32 * ni + l32;
+                float v = acc[mi][ni][e];
+                if (f32) {
+                    float* d = reinterpret_cast<float*>(out) + row * ld + col;
+                    *d = accumulate ? *d + v : v;
+                } else {
+                    uint16_t* d = reinterpret_cast<uint16_t*>(out) + row * ld + col;
+                    if (accumulate) v += bf16_to_f32(*d);
+                    *d = f32_to_bf16(v);
+                }
+            }
+        }
+}
+
+template <bool FWD, int WAVES, int WAVE>
+__device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t* t1, int mt, int ot) {
+    using G = Geo<WAVES>;
+    f32x16 acc[G::kMI][kNI];
+#pragma unroll
+    for (int mi = 0; mi < G::kMI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = (f32x16){};
+    const int lane = threadIdx.x & 63;
+    const int64_t red = FWD ? p.K : p.N;
+    const Wave<FWD, WAVES, WAVE> w{p, red, (int64_t)mt * kBM + G::kWaveM * WAVE, (int64_t)ot * kBN,
+                                   act_tile_blocks(p.T) * kBlock, lane, (int)(red / kStep)};
+    w.run(p.act, t0, t1, acc);
+    if (p.rank > 0) adapter<G::kMI>(p.P, p.Q, p.rank, w.m0, w.o0, p.T, lane, acc);
+    store<G::kMI>(acc, p.out, FWD ? p.N : p.K, w.m0, w.o0, p.T, lane, p.out_f32, FWD ? 0 : p.accumulate);
+}
+
+template <bool FWD, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void qlinear_rt_kernel(const Params p) {
+    __shared__ __attribute__((aligned(16))) uint8_t t0[kTileBytes], t1[kTileBytes];
+    const int tile = xcd_tile(blockIdx.x, p.mtiles * p.otiles);
+    const int mt = tile / p.otiles, ot = tile % p.otiles;
+    switch (threadIdx.x >> 6) {
+        case 0: wave_main<FWD, WAVES, 0>(p, t0, t1, mt, ot); break;
+        case 1: wave_main<FWD, WAVES, 1>(p, t0, t1, mt, ot); break;
+        case 2: wave_main<FWD, WAVES, 2>(p, t0, t1, mt, ot); break;
+        case 3: wave_main<FWD, WAVES, 3>(p, t0, t1, mt, ot); break;
+        default:
+            if constexpr (WAVES == 8) {
+                switch (threadIdx.x >> 6) {
+                    case 4: wave_main<FWD, WAVES, 4>(p, t0, t1, mt, ot); break;
+                    case 5: wave_main<FWD, WAVES, 5>(p, t0, t1, mt, ot); break;
+                    case 6: wave_main<FWD, WAVES, 6>(p, t0, t1, mt, ot); break;
+                    default: wave_main<FWD, WAVES, 7>(p, t0, t1, mt, ot); break;
+                }
+            }
+            break;
+    }
+}
+
+#ifndef R97Q_RT_WAVES
+#define R97Q_RT_WAVES 8
+#endif
+
+}  // namespace
+
+template <>
+void launch_fwd<R97Q_BITS>(const Params& p, hipStream_t s) {
+    hipLaunchKernelGGL((qlinear_rt_kernel<true, R97Q_RT_WAVES>), dim3((unsigned)(p.mtiles * p.otiles)),
+                       dim3(64 * R97Q_RT_WAVES), 0, s, p);
+}
+
+template <>
+void launch_dx<R97Q_BITS>(const Params& p, hipStream_t s) {
+    hipLaunchKernelGGL((qlinear_rt_kernel<false, R97Q_RT_WAVES>), dim3((unsigned)(p.mtiles * p.otiles)),
+                       dim3(64 * R97Q_RT_WAVES), 0, s, p);
+}
+
+}  // namespace rt
+}  // namespace r97q

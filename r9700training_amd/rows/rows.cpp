@@ -314,8 +314,14 @@ void gemm_nt_device(const AdjointCall& call) {
         if (!b.enc) refuse(rec.op, "a stored weight operand carries no encoding");
         if (K % 128 || N % 128) refuse(rec.op, "stored weight " + dims({N, K}) + ": N and K must be multiples of 128");
         const R97qWeight* w = device_weight_get(static_cast<const IqrStoredEnc*>(b.enc), N, K, s);
-        r97q_ok(r97q_qlinear_dx_base(w, d_hi, M, 0, d_dx, R97Q_F32, 0, nullptr, 0, s), "gemm_nt dX");
-        r97q_ok(r97q_qlinear_dx_base(w, d_lo, M, 0, d_dx, R97Q_F32, 1, nullptr, 0, s), "gemm_nt dX");
+        // rank 0: the prep stage only lays the cotangent half out for the fused kernel
+        const int64_t wsb = r97q_bwd_workspace_bytes(M, N, K, 0);
+        void* ws = buffer(c, "gemm_nt_ws", (size_t)wsb);
+        for (int half = 0; half < 2; ++half) {
+            r97q_ok(r97q_lora_bwd_prep(M, N, K, half ? d_lo : d_hi, nullptr, nullptr, nullptr, 0, 0.0f, ws, wsb, s),
+                    "gemm_nt dX");
+            r97q_ok(r97q_qlinear_dx_base(w, half ? d_lo : d_hi, M, 0, d_dx, R97Q_F32, half, ws, wsb, s), "gemm_nt dX");
+        }
     } else {
         std::vector<uint16_t> wb;
         to_bf16(b.value.data(), b.value.size(), wb);
