@@ -39,7 +39,7 @@ struct AdValue {
     std::vector<int64_t> shape;  // full logical shape, row-major
     std::vector<double> value;   // numel(shape) values; empty for a stored operand
     const void* raw = nullptr;   // a stored operand's bytes (device memory under the device join)
-    const void* enc = nullptr;   // a stored operand's encoding (this build: an IqrStoredEnc)
+    const void* enc = nullptr;   // a stored operand's encoding (this build: an R97Encoding, include/r97q.h)
 };
 
 struct AdjointCall {

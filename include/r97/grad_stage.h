@@ -21,7 +21,7 @@ namespace device {
 // The step's f32 accumulator (device memory) for the leaf `name` of `shape`; nullptr when the card
 // refuses it (no memory, an empty shape, or the name asked for before with another shape).
 float* grad_stage_slot(const std::string& name, const std::vector<int64_t>& shape);
-// The card bytes the step's staging holds.
+// The bytes of the step's staged f32 accumulators (0 once the step is flushed or discarded).
 int64_t grad_stage_bytes();
 // Each accumulator, rounded once to bf16, added into `grads`; the staging freed. False when a copy
 // failed or a leaf of that name has another shape (the staging is freed either way).

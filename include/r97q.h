@@ -101,6 +101,72 @@ int r97q_iqr_validate(const R97IqrDecodeDesc* desc);
  * `stream`, returns 0, or 1 when the description is outside the rules or the launch failed. */
 int r97_iqr_decode(const R97IqrDecodeDesc* desc, R97IqrStream stream);
 
+/* ------------------------------------------------------------------ the stored encoding
+ *
+ * How a stored weight's planes are named. The reference's tape hands a stored weight to a row as
+ * AdValue{raw, enc}, with `enc` radiance's RadEncoding (the container's plane table: each plane's
+ * role, kind, dtype, block and extent), and derives the decode's description from the roles
+ * (src/iqr_form.h:87-217, `r97_iqr_desc_from_planes`). radiance is not part of this build, so the
+ * plane table is stated here with the fields that derivation reads, and this build's rows read
+ * AdValue::enc as an R97Encoding and AdValue::raw as the weight's planes joined in one device
+ * buffer (each plane at the offset r97_enc_plane_offsets gives, in the encoding's plane order: the
+ * canonical planes the container holds, no relayout).
+ *
+ * Plane dtypes: the unsigned packed code widths (1..12 bits, LSB first along a row) and the
+ * element types of scales and tables. */
+#define R97_ENC_STR 32
+#define R97_ENC_MAX_PLANES 8
+enum R97EncDtype {
+    R97_DT_U1 = 1, R97_DT_U2, R97_DT_U3, R97_DT_U4, R97_DT_U5, R97_DT_U6, R97_DT_U7, R97_DT_U8,
+    R97_DT_U9, R97_DT_U10, R97_DT_U11, R97_DT_U12,
+    R97_DT_I8 = 32, R97_DT_U32, R97_DT_F32, R97_DT_BF16, R97_DT_F16, R97_DT_F8E4M3,
+};
+/* A tiled plane holds one element per block of [block[0] rows x block[1] columns] of the weight (0:
+ * the whole extent); a table holds extent[0] x extent[1] elements whatever the weight's shape. */
+enum R97EncPlaneKind { R97_PLANE_TILED = 0, R97_PLANE_TABLE = 1 };
+typedef struct R97EncPlane {
+    char role[R97_ENC_STR];  /* "codes", "scale", "trellis", "trellis.mad", "zero", "scale.1", "scale.col" */
+    uint32_t kind;
+    uint32_t dtype;
+    int64_t block[2];
+    int64_t extent[2];
+} R97EncPlane;
+typedef struct R97Encoding {
+    char scheme[R97_ENC_STR];     /* "trellis" or "affine" */
+    char transform[R97_ENC_STR];  /* "" or "fwht128" */
+    int32_t n_planes;
+    R97EncPlane plane[R97_ENC_MAX_PLANES];
+} R97Encoding;
+/* One plane's bytes as the caller holds them ({NULL, 0} when not held): the reference's
+ * R97IqrStoredPlane (src/iqr_form.h:37-40). */
+typedef struct R97IqrStoredPlane {
+    const uint8_t* data;
+    int64_t bytes;
+} R97IqrStoredPlane;
+
+/* Bits of one element of a plane dtype (0 for an unknown one). */
+int32_t r97_enc_dtype_bits(uint32_t dtype);
+/* Bytes of n elements of `dtype` packed along a row. */
+int64_t r97_enc_row_bytes(uint32_t dtype, int64_t n);
+/* A plane's element grid over a [rows, cols] weight, and its bytes. */
+void r97_enc_plane_dims(const R97EncPlane* plane, int64_t rows, int64_t cols, int64_t* prows, int64_t* pcols);
+int64_t r97_enc_plane_bytes(const R97EncPlane* plane, int64_t rows, int64_t cols);
+/* The joined layout: offsets[i] of plane i (256-byte aligned, in plane order); returns the total
+ * bytes, or -1 for an encoding with no planes or too many. */
+int64_t r97_enc_plane_offsets(const R97Encoding* enc, int64_t rows, int64_t cols, int64_t* offsets);
+/* The description of the whole weight [rows, cols] from `enc`'s planes (`plane[i]` is plane i's
+ * bytes; the out_* fields are left NULL): 1, or 0 when the encoding is not a form the decode reads
+ * or a plane it needs is missing or short. Restates r97_iqr_desc_from_planes
+ * (src/iqr_form.h:87-183) rule for rule. The planes may be device planes, except "trellis.mad",
+ * whose two words the description carries by value: that one is read here, so it is a host copy. */
+int r97_iqr_desc_from_encoding(const R97Encoding* enc, const R97IqrStoredPlane* plane, int64_t rows, int64_t cols,
+                               R97IqrDecodeDesc* out);
+/* The scale.col factor the description cannot carry (src/iqr_form.h:199-216): *factor = the f32
+ * plane (cols/128 values), or NULL when the encoding has none; 0 when it has one the fold refuses
+ * (not f32, short, or beside a scale that is not one f32 a row). */
+int r97_iqr_scale_col(const R97Encoding* enc, const R97IqrStoredPlane* plane, int64_t rows, int64_t cols,
+                      const float** factor);
+
 /* ------------------------------------------------------------------ the prepared weight
  *
  * The fused kernels read a weight in a GPU layout made once per weight (the weight is frozen):
@@ -291,11 +357,16 @@ int r97q_gemm_nt_q_dx(const R97qWeight* w, const uint16_t* dY, int64_t T, const 
  *   da [T, K]      += g * a_scale        (the code's cotangent)
  *   ds [T, groups] += sum over each group of g * a   (the scale's cotangent)
  *   dA [r, K]      += t_cot^T . x
- * t_cot f32 [T, r]; any output may be NULL; K a multiple of 128. */
+ * a [T, K] is int8 codes (a_dtype R97Q_I8) or f32 code values (R97Q_F32: the fp8 code dtypes, whose
+ * values an f32 holds exactly). Column k belongs to group k / group_width; group_width 0 takes the
+ * reference's rule group_width(K, groups). A caller serving a K that is not a multiple of 128 pads
+ * a, A and da with zero columns and passes the unpadded K's width: a padded column past the last
+ * group adds nothing. t_cot f32 [T, r]; any output may be NULL; K a multiple of 128. */
+#define R97Q_I8 2
 int64_t r97q_lora_shrink_q_bwd_workspace_bytes(int64_t T, int64_t K, int32_t rank);
-int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const int8_t* a, const float* a_scale, int64_t groups,
-                           const uint16_t* A, int32_t rank, const float* t_cot, float* da, float* ds, float* dA,
-                           void* workspace, int64_t workspace_bytes, R97IqrStream stream);
+int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const void* a, int32_t a_dtype, const float* a_scale, int64_t groups,
+                           int64_t group_width, const uint16_t* A, int32_t rank, const float* t_cot, float* da,
+                           float* ds, float* dA, void* workspace, int64_t workspace_bytes, R97IqrStream stream);
 
 /* ------------------------------------------------------------------ the step's far side: AdamW
  *

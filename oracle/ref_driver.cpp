@@ -469,4 +469,24 @@ int ref_adamw_run(const RefAdamWConfig* c, const int64_t* n, const int32_t* deca
     }
 }
 
+// The reference registry's answer for (op, side, dtype): the row's function pointer, or null. With
+// this build's libr97rows.so loaded after this library into the same global symbol scope, its
+// device rows register here (its registry definitions are weak, this one's are the reference's).
+const void* ref_adjoint_find(const char* op, int32_t device, const char* dtype, int64_t group) {
+    std::vector<OpParam> params = {{"dtype", std::string(dtype)}};
+    if (group > 0) params.push_back({"group", group});
+    std::string err;
+    AdjointFn fn = adjoint_find(op, device ? Side::device : Side::host, params, &err);
+    return reinterpret_cast<const void*>(fn);
+}
+
+// The frozen positions the reference registry holds for that row, as a count and the first four.
+int32_t ref_adjoint_frozen(const char* op, int32_t device, const char* dtype, int64_t group, int32_t* first4) {
+    std::vector<OpParam> params = {{"dtype", std::string(dtype)}};
+    if (group > 0) params.push_back({"group", group});
+    const std::vector<int> f = adjoint_frozen(op, device ? Side::device : Side::host, params);
+    for (size_t i = 0; i < f.size() && i < 4; ++i) first4[i] = f[i];
+    return (int32_t)f.size();
+}
+
 }  // extern "C"

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(HERE, "libr97q.so")
 
 R97Q_F32 = 0
 R97Q_BF16 = 1
+R97Q_I8 = 2
 R97Q_CODES8 = 8  # R97qWeight.bits of the int8-code form (include/r97q.h)
 R97Q_ADAMW_GRADS_STAGED = 1  # r97q_adamw_step flags: the gradients are staging buffers (include/r97q.h)
 
@@ -79,11 +80,56 @@ class VocabPlan(C.Structure):
                 ("transform", C.c_int64), ("classes", C.c_int32), ("cls", VocabClass * 4)]
 
 
+R97_ENC_STR = 32
+R97_ENC_MAX_PLANES = 8
+# R97EncDtype (include/r97q.h)
+R97_DT_U = {b: b for b in range(1, 13)}  # unsigned packed code widths 1..12
+R97_DT_I8, R97_DT_U32, R97_DT_F32, R97_DT_BF16, R97_DT_F16, R97_DT_F8E4M3 = 32, 33, 34, 35, 36, 37
+R97_PLANE_TILED, R97_PLANE_TABLE = 0, 1
+
+
+class EncPlane(C.Structure):
+    """R97EncPlane (include/r97q.h): one plane of a stored weight's encoding."""
+
+    _fields_ = [("role", C.c_char * R97_ENC_STR), ("kind", C.c_uint32), ("dtype", C.c_uint32),
+                ("block", C.c_int64 * 2), ("extent", C.c_int64 * 2)]
+
+
+class Encoding(C.Structure):
+    """R97Encoding (include/r97q.h): a stored weight's plane table (what AdValue::enc points at)."""
+
+    _fields_ = [("scheme", C.c_char * R97_ENC_STR), ("transform", C.c_char * R97_ENC_STR), ("n_planes", C.c_int32),
+                ("plane", EncPlane * R97_ENC_MAX_PLANES)]
+
+    def add(self, role: str, kind: int, dtype: int, block=(0, 0), extent=(0, 0)) -> int:
+        i = self.n_planes
+        p = self.plane[i]
+        p.role, p.kind, p.dtype = role.encode(), kind, dtype
+        p.block[0], p.block[1] = block
+        p.extent[0], p.extent[1] = extent
+        self.n_planes = i + 1
+        return i
+
+
+class StoredPlane(C.Structure):
+    """R97IqrStoredPlane (include/r97q.h): one plane's bytes."""
+
+    _fields_ = [("data", C.c_void_p), ("bytes", C.c_int64)]
+
+
 # every symbol include/r97q.h declares, with its ctypes signature
 _P, _I, _i = C.c_void_p, C.c_int64, C.c_int32
 SIGNATURES = {
     "r97q_last_error": (C.c_char_p, []),
     "r97q_iqr_validate": (C.c_int, [C.POINTER(Desc)]),
+    "r97_enc_dtype_bits": (C.c_int32, [C.c_uint32]),
+    "r97_enc_row_bytes": (C.c_int64, [C.c_uint32, _I]),
+    "r97_enc_plane_dims": (None, [C.POINTER(EncPlane), _I, _I, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+    "r97_enc_plane_bytes": (C.c_int64, [C.POINTER(EncPlane), _I, _I]),
+    "r97_enc_plane_offsets": (C.c_int64, [C.POINTER(Encoding), _I, _I, C.POINTER(C.c_int64)]),
+    "r97_iqr_desc_from_encoding": (C.c_int, [C.POINTER(Encoding), C.POINTER(StoredPlane), _I, _I, C.POINTER(Desc)]),
+    "r97_iqr_scale_col": (C.c_int, [C.POINTER(Encoding), C.POINTER(StoredPlane), _I, _I,
+                                    C.POINTER(C.POINTER(C.c_float))]),
     "r97_iqr_decode": (C.c_int, [C.POINTER(Desc), _P]),
     "r97q_weight_stream_bytes": (C.c_int64, [C.POINTER(Desc)]),
     "r97q_weight_prepare": (C.c_int, [C.POINTER(Desc), _P, _P, _P, C.POINTER(Weight), _P]),
@@ -107,7 +153,7 @@ SIGNATURES = {
     "r97q_qlinear_dx_base": (C.c_int, [C.POINTER(Weight), _P, _I, _i, _P, _i, _i, _P, _I, _P]),
     "r97q_gemm_nt_q_dx": (C.c_int, [C.POINTER(Weight), _P, _I, _P, _P, _i, _i, _P]),
     "r97q_lora_shrink_q_bwd_workspace_bytes": (_I, [_I, _I, _i]),
-    "r97q_lora_shrink_q_bwd": (C.c_int, [_I, _I, _P, _P, _I, _P, _i, _P, _P, _P, _P, _P, _I, _P]),
+    "r97q_lora_shrink_q_bwd": (C.c_int, [_I, _I, _P, _i, _P, _I, _I, _P, _i, _P, _P, _P, _P, _P, _I, _P]),
     "r97q_scheduled_lr": (C.c_float, [C.POINTER(AdamWConfig), _i]),
     "r97q_adamw_workspace_bytes": (_I, [C.POINTER(AdamWParam), _i]),
     "r97q_adamw_step": (C.c_int, [C.POINTER(AdamWConfig), C.POINTER(AdamWParam), C.POINTER(C.c_void_p), _i, _i,

@@ -61,14 +61,15 @@ int launch_transpose2(const uint16_t* B, uint16_t* Bt, int64_t N, const uint16_t
 // P [T, 2r] / Pt [2r, ldt] = [hi | lo](scale * U), U f32 [T, r]; either output may be null
 int launch_split(const float* U, int64_t T, int r, int64_t ldt, float scale, uint16_t* P, uint16_t* Pt,
                  hipStream_t s);
-// the coded activation (int8 codes `code` [T, K], f32 scale a_scale [T, groups], group width gw):
+// the coded activation (codes [T, K]: int8, or f32 code values when code_f32; f32 scale a_scale
+// [T, groups], group width gw):
 //   da [T, K] += g * a_scale;  ds [T, groups] += sum over each group of g * code  (g f32 [T, K];
 //   da or ds may be null)
-int launch_coded_cot(const float* g, const int8_t* code, const float* a_scale, int64_t T, int64_t K, int64_t groups,
-                     int64_t gw, float* da, float* ds, hipStream_t s);
+int launch_coded_cot(const float* g, const void* code, int code_f32, const float* a_scale, int64_t T, int64_t K,
+                     int64_t groups, int64_t gw, float* da, float* ds, hipStream_t s);
 //   x = code * a_scale as [hi | lo] bf16 [T, K] each
-int launch_coded_x(const int8_t* code, const float* a_scale, int64_t T, int64_t K, int64_t groups, int64_t gw,
-                   uint16_t* xhi, uint16_t* xlo, hipStream_t s);
+int launch_coded_x(const void* code, int code_f32, const float* a_scale, int64_t T, int64_t K, int64_t groups,
+                   int64_t gw, uint16_t* xhi, uint16_t* xlo, hipStream_t s);
 // out [T, C] f32 (+)= [hi | lo](P) . [Q | Q]^T: P [T, 2r] bf16, Q [C, r] bf16 (C a multiple of 128)
 int launch_lora_up(const uint16_t* P, const uint16_t* Q, int64_t T, int64_t C, int r, float* out, int accumulate,
                    hipStream_t s);

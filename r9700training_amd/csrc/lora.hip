@@ -417,10 +417,16 @@ __global__ __launch_bounds__(256) void lora_up_kernel(const uint16_t* __restrict
 }
 
 // ---------------------------------------------------------------- the coded activation
-// One workgroup a (row m, scale group q), group width gw (the last group may be short):
+// The code values: int8 codes, or f32 values (the fp8 code dtypes, decoded exactly by the caller).
+__device__ __forceinline__ float code_value(const int8_t* c, int64_t i) { return (float)c[i]; }
+__device__ __forceinline__ float code_value(const float* c, int64_t i) { return c[i]; }
+
+// One workgroup a (row m, scale group q), group width gw (the last group may be short; columns past
+// groups * gw, the caller's zero padding, belong to no group):
 //   da[m, k] += g[m, k] * s[m, q];   ds[m, q] += sum_{k in q} g[m, k] * code[m, k]
 // the sum reduced in a fixed tree order (the same bits on every call).
-__global__ __launch_bounds__(256) void coded_cot_kernel(const float* __restrict__ g, const int8_t* __restrict__ code,
+template <class Code>
+__global__ __launch_bounds__(256) void coded_cot_kernel(const float* __restrict__ g, const Code* __restrict__ code,
                                                         const float* __restrict__ s, int64_t K, int64_t groups,
                                                         int64_t gw, float* __restrict__ da, float* __restrict__ ds) {
     __shared__ float red[256];
@@ -431,7 +437,7 @@ __global__ __launch_bounds__(256) void coded_cot_kernel(const float* __restrict_
     for (int64_t k = k0 + threadIdx.x; k < k1; k += blockDim.x) {
         const float gv = g[m * K + k];
         if (da) da[m * K + k] += gv * sc;
-        part += gv * (float)code[m * K + k];
+        part += gv * code_value(code, m * K + k);
     }
     if (!ds) return;
     red[threadIdx.x] = part;
@@ -443,15 +449,18 @@ __global__ __launch_bounds__(256) void coded_cot_kernel(const float* __restrict_
     if (threadIdx.x == 0) ds[m * groups + q] += red[0];
 }
 
-// x[m, k] = code[m, k] * s[m, k / gw] (exact in f32: an 8-bit code times an f32 scale rounds once),
-// as hi = bf16(x), lo = bf16(x - hi)
-__global__ __launch_bounds__(256) void coded_x_kernel(const int8_t* __restrict__ code, const float* __restrict__ s,
+// x[m, k] = code[m, k] * s[m, k / gw] (exact in f32 for an 8-bit code times an f32 scale: one
+// rounding), as hi = bf16(x), lo = bf16(x - hi); a column past the last group takes the last group's
+// scale (the caller's zero padding: x = 0)
+template <class Code>
+__global__ __launch_bounds__(256) void coded_x_kernel(const Code* __restrict__ code, const float* __restrict__ s,
                                                       int64_t T, int64_t K, int64_t groups, int64_t gw,
                                                       uint16_t* __restrict__ xhi, uint16_t* __restrict__ xlo) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= T * K) return;
     const int64_t m = i / K, k = i % K;
-    const float x = (float)code[i] * s[m * groups + k / gw];
+    const int64_t q = k / gw < groups ? k / gw : groups - 1;
+    const float x = code_value(code, i) * s[m * groups + q];
     uint16_t hi, lo;
     split(x, hi, lo);
     xhi[i] = hi;
@@ -575,17 +584,27 @@ int launch_lora_up(const uint16_t* P, const uint16_t* Q, int64_t T, int64_t C, i
     return launch_status("lora_up_kernel");
 }
 
-int launch_coded_cot(const float* g, const int8_t* code, const float* a_scale, int64_t T, int64_t K, int64_t groups,
-                     int64_t gw, float* da, float* ds, hipStream_t s) {
-    hipLaunchKernelGGL(coded_cot_kernel, dim3((unsigned)T, (unsigned)groups), dim3(gw >= 256 ? 256 : 128), 0, s, g,
-                       code, a_scale, K, groups, gw, da, ds);
+int launch_coded_cot(const float* g, const void* code, int code_f32, const float* a_scale, int64_t T, int64_t K,
+                     int64_t groups, int64_t gw, float* da, float* ds, hipStream_t s) {
+    const dim3 grid((unsigned)T, (unsigned)groups), block(gw >= 256 ? 256 : 128);
+    if (code_f32)
+        hipLaunchKernelGGL(coded_cot_kernel<float>, grid, block, 0, s, g, static_cast<const float*>(code), a_scale, K,
+                           groups, gw, da, ds);
+    else
+        hipLaunchKernelGGL(coded_cot_kernel<int8_t>, grid, block, 0, s, g, static_cast<const int8_t*>(code), a_scale,
+                           K, groups, gw, da, ds);
     return launch_status("coded_cot_kernel");
 }
 
-int launch_coded_x(const int8_t* code, const float* a_scale, int64_t T, int64_t K, int64_t groups, int64_t gw,
-                   uint16_t* xhi, uint16_t* xlo, hipStream_t s) {
-    hipLaunchKernelGGL(coded_x_kernel, dim3((unsigned)((T * K + 255) / 256)), dim3(256), 0, s, code, a_scale, T, K,
-                       groups, gw, xhi, xlo);
+int launch_coded_x(const void* code, int code_f32, const float* a_scale, int64_t T, int64_t K, int64_t groups,
+                   int64_t gw, uint16_t* xhi, uint16_t* xlo, hipStream_t s) {
+    const dim3 grid((unsigned)((T * K + 255) / 256));
+    if (code_f32)
+        hipLaunchKernelGGL(coded_x_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(code), a_scale, T,
+                           K, groups, gw, xhi, xlo);
+    else
+        hipLaunchKernelGGL(coded_x_kernel<int8_t>, grid, dim3(256), 0, s, static_cast<const int8_t*>(code), a_scale,
+                           T, K, groups, gw, xhi, xlo);
     return launch_status("coded_x_kernel");
 }
 

@@ -519,14 +519,24 @@ int64_t r97q_lora_shrink_q_bwd_workspace_bytes(int64_t T, int64_t K, int32_t ran
     return rank_ok(rank) && T > 0 && K > 0 ? shrink_q_ws(T, K, rank).total : -1;
 }
 
-int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const int8_t* a, const float* a_scale, int64_t groups,
-                           const uint16_t* A, int32_t rank, const float* t_cot, float* da, float* ds, float* dA,
-                           void* workspace, int64_t workspace_bytes, R97IqrStream stream) {
+int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const void* a, int32_t a_dtype, const float* a_scale, int64_t groups,
+                           int64_t group_width_cols, const uint16_t* A, int32_t rank, const float* t_cot, float* da,
+                           float* ds, float* dA, void* workspace, int64_t workspace_bytes, R97IqrStream stream) {
     clear_error();
     const char* who = "r97q_lora_shrink_q_bwd";
     if (T <= 0 || K <= 0 || K % kBN || groups <= 0 || groups > K) {
         set_error("%s: T %lld K %lld groups %lld (T > 0, K a multiple of 128, 0 < groups <= K)", who, (long long)T,
                   (long long)K, (long long)groups);
+        return R97Q_EINVAL;
+    }
+    if (a_dtype != R97Q_I8 && a_dtype != R97Q_F32) {
+        set_error("%s: a_dtype %d (R97Q_I8 codes or R97Q_F32 code values)", who, (int)a_dtype);
+        return R97Q_EINVAL;
+    }
+    const int64_t gw = group_width_cols > 0 ? group_width_cols : group_width(K, groups);
+    if ((groups - 1) * gw >= K) {
+        set_error("%s: %lld groups of %lld columns do not fit K %lld", who, (long long)groups, (long long)gw,
+                  (long long)K);
         return R97Q_EINVAL;
     }
     if (int e = check_rank(rank, who)) return e;
@@ -540,7 +550,7 @@ int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const int8_t* a, const float* a
     uint8_t* wsb = static_cast<uint8_t*>(workspace);
     const hipStream_t s = (hipStream_t)stream;
     const int64_t ldt = grad_ld(T);
-    const int64_t gw = group_width(K, groups);
+    const int code_f32 = a_dtype == R97Q_F32;
     uint16_t* P = reinterpret_cast<uint16_t*>(wsb + ws.P);
     uint16_t* Pt = reinterpret_cast<uint16_t*>(wsb + ws.Pt);
     if (int e = launch_split(t_cot, T, rank, ldt, 1.0f, P, dA ? Pt : nullptr, s)) return e;
@@ -550,13 +560,13 @@ int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const int8_t* a, const float* a
         float* g = reinterpret_cast<float*>(wsb + ws.g);
         if (int e = launch_transpose2(nullptr, nullptr, 0, A, At, K, rank, s)) return e;
         if (int e = launch_lora_up(P, At, T, K, rank, g, 0, s)) return e;
-        if (int e = launch_coded_cot(g, a, a_scale, T, K, groups, gw, da, ds, s)) return e;
+        if (int e = launch_coded_cot(g, a, code_f32, a_scale, T, K, groups, gw, da, ds, s)) return e;
     }
     if (dA) {
         // dA += t_cot^T . x with x = [hi | lo](a * a_scale): two gradient passes, one a half
         uint16_t* xhi = reinterpret_cast<uint16_t*>(wsb + ws.xhi);
         uint16_t* xlo = reinterpret_cast<uint16_t*>(wsb + ws.xlo);
-        if (int e = launch_coded_x(a, a_scale, T, K, groups, gw, xhi, xlo, s)) return e;
+        if (int e = launch_coded_x(a, code_f32, a_scale, T, K, groups, gw, xhi, xlo, s)) return e;
         for (const uint16_t* x : {xhi, xlo}) {
             GradArgs g{};
             g.T = T;

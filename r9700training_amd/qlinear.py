@@ -9,7 +9,7 @@ import ctypes as C
 
 import torch
 
-from . import Desc, R97Q_BF16, R97Q_F32, Weight, _ptr, _stream, check, lib
+from . import Desc, R97Q_BF16, R97Q_F32, R97Q_I8, Weight, _ptr, _stream, check, lib
 
 
 def device_desc(planes: dict, rows: int, cols: int, fields: dict) -> Desc:
@@ -196,9 +196,10 @@ def gemm_nt_q_dx(w: QWeight, dY, a_scale, dA=None, accumulate=False, da_dtype=to
 
 
 def lora_shrink_q_bwd(a, a_scale, A, t_cot, da=None, ds=None, dA=None, want=("da", "ds", "dA"), workspace=None,
-                      stream=None):
-    """The coded shrink's adjoint: a int8 [T, K] codes, a_scale f32 [T, groups], A bf16 [r, K],
-    t_cot f32 [T, r]. Adds into (and returns) da f32 [T, K], ds f32 [T, groups], dA f32 [r, K]."""
+                      stream=None, group_width=0):
+    """The coded shrink's adjoint: a [T, K] int8 codes (or f32 code values), a_scale f32 [T, groups],
+    A bf16 [r, K], t_cot f32 [T, r]. Adds into (and returns) da f32 [T, K], ds f32 [T, groups], dA f32
+    [r, K]. group_width 0: the reference's width rule over (K, groups)."""
     T, K = a.shape
     groups = a_scale.shape[1]
     rank = A.shape[0]
@@ -211,7 +212,9 @@ def lora_shrink_q_bwd(a, a_scale, A, t_cot, da=None, ds=None, dA=None, want=("da
         dA = torch.zeros((rank, K), dtype=torch.float32, device=dev)
     if workspace is None:
         workspace = _workspace(lib().r97q_lora_shrink_q_bwd_workspace_bytes(T, K, rank), dev, "lora_shrink_q_bwd")
-    rc = lib().r97q_lora_shrink_q_bwd(T, K, _ptr(a), _ptr(a_scale), groups, _ptr(A), rank, _ptr(t_cot),
+    a_dtype = R97Q_F32 if a.dtype == torch.float32 else R97Q_I8
+    rc = lib().r97q_lora_shrink_q_bwd(T, K, _ptr(a), a_dtype, _ptr(a_scale), groups, group_width, _ptr(A), rank,
+                                      _ptr(t_cot),
                                       _ptr(da if "da" in want else None), _ptr(ds if "ds" in want else None),
                                       _ptr(dA if "dA" in want else None), _ptr(workspace), workspace.numel(),
                                       _stream(stream))

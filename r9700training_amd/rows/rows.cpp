@@ -92,8 +92,9 @@ bool serves_i8a8h(const std::vector<OpParam>& params) {
     return param_is(params, "dtype", "i8a8h") && gv && *gv == 128;
 }
 
-// the shrink's activation is int8 codes with a group scale (the fp8 code dtypes are not served)
-bool coded_i8_act(const std::vector<OpParam>& params) { return param_is(params, "dtype", "i8"); }
+// the shrink's activation is a code stream with a group scale: int8 codes or the fp8 code dtypes
+// (the reference's coded_act, src/adjoint/host/lora.cpp:92-101)
+bool coded_act(const std::vector<OpParam>& params) { return !float_act(params); }
 
 // a scale operand's value for (row, group), the reference's layout rule for a grouped scale
 // (src/adjoint/host/linear.cpp:99-112): [rows, groups], one value, [groups] or [rows]
@@ -118,7 +119,36 @@ int64_t group_width(int64_t k, int64_t groups) {
     return (k + b - 1) / b == groups ? b : lo;
 }
 
-bool rank_served(int64_t r) { return r == 8 || r == 16 || r == 32 || r == 64; }
+// ---------------------------------------------------------------- served shapes
+// The kernels serve ranks 8, 16, 32 and 64 and widths (K of a shrink, N of an expand) that are
+// multiples of 128. Every other shape a record carries is served exactly through zero padding: the
+// rank in chunks of at most 64 columns, each padded to the next served rank, and a width padded to
+// the next multiple of 128. A zero row of A, column of B, column of a cotangent or column of an
+// activation adds nothing to any sum, and the padded parts of the outputs are never read back.
+struct RankChunk {
+    int64_t j0, rc, rp;  // the chunk's first rank column, its column count, the served rank it runs at
+};
+
+std::vector<RankChunk> rank_chunks(int64_t R) {
+    std::vector<RankChunk> out;
+    for (int64_t j0 = 0; j0 < R; j0 += 64) {
+        const int64_t rc = std::min<int64_t>(64, R - j0);
+        out.push_back({j0, rc, rc <= 8 ? 8 : rc <= 16 ? 16 : rc <= 32 ? 32 : 64});
+    }
+    return out;
+}
+
+int64_t pad128(int64_t n) { return (n + 127) / 128 * 128; }
+
+// rows x cols of `src` (row stride ld) as a zero-padded [rows_p, cols_p] block, converted by `cvt`
+template <class T, class F>
+std::vector<T> padded(const double* src, int64_t ld, int64_t rows, int64_t cols, int64_t rows_p, int64_t cols_p,
+                      F cvt) {
+    std::vector<T> out((size_t)(rows_p * cols_p), T{});
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) out[(size_t)(r * cols_p + c)] = cvt(src[r * ld + c]);
+    return out;
+}
 
 [[noreturn]] void refuse(const std::string& op, const std::string& why) {
     throw std::runtime_error(op + " (MI355X device row): " + why);
@@ -175,13 +205,14 @@ bool stage_refused(const std::vector<float*>& dest, const std::vector<char>& use
     return false;
 }
 
-// dst[r * ld + c] += src[r * cols + c]: a slot's [N, R] factor gradient into its columns of a fused
-// [N, S*R] accumulator
-__global__ void add_columns_kernel(float* dst, int64_t ld, const float* src, int64_t rows, int64_t cols) {
+// dst[r * ld_dst + c] += src[r * ld_src + c] for r < rows, c < cols: a served chunk's f32 sum into its
+// block of a staged leaf (a slot's rank columns of a fused [N, S*R] factor, or the unpadded part)
+__global__ void add_block_kernel(float* dst, int64_t ld_dst, const float* src, int64_t ld_src, int64_t rows,
+                                 int64_t cols) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= rows * cols) return;
     const int64_t r = i / cols, c = i % cols;
-    dst[r * ld + c] += src[i];
+    dst[r * ld_dst + c] += src[r * ld_src + c];
 }
 
 // row m's adapter slot, or -1 for a base row (negative, NaN or past the pool)
@@ -284,6 +315,25 @@ std::vector<float> download(Card& c, const float* d, size_t n) {
     return h;
 }
 
+void add_block(hipStream_t s, float* dst, int64_t ld_dst, const float* src, int64_t ld_src, int64_t rows, int64_t cols) {
+    hipLaunchKernelGGL(add_block_kernel, dim3((unsigned)((rows * cols + 255) / 256)), dim3(256), 0, s, dst, ld_dst, src,
+                       ld_src, rows, cols);
+    hip_ok(hipGetLastError(), "add_block_kernel");
+}
+
+// a [rows, cols] block of host f64 values, added into the f64 slot `dst` (row stride ld_dst) from a
+// downloaded f32 block of row stride ld_src
+void add_host(double* dst, int64_t ld_dst, const std::vector<float>& src, int64_t ld_src, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) dst[r * ld_dst + c] += (double)src[(size_t)(r * ld_src + c)];
+}
+
+// The prepared weight of a stored operand: its encoding (AdValue::enc, an R97Encoding) over its
+// joined device planes (AdValue::raw).
+const R97qWeight* stored_weight_of(const AdValue& b, int64_t rows, int64_t cols, hipStream_t s) {
+    return device_weight_get(static_cast<const R97Encoding*>(b.enc), b.raw, rows, cols, s);
+}
+
 // ---------------------------------------------------------------- gemm_nt
 // The reference's gemm_nt adjoint (src/adjoint/host/linear.cpp:221-243, device row
 // src/adjoint/device/linear.hip:745): dx[m, k] += sum_n dy[m, n] W(n, k).
@@ -313,7 +363,8 @@ void gemm_nt_device(const AdjointCall& call) {
     if (stored) {
         if (!b.enc) refuse(rec.op, "a stored weight operand carries no encoding");
         if (K % 128 || N % 128) refuse(rec.op, "stored weight " + dims({N, K}) + ": N and K must be multiples of 128");
-        const R97qWeight* w = device_weight_get(static_cast<const IqrStoredEnc*>(b.enc), N, K, s);
+        if (!b.raw) refuse(rec.op, "a stored weight operand carries no planes");
+        const R97qWeight* w = stored_weight_of(b, N, K, s);
         // rank 0: the prep stage only lays the cotangent half out for the fused kernel
         const int64_t wsb = r97q_bwd_workspace_bytes(M, N, K, 0);
         void* ws = buffer(c, "gemm_nt_ws", (size_t)wsb);
@@ -349,6 +400,7 @@ void gemm_nt_device(const AdjointCall& call) {
 // The float shrink's adjoint (src/adjoint/host/lora.cpp:260-328): schema a, a_scale (absent, dtype
 // "invalid"), slot, lora_a [S, R, K], t. Per slot s, over that slot's rows:
 //   dc[a][m, k] += sum_j t_cot[m, j] A[s, j, k];   lora_A(s)[j, k] += sum_m t_cot[m, j] x[m, k]
+// Any rank and K: rank chunks of at most 64 and K padded to 128 (see "served shapes").
 void lora_shrink_device(const AdjointCall& call) {
     const std::vector<AdValue>& v = call.fwd;
     if ((v.size() != 4 && v.size() != 5) || call.cot.empty() || !call.dc) return;
@@ -362,14 +414,12 @@ void lora_shrink_device(const AdjointCall& call) {
     const AdValue& t_cot = call.cot[0];
     AdValue& a_cot = call.dc->at(0);
     if ((int64_t)t_cot.value.size() != M * R || (int64_t)a_cot.value.size() != M * K) return;
-    if (!rank_served(R) || K % 128)
-        refuse(call.rec.op, "rank " + std::to_string(R) + ", K " + std::to_string(K) +
-                                " not served (ranks 8, 16, 32, 64; K a multiple of 128)");
     std::vector<char> used((size_t)S, 0);
     for (int64_t m = 0; m < M; ++m) {
         const int64_t sl = row_slot(slot, m, S);
         if (sl >= 0) used[(size_t)sl] = 1;
     }
+    if (std::find(used.begin(), used.end(), 1) == used.end()) return;  // every row a base row
     // dA waits in the step's staging on the card (r97/grad_stage.h)
     const std::vector<int64_t> a_shape = call.fused_slots ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
     const std::vector<float*> d_dA = stage_dest(call, "lora_A", S, used, a_shape, R * K);
@@ -378,31 +428,34 @@ void lora_shrink_device(const AdjointCall& call) {
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
     const hipStream_t s = stream_of(c);
-    std::vector<uint16_t> xb;
-    to_bf16(a.value.data(), a.value.size(), xb);
-    const uint16_t* d_x = upload(c, "x", xb);
-    float* d_dx = static_cast<float*>(buffer(c, "dx", (size_t)(M * K) * 4));
-    const int64_t wsb = r97q_lora_shrink_bwd_workspace_bytes(M, K, (int32_t)R);
+    const int64_t Kp = pad128(K);
+    const std::vector<RankChunk> chunks = rank_chunks(R);
+    const uint16_t* d_x = upload(c, "x", padded<uint16_t>(a.value.data(), K, M, K, M, Kp, [](double d) { return to_bf16((float)d); }));
+    float* d_dx = zeros(c, "dx", (size_t)(M * Kp));
+    const int64_t wsb = r97q_lora_shrink_bwd_workspace_bytes(M, Kp, (int32_t)chunks[0].rp);
     void* d_ws = buffer(c, "ws", (size_t)wsb);
-    bool first = true;
+    const bool direct = Kp == K;  // a chunk's dA lands in the leaf as it is (unpadded K, rank rc == rp)
     for (int64_t sl = 0; sl < S; ++sl) {
         if (!used[(size_t)sl]) continue;
-        std::vector<uint16_t> ab;
-        to_bf16(la.value.data() + sl * R * K, (size_t)(R * K), ab);
-        const uint16_t* d_a = upload(c, "a_s", ab);
-        std::vector<float> tc((size_t)(M * R), 0.0f);
-        for (int64_t m = 0; m < M; ++m)
-            if (row_slot(slot, m, S) == sl)
-                for (int64_t j = 0; j < R; ++j) tc[(size_t)(m * R + j)] = (float)t_cot.value[(size_t)(m * R + j)];
-        const float* d_tc = upload(c, "t_cot", tc);
-        r97q_ok(r97q_lora_shrink_bwd(M, K, d_x, d_a, (int32_t)R, d_tc, d_dx, first ? 0 : 1,
-                                     call.grads ? d_dA[(size_t)sl] : nullptr, d_ws, wsb, s),
-                "lora_shrink adjoint");
-        first = false;
+        for (const RankChunk& ch : chunks) {
+            const double* arow = la.value.data() + (sl * R + ch.j0) * K;
+            const uint16_t* d_a =
+                upload(c, "a_s", padded<uint16_t>(arow, K, ch.rc, K, ch.rp, Kp, [](double d) { return to_bf16((float)d); }));
+            std::vector<float> tc((size_t)(M * ch.rp), 0.0f);
+            for (int64_t m = 0; m < M; ++m)
+                if (row_slot(slot, m, S) == sl)
+                    for (int64_t j = 0; j < ch.rc; ++j)
+                        tc[(size_t)(m * ch.rp + j)] = (float)t_cot.value[(size_t)(m * R + ch.j0 + j)];
+            const float* d_tc = upload(c, "t_cot", tc);
+            float* leaf = call.grads ? d_dA[(size_t)sl] + ch.j0 * K : nullptr;
+            const bool via = leaf && !(direct && ch.rc == ch.rp);
+            float* dA = via ? zeros(c, "dA_chunk", (size_t)(ch.rp * Kp)) : leaf;
+            r97q_ok(r97q_lora_shrink_bwd(M, Kp, d_x, d_a, (int32_t)ch.rp, d_tc, d_dx, 1, dA, d_ws, wsb, s),
+                    "lora_shrink adjoint");
+            if (via) add_block(s, leaf, K, dA, Kp, ch.rc, K);
+        }
     }
-    if (first) return;  // every row a base row
-    const std::vector<float> h = download(c, d_dx, (size_t)(M * K));
-    for (size_t i = 0; i < h.size(); ++i) a_cot.value[i] += (double)h[i];
+    add_host(a_cot.value.data(), K, download(c, d_dx, (size_t)(M * Kp)), Kp, M, K);
 }
 
 // ---------------------------------------------------------------- lora_expand
@@ -410,7 +463,8 @@ void lora_shrink_device(const AdjointCall& call) {
 // scale [S, N] (absent in a float trunk's 4-operand record: 1), y. Per slot s, over its rows:
 //   dc[t][m, j] += sum_n y_cot[m, n] scale[s, n] B[s, n, j]
 //   lora_B(s)[n, j] += sum_m y_cot[m, n] scale[s, n] t[m, j]
-// and an in-place write's slot takes y_cot back unchanged.
+// and an in-place write's slot takes y_cot back unchanged. Any rank and N: rank chunks of at most
+// 64 and N padded to 128.
 void lora_expand_device(const AdjointCall& call) {
     const OpRecord& rec = call.rec;
     const std::vector<AdValue>& v = call.fwd;
@@ -429,9 +483,6 @@ void lora_expand_device(const AdjointCall& call) {
     const AdValue& y_cot = call.cot[0];
     AdValue& t_cot = call.dc->at(0);
     if ((int64_t)y_cot.value.size() != M * N || (int64_t)t_cot.value.size() != M * R) return;
-    if (!rank_served(R) || N % 128)
-        refuse(rec.op, "rank " + std::to_string(R) + ", N " + std::to_string(N) +
-                           " not served (ranks 8, 16, 32, 64; N a multiple of 128)");
     // the in-place write's direct path
     for (size_t i = 0; i < rec.operands.size() && i < call.dc->size(); ++i)
         if (rec.operands[i].written && rec.operands[i].in_place) {
@@ -444,56 +495,64 @@ void lora_expand_device(const AdjointCall& call) {
         const int64_t sl = row_slot(slot, m, S);
         if (sl >= 0) used[(size_t)sl] = 1;
     }
+    if (std::find(used.begin(), used.end(), 1) == used.end()) return;
     // dB waits in the step's staging on the card: a slot's [N, R] leaf, or its R columns of the
     // fused [N, S*R] one
     const std::vector<int64_t> b_shape = call.fused_slots ? std::vector<int64_t>{N, S * R} : std::vector<int64_t>{N, R};
     const std::vector<float*> d_dB = stage_dest(call, "lora_B", S, used, b_shape, R);
     if (stage_refused(d_dB, used, call.grads != nullptr)) return;
+    const int64_t ld_leaf = call.fused_slots ? S * R : R;
 
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
     const hipStream_t s = stream_of(c);
-    std::vector<float> tf(t.value.begin(), t.value.end());
-    const float* d_t = upload(c, "t", tf);
-    float* d_tc = zeros(c, "t_cot", (size_t)(M * R));
-    const int64_t wsb = r97q_lora_expand_bwd_workspace_bytes(M, N, (int32_t)R);
+    const int64_t Np = pad128(N);
+    const std::vector<RankChunk> chunks = rank_chunks(R);
+    const int64_t wsb = r97q_lora_expand_bwd_workspace_bytes(M, Np, (int32_t)chunks[0].rp);
     void* d_ws = buffer(c, "ws", (size_t)wsb);
-    bool any = false;
     for (int64_t sl = 0; sl < S; ++sl) {
         if (!used[(size_t)sl]) continue;
-        any = true;
         std::vector<double> dys((size_t)(M * N), 0.0);
         for (int64_t m = 0; m < M; ++m) {
             if (row_slot(slot, m, S) != sl) continue;
             for (int64_t k = 0; k < N; ++k)
                 dys[(size_t)(m * N + k)] = y_cot.value[(size_t)(m * N + k)] * (sc ? sc->value[(size_t)(sl * N + k)] : 1.0);
         }
-        std::vector<uint16_t> hi, lo, bb;
+        std::vector<uint16_t> hi, lo;
         split_bf16(dys, hi, lo);
-        to_bf16(lb.value.data() + sl * N * R, (size_t)(N * R), bb);
-        const uint16_t* d_hi = upload(c, "dy_hi", hi);
-        const uint16_t* d_lo = upload(c, "dy_lo", lo);
-        const uint16_t* d_b = upload(c, "b_s", bb);
-        // a fused leaf's columns are strided: the slot's [N, R] sum goes through a buffer
-        float* d_db = !call.grads ? nullptr : call.fused_slots ? zeros(c, "db", (size_t)(N * R)) : d_dB[(size_t)sl];
-        r97q_ok(r97q_lora_expand_bwd(M, N, d_hi, d_b, (int32_t)R, 1.0f, d_t, d_tc, d_db, d_ws, wsb, s), "lora_expand adjoint");
-        r97q_ok(r97q_lora_expand_bwd(M, N, d_lo, d_b, (int32_t)R, 1.0f, d_t, d_tc, d_db, d_ws, wsb, s), "lora_expand adjoint");
-        if (call.grads && call.fused_slots) {
-            hipLaunchKernelGGL(add_columns_kernel, dim3((unsigned)((N * R + 255) / 256)), dim3(256), 0, s, d_dB[(size_t)sl],
-                               S * R, d_db, N, R);
-            hip_ok(hipGetLastError(), "add_columns_kernel");
+        const auto widen = [&](const std::vector<uint16_t>& h) {
+            std::vector<uint16_t> out((size_t)(M * Np), 0);
+            for (int64_t m = 0; m < M; ++m) std::memcpy(&out[(size_t)(m * Np)], &h[(size_t)(m * N)], (size_t)N * 2);
+            return out;
+        };
+        const uint16_t* d_hi = upload(c, "dy_hi", widen(hi));
+        const uint16_t* d_lo = upload(c, "dy_lo", widen(lo));
+        for (const RankChunk& ch : chunks) {
+            const uint16_t* d_b = upload(c, "b_s", padded<uint16_t>(lb.value.data() + sl * N * R + ch.j0, R, N, ch.rc, Np,
+                                                                    ch.rp, [](double d) { return to_bf16((float)d); }));
+            const float* d_t = upload(c, "t", padded<float>(t.value.data() + ch.j0, R, M, ch.rc, M, ch.rp,
+                                                            [](double d) { return (float)d; }));
+            float* d_tc = zeros(c, "t_cot", (size_t)(M * ch.rp));
+            float* leaf = call.grads ? d_dB[(size_t)sl] + ch.j0 : nullptr;
+            float* d_db = leaf ? zeros(c, "db", (size_t)(Np * ch.rp)) : nullptr;
+            r97q_ok(r97q_lora_expand_bwd(M, Np, d_hi, d_b, (int32_t)ch.rp, 1.0f, d_t, d_tc, d_db, d_ws, wsb, s),
+                    "lora_expand adjoint");
+            r97q_ok(r97q_lora_expand_bwd(M, Np, d_lo, d_b, (int32_t)ch.rp, 1.0f, d_t, d_tc, d_db, d_ws, wsb, s),
+                    "lora_expand adjoint");
+            if (leaf) add_block(s, leaf, ld_leaf, d_db, ch.rp, N, ch.rc);
+            add_host(t_cot.value.data() + ch.j0, R, download(c, d_tc, (size_t)(M * ch.rp)), ch.rp, M, ch.rc);
         }
     }
-    if (!any) return;
-    const std::vector<float> h = download(c, d_tc, (size_t)(M * R));
-    for (size_t i = 0; i < h.size(); ++i) t_cot.value[i] += (double)h[i];
 }
 
 // ---------------------------------------------------------------- gemm_nt_q
 // gemm_nt_q's adjoint (src/adjoint/host/linear.cpp:284-317, device row
 // src/adjoint/device/linear.hip:744-760): schema a [M, K] codes, a_scale, b [N, K], b_scale, y;
 //   dc[a][m, k] += a_scale[m, k/128] . sum_n dy[m, n] code[n, k] b_scale[n, k/128]
-// the cotangent of the int8 codes (not a code itself: f64, added in unrounded).
+// the cotangent of the int8 codes (not a code itself: f64, added in unrounded). A stored weight is
+// the prepared weight of its encoding; a weight carried as codes and their scale becomes the same
+// int8-code form on the card for the call (N and K zero-padded to 128), read by the same fused
+// kernel with the activation's scale in its epilogue.
 void gemm_nt_q_device(const AdjointCall& call) {
     const OpRecord& rec = call.rec;
     const int ia = operand_pos(rec, "a"), ias = operand_pos(rec, "a_scale"), ib = operand_pos(rec, "b"),
@@ -512,8 +571,9 @@ void gemm_nt_q_device(const AdjointCall& call) {
     if (M <= 0 || N <= 0 || K <= 0 || (int64_t)dy.value.size() != M * N || (int64_t)da.value.size() != M * K) return;
     const bool stored = b.raw != nullptr || b.enc != nullptr;
     if (!stored && ((int64_t)b.value.size() != N * K || ibs < 0)) return;
-    if (K % 128 || N % 128) refuse(rec.op, "weight " + dims({N, K}) + ": N and K must be multiples of 128");
-    const int64_t groups = K / 128;
+    if (stored && (K % 128 || N % 128)) refuse(rec.op, "stored weight " + dims({N, K}) + ": N and K must be multiples of 128");
+    const int64_t Kp = pad128(K), Np = pad128(N);
+    const int64_t groups = Kp / 128;  // the record's 128-wide groups, the last one short when K is
     std::vector<float> sa((size_t)(M * groups));
     for (int64_t m = 0; m < M; ++m)
         for (int64_t g = 0; g < groups; ++g) sa[(size_t)(m * groups + g)] = (float)scale_at(as, m, g, M, groups);
@@ -523,53 +583,49 @@ void gemm_nt_q_device(const AdjointCall& call) {
     const hipStream_t s = stream_of(c);
     std::vector<uint16_t> hi, lo;
     split_bf16(dy.value, hi, lo);
-    const uint16_t* d_hi = upload(c, "dy_hi", hi);
-    const uint16_t* d_lo = upload(c, "dy_lo", lo);
-    float* d_da = static_cast<float*>(buffer(c, "dx", (size_t)(M * K) * 4));
-    std::vector<float> h;
+    const auto widen = [&](const std::vector<uint16_t>& h) {
+        std::vector<uint16_t> out((size_t)(M * Np), 0);
+        for (int64_t m = 0; m < M; ++m) std::memcpy(&out[(size_t)(m * Np)], &h[(size_t)(m * N)], (size_t)N * 2);
+        return out;
+    };
+    const uint16_t* d_hi = upload(c, "dy_hi", widen(hi));
+    const uint16_t* d_lo = upload(c, "dy_lo", widen(lo));
+    float* d_da = static_cast<float*>(buffer(c, "dx", (size_t)(M * Kp) * 4));
+    const float* d_sa = upload(c, "a_scale", sa);
+    const R97qWeight* w = nullptr;
+    R97qWeight dense{};
     if (stored) {
         if (!b.enc) refuse(rec.op, "a stored weight operand carries no encoding");
-        const R97qWeight* w = device_weight_get(static_cast<const IqrStoredEnc*>(b.enc), N, K, s);
-        const float* d_sa = upload(c, "a_scale", sa);
-        r97q_ok(r97q_gemm_nt_q_dx(w, d_hi, M, d_sa, d_da, R97Q_F32, 0, s), "gemm_nt_q dA");
-        r97q_ok(r97q_gemm_nt_q_dx(w, d_lo, M, d_sa, d_da, R97Q_F32, 1, s), "gemm_nt_q dA");
-        h = download(c, d_da, (size_t)(M * K));
+        if (!b.raw) refuse(rec.op, "a stored weight operand carries no planes");
+        w = stored_weight_of(b, N, K, s);
     } else {
-        // a weight carried as codes and their scale: W = bf16(code . scale), one rocBLAS product,
-        // then the activation's group scale on the way out
         const AdValue& bs = call.fwd[(size_t)ibs];
-        std::vector<uint16_t> wb((size_t)(N * K));
-        for (int64_t n = 0; n < N; ++n)
-            for (int64_t k = 0; k < K; ++k)
-                wb[(size_t)(n * K + k)] = to_bf16((float)(b.value[(size_t)(n * K + k)] * scale_at(bs, n, k / 128, N, groups)));
-        const uint16_t* d_w = upload(c, "w", wb);
-        if (!c.blas) {
-            if (rocblas_create_handle(&c.blas) != rocblas_status_success) refuse(rec.op, "rocblas_create_handle failed");
+        std::vector<int8_t> codes((size_t)(Np * Kp), 0);
+        std::vector<uint16_t> scale((size_t)(Np * groups), 0);
+        for (int64_t n = 0; n < N; ++n) {
+            for (int64_t k = 0; k < K; ++k) codes[(size_t)(n * Kp + k)] = (int8_t)std::lrint(b.value[(size_t)(n * K + k)]);
+            for (int64_t g = 0; g < groups; ++g) scale[(size_t)(n * groups + g)] = to_bf16((float)scale_at(bs, n, g, N, groups));
         }
-        rocblas_set_stream(c.blas, s);
-        const float one = 1.0f, zero = 0.0f;
-        for (int half = 0; half < 2; ++half) {
-            const rocblas_status st = rocblas_gemm_ex(
-                c.blas, rocblas_operation_none, rocblas_operation_none, (rocblas_int)K, (rocblas_int)M, (rocblas_int)N,
-                &one, d_w, rocblas_datatype_bf16_r, (rocblas_int)K, half ? d_lo : d_hi, rocblas_datatype_bf16_r,
-                (rocblas_int)N, half ? &one : &zero, d_da, rocblas_datatype_f32_r, (rocblas_int)K, d_da,
-                rocblas_datatype_f32_r, (rocblas_int)K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-            if (st != rocblas_status_success) refuse(rec.op, std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(st));
-        }
-        h = download(c, d_da, (size_t)(M * K));
-        for (int64_t m = 0; m < M; ++m)
-            for (int64_t k = 0; k < K; ++k) h[(size_t)(m * K + k)] *= sa[(size_t)(m * groups + k / 128)];
+        const int8_t* d_codes = upload(c, "w_codes", codes);
+        const uint16_t* d_scale = upload(c, "w_scale", scale);
+        int8_t* d_form = static_cast<int8_t*>(buffer(c, "w_form", (size_t)(Np * Kp)));
+        uint16_t* d_st = static_cast<uint16_t*>(buffer(c, "w_scale_t", (size_t)(Np * groups) * 2));
+        r97q_ok(r97q_weight_from_decoded(d_codes, d_scale, Np, Kp, d_form, d_st, &dense, s), "gemm_nt_q weight");
+        w = &dense;
     }
-    for (size_t i = 0; i < h.size(); ++i) da.value[i] += (double)h[i];
+    r97q_ok(r97q_gemm_nt_q_dx(w, d_hi, M, d_sa, d_da, R97Q_F32, 0, s), "gemm_nt_q dA");
+    r97q_ok(r97q_gemm_nt_q_dx(w, d_lo, M, d_sa, d_da, R97Q_F32, 1, s), "gemm_nt_q dA");
+    add_host(da.value.data(), K, download(c, d_da, (size_t)(M * Kp)), Kp, M, K);
 }
 
 // ---------------------------------------------------------------- the coded lora_shrink
 // The coded shrink's adjoint (src/adjoint/host/lora.cpp:246-328, device row
-// src/adjoint/device/lora.hip:437-577): schema a [M, K] int8 codes, a_scale [M, groups] f32, slot,
-// lora_a [S, R, K], t. With x = a * a_scale[m, k / group_width(K, groups)] and, per slot s over its
-// rows, g = t_cot . A_s:
+// src/adjoint/device/lora.hip:437-577): schema a [M, K] codes (int8, or an fp8 code dtype), a_scale
+// [M, groups] f32, slot, lora_a [S, R, K], t. With x = a * a_scale[m, k / group_width(K, groups)]
+// and, per slot s over its rows, g = t_cot . A_s:
 //   dc[a] += g * a_scale;  dc[a_scale][m, q] += sum_{k in q} g[m, k] a[m, k];
 //   lora_A(s) += t_cot^T . x
+// Any rank and K: rank chunks of at most 64, K padded to 128 with the unpadded K's group width.
 void lora_shrink_q_device(const AdjointCall& call) {
     const std::vector<AdValue>& v = call.fwd;
     if ((v.size() != 4 && v.size() != 5) || call.cot.empty() || !call.dc || call.dc->size() < 2) return;
@@ -579,7 +635,7 @@ void lora_shrink_q_device(const AdjointCall& call) {
     const int64_t M = a.shape[0], K = a.shape[1], S = la.shape[0], R = la.shape[1];
     if (M <= 0 || K <= 0 || R <= 0 || S <= 0 || la.shape[2] != K || slot.shape[0] != M) return;
     const int64_t groups = held.shape[1];
-    if (held.shape[0] != M || groups <= 0 || (int64_t)held.value.size() != M * groups) return;
+    if (held.shape[0] != M || groups <= 0 || groups > K || (int64_t)held.value.size() != M * groups) return;
     if ((int64_t)a.value.size() != M * K || (int64_t)slot.value.size() != M || (int64_t)la.value.size() != S * R * K)
         return;
     // the record's `group` states the same grid the scale's columns give (lora.cpp:183-191)
@@ -592,17 +648,12 @@ void lora_shrink_q_device(const AdjointCall& call) {
     if ((int64_t)t_cot.value.size() != M * R || (int64_t)a_cot.value.size() != M * K ||
         (int64_t)s_cot.value.size() != M * groups)
         return;
-    if (!rank_served(R) || K % 128)
-        refuse(call.rec.op, "rank " + std::to_string(R) + ", K " + std::to_string(K) +
-                                " not served (ranks 8, 16, 32, 64; K a multiple of 128)");
     std::vector<char> used((size_t)S, 0);
     for (int64_t m = 0; m < M; ++m) {
         const int64_t sl = row_slot(slot, m, S);
         if (sl >= 0) used[(size_t)sl] = 1;
     }
-    bool any = false;
-    for (char u : used) any = any || u;
-    if (!any) return;  // every row a base row
+    if (std::find(used.begin(), used.end(), 1) == used.end()) return;  // every row a base row
     const std::vector<int64_t> a_shape = call.fused_slots ? std::vector<int64_t>{S * R, K} : std::vector<int64_t>{R, K};
     const std::vector<float*> d_dA = stage_dest(call, "lora_A", S, used, a_shape, R * K);
     if (stage_refused(d_dA, used, call.grads != nullptr)) return;
@@ -610,33 +661,44 @@ void lora_shrink_q_device(const AdjointCall& call) {
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
     const hipStream_t s = stream_of(c);
-    std::vector<int8_t> codes((size_t)(M * K));
-    for (size_t i = 0; i < codes.size(); ++i) codes[i] = (int8_t)std::lrint(a.value[i]);
+    const int64_t Kp = pad128(K);
+    const std::vector<RankChunk> chunks = rank_chunks(R);
+    // int8 codes travel as int8; an fp8 code's value is exact in f32
+    const bool i8 = param_is(call.rec.params, "dtype", "i8");
+    const void* d_a = i8 ? (const void*)upload(c, "codes", padded<int8_t>(a.value.data(), K, M, K, M, Kp,
+                                                                         [](double d) { return (int8_t)std::lrint(d); }))
+                         : (const void*)upload(c, "codes", padded<float>(a.value.data(), K, M, K, M, Kp,
+                                                                        [](double d) { return (float)d; }));
     std::vector<float> sc(held.value.begin(), held.value.end());
-    const int8_t* d_a = upload(c, "codes", codes);
     const float* d_s = upload(c, "a_scale", sc);
-    float* d_da = zeros(c, "dx", (size_t)(M * K));
+    float* d_da = zeros(c, "dx", (size_t)(M * Kp));
     float* d_ds = zeros(c, "ds", (size_t)(M * groups));
-    const int64_t wsb = r97q_lora_shrink_q_bwd_workspace_bytes(M, K, (int32_t)R);
+    const int64_t wsb = r97q_lora_shrink_q_bwd_workspace_bytes(M, Kp, (int32_t)chunks[0].rp);
     void* d_ws = buffer(c, "ws", (size_t)wsb);
+    const bool direct = Kp == K;
     for (int64_t sl = 0; sl < S; ++sl) {
         if (!used[(size_t)sl]) continue;
-        std::vector<uint16_t> ab;
-        to_bf16(la.value.data() + sl * R * K, (size_t)(R * K), ab);
-        const uint16_t* d_A = upload(c, "a_s", ab);
-        std::vector<float> tc((size_t)(M * R), 0.0f);
-        for (int64_t m = 0; m < M; ++m)
-            if (row_slot(slot, m, S) == sl)
-                for (int64_t j = 0; j < R; ++j) tc[(size_t)(m * R + j)] = (float)t_cot.value[(size_t)(m * R + j)];
-        const float* d_tc = upload(c, "t_cot", tc);
-        r97q_ok(r97q_lora_shrink_q_bwd(M, K, d_a, d_s, groups, d_A, (int32_t)R, d_tc, d_da, d_ds,
-                                       call.grads ? d_dA[(size_t)sl] : nullptr, d_ws, wsb, s),
-                "lora_shrink (coded) adjoint");
+        for (const RankChunk& ch : chunks) {
+            const double* arow = la.value.data() + (sl * R + ch.j0) * K;
+            const uint16_t* d_A =
+                upload(c, "a_s", padded<uint16_t>(arow, K, ch.rc, K, ch.rp, Kp, [](double d) { return to_bf16((float)d); }));
+            std::vector<float> tc((size_t)(M * ch.rp), 0.0f);
+            for (int64_t m = 0; m < M; ++m)
+                if (row_slot(slot, m, S) == sl)
+                    for (int64_t j = 0; j < ch.rc; ++j)
+                        tc[(size_t)(m * ch.rp + j)] = (float)t_cot.value[(size_t)(m * R + ch.j0 + j)];
+            const float* d_tc = upload(c, "t_cot", tc);
+            float* leaf = call.grads ? d_dA[(size_t)sl] + ch.j0 * K : nullptr;
+            const bool via = leaf && !(direct && ch.rc == ch.rp);
+            float* dA = via ? zeros(c, "dA_chunk", (size_t)(ch.rp * Kp)) : leaf;
+            r97q_ok(r97q_lora_shrink_q_bwd(M, Kp, d_a, i8 ? R97Q_I8 : R97Q_F32, d_s, groups, gw, d_A, (int32_t)ch.rp,
+                                           d_tc, d_da, d_ds, dA, d_ws, wsb, s),
+                    "lora_shrink (coded) adjoint");
+            if (via) add_block(s, leaf, K, dA, Kp, ch.rc, K);
+        }
     }
-    const std::vector<float> h = download(c, d_da, (size_t)(M * K));
-    for (size_t i = 0; i < h.size(); ++i) a_cot.value[i] += (double)h[i];
-    const std::vector<float> hs = download(c, d_ds, (size_t)(M * groups));
-    for (size_t i = 0; i < hs.size(); ++i) s_cot.value[i] += (double)hs[i];
+    add_host(a_cot.value.data(), K, download(c, d_da, (size_t)(M * Kp)), Kp, M, K);
+    add_host(s_cot.value.data(), groups, download(c, d_ds, (size_t)(M * groups)), groups, M, groups);
 }
 
 // ---------------------------------------------------------------- the activation quantiser
@@ -700,7 +762,7 @@ R97_REGISTER_ADJOINT_IF("had_quant_act_i8g", device, had_quant_device, serves_ro
 R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_device, float_act, 1, 2, 3)
 R97_REGISTER_ADJOINT_F("lora_expand", device, lora_expand_device, 1, 2, 3)
 R97_REGISTER_ADJOINT_IF_F("gemm_nt_q", device, gemm_nt_q_device, serves_i8a8h, 1, 2, 3)
-R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_q_device, coded_i8_act, 2, 3)
+R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_q_device, coded_act, 2, 3)
 
 R97_REGISTER_ADJOINT_FAMILY(Linear, "gemm_nt", "gemm_nt_q");
 R97_REGISTER_ADJOINT_FAMILY(Lora, "lora_shrink", "lora_expand");

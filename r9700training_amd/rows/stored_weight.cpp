@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <stdexcept>
@@ -12,13 +13,21 @@
 namespace r97 {
 namespace {
 
+// The first and last 64 bytes of the codes and scale planes: a new weight written into the same
+// buffers under the same encoding (a buffer reused after a free) differs there.
+struct Print {
+    uint8_t b[4][64];
+};
+
 struct Entry {
+    R97Encoding enc{};  // the encoding the weight was prepared from, compared on every lookup
+    Print print{};      // and its planes' print
     R97qWeight w{};
     void* stream_buf = nullptr;
     void* scale_buf = nullptr;
     int64_t bytes = 0;
 };
-using Key = std::tuple<const void*, int64_t, int64_t>;
+using Key = std::tuple<const void*, const void*, int64_t, int64_t>;
 
 struct Store {
     std::mutex mu;
@@ -41,28 +50,97 @@ void release(Entry& e) {
                              "]: " + what);
 }
 
+// the encodings say the same thing (field by field: the struct's padding is not compared)
+bool same(const R97Encoding& a, const R97Encoding& b) {
+    if (std::strncmp(a.scheme, b.scheme, R97_ENC_STR) || std::strncmp(a.transform, b.transform, R97_ENC_STR) ||
+        a.n_planes != b.n_planes || a.n_planes < 0 || a.n_planes > R97_ENC_MAX_PLANES)
+        return false;
+    for (int i = 0; i < a.n_planes; ++i) {
+        const R97EncPlane &p = a.plane[i], &q = b.plane[i];
+        if (std::strncmp(p.role, q.role, R97_ENC_STR) || p.kind != q.kind || p.dtype != q.dtype ||
+            p.block[0] != q.block[0] || p.block[1] != q.block[1] || p.extent[0] != q.extent[0] ||
+            p.extent[1] != q.extent[1])
+            return false;
+    }
+    return true;
+}
+
+// The description of the weight's joined device planes `raw` under `enc`, and its scale.col
+// factor (device, or null).
+R97IqrDecodeDesc describe(const R97Encoding* enc, const void* raw, int64_t rows, int64_t cols, const float** factor) {
+    int64_t off[R97_ENC_MAX_PLANES] = {};
+    if (r97_enc_plane_offsets(enc, rows, cols, off) < 0) fail("the encoding has no planes, or too many", rows, cols);
+    R97IqrStoredPlane plane[R97_ENC_MAX_PLANES] = {};
+    const uint8_t* base = static_cast<const uint8_t*>(raw);
+    uint32_t mad_words[2] = {0, 0};
+    for (int i = 0; i < enc->n_planes; ++i) {
+        plane[i].data = base + off[i];
+        plane[i].bytes = r97_enc_plane_bytes(&enc->plane[i], rows, cols);
+        // the computed codebook's two words travel in the description by value: read them here
+        if (std::strncmp(enc->plane[i].role, "trellis.mad", R97_ENC_STR) == 0 && plane[i].bytes >= 8) {
+            if (hipMemcpy(mad_words, plane[i].data, sizeof mad_words, hipMemcpyDeviceToHost) != hipSuccess)
+                fail("reading the trellis.mad plane failed", rows, cols);
+            plane[i].data = reinterpret_cast<const uint8_t*>(mad_words);
+        }
+    }
+    R97IqrDecodeDesc d;
+    if (!r97_iqr_desc_from_encoding(enc, plane, rows, cols, &d))
+        fail(std::string("the encoding (scheme '") + std::string(enc->scheme, strnlen(enc->scheme, R97_ENC_STR)) +
+                 "') is not a form the decode reads, or a plane it needs is missing",
+             rows, cols);
+    if (!r97_iqr_scale_col(enc, plane, rows, cols, factor))
+        fail("the scale.col factor is not one f32 a 128 columns beside one f32 scale a row", rows, cols);
+    return d;
+}
+
+Print print_of(const R97Encoding* enc, const void* raw, int64_t rows, int64_t cols) {
+    Print p{};
+    int64_t off[R97_ENC_MAX_PLANES] = {};
+    if (r97_enc_plane_offsets(enc, rows, cols, off) < 0) return p;
+    int at = 0;
+    for (int i = 0; i < enc->n_planes && at < 4; ++i) {
+        const char* role = enc->plane[i].role;
+        if (std::strncmp(role, "codes", R97_ENC_STR) && std::strncmp(role, "scale", R97_ENC_STR)) continue;
+        const int64_t bytes = r97_enc_plane_bytes(&enc->plane[i], rows, cols);
+        const int64_t n = bytes < 64 ? bytes : 64;
+        const uint8_t* base = static_cast<const uint8_t*>(raw) + off[i];
+        if (hipMemcpy(p.b[at++], base, (size_t)n, hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(p.b[at++], base + bytes - n, (size_t)n, hipMemcpyDeviceToHost) != hipSuccess)
+            fail("reading the planes failed", rows, cols);
+    }
+    return p;
+}
+
 }  // namespace
 
-const R97qWeight* device_weight_get(const IqrStoredEnc* enc, int64_t rows, int64_t cols, R97IqrStream stream) {
+const R97qWeight* device_weight_get(const R97Encoding* enc, const void* raw, int64_t rows, int64_t cols,
+                                    R97IqrStream stream) {
     if (enc == nullptr) fail("no encoding", rows, cols);
+    if (raw == nullptr) fail("no planes", rows, cols);
     Store& s = store();
     std::lock_guard<std::mutex> lock(s.mu);
-    const Key key{enc, rows, cols};
+    const Key key{enc, raw, rows, cols};
+    const Print print = print_of(enc, raw, rows, cols);
     const auto it = s.weights.find(key);
-    if (it != s.weights.end()) return &it->second.w;
-    if (enc->desc.rows != rows || enc->desc.cols != cols)
-        fail("the description covers [" + std::to_string(enc->desc.rows) + ", " + std::to_string(enc->desc.cols) +
-                 "]",
-             rows, cols);
-    const int64_t sbytes = r97q_weight_stream_bytes(&enc->desc);
+    if (it != s.weights.end()) {
+        if (same(it->second.enc, *enc) && std::memcmp(&it->second.print, &print, sizeof print) == 0)
+            return &it->second.w;
+        release(it->second);  // another weight at these addresses: prepare again
+        s.weights.erase(it);
+    }
+    const float* factor = nullptr;
+    const R97IqrDecodeDesc desc = describe(enc, raw, rows, cols, &factor);
+    const int64_t sbytes = r97q_weight_stream_bytes(&desc);
     if (sbytes < 0) fail(std::string("form not served by the fused kernels: ") + r97q_last_error(), rows, cols);
     Entry e;
+    e.enc = *enc;
+    e.print = print;
     const int64_t tbytes = (cols / 128) * rows * 2;
     if (hipMalloc(&e.stream_buf, (size_t)sbytes) != hipSuccess || hipMalloc(&e.scale_buf, (size_t)tbytes) != hipSuccess) {
         release(e);
         fail("device allocation failed", rows, cols);
     }
-    const int rc = r97q_weight_prepare(&enc->desc, enc->scale_col, static_cast<uint32_t*>(e.stream_buf),
+    const int rc = r97q_weight_prepare(&desc, factor, static_cast<uint32_t*>(e.stream_buf),
                                        static_cast<uint16_t*>(e.scale_buf), &e.w, stream);
     if (rc != R97Q_OK || hipStreamSynchronize(static_cast<hipStream_t>(stream)) != hipSuccess) {
         const std::string msg = rc != R97Q_OK ? r97q_last_error() : "stream synchronisation failed";
@@ -73,11 +151,12 @@ const R97qWeight* device_weight_get(const IqrStoredEnc* enc, int64_t rows, int64
     return &s.weights.emplace(key, e).first->second.w;
 }
 
-const R97qWeight* device_weight_find(const void* enc, int64_t rows, int64_t cols) {
+const R97qWeight* device_weight_find(const R97Encoding* enc, const void* raw, int64_t rows, int64_t cols) {
+    if (enc == nullptr) return nullptr;
     Store& s = store();
     std::lock_guard<std::mutex> lock(s.mu);
-    const auto it = s.weights.find(Key{enc, rows, cols});
-    return it == s.weights.end() ? nullptr : &it->second.w;
+    const auto it = s.weights.find(Key{enc, raw, rows, cols});
+    return it == s.weights.end() || !same(it->second.enc, *enc) ? nullptr : &it->second.w;
 }
 
 int64_t device_weight_count() {

@@ -78,3 +78,11 @@ def rel_l2(got: np.ndarray, want: np.ndarray) -> float:
     num = np.linalg.norm((np.asarray(got, np.float64) - np.asarray(want, np.float64)).ravel())
     den = np.linalg.norm(np.asarray(want, np.float64).ravel())
     return float(num / den) if den > 0 else float(num)
+
+
+def stored_operand(p: S.Planes, keep: list):
+    """The stored operand the rows read for `p`: (its R97Encoding, the joined planes on the device)."""
+    e, buf = S.joined(p)
+    d = dev(buf)
+    keep.append(d)
+    return e, d

@@ -220,3 +220,52 @@ AFFINE_CASES = [
     ("drafter-narrow-zero", dict(rows=300, cols=384, bits=2, zero_bits=4, scale_dtype=F16, seed=78)),
     ("drafter-bf16", dict(rows=300, cols=256, bits=4, zero_bits=8, scale_dtype=BF16, seed=79)),
 ]
+
+
+# ---------------------------------------------------------------- the encoding of a weight
+# The plane table a container would write for these planes (include/r97q.h, R97Encoding), the
+# plane roles src/iqr_form.h:87-217 reads, and each plane's bytes in plane order.
+def encoding(p: Planes):
+    """(R97Encoding, [host bytes of each plane, in plane order]) for the planes of `p`."""
+    import r9700training_amd as R
+
+    dt_of = {F32: R.R97_DT_F32, BF16: R.R97_DT_BF16, E4M3: R.R97_DT_F8E4M3, F16: R.R97_DT_F16}
+    e = R.Encoding()
+    e.scheme = b"affine" if p.affine else b"trellis"
+    planes = []
+    e.add("codes", R.R97_PLANE_TILED, p.bits, block=(1, 1))
+    planes.append(p.codes)
+    e.add("scale", R.R97_PLANE_TILED, dt_of[p.scale_dtype], block=(1, p.scale_block_cols))
+    planes.append(p.scale)
+    if p.affine:
+        e.add("zero", R.R97_PLANE_TILED, p.zero_bits, block=(1, 128))
+        planes.append(p.zero)
+    else:
+        e.add("trellis", R.R97_PLANE_TABLE, R.R97_DT_I8, block=(p.run_rows, p.rb), extent=(1 << p.state_bits, 1))
+        planes.append(p.lut.view(np.uint8))
+        if p.mad:
+            e.add("trellis.mad", R.R97_PLANE_TABLE, R.R97_DT_U32, extent=(2, 1))
+            planes.append(np.array([p.mad_a, p.mad_b], np.uint32).view(np.uint8))
+    if p.scale2 is not None:
+        e.add("scale.1", R.R97_PLANE_TILED, dt_of[p.scale2_dtype], block=(0, 0))
+        planes.append(p.scale2)
+    if p.scale_col is not None:
+        e.add("scale.col", R.R97_PLANE_TILED, R.R97_DT_F32, block=(0, 128))
+        planes.append(p.scale_col.view(np.uint8))
+    return e, [np.ascontiguousarray(a).view(np.uint8).reshape(-1) for a in planes]
+
+
+def joined(p: Planes):
+    """(R97Encoding, one host byte buffer holding every plane at the library's joined offsets)."""
+    import r9700training_amd as R
+
+    e, planes = encoding(p)
+    off = (C.c_int64 * R.R97_ENC_MAX_PLANES)()
+    total = R.lib().r97_enc_plane_offsets(C.byref(e), p.rows, p.cols, off)
+    assert total > 0
+    buf = np.zeros(total, np.uint8)
+    for i, a in enumerate(planes):
+        n = R.lib().r97_enc_plane_bytes(C.byref(e.plane[i]), p.rows, p.cols)
+        assert n == a.size, (e.plane[i].role, n, a.size)
+        buf[off[i]:off[i] + n] = a
+    return e, buf

@@ -45,12 +45,6 @@ AdValue val(const char* dtype, std::vector<int64_t> shape, const double* v) {
     return a;
 }
 
-// the stored-weight encodings handed out, one stable object per plane pointer
-std::map<const void*, IqrStoredEnc>& encs() {
-    static std::map<const void*, IqrStoredEnc> m;
-    return m;
-}
-
 AdjointFn row(const char* op, const std::vector<OpParam>& params) {
     std::string err;
     AdjointFn fn = adjoint_find(op, Side::device, params, &err);
@@ -138,13 +132,14 @@ int rh_registry_selftest() {
     CHECK(adjoint_find("gemm_nt", Side::device, f32, nullptr) == nullptr);
     CHECK(adjoint_find("lora_shrink", Side::device, bf16, nullptr) != nullptr);
     CHECK(adjoint_frozen("lora_shrink", Side::device, bf16) == (std::vector<int>{1, 2, 3}));
-    // the coded trunk: the i8 shrink and gemm_nt_q (i8a8h, group 128) have device rows; fp8 codes and
-    // another group width do not
+    // the coded trunk: the coded shrink (i8 and both fp8 code dtypes, the reference's coded_act) and
+    // gemm_nt_q (i8a8h, group 128) have device rows; another group width does not
     CHECK(adjoint_find("lora_shrink", Side::device, i8, nullptr) != nullptr);
     CHECK(adjoint_find("lora_shrink", Side::device, i8, nullptr) != adjoint_find("lora_shrink", Side::device, bf16, nullptr));
     CHECK(adjoint_frozen("lora_shrink", Side::device, i8) == (std::vector<int>{2, 3}));
-    const std::vector<OpParam> fp8 = {{"dtype", std::string("fp8_e4m3")}};
-    CHECK(adjoint_find("lora_shrink", Side::device, fp8, nullptr) == nullptr);
+    for (const char* fp8 : {"fp8_e4m3", "fp8_e5m2"})
+        CHECK(adjoint_find("lora_shrink", Side::device, {{"dtype", std::string(fp8)}}, nullptr) ==
+              adjoint_find("lora_shrink", Side::device, i8, nullptr));
     const std::vector<OpParam> q128 = {{"dtype", std::string("i8a8h")}, {"group", int64_t(128)}},
                                q64 = {{"dtype", std::string("i8a8h")}, {"group", int64_t(64)}};
     CHECK(adjoint_find("gemm_nt_q", Side::device, q128, nullptr) != nullptr);
@@ -159,10 +154,10 @@ int rh_registry_selftest() {
     return 0;
 }
 
-// dx[M, K] += dy[M, N] . W: W the stored IQR weight `desc` (device planes; scale_col device or
-// null) when w_dense is null, else the dense bf16-valued W[N, K].
-int rh_gemm_nt(int64_t M, int64_t N, int64_t K, const double* dy, const R97IqrDecodeDesc* desc,
-               const float* scale_col, const double* w_dense, double* dx) {
+// dx[M, K] += dy[M, N] . W: W the stored IQR weight (its encoding `enc` over the joined device
+// planes `raw`, the operand the tape hands) when w_dense is null, else the dense bf16-valued W[N, K].
+int rh_gemm_nt(int64_t M, int64_t N, int64_t K, const double* dy, const R97Encoding* enc, const void* raw,
+               const double* w_dense, double* dx) {
     try {
         OpRecord rec;
         rec.op = "gemm_nt";
@@ -175,12 +170,9 @@ int rh_gemm_nt(int64_t M, int64_t N, int64_t K, const double* dy, const R97IqrDe
         if (w_dense) {
             fwd[1].value.assign(w_dense, w_dense + N * K);
         } else {
-            IqrStoredEnc& e = encs()[desc->codes];
-            e.desc = *desc;
-            e.scale_col = scale_col;
-            fwd[1].raw = desc->codes;
-            fwd[1].enc = &e;
-            rec.operands[1].enc = &e;
+            fwd[1].raw = raw;
+            fwd[1].enc = enc;
+            rec.operands[1].enc = enc;
         }
         fwd[2].dtype = "bf16";
         fwd[2].shape = {M, N};
@@ -289,13 +281,12 @@ int rh_lora_expand(int64_t M, int64_t N, int64_t R, int64_t S, const double* t, 
 }
 
 // gemm_nt_q's row (the coded trunk): da[M, K] += ..., a codes (values unused by the adjoint),
-// a_scale [M, K/128], the weight stored (desc) or, when w_codes is given, carried as codes
-// [N, K] with b_scale [N, K/128]
-int rh_gemm_nt_q(int64_t M, int64_t N, int64_t K, const double* dy, const double* a_scale,
-                 const R97IqrDecodeDesc* desc, const float* scale_col, const double* w_codes, const double* b_scale,
-                 double* da) {
+// a_scale [M, ceil(K/128)], the weight stored (enc over raw) or, when w_codes is given, carried as
+// codes [N, K] with b_scale [N, ceil(K/128)]
+int rh_gemm_nt_q(int64_t M, int64_t N, int64_t K, const double* dy, const double* a_scale, const R97Encoding* enc,
+                 const void* raw, const double* w_codes, const double* b_scale, double* da) {
     try {
-        const int64_t G = K / 128;
+        const int64_t G = (K + 127) / 128;
         OpRecord rec;
         rec.op = "gemm_nt_q";
         rec.params = {{"M", M}, {"N", N}, {"K", K}, {"group", int64_t(128)}, {"dtype", std::string("i8a8h")}};
@@ -308,12 +299,9 @@ int rh_gemm_nt_q(int64_t M, int64_t N, int64_t K, const double* dy, const double
         if (w_codes) {
             fwd[2].value.assign(w_codes, w_codes + N * K);
         } else {
-            IqrStoredEnc& e = encs()[desc->codes];
-            e.desc = *desc;
-            e.scale_col = scale_col;
-            fwd[2].raw = desc->codes;
-            fwd[2].enc = &e;
-            rec.operands[2].enc = &e;
+            fwd[2].raw = raw;
+            fwd[2].enc = enc;
+            rec.operands[2].enc = enc;
         }
         const std::vector<AdValue> cot = {val("f32", {M, N}, dy)};
         std::vector<AdValue> dc = {val("i8", {M, K}, da), AdValue{}, AdValue{}, AdValue{}, AdValue{}};
@@ -329,19 +317,19 @@ int rh_gemm_nt_q(int64_t M, int64_t N, int64_t K, const double* dy, const double
 
 // the coded shrink's row: da[M, K] and ds[M, groups] += ..., dA: the lora_A leaves as [S, R, K]
 // (fused: the one [S*R, K] leaf)
-int rh_lora_shrink_q(int64_t M, int64_t K, int64_t R, int64_t S, int64_t groups, int64_t group, const double* a,
-                     const double* a_scale, const double* slot, const double* la, const double* t_cot, double* da,
-                     double* ds, float* dA, int fused) {
+int rh_lora_shrink_q(int64_t M, int64_t K, int64_t R, int64_t S, int64_t groups, int64_t group, const char* dtype,
+                     const double* a, const double* a_scale, const double* slot, const double* la, const double* t_cot,
+                     double* da, double* ds, float* dA, int fused) {
     try {
         OpRecord rec;
         rec.op = "lora_shrink";
-        rec.params = {{"M", M}, {"K", K}, {"R", R}, {"S", S}, {"group", group}, {"dtype", std::string("i8")}};
-        rec.operands = {opd("a", "i8", {M, K}), opd("a_scale", "f32", {M, groups}), opd("slot", "i32", {M}),
+        rec.params = {{"M", M}, {"K", K}, {"R", R}, {"S", S}, {"group", group}, {"dtype", std::string(dtype)}};
+        rec.operands = {opd("a", dtype, {M, K}), opd("a_scale", "f32", {M, groups}), opd("slot", "i32", {M}),
                         opd("lora_a", "bf16", {S, R, K}), opd("t", "f32", {M, R}, true)};
-        const std::vector<AdValue> fwd = {val("i8", {M, K}, a), val("f32", {M, groups}, a_scale), val("i32", {M}, slot),
+        const std::vector<AdValue> fwd = {val(dtype, {M, K}, a), val("f32", {M, groups}, a_scale), val("i32", {M}, slot),
                                           val("bf16", {S, R, K}, la), val("f32", {M, R}, nullptr)};
         const std::vector<AdValue> cot = {val("f32", {M, R}, t_cot)};
-        std::vector<AdValue> dc = {val("i8", {M, K}, da), val("f32", {M, groups}, ds), AdValue{}, AdValue{}, AdValue{}};
+        std::vector<AdValue> dc = {val(dtype, {M, K}, da), val("f32", {M, groups}, ds), AdValue{}, AdValue{}, AdValue{}};
         ParamSet grads;
         AdjointCall call{rec, fwd, cot, &dc, dA ? &grads : nullptr, "layers.1.q", {}, fused != 0, nullptr, nullptr};
         if (!fused) call.slot_prefix = [](int64_t s) { return "adapter" + std::to_string(s); };

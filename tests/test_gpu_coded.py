@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import iqr_synth as S
-from gpu_util import bf16_tensor, dev, device_desc, f64, host_weight, prepared, rel_l2
+from gpu_util import bf16_tensor, dev, device_desc, f64, host_weight, prepared, rel_l2, stored_operand
 from oracle import oracle as O
 from test_rows import bf16_round, check, hook, p
 
@@ -90,7 +90,6 @@ def test_lora_shrink_q_bwd(T, K, r, groups):
 def test_gemm_nt_q_row(M, N, K, carried):
     print(f"case gemm_nt_q row M={M} N={N} K={K} carried={carried}", flush=True)
     L = hook()
-    L.rh_weights_clear()  # an earlier case's encoding entry may sit at this case's device addresses
     L.rh_gemm_nt_q.argtypes = [C.c_int64] * 3 + [C.c_void_p] * 7
     rng = np.random.default_rng(M + N + K + 7)
     dy = rng.standard_normal((M, N))
@@ -105,10 +104,8 @@ def test_gemm_nt_q_row(M, N, K, carried):
         check(L, L.rh_gemm_nt_q(M, N, K, p(dy), p(a_scale), None, None, p(wc), p(bsc), p(da)))
     else:
         keep = []
-        d = device_desc(planes, keep)
-        sc = dev(planes.scale_col)
-        keep.append(sc)
-        check(L, L.rh_gemm_nt_q(M, N, K, p(dy), p(a_scale), C.addressof(d), sc.data_ptr(), None, None, p(da)))
+        enc, raw = stored_operand(planes, keep)
+        check(L, L.rh_gemm_nt_q(M, N, K, p(dy), p(a_scale), C.addressof(enc), raw.data_ptr(), None, None, p(da)))
     want = O.gemm_nt_q_adjoint(dy, codes, scale, a_scale, da=da0)
     e = rel_l2(da - da0, want - da0)
     print(f"  rel L2 da {e:.3e}", flush=True)
@@ -120,7 +117,7 @@ def test_gemm_nt_q_row(M, N, K, carried):
 def test_lora_shrink_q_row(M, K, R, S_, groups, fused):
     print(f"case coded lora_shrink row M={M} K={K} R={R} S={S_} groups={groups} fused={fused}", flush=True)
     L = hook()
-    L.rh_lora_shrink_q.argtypes = [C.c_int64] * 6 + [C.c_void_p] * 8 + [C.c_int]
+    L.rh_lora_shrink_q.argtypes = [C.c_int64] * 6 + [C.c_char_p] + [C.c_void_p] * 8 + [C.c_int]
     rng = np.random.default_rng(M + K + R)
     a, a_scale = codes_and_scales(rng, M, K, groups)
     slot = np.array([-1 if m == 1 else (S_ if m == 2 else m % S_) for m in range(M)], np.float64)
@@ -131,8 +128,8 @@ def test_lora_shrink_q_row(M, K, R, S_, groups, fused):
     da, ds = da0.copy(), ds0.copy()
     dA = np.zeros((S_ * R, K), np.float32)
     group = O.group_width(K, groups)
-    check(L, L.rh_lora_shrink_q(M, K, R, S_, groups, group, p(a), p(a_scale), p(slot), p(la), p(ct), p(da), p(ds),
-                                p(dA), int(fused)))
+    check(L, L.rh_lora_shrink_q(M, K, R, S_, groups, group, b"i8", p(a), p(a_scale), p(slot), p(la), p(ct), p(da),
+                                p(ds), p(dA), int(fused)))
     want_da, want_ds, want_dA = O.lora_shrink_q_adjoint(a, a_scale, slot, la, ct, da=da0, ds=ds0, fused=True)
     e_da, e_ds, e_dA = rel_l2(da - da0, want_da - da0), rel_l2(ds - ds0, want_ds - ds0), rel_l2(dA, want_dA)
     print(f"  rel L2 da {e_da:.3e} ds {e_ds:.3e} dA {e_dA:.3e}", flush=True)
@@ -141,24 +138,17 @@ def test_lora_shrink_q_row(M, K, R, S_, groups, fused):
     assert np.array_equal(da[1:3], da0[1:3]) and np.array_equal(ds[1:3], ds0[1:3])
 
 
-def test_coded_refusals():
+def test_coded_entry_refusals():
+    """The C entry serves K a multiple of 128 (the rows pad other widths) and a group width whose
+    groups fit K; it refuses the rest by name."""
     from r9700training_amd import R97qError
     from r9700training_amd.qlinear import lora_shrink_q_bwd
 
-    L = hook()
-    L.rh_lora_shrink_q.argtypes = [C.c_int64] * 6 + [C.c_void_p] * 8 + [C.c_int]
-    # the reference's coded sites have rank 4 and K 300: outside this build's kernels, refused by name
-    z = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden",
-                                           "lora_coded_up_proj.npz"))
-    a, a_scale, slot, la, ct = (z[k] for k in ("a", "a_scale", "slot", "la", "ct"))
-    S_, R, K = la.shape
-    M, groups = a_scale.shape
-    da, ds = np.zeros((M, K)), np.zeros((M, groups))
-    rc = L.rh_lora_shrink_q(M, K, R, S_, groups, O.group_width(K, groups), p(a), p(a_scale), p(slot), p(la), p(ct),
-                            p(da), p(ds), None, 0)
-    assert rc != 0 and b"not served" in L.rh_last_error()
-    assert not da.any() and not ds.any()
     with pytest.raises(R97qError, match="K a multiple of 128"):
         lora_shrink_q_bwd(torch.zeros((8, 300), dtype=torch.int8, device="cuda"),
                           torch.ones((8, 3), device="cuda"), torch.zeros((16, 300), dtype=torch.bfloat16, device="cuda"),
                           torch.zeros((8, 16), device="cuda"))
+    with pytest.raises(R97qError, match="do not fit K"):
+        lora_shrink_q_bwd(torch.zeros((8, 256), dtype=torch.int8, device="cuda"),
+                          torch.ones((8, 3), device="cuda"), torch.zeros((16, 256), dtype=torch.bfloat16, device="cuda"),
+                          torch.zeros((8, 16), device="cuda"), group_width=128)

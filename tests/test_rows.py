@@ -67,15 +67,11 @@ def test_gemm_nt_row_other_forms(form):
     """A stored weight in a form the kernels do not decode themselves (a stored LUT with bf16 block
     scales, rb > 1 row blocks, e4m3 block scales with scale.1) reaches the row through the same
     stored-weight store, prepared once into the int8-code form."""
-    from gpu_util import device_desc, dev, host_weight
+    from gpu_util import host_weight, stored_operand
     from oracle import oracle as O
 
     print(f"case gemm_nt stored form {form}", flush=True)
     L = hook()
-    # the store is keyed by the encoding, as the reference's is; this test's planes may reuse an
-    # earlier case's device addresses (and so its encoding entry), so it starts from an empty store,
-    # as the reference's walk does at every step (stored_weight_clear)
-    L.rh_weights_clear()
     M, N, K = 72, 256, 384
     rng = np.random.default_rng(len(form))
     kw = {"lut-bf16": dict(bits=4, state_bits=16, run_rows=128, rb=1, mad=0, scale_dtype=S.BF16),
@@ -83,15 +79,11 @@ def test_gemm_nt_row_other_forms(form):
           "e4m3-scale1": dict(bits=5, state_bits=12, run_rows=128, rb=1, mad=0, scale_dtype=S.E4M3, second=True)}[form]
     planes = S.trellis(rows=N, cols=K, seed=7, **kw)
     keep = []
-    d = device_desc(planes, keep)
-    sc = None
-    if planes.scale_col is not None:
-        sc = dev(planes.scale_col)
-        keep.append(sc)
+    enc, raw = stored_operand(planes, keep)
     dy = rng.standard_normal((M, N))
     dx0 = rng.standard_normal((M, K))
     dx = dx0.copy()
-    check(L, L.rh_gemm_nt(M, N, K, p(dy), C.addressof(d), sc.data_ptr() if sc is not None else None, None, p(dx)))
+    check(L, L.rh_gemm_nt(M, N, K, p(dy), C.addressof(enc), raw.data_ptr(), None, p(dx)))
     codes, scale = host_weight(planes)
     want = O.gemm_nt_adjoint(dy, codes, scale, dx=dx0)
     e = rel_l2(dx - dx0, want - dx0)
@@ -102,12 +94,11 @@ def test_gemm_nt_row_other_forms(form):
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,N,K,dense", [(96, 256, 384, False), (200, 512, 256, False), (64, 384, 256, True)])
 def test_gemm_nt_row(M, N, K, dense):
-    from gpu_util import device_desc, dev, host_weight
+    from gpu_util import host_weight, stored_operand
     from oracle import oracle as O
 
     print(f"case gemm_nt M={M} N={N} K={K} dense={dense}", flush=True)
     L = hook()
-    L.rh_weights_clear()  # an earlier case's encoding entry may sit at this case's device addresses
     rng = np.random.default_rng(M + N + K)
     dy = rng.standard_normal((M, N))
     dx0 = rng.standard_normal((M, K))
@@ -120,16 +111,14 @@ def test_gemm_nt_row(M, N, K, dense):
         planes = S.trellis(rows=N, cols=K, bits=5, state_bits=16, run_rows=128, rb=1, mad=1, scale_dtype=S.F32,
                            rowf=True, seed=M, scale_col=(0.75 + 0.5 * rng.random(K // 128)).astype(np.float32))
         keep = []
-        d = device_desc(planes, keep)
-        sc = dev(planes.scale_col)
-        keep.append(sc)
-        check(L, L.rh_gemm_nt(M, N, K, p(dy), C.addressof(d), sc.data_ptr(), None, p(dx)))
+        enc, raw = stored_operand(planes, keep)
+        check(L, L.rh_gemm_nt(M, N, K, p(dy), C.addressof(enc), raw.data_ptr(), None, p(dx)))
         codes, scale = host_weight(planes)
         want = O.gemm_nt_adjoint(dy, codes, scale, dx=dx0)
         # a second call reuses the prepared weight
         before = L.rh_weights_prepared()
         dx2 = dx0.copy()
-        check(L, L.rh_gemm_nt(M, N, K, p(dy), C.addressof(d), sc.data_ptr(), None, p(dx2)))
+        check(L, L.rh_gemm_nt(M, N, K, p(dy), C.addressof(enc), raw.data_ptr(), None, p(dx2)))
         assert L.rh_weights_prepared() == before and np.array_equal(dx2, dx)
     e = rel_l2(dx - dx0, want - dx0)
     print(f"  rel L2 dx {e:.3e}", flush=True)
@@ -194,16 +183,27 @@ def test_lora_expand_row(M, N, R, S, scaled, fused, in_place):
 
 
 @pytest.mark.gpu
-def test_unserved_rank_is_refused():
+@pytest.mark.parametrize("M,K,R,S,fused", [(32, 200, 12, 1, False), (20, 128, 100, 2, True)])
+def test_lora_shrink_row_any_rank_and_width(M, K, R, S, fused):
+    """A rank the kernels do not run at (12: padded to 16; 100: a chunk of 64 and one of 36, padded
+    to 64) and a K off a multiple of 128 (200: padded to 256) are served exactly."""
+    from oracle import oracle as O
+
+    print(f"case lora_shrink padded M={M} K={K} R={R} S={S} fused={fused}", flush=True)
     L = hook()
-    M, K, R = 32, 256, 12
-    x = np.zeros((M, K))
-    la = np.zeros((1, R, K))
-    slot = np.zeros(M)
-    ct = np.zeros((M, R))
-    dx = np.zeros((M, K))
-    assert L.rh_lora_shrink(M, K, R, 1, p(x), p(slot), p(la), p(ct), p(dx), None, 0) != 0
-    assert b"rank 12" in L.rh_last_error()
+    rng = np.random.default_rng(M + K + R)
+    x = bf16_round(rng.standard_normal((M, K)))
+    la = bf16_round(0.02 * rng.standard_normal((S, R, K)))
+    slot = np.array([-1 if m == 1 else (S if m == 2 else m % S) for m in range(M)], np.float64)
+    ct = rng.standard_normal((M, R)).astype(np.float32).astype(np.float64)
+    dx0 = rng.standard_normal((M, K))
+    dx = dx0.copy()
+    dA = np.zeros(S * R * K, np.float32)
+    check(L, L.rh_lora_shrink(M, K, R, S, p(x), p(slot), p(la), p(ct), p(dx), p(dA), int(fused)))
+    ref_dx, ref_da = O.lora_shrink_adjoint(x, slot, la, ct, dx=dx0, fused=True)
+    e_dx, e_da = rel_l2(dx - dx0, ref_dx - dx0), rel_l2(dA, ref_da.ravel())
+    print(f"  rel L2 dx {e_dx:.3e} dA {e_da:.3e}", flush=True)
+    assert e_dx <= TOL and e_da <= TOL
 
 
 @pytest.mark.gpu
