@@ -316,6 +316,18 @@ int r97q_qlinear_dx_base(const R97qWeight* w, const uint16_t* dY, int64_t T, int
                          int32_t dx_dtype, int32_t dx_accumulate, void* workspace,
                          int64_t workspace_bytes, R97IqrStream stream);
 
+/* The forward with no allocation and no workspace argument. No counterpart in the reference: for
+ * callers that cannot allocate or hand over device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, results and status as
+ * r97q_qlinear_lora_fwd without the workspace pair; the workspace is a device array of the
+ * library's own, one per GPU, of r97q_qlinear_lora_fwd_noalloc_max_bytes() bytes (48 MiB: T*K*2
+ * plus T*r*4 and a little, e.g. T = K = 4096 at rank 16). A larger shape gets R97Q_EWORKSPACE.
+ * Calls that overlap on one GPU share that array and race: serialise them (one stream, or events). */
+int64_t r97q_qlinear_lora_fwd_noalloc_max_bytes(void);
+int r97q_qlinear_lora_fwd_noalloc(const R97qWeight* w, const uint16_t* X, int64_t T, const uint16_t* A,
+                                  const uint16_t* B, int32_t rank, float scale, void* Y, int32_t y_dtype,
+                                  float* t_out, R97IqrStream stream);
+
 /* ------------------------------------------------------------------ the adapter's rows on their own
  *
  * The shrink's and the expand's adjoints as separate calls, for a caller whose backward walk runs

@@ -138,6 +138,8 @@ SIGNATURES = {
     "r97q_fwd_workspace_bytes": (C.c_int64, [_I, _I, _I, _i]),
     "r97q_bwd_workspace_bytes": (C.c_int64, [_I, _I, _I, _i]),
     "r97q_qlinear_lora_fwd": (C.c_int, [C.POINTER(Weight), _P, _I, _P, _P, _i, C.c_float, _P, _i, _P, _P, _I, _P]),
+    "r97q_qlinear_lora_fwd_noalloc_max_bytes": (C.c_int64, []),
+    "r97q_qlinear_lora_fwd_noalloc": (C.c_int, [C.POINTER(Weight), _P, _I, _P, _P, _i, C.c_float, _P, _i, _P, _P]),
     "r97q_qlinear_lora_bwd": (C.c_int, [C.POINTER(Weight), _P, _P, _I, _P, _P, _i, C.c_float, _P, _P, _i, _i,
                                         _P, _P, _P, _I, _P]),
     "r97q_iqr_encode_trellis": (C.c_int, [_P, _I, _I, _i, _i, _i, C.c_uint32, C.c_uint32, _P, _P, _P, _i,

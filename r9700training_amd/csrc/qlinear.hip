@@ -360,6 +360,41 @@ int shape_ok(int64_t T, int64_t N, int64_t K, const char* who) {
 
 }  // namespace
 
+// ---------------------------------------------------------------- the forward with no allocation
+// The forward's workspace (the token operand's tiled copy, the adapter's [hi | lo] splits) held in a
+// file-scope device array instead of a caller's buffer, for callers that cannot allocate. Each GPU
+// holds its own copy of the array; host code reaches it only through the address
+// hipGetSymbolAddress gives on that device (the array's name is a host-side stand-in there). Calls
+// that overlap on one GPU share it and race; nothing in it needs to start at zero (the forward
+// writes every byte it reads).
+constexpr int64_t kNoAllocScratchBytes = int64_t(48) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kNoAllocDevices = 64;
+void* g_scratch_at[kNoAllocDevices] = {};
+
+// this device's scratch address, looked up once per device with that device current
+int scratch_of_current_device(uint8_t** at, const char* who) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kNoAllocDevices) {
+        set_error("%s: no current device (or device %d past %d)", who, dev, kNoAllocDevices);
+        return R97Q_ELAUNCH;
+    }
+    void* p = __atomic_load_n(&g_scratch_at[dev], __ATOMIC_ACQUIRE);
+    if (p == nullptr) {
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_error("%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev, hipGetErrorString(e));
+            return R97Q_ELAUNCH;
+        }
+        __atomic_store_n(&g_scratch_at[dev], p, __ATOMIC_RELEASE);
+    }
+    *at = static_cast<uint8_t*>(p);
+    return R97Q_OK;
+}
+}  // namespace
+
 extern "C" {
 
 int64_t r97q_fwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank) {
@@ -677,4 +712,37 @@ int r97q_lora_expand_bwd(int64_t T, int64_t N, const uint16_t* dY, const uint16_
     return R97Q_OK;
 }
 
+int64_t r97q_qlinear_lora_fwd_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+int r97q_qlinear_lora_fwd_noalloc(const R97qWeight* w, const uint16_t* X, int64_t T, const uint16_t* A,
+                                  const uint16_t* B, int32_t rank, float scale, void* Y, int32_t y_dtype,
+                                  float* t_out, R97IqrStream stream) {
+    clear_error();
+    const char* who = "r97q_qlinear_lora_fwd_noalloc";
+    if (int e = check_weight(w)) return e;
+    if (int e = check_rank(rank, who)) return e;
+    if (!X || !Y || T <= 0) {
+        set_error("%s: null X / Y or T <= 0", who);
+        return R97Q_EINVAL;
+    }
+    if (rank > 0 && (!A || !B || !t_out)) {
+        set_error("%s: rank %d needs A, B and t_out", who, (int)rank);
+        return R97Q_EINVAL;
+    }
+    const Shape sh{T, w->rows, w->cols, rank};
+    const int64_t need = fwd_ws(sh).total;
+    if (need > kNoAllocScratchBytes) {
+        set_error("%s: T %lld x K %lld at rank %d needs %lld workspace bytes, past the %lld this entry holds "
+                  "(use r97q_qlinear_lora_fwd with a workspace)",
+                  who, (long long)T, (long long)w->cols, (int)rank, (long long)need, (long long)kNoAllocScratchBytes);
+        return R97Q_EWORKSPACE;
+    }
+    uint8_t* wsb = nullptr;
+    if (int e = scratch_of_current_device(&wsb, who)) return e;
+    const hipStream_t s = (hipStream_t)stream;
+    if (int e = fwd_prep(sh, X, A, scale, t_out, wsb, s)) return e;
+    return fwd_base(w, sh, B, Y, y_dtype, wsb, s);
+}
+
 }  // extern "C"
+
