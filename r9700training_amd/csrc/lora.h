@@ -8,6 +8,7 @@ namespace r97q {
 
 // v[m][j] = sum_k In[m][k] W[j][k] for m < T, j < r (W row-major [down_rank(r), Kin], rows past r
 // zero; Kin a multiple of 128). Writes, each when non-null:
+//   tiled              the fused kernels' tiled copy of In (act_tiles.h), rows T..32*ceil(T/32) zero
 //   out [T, r] f32    = sa * v   (+= when out_add)
 //   P   [T, 2r] bf16  = [hi | lo](sb * v)                    (row-major)
 //   Pt  [2r, ldt] bf16 = [hi | lo](sb * v), transposed       (zero for T <= m < ldt)
@@ -25,6 +26,7 @@ struct DownArgs {
     float s2;
     uint16_t* Pt2;
     int out_add;  // out += (instead of =)
+    uint16_t* tiled;
 };
 
 // out += scale * sum_m (Pt[j][m] + Pt[r+j][m]) V[m][c]: V bf16 [T, C] (C a multiple of 128), out

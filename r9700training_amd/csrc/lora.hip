@@ -33,6 +33,7 @@
 
 #include <cstdint>
 
+#include "act_tiles.h"
 #include "iqr_device.h"
 #include "lora.h"
 #include "status.h"
@@ -95,6 +96,15 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
     constexpr int U = 8 / NB;
     constexpr int CH = 32 * U;
     const int64_t nch = kq / CH;
+    // the tiled copy: every value this lane loads, at the lane's true row (a row past T, up to the
+    // copy's 32-row padding, is written as zeros)
+    const int64_t mt = m0 + row16;
+    const bool tile_row = a.tiled != nullptr && mt < (a.T + 31) / 32 * 32;
+    auto tile = [&](int64_t k, const uint4& v) {
+        if (tile_row)
+            *reinterpret_cast<uint4*>(a.tiled + act_tile_index(mt, wave * kq + 8 * grp + k, a.T)) =
+                mt < a.T ? v : uint4{0u, 0u, 0u, 0u};
+    };
     uint4 xv[2][U], fv[2][U][NB];
     auto load = [&](int64_t k, uint4 (&x)[U], uint4 (&f)[U][NB]) {
 #pragma unroll
@@ -105,23 +115,27 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
                 f[u][nb] = *reinterpret_cast<const uint4*>(wp + (int64_t)16 * nb * a.Kin + k + 32 * u);
         }
     };
-    auto mult = [&](const uint4 (&x)[U], const uint4 (&f)[U][NB]) {
+    auto mult = [&](int64_t k, const uint4 (&x)[U], const uint4 (&f)[U][NB]) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+        for (int u = 0; u < U; ++u) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16(as_bf16x8(x[u]), as_bf16x8(f[u][nb]), acc[nb]);
+            tile(k + 32 * u, x[u]);
+        }
     };
     int64_t c = 0;
     if (nch > 0) load(0, xv[0], fv[0]);
     for (; c + 2 <= nch; c += 2) {
         load((c + 1) * CH, xv[1], fv[1]);
-        mult(xv[0], fv[0]);
+        mult(c * CH, xv[0], fv[0]);
         if (c + 2 < nch) load((c + 2) * CH, xv[0], fv[0]);
-        mult(xv[1], fv[1]);
+        mult((c + 1) * CH, xv[1], fv[1]);
     }
-    if (c < nch) mult(xv[0], fv[0]);  // an odd chunk count: the last one sits in set 0
+    if (c < nch) mult(c * CH, xv[0], fv[0]);  // an odd chunk count: the last one sits in set 0
     for (int64_t k = nch * CH; k < kq; k += 32) {
-        const bf16x8 av = as_bf16x8(*reinterpret_cast<const uint4*>(ap + k));
+        const uint4 xr = *reinterpret_cast<const uint4*>(ap + k);
+        tile(k, xr);
+        const bf16x8 av = as_bf16x8(xr);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
             acc[nb] = mfma16(av, as_bf16x8(*reinterpret_cast<const uint4*>(wp + (int64_t)16 * nb * a.Kin + k)), acc[nb]);
@@ -504,7 +518,9 @@ __global__ __launch_bounds__(256) void transpose2_kernel(const uint16_t* __restr
 template <int RD>
 int down_r(const DownArgs& a, hipStream_t s) {
     const int nw = a.Kin % 256 == 0 ? kDownWavesMax : 4;
-    hipLaunchKernelGGL(lora_down_kernel<RD>, dim3((unsigned)((a.ldt + 15) / 16)), dim3(64 * nw), 0, s, a);
+    // the workgroups cover the splits' ldt rows and, when the tiled copy is written, its 32-row padding
+    const int64_t rows = a.tiled && (a.T + 31) / 32 * 32 > a.ldt ? (a.T + 31) / 32 * 32 : a.ldt;
+    hipLaunchKernelGGL(lora_down_kernel<RD>, dim3((unsigned)((rows + 15) / 16)), dim3(64 * nw), 0, s, a);
     return launch_status("lora_down_kernel");
 }
 

@@ -195,8 +195,9 @@ int check_ws(int64_t have, int64_t need, const void* ws, const char* who) {
 int fwd_prep(const Shape& sh, const uint16_t* X, const uint16_t* A, float scale, float* t_out,
              uint8_t* wsb, hipStream_t s) {
     const FwdWs ws = fwd_ws(sh);
-    if (int e = launch_act_tile(X, sh.T, sh.K, reinterpret_cast<uint16_t*>(wsb + ws.Xt), s)) return e;
-    if (sh.r == 0) return R97Q_OK;
+    uint16_t* Xt = reinterpret_cast<uint16_t*>(wsb + ws.Xt);
+    // rank 0: the tiled copy alone; else the down product writes it as it reads X
+    if (sh.r == 0) return launch_act_tile(X, sh.T, sh.K, Xt, s);
     const int rank = sh.r, rd = down_rank(rank);
     const uint16_t* Wd = A;
     if (rd != rank) {
@@ -217,6 +218,7 @@ int fwd_prep(const Shape& sh, const uint16_t* X, const uint16_t* A, float scale,
     a.sb = scale;
     a.out = t_out;
     a.P = reinterpret_cast<uint16_t*>(wsb + ws.P);
+    a.tiled = Xt;
     return launch_lora_down(a, s);
 }
 
@@ -264,8 +266,8 @@ int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* B, void* Y, i
 int bwd_prep(const Shape& sh, const uint16_t* dY, const uint16_t* A, const uint16_t* B, const float* t,
              float scale, uint8_t* wsb, hipStream_t s) {
     const BwdWs ws = bwd_ws(sh);
-    if (int e = launch_act_tile(dY, sh.T, sh.N, reinterpret_cast<uint16_t*>(wsb + ws.dYt), s)) return e;
-    if (sh.r == 0) return R97Q_OK;
+    uint16_t* dYt = reinterpret_cast<uint16_t*>(wsb + ws.dYt);
+    if (sh.r == 0) return launch_act_tile(dY, sh.T, sh.N, dYt, s);
     uint16_t* Bt = reinterpret_cast<uint16_t*>(wsb + ws.Bt);
     uint16_t* At = reinterpret_cast<uint16_t*>(wsb + ws.At);
     if (int e = launch_transpose2(B, Bt, sh.N, A, At, sh.K, sh.r, s)) return e;
@@ -280,6 +282,7 @@ int bwd_prep(const Shape& sh, const uint16_t* dY, const uint16_t* A, const uint1
     a.sb = scale;
     a.P = reinterpret_cast<uint16_t*>(wsb + ws.P);
     a.Pt = reinterpret_cast<uint16_t*>(wsb + ws.PtA);
+    a.tiled = dYt;
     if (t) {
         a.U2 = t;
         a.s2 = scale;
