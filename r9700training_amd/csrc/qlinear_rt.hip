@@ -186,6 +186,20 @@ struct Wave {
     int64_t sstride; // elements between consecutive steps of the tiled operand
     int lane;
     int nsteps;
+    // forward, trellis forms: the stream offsets of the lane's 32-row segment g and of its halo (the
+    // segment below, or the run's top one at the tail-biting seam)
+    int64_t fwd_seg = 0, fwd_halo = 0;
+
+    __device__ __forceinline__ void setup() {
+        if constexpr (FWD && !C8) {
+            const int64_t rs = p.run_rows >> 5, ns = p.N >> 5;
+            const int64_t g = (o0 >> 5) + (lane >> 4);
+            const int64_t top = (g / rs + 1) * rs;
+            const int64_t gh = g % rs != 0 ? g - 1 : (top < ns ? top : ns) - 1;
+            fwd_seg = g * BITS * (p.K >> 2) * 4;
+            fwd_halo = gh * BITS * (p.K >> 2) * 4;
+        }
+    }
 
     // ------------------------------------------------ the weight words of step s
     __device__ __forceinline__ void words(int s, LW& wd) const {
@@ -226,14 +240,15 @@ struct Wave {
             using S = Span<BITS, ROWS, SLICE>;
             const int64_t rs = p.run_rows >> 5;  // segments a run
             if constexpr (FWD) {
-                const int seg = lane >> 4, cg = lane & 15;
-                const int64_t g = (o0 >> 5) + seg;
-                const int64_t gh = g % rs != 0 ? g - 1 : (((g / rs + 1) * rs < (N >> 5) ? (g / rs + 1) * rs : (N >> 5)) - 1);
-                const int64_t col4 = (int64_t)s * (kStep / 4) + cg;  // 4-column group
+                // the lane's segment and its halo segment are the same every step: their stream
+                // offsets (fwd_seg, fwd_halo) are set up once, before the walk
+                (void)rs;
+                const int64_t g = (o0 >> 5) + (lane >> 4);
+                const int64_t col4 = ((int64_t)s * (kStep / 4) + (lane & 15)) * 4;  // 4-column group
 #pragma unroll
                 for (int t = 0; t < S::NW; ++t) {
                     const int d = S::D0 + t;
-                    const int64_t idx = d < BITS ? ((g * BITS + d) * (K >> 2) + col4) * 4 : (gh * BITS * (K >> 2) + col4) * 4;
+                    const int64_t idx = d < BITS ? fwd_seg + d * (K >> 2) * 4 + col4 : fwd_halo + col4;
                     wd.w[t] = *reinterpret_cast<const uint4*>(p.stream + idx);
                 }
                 load_scales<ROWS>(p.scale_t + (((int64_t)s * kStep) >> 7) * N + 32 * g + ROWS * SLICE, wd.s);
@@ -510,8 +525,9 @@ __device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t*
         for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = (f32x16){};
     const int lane = threadIdx.x & 63;
     const int64_t red = FWD ? p.K : p.N;
-    const Wave<FWD, WAVES, WAVE> w{p, red, (int64_t)mt * kBM + G::kWaveM * WAVE, (int64_t)ot * kBN,
-                                   act_tile_blocks(p.T) * kBlock, lane, (int)(red / kStep)};
+    Wave<FWD, WAVES, WAVE> w{p, red, (int64_t)mt * kBM + G::kWaveM * WAVE, (int64_t)ot * kBN,
+                             act_tile_blocks(p.T) * kBlock, lane, (int)(red / kStep)};
+    w.setup();
     w.run(p.act, t0, t1, acc);
     if (p.rank > 0) adapter<G::kMI>(p.P, p.Q, p.rank, w.m0, w.o0, p.T, lane, acc);
     store<G::kMI>(acc, p.out, FWD ? p.N : p.K, w.m0, w.o0, p.T, lane, p.out_f32, FWD ? 0 : p.accumulate);
