@@ -47,6 +47,10 @@
 #error "compile with -DR97Q_BITS=<code width>"
 #endif
 
+#ifndef R97Q_RT_WAVES
+#define R97Q_RT_WAVES 8
+#endif
+
 namespace r97q {
 namespace rt {
 namespace {
@@ -253,16 +257,17 @@ struct Wave {
                 }
                 load_scales<ROWS>(p.scale_t + (((int64_t)s * kStep) >> 7) * N + 32 * g + ROWS * SLICE, wd.s);
             } else {
-                // the wave's segment is uniform: its halo is computed once, in scalar registers
+                // the wave's segment is uniform: its halo (needed by the slice whose windows reach
+                // the next segment) is computed in scalar registers, without a branch
                 const int64_t g = 2 * (int64_t)s + SEG;
-                const int gi = __builtin_amdgcn_readfirstlane((int)g);
-                const int rsi = (int)rs, ns = (int)(N >> 5);
-                int ghi = gi - 1;
-                if (gi % rsi == 0) {
-                    const int top = (gi / rsi + 1) * rsi;
-                    ghi = (top < ns ? top : ns) - 1;
+                int64_t gh = 0;
+                if constexpr (S::D1 == BITS) {
+                    const int gi = __builtin_amdgcn_readfirstlane((int)g);
+                    const int rsi = (int)rs, ns = (int)(N >> 5);
+                    const int q = gi / rsi;
+                    const int top = (q + 1) * rsi;
+                    gh = gi - q * rsi != 0 ? gi - 1 : (top < ns ? top : ns) - 1;
                 }
-                const int64_t gh = ghi;
                 const int64_t col = o0 + 2 * lane;
 #pragma unroll
                 for (int t = 0; t < S::NW; ++t) {
@@ -555,10 +560,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qlinear_rt_kernel(const Params 
             break;
     }
 }
-
-#ifndef R97Q_RT_WAVES
-#define R97Q_RT_WAVES 8
-#endif
 
 }  // namespace
 
