@@ -87,7 +87,8 @@ def profiled_traffic(kernel, config):
     if config != "c2" or h.hexdigest()[:16] != prof.get("sources_sha256_16"):
         return None
     kernels = prof.get("kernels", {})
-    # the profiler names a template instance with its arguments (qlinear_dx_kernel<false>)
+    # a kernel is looked up by the name the line gives it (qlinear_rt_kernel<dx>), or by its name
+    # without template arguments
     k = kernels.get(kernel) or next((v for n, v in kernels.items() if n.split("<")[0] == kernel), None)
     return None if k is None else k["traffic_bytes"]
 
@@ -122,16 +123,26 @@ def make_inputs(T, N, K, r, seed, device, weight_form="trellis"):
     return dict(w=w, q=q, X=X, dY=dY, A=A, B=B, keep=(codes, scale, col))
 
 
-def cpu_baseline(inp, T, N, K, r, s, target_s):
+def host_cores():
+    """The host cores this process may use: its CPU affinity, at most 16 (one GPU's share of a GPU
+    box's cores)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline(inp, T, N, K, r, s, target_s, nthreads):
     """The reference's own host path (oracle/_ref: its r97_iqr_decode_host, gemm_nt twin and
-    adjoint, float lora_shrink / lora_expand twins and adjoints, f64 with its parallel_for) on a
-    row sample of the same workload, extrapolated linearly in tokens to the whole step."""
+    adjoint, float lora_shrink / lora_expand twins and adjoints, f64 with its parallel_for) on
+    `nthreads` threads, on a row sample of the same workload, extrapolated linearly in tokens to the
+    whole step."""
     import numpy as np
 
     from oracle import oracle as O
 
     use_ref = O.ref() is not None
-    nthreads = min(8, os.cpu_count() or 1)
     os.environ["R97_THREADS"] = str(nthreads)
     O.set_threads(nthreads)
     q = inp["q"]
@@ -188,7 +199,7 @@ def cpu_baseline(inp, T, N, K, r, s, target_s):
         "sample": f"{n} of {T} token rows (evenly spaced) through decode + gemm_nt twin/adjoint + "
                   f"lora shrink/expand twins/adjoints, f64, {nthreads} threads; extrapolated "
                   f"linearly in tokens ({t_rows:.1f} s sampled + {t_decode:.2f} s decode; "
-                  f"{step_s:.1f} s per full step; nproc {os.cpu_count()})",
+                  f"{step_s:.1f} s per full step; nproc {os.cpu_count()}, affinity {host_cores()})",
     }
 
 
@@ -463,12 +474,16 @@ def main():
     total_flops = flops(T, N, K, r)
     value = total_flops / (ms_step * 1e-3) / 1e12
     # the dominant kernel and its algorithmic work per launch
-    kern = {"qlinear_fwd_kernel": (fwd_ms, 2 * T * N * K + 2 * T * N * r),
-            "qlinear_dx_kernel": (dx_ms, 2 * T * N * K + 2 * T * K * r)}
+    kern = {"qlinear_rt_kernel<fwd>": (fwd_ms, 2 * T * N * K + 2 * T * N * r),
+            "qlinear_rt_kernel<dx>": (dx_ms, 2 * T * N * K + 2 * T * K * r)}
     name = max(kern, key=lambda k: kern[k][0])
     kms, kfl = kern[name]
     achieved = kfl / (kms * 1e-3) / 1e12
+    traffic = profiled_traffic(name, args.config) if args.weight_form == "trellis" else None
+    # the packed weight as the kernel reads it: every 512-token panel's workgroups walk the whole
+    # stream (the panels sit on different XCDs, each with its own L2), so it is fetched once a panel
     packed_bytes = N * K if args.weight_form == "codes8" else N * K * 5 // 8
+    panels = (T + 511) // 512
     line = {
         "metric": "qlinear+LoRA fwd+bwd TFLOP/s, % MFMA/HBM roofline; LoRA-step tokens/s",
         "value": round(value, 3),
@@ -493,16 +508,21 @@ def main():
         "lora_step": {"tokens_per_s": round(T / (ms_lora_step * 1e-3), 1), "ms": round(ms_lora_step, 4),
                       "what": "fwd+bwd + the staged dA/dB flushed into AdamW on A, B (device, f32 masters) + their bf16 copies"},
         "flops_per_step": total_flops,
-        "kernels_ms": {"qlinear_fwd_kernel": round(fwd_ms, 4), "qlinear_dx_kernel": round(dx_ms, 4),
+        "kernels_ms": {"qlinear_rt_kernel<fwd>": round(fwd_ms, 4), "qlinear_rt_kernel<dx>": round(dx_ms, 4),
                        "other": round(ms_step_ev - fwd_ms - dx_ms, 4), "ms_per_step_with_events": round(ms_step_ev, 4)},
         "roofline": {"bound": "mfma", "kernel": name, "achieved": round(achieved, 3),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": profiled_traffic(name, args.config) if args.weight_form == "trellis" else None,
-                     "packed_weight_GBs": round(packed_bytes / (kms * 1e-3) / 1e9, 2)},
+                     "traffic": traffic,
+                     "hbm_GBs": None if traffic is None else round(traffic / (kms * 1e-3) / 1e9, 1),
+                     "weight_stream_fetched_GBs": round(panels * packed_bytes / (kms * 1e-3) / 1e9, 1),
+                     "weight_stream_note": f"the {packed_bytes / 1e6:.1f} MB packed weight fetched once by each "
+                                           f"of the {panels} token panels' workgroups"},
         "quantizer_rel_err": round(inp["q"]["rel_err"], 4),
     }
     if args.cpu_seconds > 0:
-        line["cpu_baseline"] = cpu_baseline(inp, T, N, K, r, s, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(inp, T, N, K, r, s, args.cpu_seconds, min(8, host_cores()))
+        line["cpu_baseline_all_cores"] = (cpu_baseline(inp, T, N, K, r, s, args.cpu_seconds, host_cores())
+                                          if host_cores() > 8 else line["cpu_baseline"])
     print(json.dumps(line), flush=True)
 
 

@@ -298,8 +298,9 @@ int r97q_qlinear_fwd_base(const R97qWeight* w, const uint16_t* X, int64_t T, con
                           int32_t rank, void* Y, int32_t y_dtype, void* workspace,
                           int64_t workspace_bytes, R97IqrStream stream);
 /* Backward: dt = scale.dY.B (in the workspace, as the adapter operands of the fused dX kernel and of
- * dA) (lora_expand_host_adjoint's dt, src/adjoint/host/lora.cpp:495-506), and, when t is given,
- * scale.t as dB's operand. rank 0: a no-op. */
+ * dA) (lora_expand_host_adjoint's dt, src/adjoint/host/lora.cpp:495-506), and scale.t as dB's
+ * operand: t (the forward's f32 t) is required when rank > 0 (R97Q_EINVAL without it). rank 0:
+ * only the tiled copy of dY. */
 int r97q_lora_bwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* dY, const uint16_t* A,
                        const uint16_t* B, const float* t, int32_t rank, float scale, void* workspace,
                        int64_t workspace_bytes, R97IqrStream stream);

@@ -13,6 +13,7 @@ namespace r97q {
 //   P   [T, 2r] bf16  = [hi | lo](sb * v)                    (row-major)
 //   Pt  [2r, ldt] bf16 = [hi | lo](sb * v), transposed       (zero for T <= m < ldt)
 //   Pt2 [2r, ldt] bf16 = [hi | lo](s2 * U2[m][j]), transposed (U2 f32 [T, r])
+//   zero [nzero]      = 0 (a following gradient launch's counters)
 struct DownArgs {
     const uint16_t* In;
     const uint16_t* W;
@@ -27,11 +28,15 @@ struct DownArgs {
     uint16_t* Pt2;
     int out_add;  // out += (instead of =)
     uint16_t* tiled;
+    int* zero;
+    int nzero;
 };
 
 // out += scale * sum_m (Pt[j][m] + Pt[r+j][m]) V[m][c]: V bf16 [T, C] (C a multiple of 128), out
 // [r, C] row-major or, `transposed`, [C, r]; Pt bf16 [2r, ldt]. The token chunks' partial sums go
-// to `part` (f32 [grad_chunks, r, C]) and are added into out in chunk order.
+// to `part` (f32 [grad_chunks, r, C]) and are added into out in chunk order by the last chunk of
+// each column block to finish, counted on `done` (grad_blocks(C) counters, zero at the launch --
+// the launch before it clears them -- and zero again after it).
 struct GradOne {
     const uint16_t* Pt;
     const uint16_t* V;
@@ -40,6 +45,7 @@ struct GradOne {
     float scale;
     int transposed;
     float* part;
+    int* done;
 };
 struct GradArgs {
     GradOne one[2];
@@ -49,6 +55,7 @@ struct GradArgs {
 
 int down_rank(int r);          // r rounded up to a multiple of 16
 int64_t grad_ld(int64_t T);    // the transposed splits' row length: T rounded up to 64
+int64_t grad_blocks(int64_t C);  // the gradient launch's column blocks over C columns (its counters)
 // the gradient launch's token chunks (at most this many) and their length in tokens, for dA over K
 // columns and dB over N
 int64_t grad_chunks(int64_t T, int64_t K, int64_t N);
@@ -60,9 +67,10 @@ int launch_lora_grads(int r, const GradArgs& g, int nz, hipStream_t s);
 int launch_act_tile(const uint16_t* act, int64_t T, int64_t R, uint16_t* dst, hipStream_t s);
 int launch_transpose2(const uint16_t* B, uint16_t* Bt, int64_t N, const uint16_t* A, uint16_t* At,
                       int64_t K, int r, hipStream_t s);
-// P [T, 2r] / Pt [2r, ldt] = [hi | lo](scale * U), U f32 [T, r]; either output may be null
+// P [T, 2r] / Pt [2r, ldt] = [hi | lo](scale * U), U f32 [T, r]; either output may be null;
+// zero [nzero] = 0 (a following gradient launch's counters)
 int launch_split(const float* U, int64_t T, int r, int64_t ldt, float scale, uint16_t* P, uint16_t* Pt,
-                 hipStream_t s);
+                 int* zero, int nzero, hipStream_t s);
 // the coded activation (codes [T, K]: int8, or f32 code values when code_f32; f32 scale a_scale
 // [T, groups], group width gw):
 //   da [T, K] += g * a_scale;  ds [T, groups] += sum over each group of g * code  (g f32 [T, K];

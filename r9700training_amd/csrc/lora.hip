@@ -12,14 +12,14 @@
 //                      fixed order; it writes the f32 result and its [hi | lo] splits for the
 //                      fused kernels' epilogues (row-major) and for the gradient kernel
 //                      (transposed).
-//   lora_grads_kernel  dA and dB in one launch: a workgroup = 512 output columns x a token
+//   lora_grads_kernel  dA and dB in one launch: a workgroup = 256 output columns x a token
 //                      chunk; the token tile (X or dY) and the Pt rows stream through registers
 //                      into two LDS slots, loaded three tiles ahead; the token tile is read back
 //                      transposed with ds_read_b64_tr_b16, the [hi | lo] split of dt or s.t is
-//                      the other operand; each chunk writes its own partial sums.
-//   grad_reduce_kernel adds the chunks' partials into dA and dB in chunk order (deterministic; the
-//                      leaves are added into, as the reference's rows add into the step's f32
-//                      gradients).
+//                      the other operand; each chunk writes its own partial sums, and the last
+//                      chunk of a column block to finish adds them into dA or dB in chunk order
+//                      (deterministic; the leaves are added into, as the reference's rows add
+//                      into the step's f32 gradients).
 //   split_kernel       an f32 [T, r] operand (a cotangent handed in) -> its [hi | lo] splits.
 //   lora_up_kernel     the up-projection t_cot . A of the shrink's adjoint, on its own (the fused
 //                      dX kernel carries it in its epilogue when the base product runs too).
@@ -80,6 +80,8 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row16 = lane & 15, grp = lane >> 4;
     const int64_t m0 = (int64_t)blockIdx.x * 16;
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < a.nzero; i += blockDim.x) a.zero[i] = 0;
     int64_t row = m0 + row16;
     if (row > a.T - 1) row = a.T - 1;
     const int64_t kq = a.Kin / nw;  // a multiple of 32
@@ -176,35 +178,46 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
 }
 
 // ---------------------------------------------------------------- grads
+// device-scope (every XCD) store and load of one f32: written through to, and read from, the
+// memory all XCDs share, bypassing the XCD's own L2
+__device__ __forceinline__ void device_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float device_load(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // part[chunk][j][c] = scale * sum_{m in chunk} (Pt[j][m] + Pt[r+j][m]) V[m][c]   (j < r)
-// computed as C[v][c] = sum_m Pt[v][m] V[m][c] over the 2r [hi | lo] rows v, then out (+)= the
-// sum of the chunks' parts in chunk order (grad_reduce_kernel): no atomics, so dA and dB are the
-// same bits on every call.
+// computed as C[v][c] = sum_m Pt[v][m] V[m][c] over the 2r [hi | lo] rows v; then out (+)= the
+// sum of the chunks' parts in chunk order. No atomics on the values, so dA and dB are the same
+// bits on every call: each workgroup counts itself done on its column block's counter (after its
+// partial sums are visible device-wide), and the last of the block's chunks adds them all.
 //
-// A workgroup = 512 columns (8 waves x 64) x a token chunk, walked TOK tokens at a time. Tiles
-// stream global -> registers -> LDS: each wave loads TOK/8 token rows (one 1 KiB row each) of a
-// tile and NP 1 KiB pieces of the tile's Pt rows (2r rows x TOK tokens); a tile is loaded three
+// A workgroup = 256 columns (8 waves x 32) x a token chunk, walked TOK tokens at a time. Tiles
+// stream global -> registers -> LDS: each wave loads TOK/8 token rows of a tile (two 512-byte rows
+// a load) and NP 1 KiB pieces of the tile's Pt rows (2r rows x TOK tokens); a tile is loaded three
 // iterations before it is multiplied (two register sets in flight) and written to one of two LDS
 // slots the iteration before. The token tile is read back transposed with ds_read_b64_tr_b16
-// (the MFMA's B operand), the Pt rows straight (the A operand). Token rows are padded to 1088
+// (the MFMA's B operand), the Pt rows straight (the A operand). Token rows are padded to 576
 // bytes so the transposing reads of four consecutive rows land on distinct banks.
-constexpr int kGradCols = 512;
+constexpr int kGradCols = 256;
 constexpr int kGradRow = 2 * kGradCols + 64;
 
 template <int R>
 struct GradShape {
     static constexpr int R2 = 2 * R;
     static constexpr int VB = R2 / 16;                  // 16-row blocks of Pt (R is 8, 16, 32 or 64)
-    static constexpr int TOK = R == 64 ? 32 : 64;       // tokens a tile (two LDS slots fit 160 KiB)
+    static constexpr int TOK = R == 64 ? 32 : 64;       // tokens a tile
     static constexpr int ROWS = TOK / 8;                // token rows a wave loads
+    static constexpr int LOADS = ROWS / 2;              // two rows a load (32 lanes x 16 bytes each)
     static constexpr int PTB = R2 * TOK * 2;            // Pt bytes a tile
     static constexpr int NP = (PTB / 1024 + 7) / 8;     // 1 KiB Pt pieces a wave loads
-    static constexpr int NREG = ROWS + NP;
+    static constexpr int NREG = LOADS + NP;
     static constexpr int VTILE = TOK * kGradRow;
     static constexpr int SLOT = VTILE + PTB;
 };
 
-// one lane's loads of a gradient tile: its token rows (16 bytes each) and Pt pieces
+// one lane's loads of a gradient tile: its token row halves (16 bytes each) and Pt pieces
 struct GradLane {
     const uint16_t* V;
     const uint16_t* Pt;
@@ -217,8 +230,8 @@ __device__ __forceinline__ void grad_load(const GradLane& L, int it, u32x4 (&r)[
     using S = GradShape<R>;
     if (it > L.niter - 1) it = L.niter - 1;  // past the chunk: its last tile again (never multiplied)
 #pragma unroll
-    for (int q = 0; q < S::ROWS; ++q) {  // token rows ROWS*wave + q
-        int64_t row = L.mb + S::TOK * it + S::ROWS * L.wave + q;
+    for (int q = 0; q < S::LOADS; ++q) {  // token row ROWS*wave + 2q + (lane >= 32)
+        int64_t row = L.mb + S::TOK * it + S::ROWS * L.wave + 2 * q + (L.lane >> 5);
         if (row > L.T - 1) row = L.T - 1;  // rows past T meet zero splits
         r[q] = *reinterpret_cast<const u32x4*>(L.V + row * L.C + L.gcol);
     }
@@ -230,7 +243,7 @@ __device__ __forceinline__ void grad_load(const GradLane& L, int it, u32x4 (&r)[
         if (piece >= S::PTB / 1024) piece = 0;
         const int byte = 1024 * piece + 16 * L.lane;
         const int v = byte / (2 * S::TOK), m = (byte % (2 * S::TOK)) / 2;
-        r[S::ROWS + u] = *reinterpret_cast<const u32x4*>(L.Pt + (int64_t)v * L.ldt + L.mb + S::TOK * it + m);
+        r[S::LOADS + u] = *reinterpret_cast<const u32x4*>(L.Pt + (int64_t)v * L.ldt + L.mb + S::TOK * it + m);
     }
 }
 
@@ -238,18 +251,19 @@ template <int R>
 __device__ __forceinline__ void grad_store(const GradLane& L, const u32x4 (&r)[GradShape<R>::NREG], uint8_t* st) {
     using S = GradShape<R>;
 #pragma unroll
-    for (int q = 0; q < S::ROWS; ++q)
-        *reinterpret_cast<u32x4*>(st + (S::ROWS * L.wave + q) * kGradRow + 16 * L.lane) = r[q];
+    for (int q = 0; q < S::LOADS; ++q)
+        *reinterpret_cast<u32x4*>(st + (S::ROWS * L.wave + 2 * q + (L.lane >> 5)) * kGradRow + 16 * (L.lane & 31)) =
+            r[q];
 #pragma unroll
     for (int u = 0; u < S::NP; ++u) {
         const int piece = L.wave + 8 * u;
-        if (piece < S::PTB / 1024) *reinterpret_cast<u32x4*>(st + S::VTILE + 1024 * piece + 16 * L.lane) = r[S::ROWS + u];
+        if (piece < S::PTB / 1024) *reinterpret_cast<u32x4*>(st + S::VTILE + 1024 * piece + 16 * L.lane) = r[S::LOADS + u];
     }
 }
 
 template <int R>
 __device__ __forceinline__ void grad_multiply(const uint8_t* st, int wave, int i16, int grp,
-                                              f32x4 (&acc)[GradShape<R>::VB][4]) {
+                                              f32x4 (&acc)[GradShape<R>::VB][2]) {
     using S = GradShape<R>;
 #pragma unroll
     for (int ks = 0; ks < S::TOK / 32; ++ks) {
@@ -259,8 +273,8 @@ __device__ __forceinline__ void grad_multiply(const uint8_t* st, int wave, int i
             pa[vb] = as_bf16x8(*reinterpret_cast<const uint4*>(st + S::VTILE + (16 * vb + i16) * (2 * S::TOK) +
                                                                 2 * (32 * ks + 8 * grp)));
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            const int col = 64 * wave + 16 * cb;
+        for (int cb = 0; cb < 2; ++cb) {
+            const int col = 32 * wave + 16 * cb;
             const int e = i16 >> 2, q = i16 & 3;
             const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_s16x4*)(st + (32 * ks + 8 * grp + e) * kGradRow + (col + 4 * q) * 2));
@@ -278,6 +292,7 @@ __global__ __launch_bounds__(512) void lora_grads_kernel(GradArgs ga) {
     using S = GradShape<R>;
     constexpr int VB = S::VB;
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * S::SLOT];
+    __shared__ int last;
     const GradOne& g = ga.one[blockIdx.z];
     const int64_t C = g.C;
     const int64_t c0 = (int64_t)blockIdx.x * kGradCols;
@@ -288,15 +303,15 @@ __global__ __launch_bounds__(512) void lora_grads_kernel(GradArgs ga) {
     int64_t me = mb + ga.chunk;
     if (me > ga.ldt) me = ga.ldt;
     const int niter = (int)((me - mb) / S::TOK);
-    // the lane's 8 columns of every row it loads (columns past C read column c0 instead and their
-    // results are never stored)
-    const int64_t gcol = c0 + 8 * lane < C ? c0 + 8 * lane : c0;
+    // the lane's 8 columns of every row half it loads (columns past C read column c0 instead and
+    // their results are never stored)
+    const int64_t gcol = c0 + 8 * (lane & 31) < C ? c0 + 8 * (lane & 31) : c0;
 
-    f32x4 acc[VB][4];
+    f32x4 acc[VB][2];
 #pragma unroll
     for (int vb = 0; vb < VB; ++vb)
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[vb][cb] = (f32x4){};
+        for (int cb = 0; cb < 2; ++cb) acc[vb][cb] = (f32x4){};
     const GradLane L{g.V, g.Pt, C, ga.T, ga.ldt, mb, gcol, wave, lane, niter};
     // iteration it: multiply slot it&1, write tile it+1 (its registers) into the other slot (a
     // tile past the chunk's end goes into the slot no wave reads again), one barrier, then reload
@@ -318,49 +333,83 @@ __global__ __launch_bounds__(512) void lora_grads_kernel(GradArgs ga) {
         __syncthreads();
         grad_load<R>(L, it + 4, ra);
     }
-    // acc element e of block (vb, cb): row v = 16vb + 4grp + e, column c0 + 64*wave + 16cb + i16.
+    // acc element e of block (vb, cb): row v = 16vb + 4grp + e, column c0 + 32*wave + 16cb + i16.
     // Row j (< R) pairs with row R + j: the same lane and element VB/2 blocks on, or, for R = 8
-    // (one block), the lane 32 on.
+    // (one block), the lane 32 on. The partial sums are stored at device scope (through to the
+    // memory every XCD reads; no cache write-back or invalidation of the whole L2).
     float* part = g.part + (int64_t)blockIdx.y * R * C;
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-        const int64_t c = c0 + 64 * wave + 16 * cb + i16;
+    for (int cb = 0; cb < 2; ++cb) {
+        const int64_t c = c0 + 32 * wave + 16 * cb + i16;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if constexpr (R >= 16) {
 #pragma unroll
                 for (int vb = 0; vb < VB / 2; ++vb) {
                     const int j = 16 * vb + 4 * grp + e;
-                    if (c < C) part[(int64_t)j * C + c] = g.scale * (acc[vb][cb][e] + acc[vb + VB / 2][cb][e]);
+                    if (c < C) device_store(part + (int64_t)j * C + c, g.scale * (acc[vb][cb][e] + acc[vb + VB / 2][cb][e]));
                 }
             } else {
                 const float other = __shfl_xor(acc[0][cb][e], 32);
                 const int j = 4 * grp + e;
-                if (grp < 2 && c < C) part[(int64_t)j * C + c] = g.scale * (acc[0][cb][e] + other);
+                if (grp < 2 && c < C) device_store(part + (int64_t)j * C + c, g.scale * (acc[0][cb][e] + other));
             }
         }
     }
-}
-
-// out (+)= sum over chunks, in chunk order, of part[chunk][j][c]; out is [r, C] row-major or,
-// `transposed`, [C, r]. One thread a (j, c).
-__global__ __launch_bounds__(256) void grad_reduce_kernel(GradArgs ga, int r, int nchunks) {
-    const GradOne& g = ga.one[blockIdx.y];
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)r * g.C) return;
-    const int64_t j = i / g.C, c = i % g.C;
-    float v = 0.0f;
-    for (int ch = 0; ch < nchunks; ++ch) v += g.part[((int64_t)ch * r + j) * g.C + c];
-    float* d = g.transposed ? g.out + c * r + j : g.out + i;
-    *d += v;
+    // every store of the workgroup acknowledged, then the chunk counted done; the last of the
+    // column block's chunks reads the others' sums at device scope
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(g.done + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (int)gridDim.y - 1;
+    __syncthreads();
+    if (!last) return;
+    // out (+)= the chunks' sums in chunk order; out is [r, C] row-major or, `transposed`, [C, r].
+    // A thread takes PAIRS (j, c) pairs; their loads are issued U chunks at a time (32 in flight).
+    constexpr int PAIRS = R * kGradCols / 512;
+    constexpr int U = PAIRS >= 32 ? 1 : 32 / PAIRS;
+    const int nch = (int)gridDim.y;
+    float sum[PAIRS];
+#pragma unroll
+    for (int q = 0; q < PAIRS; ++q) sum[q] = 0.0f;
+    for (int ch0 = 0; ch0 < nch; ch0 += U) {
+        float v[PAIRS][U];
+#pragma unroll
+        for (int q = 0; q < PAIRS; ++q) {
+            const int i = (int)threadIdx.x + 512 * q;
+            const int j = i / kGradCols;
+            int64_t c = c0 + i % kGradCols;
+            if (c >= C) c = c0;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                v[q][u] = ch0 + u < nch ? device_load(g.part + ((int64_t)(ch0 + u) * R + j) * C + c) : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < PAIRS; ++q)
+#pragma unroll
+            for (int u = 0; u < U; ++u) sum[q] += v[q][u];
+    }
+#pragma unroll
+    for (int q = 0; q < PAIRS; ++q) {
+        const int i = (int)threadIdx.x + 512 * q;
+        const int j = i / kGradCols;
+        const int64_t c = c0 + i % kGradCols;
+        if (c >= C) continue;
+        float* d = g.transposed ? g.out + c * R + j : g.out + (int64_t)j * C + c;
+        *d += sum[q];
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(g.done + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- split and up
 // P [T, 2r] = [hi | lo](s * U[m][j]) row-major, Pt [2r, ldt] the same transposed (zero for
 // T <= m < ldt). One thread an (m, j), m < ldt.
 __global__ __launch_bounds__(256) void split_kernel(const float* __restrict__ U, int64_t T, int r, int64_t ldt,
-                                                    float s, uint16_t* __restrict__ P, uint16_t* __restrict__ Pt) {
+                                                    float s, uint16_t* __restrict__ P, uint16_t* __restrict__ Pt,
+                                                    int* __restrict__ zero, int nzero) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < nzero) zero[i] = 0;
     if (i >= ldt * r) return;
     const int64_t m = i / r;
     const int j = (int)(i % r);
@@ -530,10 +579,7 @@ int grads_r(const GradArgs& g, int64_t cmax, int nz, hipStream_t s) {
     hipLaunchKernelGGL(lora_grads_kernel<R>, dim3((unsigned)((cmax + kGradCols - 1) / kGradCols), (unsigned)chunks,
                                                   (unsigned)nz),
                        dim3(512), 0, s, g);
-    if (int e = launch_status("lora_grads_kernel")) return e;
-    hipLaunchKernelGGL(grad_reduce_kernel, dim3((unsigned)((R * cmax + 255) / 256), (unsigned)nz), dim3(256), 0, s, g,
-                       R, (int)chunks);
-    return launch_status("grad_reduce_kernel");
+    return launch_status("lora_grads_kernel");
 }
 
 }  // namespace
@@ -553,11 +599,12 @@ int launch_lora_down(const DownArgs& a, hipStream_t s) {
     }
 }
 
+int64_t grad_blocks(int64_t C) { return (C + kGradCols - 1) / kGradCols; }
+
 int64_t grad_chunks(int64_t T, int64_t K, int64_t N) {
-    // about 128 workgroups over dA's and dB's column blocks (measured at C2 against 256 and 512:
-    // fewer chunk partials for grad_reduce to add outweigh the idle half of the chip, 2 us a step)
-    const int64_t cols = (K + kGradCols - 1) / kGradCols + (N + kGradCols - 1) / kGradCols;
-    int64_t chunks = (128 + cols - 1) / cols;
+    // about 256 workgroups (one a CU) over dA's and dB's column blocks
+    const int64_t cols = grad_blocks(K) + grad_blocks(N);
+    int64_t chunks = (256 + cols - 1) / cols;
     const int64_t tiles = grad_ld(T) / 64;  // no chunk smaller than one 64-token tile
     if (chunks > tiles) chunks = tiles;
     return chunks < 1 ? 1 : chunks;
@@ -587,9 +634,10 @@ int launch_lora_grads(int r, const GradArgs& g, int nz, hipStream_t s) {
 }
 
 int launch_split(const float* U, int64_t T, int r, int64_t ldt, float scale, uint16_t* P, uint16_t* Pt,
-                 hipStream_t s) {
-    hipLaunchKernelGGL(split_kernel, dim3((unsigned)((ldt * r + 255) / 256)), dim3(256), 0, s, U, T, r, ldt, scale, P,
-                       Pt);
+                 int* zero, int nzero, hipStream_t s) {
+    const int64_t n = ldt * r > nzero ? ldt * r : nzero;
+    hipLaunchKernelGGL(split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, U, T, r, ldt, scale, P,
+                       Pt, zero, nzero);
     return launch_status("split_kernel");
 }
 

@@ -39,7 +39,8 @@ struct Shape {
 // Workspace layout. Forward: Xt (X's tiled copy, act_tiles.h) | P [T, 2r] | Apad [rd, K] (when r
 // is not a multiple of 16).
 // Backward: dYt (dY's tiled copy) | Bt [rd, N] | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt]
-// | partA [chunks, r, K] | partB [chunks, r, N] (f32 partial sums of the factor gradients).
+// | partA [chunks, r, K] | partB [chunks, r, N] (f32 partial sums of the factor gradients) | done
+// (the gradient launch's column-block counters, dA's then dB's).
 struct FwdWs {
     int64_t Xt, P, Apad, total;
 };
@@ -57,7 +58,7 @@ FwdWs fwd_ws(const Shape& s) {
     return w;
 }
 struct BwdWs {
-    int64_t dYt, Bt, At, P, PtA, PtB, partA, partB, total;
+    int64_t dYt, Bt, At, P, PtA, PtB, partA, partB, done, total;
 };
 BwdWs bwd_ws(const Shape& s) {
     BwdWs w{};
@@ -76,15 +77,16 @@ BwdWs bwd_ws(const Shape& s) {
     const int64_t chunks = grad_chunks(s.T, s.K, s.N);
     w.partA = w.PtB + align256(2 * s.r * ldt * 2);
     w.partB = w.partA + align256(chunks * s.r * s.K * 4);
-    w.total = w.partB + align256(chunks * s.r * s.N * 4);
+    w.done = w.partB + align256(chunks * s.r * s.N * 4);
+    w.total = w.done + align256((grad_blocks(s.K) + grad_blocks(s.N)) * 4);
     return w;
 }
 
 // The adapter rows on their own (the shrink's and the expand's adjoints), workspace layouts:
-// shrink: P [T, 2r] | Pt [2r, ldt] | At [K, r] | part [chunks, r, K]
-// expand: Bt [rd, N] | Pt2 [2r, ldt] | part [chunks, r, N]
+// shrink: P [T, 2r] | Pt [2r, ldt] | At [K, r] | part [chunks, r, K] | done
+// expand: Bt [rd, N] | Pt2 [2r, ldt] | part [chunks, r, N] | done
 struct ShrinkWs {
-    int64_t P, Pt, At, part, total;
+    int64_t P, Pt, At, part, done, total;
 };
 ShrinkWs shrink_ws(int64_t T, int64_t K, int r) {
     ShrinkWs w{};
@@ -94,11 +96,12 @@ ShrinkWs shrink_ws(int64_t T, int64_t K, int r) {
     w.Pt = w.P + align256(T * 2 * r * 2);
     w.At = w.Pt + align256(2 * r * ldt * 2);
     w.part = w.At + align256(K * r * 2);
-    w.total = w.part + align256(grad_chunks(T, K, 0) * r * K * 4);
+    w.done = w.part + align256(grad_chunks(T, K, 0) * r * K * 4);
+    w.total = w.done + align256(grad_blocks(K) * 4);
     return w;
 }
 struct ExpandWs {
-    int64_t Bt, Pt2, part, total;
+    int64_t Bt, Pt2, part, done, total;
 };
 ExpandWs expand_ws(int64_t T, int64_t N, int r) {
     ExpandWs w{};
@@ -107,14 +110,15 @@ ExpandWs expand_ws(int64_t T, int64_t N, int r) {
     w.Bt = 0;
     w.Pt2 = w.Bt + align256((int64_t)down_rank(r) * N * 2);
     w.part = w.Pt2 + align256(2 * r * ldt * 2);
-    w.total = w.part + align256(grad_chunks(T, 0, N) * r * N * 4);
+    w.done = w.part + align256(grad_chunks(T, 0, N) * r * N * 4);
+    w.total = w.done + align256(grad_blocks(N) * 4);
     return w;
 }
 
 // The coded shrink's adjoint: P [T, 2r] | Pt [2r, ldt] | At [K, r] | g [T, K] f32 | xhi, xlo [T, K]
-// bf16 | part [chunks, r, K] f32.
+// bf16 | part [chunks, r, K] f32 | done.
 struct ShrinkQWs {
-    int64_t P, Pt, At, g, xhi, xlo, part, total;
+    int64_t P, Pt, At, g, xhi, xlo, part, done, total;
 };
 ShrinkQWs shrink_q_ws(int64_t T, int64_t K, int r) {
     ShrinkQWs w{};
@@ -127,7 +131,8 @@ ShrinkQWs shrink_q_ws(int64_t T, int64_t K, int r) {
     w.xhi = w.g + align256(T * K * 4);
     w.xlo = w.xhi + align256(T * K * 2);
     w.part = w.xlo + align256(T * K * 2);
-    w.total = w.part + align256(grad_chunks(T, K, 0) * r * K * 4);
+    w.done = w.part + align256(grad_chunks(T, K, 0) * r * K * 4);
+    w.total = w.done + align256(grad_blocks(K) * 4);
     return w;
 }
 
@@ -283,6 +288,8 @@ int bwd_prep(const Shape& sh, const uint16_t* dY, const uint16_t* A, const uint1
     a.P = reinterpret_cast<uint16_t*>(wsb + ws.P);
     a.Pt = reinterpret_cast<uint16_t*>(wsb + ws.PtA);
     a.tiled = dYt;
+    a.zero = reinterpret_cast<int*>(wsb + ws.done);
+    a.nzero = (int)(grad_blocks(sh.K) + grad_blocks(sh.N));
     if (t) {
         a.U2 = t;
         a.s2 = scale;
@@ -300,12 +307,13 @@ int bwd_grads(const Shape& sh, const uint16_t* X, const uint16_t* dY, float* dA,
     g.ldt = grad_ld(sh.T);
     g.chunk = grad_chunk_rows(sh.T, sh.K, sh.N);
     int nz = 0;
+    int* done = reinterpret_cast<int*>(wsb + ws.done);
     if (dA)
         g.one[nz++] = GradOne{reinterpret_cast<const uint16_t*>(wsb + ws.PtA), X, sh.K, dA, 1.0f, 0,
-                              reinterpret_cast<float*>(wsb + ws.partA)};
+                              reinterpret_cast<float*>(wsb + ws.partA), done};
     if (dB)
         g.one[nz++] = GradOne{reinterpret_cast<const uint16_t*>(wsb + ws.PtB), dY, sh.N, dB, 1.0f, 1,
-                              reinterpret_cast<float*>(wsb + ws.partB)};
+                              reinterpret_cast<float*>(wsb + ws.partB), done + grad_blocks(sh.K)};
     if (nz == 0) return R97Q_OK;
     return launch_lora_grads(sh.r, g, nz, s);
 }
@@ -471,8 +479,10 @@ int r97q_lora_bwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* dY, cons
     const char* who = "r97q_lora_bwd_prep";
     if (int e = shape_ok(T, N, K, who)) return e;
     if (int e = check_rank(rank, who)) return e;
-    if (!dY || (rank > 0 && (!A || !B))) {
-        set_error("%s: null dY, or A or B with rank > 0", who);
+    // t is required with rank > 0: dB's operand is written here, and r97q_lora_bwd_grads cannot
+    // tell a workspace without it
+    if (!dY || (rank > 0 && (!A || !B || !t))) {
+        set_error("%s: null dY, or A, B or t with rank > 0", who);
         return R97Q_EINVAL;
     }
     const Shape sh{T, N, K, rank};
@@ -591,7 +601,8 @@ int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const void* a, int32_t a_dtype,
     const int code_f32 = a_dtype == R97Q_F32;
     uint16_t* P = reinterpret_cast<uint16_t*>(wsb + ws.P);
     uint16_t* Pt = reinterpret_cast<uint16_t*>(wsb + ws.Pt);
-    if (int e = launch_split(t_cot, T, rank, ldt, 1.0f, P, dA ? Pt : nullptr, s)) return e;
+    int* done = reinterpret_cast<int*>(wsb + ws.done);
+    if (int e = launch_split(t_cot, T, rank, ldt, 1.0f, P, dA ? Pt : nullptr, done, (int)grad_blocks(K), s)) return e;
     if (da || ds) {
         // g = t_cot . A, then its two code-basis cotangents
         uint16_t* At = reinterpret_cast<uint16_t*>(wsb + ws.At);
@@ -610,7 +621,7 @@ int r97q_lora_shrink_q_bwd(int64_t T, int64_t K, const void* a, int32_t a_dtype,
             g.T = T;
             g.ldt = ldt;
             g.chunk = grad_chunk_rows(T, K, 0);
-            g.one[0] = GradOne{Pt, x, K, dA, 1.0f, 0, reinterpret_cast<float*>(wsb + ws.part)};
+            g.one[0] = GradOne{Pt, x, K, dA, 1.0f, 0, reinterpret_cast<float*>(wsb + ws.part), done};
             if (int e = launch_lora_grads(rank, g, 1, s)) return e;
         }
     }
@@ -644,7 +655,8 @@ int r97q_lora_shrink_bwd(int64_t T, int64_t K, const uint16_t* X, const uint16_t
     uint16_t* P = reinterpret_cast<uint16_t*>(wsb + ws.P);
     uint16_t* Pt = reinterpret_cast<uint16_t*>(wsb + ws.Pt);
     uint16_t* At = reinterpret_cast<uint16_t*>(wsb + ws.At);
-    if (int e = launch_split(t_cot, T, rank, ldt, 1.0f, P, dA ? Pt : nullptr, s)) return e;
+    int* done = reinterpret_cast<int*>(wsb + ws.done);
+    if (int e = launch_split(t_cot, T, rank, ldt, 1.0f, P, dA ? Pt : nullptr, done, (int)grad_blocks(K), s)) return e;
     if (dX) {
         if (int e = launch_transpose2(nullptr, nullptr, 0, A, At, K, rank, s)) return e;
         if (int e = launch_lora_up(P, At, T, K, rank, dX, dx_accumulate, s)) return e;
@@ -654,7 +666,7 @@ int r97q_lora_shrink_bwd(int64_t T, int64_t K, const uint16_t* X, const uint16_t
         g.T = T;
         g.ldt = ldt;
         g.chunk = grad_chunk_rows(T, K, 0);
-        g.one[0] = GradOne{Pt, X, K, dA, 1.0f, 0, reinterpret_cast<float*>(wsb + ws.part)};
+        g.one[0] = GradOne{Pt, X, K, dA, 1.0f, 0, reinterpret_cast<float*>(wsb + ws.part), done};
         if (int e = launch_lora_grads(rank, g, 1, s)) return e;
     }
     return R97Q_OK;
@@ -698,6 +710,8 @@ int r97q_lora_expand_bwd(int64_t T, int64_t N, const uint16_t* dY, const uint16_
     a.sb = scale;
     a.out = t_cot;
     a.out_add = 1;
+    a.zero = reinterpret_cast<int*>(wsb + ws.done);
+    a.nzero = (int)grad_blocks(N);
     if (dB) {
         a.U2 = t;
         a.s2 = scale;
@@ -709,7 +723,8 @@ int r97q_lora_expand_bwd(int64_t T, int64_t N, const uint16_t* dY, const uint16_
         g.T = T;
         g.ldt = ldt;
         g.chunk = grad_chunk_rows(T, 0, N);
-        g.one[0] = GradOne{Pt2, dY, N, dB, 1.0f, 1, reinterpret_cast<float*>(wsb + ws.part)};
+        g.one[0] = GradOne{Pt2, dY, N, dB, 1.0f, 1, reinterpret_cast<float*>(wsb + ws.part),
+                           reinterpret_cast<int*>(wsb + ws.done)};
         if (int e = launch_lora_grads(rank, g, 1, s)) return e;
     }
     return R97Q_OK;
