@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_INT8_TOPS = 5000.0     # MI355X dense int8 MFMA
 
 CONFIGS = {
     # name: (T, N, K, rank, alpha)
@@ -53,10 +54,11 @@ def parse():
     ap.add_argument("--weight-form", default="trellis", choices=["trellis", "codes8"],
                     help="the prepared weight the kernels read: the trellis stream (decoded inside the "
                          "kernels), or the same weight in the int8-code form")
-    ap.add_argument("--workload", default="qlinear", choices=["qlinear", "vocab_head", "c5_stack"],
+    ap.add_argument("--workload", default="qlinear", choices=["qlinear", "vocab_head", "c5_stack", "coded_fwd"],
                     help="qlinear: the C2 fwd+bwd step (the headline); vocab_head: the vocabulary head's "
                          "transposed product at a 248320-row head, n_embd 2048, --vocab-rows token rows; "
-                         "c5_stack: one whole LoRA step of the 24-layer stack (T=32768, rank 16 on every projection)")
+                         "c5_stack: one whole LoRA step of the 24-layer stack (T=32768, rank 16 on every projection); "
+                         "coded_fwd: gemm_nt_q's twin (int8 codes x the int8-code weight) at C2's square layer")
     ap.add_argument("--vocab-rows", type=int, default=4096)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (3 launches), the known-size "
@@ -270,6 +272,58 @@ C5_PROJ = [(8192, 2048), (2048, 4096), (6144, 2048), (2048, 6144)]  # (N, K)
 C5_LAYERS, C5_T, C5_R, C5_ALPHA = 24, 32768, 16, 32.0
 
 
+def coded_fwd_bench(args):
+    """gemm_nt_q's twin (r97q_gemm_nt_q_fwd) at C2's square layer: int8 activation codes a [4096, 4096]
+    with f32 scales per 128-column group, the weight (trellis.mad b5 quantized from N(0, 0.02))
+    in its int8-code form; Y f32. One step = one launch pair (the codes' tiled copy + the product)."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    from r9700training_amd import R97Q_F32, _ptr, _stream, check, lib
+
+    dev = torch.device("cuda:0")
+    T, N, K, _r, _alpha = CONFIGS["c2"]
+    inp = make_inputs(T, N, K, 16, args.seed, dev, "codes8")
+    w = inp["w"]
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    a = torch.randint(-127, 128, (T, K), dtype=torch.int8, device=dev, generator=g)
+    a_scale = 0.01 + 0.05 * torch.rand((T, K // 128), device=dev, generator=g)
+    Y = torch.empty((T, N), dtype=torch.float32, device=dev)
+    L = lib()
+    ws = torch.empty(L.r97q_gemm_nt_q_fwd_workspace_bytes(T, K), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    st = _stream(stream)
+
+    def step():
+        check(L.r97q_gemm_nt_q_fwd(C.byref(w.w), _ptr(a), _ptr(a_scale), T, _ptr(Y), R97Q_F32, _ptr(ws), ws.numel(),
+                                   st), "gemm_nt_q_fwd")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ops = 2 * T * N * K
+    tops = ops / (ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "coded forward (gemm_nt_q twin) TOP/s at C2's square layer",
+        "value": round(tops, 3), "unit": "TOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "i8", "data": "synthetic: int8 codes uniform in [-127, 127], scales U(0.01, 0.06); W ~ N(0,0.02) "
+                               "quantized by this repo's trellis quantizer, in the int8-code form",
+        "config": {"workload": f"coded_fwd: Y = sum_g (a . code^T)_g * a_scale * scale, T={T}, N={N}, K={K}, "
+                               "group 128, Y f32", "T": T, "N": N, "K": K},
+        "roofline": {"bound": "mfma", "kernel": "qlinear_q_kernel (+ qtok_tile_kernel in the step)",
+                     "achieved": round(tops, 3), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": None},
+    }), flush=True)
+
+
 def c5_stack_bench(args):
     """One complete LoRA step of the 24-layer stack on one GPU: the forward of every projection,
     layer by layer, then the backward in reverse (dX, dA, dB, the adapters' gradients staged), then
@@ -390,6 +444,8 @@ def main():
         return vocab_head_bench(args)
     if args.workload == "c5_stack":
         return c5_stack_bench(args)
+    if args.workload == "coded_fwd":
+        return coded_fwd_bench(args)
 
     from r9700training_amd import R97Q_BF16, R97Q_F32, _ptr, _stream, check, lib
     from r9700training_amd.qlinear import bwd_workspace, fwd_workspace

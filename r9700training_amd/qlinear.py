@@ -195,6 +195,22 @@ def gemm_nt_q_dx(w: QWeight, dY, a_scale, dA=None, accumulate=False, da_dtype=to
     return dA
 
 
+def gemm_nt_q_fwd(w: QWeight, a, a_scale, Y=None, y_dtype=torch.float32, workspace=None, stream=None):
+    """gemm_nt_q's twin, the coded forward: Y[m, n] = sum_g (a . code over group g)[m, n] *
+    a_scale[m, g] * scale[n, g]. a int8 [T, K], a_scale f32 [T, K/128]; w in the int8-code form
+    (QWeight(..., codes8=True)). Returns Y [T, N]."""
+    T = a.shape[0]
+    if Y is None:
+        Y = torch.empty((T, w.N), dtype=y_dtype, device=a.device)
+    if workspace is None:
+        workspace = _workspace(lib().r97q_gemm_nt_q_fwd_workspace_bytes(T, w.K), a.device, "gemm_nt_q_fwd")
+    rc = lib().r97q_gemm_nt_q_fwd(C.byref(w.w), _ptr(a), _ptr(a_scale), T, _ptr(Y),
+                                  R97Q_F32 if Y.dtype == torch.float32 else R97Q_BF16, _ptr(workspace),
+                                  workspace.numel(), _stream(stream))
+    check(rc, "r97q_gemm_nt_q_fwd")
+    return Y
+
+
 def lora_shrink_q_bwd(a, a_scale, A, t_cot, da=None, ds=None, dA=None, want=("da", "ds", "dA"), workspace=None,
                       stream=None, group_width=0):
     """The coded shrink's adjoint: a [T, K] int8 codes (or f32 code values), a_scale f32 [T, groups],

@@ -1,7 +1,11 @@
 """The coded (i8a8h) trunk on the card against the oracle's restatement of the reference's host rows
-(src/adjoint/host/linear.cpp:284-317, src/adjoint/host/lora.cpp:246-328): the C entries
-r97q_gemm_nt_q_dx and r97q_lora_shrink_q_bwd, and the device rows gemm_nt_q and the coded
-lora_shrink driven through the registry as the reference's walk drives them.
+(src/adjoint/host/linear.cpp:245-317, src/adjoint/host/lora.cpp:246-328): the C entries
+r97q_gemm_nt_q_fwd, r97q_gemm_nt_q_dx and r97q_lora_shrink_q_bwd, and the device rows gemm_nt_q
+and the coded lora_shrink driven through the registry as the reference's walk drives them.
+
+gemm_nt_q's twin sums each 128-column group exactly (int8 products, int32 sums) and folds the groups
+in f32: against the oracle's f64 loop only the f32 fold differs, so its bar is 1e-5 (bf16 Y: the
+one rounding of the output, 4e-3).
 
 Bars: gemm_nt_q's code cotangent multiplies a stored IQR weight as bf16(code * scale), one rounding
 of each weight (~1.65e-3), so it is held to the base products' 2e-3 relative L2 (a weight carried as
@@ -34,6 +38,86 @@ def codes_and_scales(rng, T, K, groups):
     a = np.rint(rng.uniform(-1.0, 1.0, (T, K)) * 60.0)
     s = (0.02 + 0.05 * rng.random((T, groups))).astype(np.float32).astype(np.float64)
     return a, s
+
+
+TOL_EXACT = 1e-5
+
+
+def full_range_codes(rng, T, K):
+    """int8 activation codes over the whole range, with per-(row, group) f32 scales."""
+    a = rng.integers(-127, 128, (T, K)).astype(np.float64)
+    s = (0.01 + 0.05 * rng.random((T, K // 128))).astype(np.float32).astype(np.float64)
+    return a, s
+
+
+@pytest.mark.parametrize("T,N,K", [(300, 256, 384), (512, 384, 256), (64, 128, 1024), (1030, 512, 512), (1, 128, 128),
+                                   (257, 640, 896)])
+def test_gemm_nt_q_fwd(T, N, K):
+    from test_gpu_codes8 import prepare
+
+    from r9700training_amd.qlinear import gemm_nt_q_fwd
+
+    print(f"case gemm_nt_q_fwd T={T} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(7 * T + N + K)
+    planes = weight_planes(N, K, seed=T + 1)
+    keep = []
+    w = prepare(planes, keep, codes8=True)
+    codes, scale = host_weight(planes)
+    a, a_scale = full_range_codes(rng, T, K)
+    ad = torch.tensor(a.astype(np.int8), device="cuda")
+    sd = torch.tensor(a_scale.astype(np.float32), device="cuda")
+    got = gemm_nt_q_fwd(w, ad, sd)
+    got_bf = gemm_nt_q_fwd(w, ad, sd, y_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    want = O.gemm_nt_q_twin(a, a_scale, codes, scale)
+    e, e_bf = rel_l2(f64(got), want), rel_l2(f64(got_bf), want)
+    print(f"  rel L2 Y {e:.3e} bf16 {e_bf:.3e}", flush=True)
+    assert e <= TOL_EXACT and e_bf <= 4e-3
+    # the activation scale is applied per group: one group's scale doubled moves the result
+    a_scale2 = a_scale.copy()
+    a_scale2[:, -1] *= 2.0
+    assert rel_l2(f64(got), O.gemm_nt_q_twin(a, a_scale2, codes, scale)) > 10 * TOL_EXACT
+
+
+def test_gemm_nt_q_fwd_c2():
+    """C2's square layer (T = N = K = 4096): the whole Y against the oracle on sampled token rows
+    (the first, tile-edge, middle and last), and every row at once through the column sums of the
+    group products (each group's sum over m of a * a_scale is one row the oracle multiplies)."""
+    from test_gpu_codes8 import prepare
+
+    from r9700training_amd.qlinear import gemm_nt_q_fwd
+
+    print("case gemm_nt_q_fwd C2", flush=True)
+    T = N = K = 4096
+    rng = np.random.default_rng(4096)
+    sc = (0.75 + 0.5 * rng.random(K // 128)).astype(np.float32)
+    planes = S.trellis(rows=N, cols=K, bits=5, state_bits=16, run_rows=256, rb=1, mad=1, scale_dtype=S.F32,
+                       rowf=True, seed=11, scale_col=sc, packed=True)
+    keep = []
+    w = prepare(planes, keep, codes8=True)
+    codes, scale = host_weight(planes)
+    a, a_scale = full_range_codes(rng, T, K)
+    got = f64(gemm_nt_q_fwd(w, torch.tensor(a.astype(np.int8), device="cuda"),
+                            torch.tensor(a_scale.astype(np.float32), device="cuda")))
+    rows = np.unique(np.array([0, 1, 31, 32, 255, 256, 2047, 2048, 3839, 3840, 4094, 4095]))
+    e = rel_l2(got[rows], O.gemm_nt_q_twin(a[rows], a_scale[rows], codes, scale))
+    # sum over m of Y[m, n] = sum_g (sum_m a[m, g-cols] * a_scale[m, g]) . code[n, g-cols] * scale[n, g]:
+    # one f64 row per group, through the oracle with unit activation scales
+    x = (a.reshape(T, K // 128, 128) * a_scale[:, :, None]).sum(axis=0).reshape(1, K)
+    want_sum = O.gemm_nt_q_twin(x, np.ones((1, K // 128)), codes, scale)[0]
+    e_sum = rel_l2(got.sum(axis=0), want_sum)
+    print(f"  rel L2 sampled rows {e:.3e} column sums {e_sum:.3e}", flush=True)
+    assert e <= TOL_EXACT and e_sum <= TOL_EXACT
+
+
+def test_gemm_nt_q_fwd_refuses_a_trellis_stream():
+    from r9700training_amd import R97qError
+    from r9700training_amd.qlinear import gemm_nt_q_fwd
+
+    keep = []
+    w = prepared(weight_planes(128, 256, seed=5), keep)
+    with pytest.raises(R97qError, match="int8-code form"):
+        gemm_nt_q_fwd(w, torch.zeros((8, 256), dtype=torch.int8, device="cuda"), torch.ones((8, 2), device="cuda"))
 
 
 @pytest.mark.parametrize("T,N,K", [(300, 256, 384), (512, 384, 256), (64, 128, 1024), (1030, 512, 512)])
