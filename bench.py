@@ -274,31 +274,26 @@ C5_LAYERS, C5_T, C5_R, C5_ALPHA = 24, 32768, 16, 32.0
 
 def coded_fwd_bench(args):
     """gemm_nt_q's twin (r97q_gemm_nt_q_fwd) at C2's square layer: int8 activation codes a [4096, 4096]
-    with f32 scales per 128-column group, the weight (trellis.mad b5 quantized from N(0, 0.02))
-    in its int8-code form; Y f32. One step = one launch pair (the codes' tiled copy + the product)."""
-    import ctypes as C
-
-    import numpy as np
+    with f32 scales per 128-column group, and a stored weight in the reference's two grids (int8
+    codes [4096, 4096], bf16 scales [4096, 32]); Y f32. One step = one launch."""
     import torch
 
     from r9700training_amd import R97Q_F32, _ptr, _stream, check, lib
 
     dev = torch.device("cuda:0")
     T, N, K, _r, _alpha = CONFIGS["c2"]
-    inp = make_inputs(T, N, K, 16, args.seed, dev, "codes8")
-    w = inp["w"]
     g = torch.Generator(device="cuda").manual_seed(args.seed)
     a = torch.randint(-127, 128, (T, K), dtype=torch.int8, device=dev, generator=g)
     a_scale = 0.01 + 0.05 * torch.rand((T, K // 128), device=dev, generator=g)
+    codes = torch.randint(-126, 127, (N, K), dtype=torch.int8, device=dev, generator=g)
+    scale = (0.0002 + 0.0004 * torch.rand((N, K // 128), device=dev, generator=g)).to(torch.bfloat16)
     Y = torch.empty((T, N), dtype=torch.float32, device=dev)
     L = lib()
-    ws = torch.empty(L.r97q_gemm_nt_q_fwd_workspace_bytes(T, K), dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream()
-    st = _stream(stream)
+    st = _stream(torch.cuda.current_stream())
 
     def step():
-        check(L.r97q_gemm_nt_q_fwd(C.byref(w.w), _ptr(a), _ptr(a_scale), T, _ptr(Y), R97Q_F32, _ptr(ws), ws.numel(),
-                                   st), "gemm_nt_q_fwd")
+        check(L.r97q_gemm_nt_q_fwd(_ptr(codes), _ptr(scale), N, K, _ptr(a), _ptr(a_scale), T, _ptr(Y), R97Q_F32, st),
+              "gemm_nt_q_fwd")
 
     for _ in range(args.warmup):
         step()
@@ -314,13 +309,12 @@ def coded_fwd_bench(args):
         "metric": "coded forward (gemm_nt_q twin) TOP/s at C2's square layer",
         "value": round(tops, 3), "unit": "TOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "i8", "data": "synthetic: int8 codes uniform in [-127, 127], scales U(0.01, 0.06); W ~ N(0,0.02) "
-                               "quantized by this repo's trellis quantizer, in the int8-code form",
-        "config": {"workload": f"coded_fwd: Y = sum_g (a . code^T)_g * a_scale * scale, T={T}, N={N}, K={K}, "
+        "dtype": "i8", "data": "synthetic: activation codes uniform in [-127, 127] with scales U(0.01, 0.06); "
+                               "weight codes uniform in [-126, 126] with bf16 scales U(2e-4, 6e-4)",
+        "config": {"workload": f"coded_fwd: Y = sum_g (a . codes^T)_g * a_scale * scale, T={T}, N={N}, K={K}, "
                                "group 128, Y f32", "T": T, "N": N, "K": K},
-        "roofline": {"bound": "mfma", "kernel": "qlinear_q_kernel (+ qtok_tile_kernel in the step)",
-                     "achieved": round(tops, 3), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": None},
+        "roofline": {"bound": "mfma", "kernel": "qlinear_q_kernel", "achieved": round(tops, 3),
+                     "peak": PEAK_INT8_TOPS, "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": None},
     }), flush=True)
 
 

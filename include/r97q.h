@@ -365,15 +365,14 @@ int r97q_lora_expand_bwd(int64_t T, int64_t N, const uint16_t* dY, const uint16_
 int r97q_gemm_nt_q_dx(const R97qWeight* w, const uint16_t* dY, int64_t T, const float* a_scale, void* dA,
                       int32_t da_dtype, int32_t accumulate, R97IqrStream stream);
 /* gemm_nt_q's twin, the coded forward (src/adjoint/host/linear.cpp:245-282, group 128 over a stored
- * weight): Y[m, n] = sum_g (sum_{k in g} a[m, k] code[n, k]) * a_scale[m, g] * scale[n, g], with
- * a int8 [T, K] activation codes, a_scale f32 [T, K/128], and w the weight's int8-code form
- * (r97q_weight_prepare_codes8; R97Q_EUNSUPPORTED for a trellis stream). The group sums are exact
- * (int8 MFMA, int32 accumulation); each group is folded into an f32 accumulator. Y f32 or bf16
- * [T, N]. workspace: r97q_gemm_nt_q_fwd_workspace_bytes(T, K) bytes (the codes' tiled copy and the
- * transposed scales). */
-int64_t r97q_gemm_nt_q_fwd_workspace_bytes(int64_t T, int64_t K);
-int r97q_gemm_nt_q_fwd(const R97qWeight* w, const int8_t* a, const float* a_scale, int64_t T, void* Y,
-                       int32_t y_dtype, void* workspace, int64_t workspace_bytes, R97IqrStream stream);
+ * weight): Y[m, n] = sum_g (sum_{k in g} a[m, k] codes[n, k]) * a_scale[m, g] * scale[n, g], with
+ * a int8 [T, K] activation codes and a_scale f32 [T, K/128], and the stored weight's two grids as
+ * the reference keeps them (src/stored_weight.h:24-33; r97_iqr_decode writes them, the scale.col
+ * fold applied): codes int8 [N, K] row-major, scale bf16 [N, K/128]. N and K multiples of 128. The
+ * group sums are exact (int8 MFMA, int32 accumulation); each group is folded into an f32
+ * accumulator. Y f32 or bf16 [T, N]. No workspace. */
+int r97q_gemm_nt_q_fwd(const int8_t* codes, const uint16_t* scale, int64_t N, int64_t K, const int8_t* a,
+                       const float* a_scale, int64_t T, void* Y, int32_t y_dtype, R97IqrStream stream);
 /* The coded lora_shrink's adjoint (the reference's device row for the coded trunk,
  * src/adjoint/device/lora.hip:437-577, registered for a coded activation; host form
  * src/adjoint/host/lora.cpp:246-328), one adapter slot, with g = t_cot . A (f32 [T, K]):

@@ -154,8 +154,7 @@ SIGNATURES = {
     "r97q_lora_expand_bwd": (C.c_int, [_I, _I, _P, _P, _i, C.c_float, _P, _P, _P, _P, _I, _P]),
     "r97q_qlinear_dx_base": (C.c_int, [C.POINTER(Weight), _P, _I, _i, _P, _i, _i, _P, _I, _P]),
     "r97q_gemm_nt_q_dx": (C.c_int, [C.POINTER(Weight), _P, _I, _P, _P, _i, _i, _P]),
-    "r97q_gemm_nt_q_fwd_workspace_bytes": (_I, [_I, _I]),
-    "r97q_gemm_nt_q_fwd": (C.c_int, [C.POINTER(Weight), _P, _P, _I, _P, _i, _P, _I, _P]),
+    "r97q_gemm_nt_q_fwd": (C.c_int, [_P, _P, _I, _I, _P, _P, _I, _P, _i, _P]),
     "r97q_lora_shrink_q_bwd_workspace_bytes": (_I, [_I, _I, _i]),
     "r97q_lora_shrink_q_bwd": (C.c_int, [_I, _I, _P, _i, _P, _I, _I, _P, _i, _P, _P, _P, _P, _P, _I, _P]),
     "r97q_scheduled_lr": (C.c_float, [C.POINTER(AdamWConfig), _i]),

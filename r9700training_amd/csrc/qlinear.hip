@@ -564,49 +564,36 @@ int r97q_gemm_nt_q_dx(const R97qWeight* w, const uint16_t* dY, int64_t T, const 
     return dx_scaled(w, sh, dY, dA, da_dtype, accumulate, (hipStream_t)stream, a_scale);
 }
 
-int64_t r97q_gemm_nt_q_fwd_workspace_bytes(int64_t T, int64_t K) {
-    if (T <= 0 || K <= 0 || K % q::kGroup) return -1;
-    return align256(q::tok_tile_bytes(T, K)) + align256(K / q::kGroup * q::tok_ld(T) * 4);
-}
-
-int r97q_gemm_nt_q_fwd(const R97qWeight* w, const int8_t* a, const float* a_scale, int64_t T, void* Y,
-                       int32_t y_dtype, void* workspace, int64_t workspace_bytes, R97IqrStream stream) {
+int r97q_gemm_nt_q_fwd(const int8_t* codes, const uint16_t* scale, int64_t N, int64_t K, const int8_t* a,
+                       const float* a_scale, int64_t T, void* Y, int32_t y_dtype, R97IqrStream stream) {
     clear_error();
     const char* who = "r97q_gemm_nt_q_fwd";
-    if (int e = check_weight(w)) return e;
-    if (w->bits != R97Q_CODES8) {
-        set_error("%s: the coded product reads the weight's int8-code form (r97q_weight_prepare_codes8)", who);
-        return R97Q_EUNSUPPORTED;
+    if (!codes || !scale || !a || !a_scale || !Y) {
+        set_error("%s: null codes / scale / a / a_scale / Y", who);
+        return R97Q_EINVAL;
     }
-    if (!a || !a_scale || !Y || T <= 0) {
-        set_error("%s: null a / a_scale / Y or T <= 0", who);
+    if (T <= 0 || N <= 0 || K <= 0 || N % q::kBN || K % q::kGroup) {
+        set_error("%s: T %lld N %lld K %lld (T > 0, N and K multiples of 128)", who, (long long)T, (long long)N,
+                  (long long)K);
         return R97Q_EINVAL;
     }
     if (y_dtype != R97Q_F32 && y_dtype != R97Q_BF16) {
         set_error("%s: y_dtype %d (R97Q_F32 or R97Q_BF16)", who, (int)y_dtype);
         return R97Q_EINVAL;
     }
-    const int64_t K = w->cols;
-    if (int e = check_ws(workspace_bytes, r97q_gemm_nt_q_fwd_workspace_bytes(T, K), workspace, who)) return e;
-    uint8_t* wsb = static_cast<uint8_t*>(workspace);
-    const hipStream_t s = (hipStream_t)stream;
-    int8_t* act = reinterpret_cast<int8_t*>(wsb);
-    float* sa_t = reinterpret_cast<float*>(wsb + align256(q::tok_tile_bytes(T, K)));
-    if (int e = q::launch_tokens(a, a_scale, T, K, act, sa_t, s)) return e;
     q::Params p{};
-    p.act = act;
-    p.sa_t = sa_t;
+    p.a = a;
+    p.a_scale = a_scale;
+    p.codes = codes;
+    p.scale = scale;
     p.T = T;
-    p.N = w->rows;
+    p.N = N;
     p.K = K;
-    p.ldt = q::tok_ld(T);
-    p.units = reinterpret_cast<const uint8_t*>(w->stream);
-    p.scale_t = w->scale_t;
     p.out = Y;
     p.out_f32 = y_dtype == R97Q_F32;
-    p.mtiles = (int)(p.ldt / q::kBM);
-    p.otiles = (int)(w->rows / q::kBN);
-    return q::launch_forward(p, s);
+    p.mtiles = (int)((T + q::kBM - 1) / q::kBM);
+    p.otiles = (int)(N / q::kBN);
+    return q::launch_forward(p, (hipStream_t)stream);
 }
 
 int64_t r97q_lora_shrink_q_bwd_workspace_bytes(int64_t T, int64_t K, int32_t rank) {

@@ -195,18 +195,16 @@ def gemm_nt_q_dx(w: QWeight, dY, a_scale, dA=None, accumulate=False, da_dtype=to
     return dA
 
 
-def gemm_nt_q_fwd(w: QWeight, a, a_scale, Y=None, y_dtype=torch.float32, workspace=None, stream=None):
-    """gemm_nt_q's twin, the coded forward: Y[m, n] = sum_g (a . code over group g)[m, n] *
-    a_scale[m, g] * scale[n, g]. a int8 [T, K], a_scale f32 [T, K/128]; w in the int8-code form
-    (QWeight(..., codes8=True)). Returns Y [T, N]."""
-    T = a.shape[0]
+def gemm_nt_q_fwd(codes, scale, a, a_scale, Y=None, y_dtype=torch.float32, stream=None):
+    """gemm_nt_q's twin, the coded forward: Y[m, n] = sum_g (a . codes over group g)[m, n] *
+    a_scale[m, g] * scale[n, g]. The stored weight's grids: codes int8 [N, K], scale bf16 [N, K/128]
+    (as uint16 bits or bfloat16); a int8 [T, K], a_scale f32 [T, K/128]. Returns Y [T, N]."""
+    T, K = a.shape
+    N = codes.shape[0]
     if Y is None:
-        Y = torch.empty((T, w.N), dtype=y_dtype, device=a.device)
-    if workspace is None:
-        workspace = _workspace(lib().r97q_gemm_nt_q_fwd_workspace_bytes(T, w.K), a.device, "gemm_nt_q_fwd")
-    rc = lib().r97q_gemm_nt_q_fwd(C.byref(w.w), _ptr(a), _ptr(a_scale), T, _ptr(Y),
-                                  R97Q_F32 if Y.dtype == torch.float32 else R97Q_BF16, _ptr(workspace),
-                                  workspace.numel(), _stream(stream))
+        Y = torch.empty((T, N), dtype=y_dtype, device=a.device)
+    rc = lib().r97q_gemm_nt_q_fwd(_ptr(codes), _ptr(scale), N, K, _ptr(a), _ptr(a_scale), T, _ptr(Y),
+                                  R97Q_F32 if Y.dtype == torch.float32 else R97Q_BF16, _stream(stream))
     check(rc, "r97q_gemm_nt_q_fwd")
     return Y
 

@@ -53,21 +53,17 @@ def full_range_codes(rng, T, K):
 @pytest.mark.parametrize("T,N,K", [(300, 256, 384), (512, 384, 256), (64, 128, 1024), (1030, 512, 512), (1, 128, 128),
                                    (257, 640, 896)])
 def test_gemm_nt_q_fwd(T, N, K):
-    from test_gpu_codes8 import prepare
-
     from r9700training_amd.qlinear import gemm_nt_q_fwd
 
     print(f"case gemm_nt_q_fwd T={T} N={N} K={K}", flush=True)
     rng = np.random.default_rng(7 * T + N + K)
-    planes = weight_planes(N, K, seed=T + 1)
-    keep = []
-    w = prepare(planes, keep, codes8=True)
-    codes, scale = host_weight(planes)
+    codes, scale = host_weight(weight_planes(N, K, seed=T + 1))
+    cd, scd = dev(codes), dev(scale)
     a, a_scale = full_range_codes(rng, T, K)
     ad = torch.tensor(a.astype(np.int8), device="cuda")
     sd = torch.tensor(a_scale.astype(np.float32), device="cuda")
-    got = gemm_nt_q_fwd(w, ad, sd)
-    got_bf = gemm_nt_q_fwd(w, ad, sd, y_dtype=torch.bfloat16)
+    got = gemm_nt_q_fwd(cd, scd, ad, sd)
+    got_bf = gemm_nt_q_fwd(cd, scd, ad, sd, y_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     want = O.gemm_nt_q_twin(a, a_scale, codes, scale)
     e, e_bf = rel_l2(f64(got), want), rel_l2(f64(got_bf), want)
@@ -83,8 +79,6 @@ def test_gemm_nt_q_fwd_c2():
     """C2's square layer (T = N = K = 4096): the whole Y against the oracle on sampled token rows
     (the first, tile-edge, middle and last), and every row at once through the column sums of the
     group products (each group's sum over m of a * a_scale is one row the oracle multiplies)."""
-    from test_gpu_codes8 import prepare
-
     from r9700training_amd.qlinear import gemm_nt_q_fwd
 
     print("case gemm_nt_q_fwd C2", flush=True)
@@ -93,11 +87,9 @@ def test_gemm_nt_q_fwd_c2():
     sc = (0.75 + 0.5 * rng.random(K // 128)).astype(np.float32)
     planes = S.trellis(rows=N, cols=K, bits=5, state_bits=16, run_rows=256, rb=1, mad=1, scale_dtype=S.F32,
                        rowf=True, seed=11, scale_col=sc, packed=True)
-    keep = []
-    w = prepare(planes, keep, codes8=True)
     codes, scale = host_weight(planes)
     a, a_scale = full_range_codes(rng, T, K)
-    got = f64(gemm_nt_q_fwd(w, torch.tensor(a.astype(np.int8), device="cuda"),
+    got = f64(gemm_nt_q_fwd(dev(codes), dev(scale), torch.tensor(a.astype(np.int8), device="cuda"),
                             torch.tensor(a_scale.astype(np.float32), device="cuda")))
     rows = np.unique(np.array([0, 1, 31, 32, 255, 256, 2047, 2048, 3839, 3840, 4094, 4095]))
     e = rel_l2(got[rows], O.gemm_nt_q_twin(a[rows], a_scale[rows], codes, scale))
@@ -110,14 +102,14 @@ def test_gemm_nt_q_fwd_c2():
     assert e <= TOL_EXACT and e_sum <= TOL_EXACT
 
 
-def test_gemm_nt_q_fwd_refuses_a_trellis_stream():
+def test_gemm_nt_q_fwd_refusals():
     from r9700training_amd import R97qError
     from r9700training_amd.qlinear import gemm_nt_q_fwd
 
-    keep = []
-    w = prepared(weight_planes(128, 256, seed=5), keep)
-    with pytest.raises(R97qError, match="int8-code form"):
-        gemm_nt_q_fwd(w, torch.zeros((8, 256), dtype=torch.int8, device="cuda"), torch.ones((8, 2), device="cuda"))
+    codes = torch.zeros((128, 300), dtype=torch.int8, device="cuda")
+    with pytest.raises(R97qError, match="multiples of 128"):
+        gemm_nt_q_fwd(codes, torch.zeros((128, 3), dtype=torch.int16, device="cuda"),
+                      torch.zeros((8, 300), dtype=torch.int8, device="cuda"), torch.ones((8, 3), device="cuda"))
 
 
 @pytest.mark.parametrize("T,N,K", [(300, 256, 384), (512, 384, 256), (64, 128, 1024), (1030, 512, 512)])
