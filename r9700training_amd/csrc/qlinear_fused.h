@@ -48,6 +48,9 @@ struct DxParams {
     // stream + z*z_w (uint32 units), scale_t + z*z_scale, dX + z*z_out (elements of dX's dtype)
     int batch;
     int64_t z_dy, z_w, z_scale, z_out;
+    // batched int8-code form with a_scale: the tile holds the low half of each weight's split,
+    // bf16(w - bf16(w)) (a second pass completing the exact weight)
+    int lo;
 };
 
 template <int BITS>

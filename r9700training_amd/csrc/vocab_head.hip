@@ -277,8 +277,14 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
             p.z_w = Np * K / 4;
             p.z_scale = nkb * Np;
             p.z_out = rows * K;
+            // each weight as the exact sum of two bf16 values: the product over the high halves,
+            // then over the low halves added in (f32 products of bf16 values are exact)
             launch_dx<R97Q_CODES8>(p, s);
             if (int e = launch_status("qlinear_dx_kernel (vocab head)")) return e;
+            p.lo = 1;
+            p.accumulate = 1;
+            launch_dx<R97Q_CODES8>(p, s);
+            if (int e = launch_status("qlinear_dx_kernel (vocab head, low halves)")) return e;
             hipLaunchKernelGGL(vocab_reduce_kernel, dim3(blocks(rows * K, 256)), dim3(256), 0, s, d_x, part, rows * K,
                                Z);
             if (int e = launch_status("vocab_reduce_kernel")) return e;
