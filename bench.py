@@ -40,6 +40,14 @@ CONFIGS = {
 }
 
 
+DECODE_MODES = {"auto": 0, "once": 1, "fused": 2}  # R97Q_DECODE_AUTO / _ONCE / _FUSED (include/r97q.h)
+DECODE_ONCE_MIN_T = 16384  # the library's automatic choice (csrc/qlinear.hip, kDecodeOnceMinT)
+
+
+def decodes_once(mode, T):
+    return mode == "once" or (mode == "auto" and T >= DECODE_ONCE_MIN_T)
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -59,6 +67,11 @@ def parse():
                          "transposed product at a 248320-row head, n_embd 2048, --vocab-rows token rows; "
                          "c5_stack: one whole LoRA step of the 24-layer stack (T=32768, rank 16 on every projection); "
                          "coded_fwd: gemm_nt_q's twin (int8 codes x the int8-code weight) at C2's square layer")
+    ap.add_argument("--decode", default="auto", choices=sorted(DECODE_MODES),
+                    help="how the base products meet the weight (r97q_set_decode_once): fused (each tile "
+                         "decoded in the product's main loop, once a 512-token panel), once (the whole weight "
+                         "decoded once a call into the workspace, then the product over the decoded tiles), "
+                         "auto (the library's choice: once from 16384 tokens on)")
     ap.add_argument("--vocab-rows", type=int, default=4096)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (3 launches), the known-size "
@@ -338,6 +351,7 @@ def c5_stack_bench(args):
     torch.cuda.set_device(dev)
     T, r, s = C5_T, C5_R, C5_ALPHA / C5_R
     L = lib()
+    L.r97q_set_decode_once(DECODE_MODES[args.decode])
     g = torch.Generator(device="cuda").manual_seed(args.seed)
     rng = np.random.default_rng(args.seed)
     weights, keep = [], []
@@ -406,7 +420,7 @@ def c5_stack_bench(args):
         "tflops": round(tf, 3),
         "config": {"workload": "C5: 24 layers x (2048->8192, 4096->2048, 2048->6144, 6144->2048) b5 trellis.mad, "
                                "LoRA r16 alpha 32 on every projection, T=32768, Y/dX f32",
-                   "T": T, "layers": C5_LAYERS, "rank": r},
+                   "T": T, "layers": C5_LAYERS, "rank": r, "decode": "once" if decodes_once(args.decode, T) else "fused"},
         "roofline": {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
         "memory_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 2),
@@ -457,9 +471,10 @@ def main():
     t = torch.empty((T, r), dtype=torch.float32, device=dev)
     dA = torch.zeros((r, K), dtype=torch.float32, device=dev)
     dB = torch.zeros((N, r), dtype=torch.float32, device=dev)
+    L = lib()
+    L.r97q_set_decode_once(DECODE_MODES[args.decode])
     wsf = fwd_workspace(T, N, K, r, dev)
     wsb = bwd_workspace(T, N, K, r, dev)
-    L = lib()
     stream = torch.cuda.current_stream()
     st = _stream(stream)
     P = lambda x: _ptr(x)
@@ -523,9 +538,13 @@ def main():
     ms_lora_step = (time.perf_counter() - t0) * 1e3 / args.steps
     total_flops = flops(T, N, K, r)
     value = total_flops / (ms_step * 1e-3) / 1e12
-    # the dominant kernel and its algorithmic work per launch
-    kern = {"qlinear_rt_kernel<fwd>": (fwd_ms, 2 * T * N * K + 2 * T * N * r),
-            "qlinear_rt_kernel<dx>": (dx_ms, 2 * T * N * K + 2 * T * K * r)}
+    # the dominant kernel and its algorithmic work per launch (with the weight decoded once a call,
+    # the event pair holds the decode launch and the product over its tiles)
+    once = decodes_once(args.decode, T)
+    kf, kd = ("predecode+qlinear_pd_kernel<fwd>", "predecode+qlinear_pd_kernel<dx>") if once else \
+        ("qlinear_rt_kernel<fwd>", "qlinear_rt_kernel<dx>")
+    kern = {kf: (fwd_ms, 2 * T * N * K + 2 * T * N * r),
+            kd: (dx_ms, 2 * T * N * K + 2 * T * K * r)}
     name = max(kern, key=lambda k: kern[k][0])
     kms, kfl = kern[name]
     achieved = kfl / (kms * 1e-3) / 1e12
@@ -553,12 +572,12 @@ def main():
                                f"Y/dX {args.out_dtype}"
                                + (", weight in the int8-code form" if args.weight_form == "codes8" else ""),
                    "T": T, "N": N, "K": K, "rank": r, "alpha": alpha, "out_dtype": args.out_dtype,
-                   "weight_form": args.weight_form},
+                   "weight_form": args.weight_form, "decode": "once" if once else "fused"},
         "tokens_per_s": round(T / (ms_step * 1e-3), 1),
         "lora_step": {"tokens_per_s": round(T / (ms_lora_step * 1e-3), 1), "ms": round(ms_lora_step, 4),
                       "what": "fwd+bwd + the staged dA/dB flushed into AdamW on A, B (device, f32 masters) + their bf16 copies"},
         "flops_per_step": total_flops,
-        "kernels_ms": {"qlinear_rt_kernel<fwd>": round(fwd_ms, 4), "qlinear_rt_kernel<dx>": round(dx_ms, 4),
+        "kernels_ms": {kf: round(fwd_ms, 4), kd: round(dx_ms, 4),
                        "other": round(ms_step_ev - fwd_ms - dx_ms, 4), "ms_per_step_with_events": round(ms_step_ev, 4)},
         "roofline": {"bound": "mfma", "kernel": name, "achieved": round(achieved, 3),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),

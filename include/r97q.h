@@ -237,6 +237,18 @@ int r97q_weight_from_decoded(const int8_t* codes, const uint16_t* scale, int64_t
 #define R97Q_BF16 1
 #define R97Q_F32 0
 
+/* How the base products meet the weight (no counterpart in the reference, whose rows decode it
+ * into their own buffers): R97Q_DECODE_FUSED decodes each weight tile inside the product's main
+ * loop, once for every 512-token panel; R97Q_DECODE_ONCE decodes the whole weight once a call into
+ * the workspace (N*K*2 more bytes) and runs the product over the decoded tiles, the same values in
+ * the same order (the results are the same bits); R97Q_DECODE_AUTO (the default) takes the second
+ * from 16384 tokens on. Process-wide; returns the previous mode, or -1 for an unknown one. The
+ * workspace sizes below follow the mode in force when they are asked. */
+#define R97Q_DECODE_AUTO 0
+#define R97Q_DECODE_ONCE 1
+#define R97Q_DECODE_FUSED 2
+int32_t r97q_set_decode_once(int32_t mode);
+
 /* Workspace the forward / backward need at this shape (bytes, 256-aligned pieces inside). */
 int64_t r97q_fwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank);
 int64_t r97q_bwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank);

@@ -16,6 +16,7 @@ R97Q_F32 = 0
 R97Q_BF16 = 1
 R97Q_I8 = 2
 R97Q_CODES8 = 8  # R97qWeight.bits of the int8-code form (include/r97q.h)
+R97Q_DECODE_AUTO, R97Q_DECODE_ONCE, R97Q_DECODE_FUSED = 0, 1, 2  # r97q_set_decode_once modes
 R97Q_ADAMW_GRADS_STAGED = 1  # r97q_adamw_step flags: the gradients are staging buffers (include/r97q.h)
 
 
@@ -135,6 +136,7 @@ SIGNATURES = {
     "r97q_weight_prepare": (C.c_int, [C.POINTER(Desc), _P, _P, _P, C.POINTER(Weight), _P]),
     "r97q_weight_prepare_codes8": (C.c_int, [C.POINTER(Desc), _P, _P, _P, C.POINTER(Weight), _P]),
     "r97q_weight_from_decoded": (C.c_int, [_P, _P, _I, _I, _P, _P, C.POINTER(Weight), _P]),
+    "r97q_set_decode_once": (C.c_int32, [_i]),
     "r97q_fwd_workspace_bytes": (C.c_int64, [_I, _I, _I, _i]),
     "r97q_bwd_workspace_bytes": (C.c_int64, [_I, _I, _I, _i]),
     "r97q_qlinear_lora_fwd": (C.c_int, [C.POINTER(Weight), _P, _I, _P, _P, _i, C.c_float, _P, _i, _P, _P, _I, _P]),

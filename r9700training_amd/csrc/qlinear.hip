@@ -24,6 +24,8 @@
 #include "qlinear_rt.h"
 #include "status.h"
 
+#include <atomic>
+
 using namespace r97q;
 
 namespace {
@@ -37,36 +39,63 @@ struct Shape {
     int r;
 };
 
+// The base products either decode each weight tile in the main loop, once for every 512-token
+// panel (the fused kernel), or decode the whole weight once a call into the workspace and run the
+// product over the decoded tiles (rt::launch_predecode, then rt::launch_pd). The second saves the
+// repeated decode's VALU work and power, but costs a launch that writes and re-reads N*K*2 bytes:
+// measured on the card, it wins at 64 panels (C5's 32768 tokens: the 24-layer step 182 ms against
+// 191 ms) and loses at 8 (C2's 4096: 328 us a step against 313). r97q_set_decode_once overrides
+// the choice; the entry that allocates nothing always runs the fused kernel.
+constexpr int64_t kDecodeOnceMinT = 32 * rt::kBM;
+std::atomic<int> g_decode_once{R97Q_DECODE_AUTO};
+bool decode_once(int64_t T) {
+    const int m = g_decode_once.load(std::memory_order_relaxed);
+    return m == R97Q_DECODE_ONCE || (m == R97Q_DECODE_AUTO && T >= kDecodeOnceMinT);
+}
+
 // Workspace layout. Forward: Xt (X's tiled copy, act_tiles.h) | P [T, 2r] | Apad [rd, K] (when r
-// is not a multiple of 16).
+// is not a multiple of 16) | Wt (the weight's decoded tiles, rt::wt_bytes, when decode_once).
 // Backward: dYt (dY's tiled copy) | Bt [rd, N] | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt]
 // | partA [chunks, r, K] | partB [chunks, r, N] (f32 partial sums of the factor gradients) | done
-// (the gradient launch's column-block counters, dA's then dB's).
+// (the gradient launch's column-block counters, dA's then dB's) | Wt (as the forward's).
+// Wt is -1 where the layout has none.
 struct FwdWs {
-    int64_t Xt, P, Apad, total;
+    int64_t Xt, P, Apad, Wt, total;
 };
-FwdWs fwd_ws(const Shape& s) {
+FwdWs fwd_ws(const Shape& s, bool fused_only = false) {
     FwdWs w{};
     w.Xt = 0;
     w.P = w.Xt + align256(act_tile_bytes(s.T, s.K));
-    if (s.r == 0) {
-        w.total = w.P;
-        return w;
+    w.total = w.P;
+    if (s.r > 0) {
+        const int rd = down_rank(s.r);
+        w.Apad = w.P + align256(s.T * 2 * s.r * 2);
+        w.total = w.Apad + (rd != s.r ? align256((int64_t)rd * s.K * 2) : 0);
     }
-    const int rd = down_rank(s.r);
-    w.Apad = w.P + align256(s.T * 2 * s.r * 2);
-    w.total = w.Apad + (rd != s.r ? align256((int64_t)rd * s.K * 2) : 0);
+    w.Wt = -1;
+    if (!fused_only && decode_once(s.T)) {
+        w.Wt = w.total;
+        w.total += align256(rt::wt_bytes(s.N, s.K));
+    }
     return w;
 }
 struct BwdWs {
-    int64_t dYt, Bt, At, P, PtA, PtB, partA, partB, done, total;
+    int64_t dYt, Bt, At, P, PtA, PtB, partA, partB, done, Wt, total;
 };
+void bwd_ws_wt(const Shape& s, BwdWs& w) {
+    w.Wt = -1;
+    if (decode_once(s.T)) {
+        w.Wt = w.total;
+        w.total += align256(rt::wt_bytes(s.N, s.K));
+    }
+}
 BwdWs bwd_ws(const Shape& s) {
     BwdWs w{};
     w.dYt = 0;
     w.Bt = w.dYt + align256(act_tile_bytes(s.T, s.N));
     if (s.r == 0) {
         w.total = w.Bt;
+        bwd_ws_wt(s, w);
         return w;
     }
     const int rd = down_rank(s.r);
@@ -80,6 +109,7 @@ BwdWs bwd_ws(const Shape& s) {
     w.partB = w.partA + align256(chunks * s.r * s.K * 4);
     w.done = w.partB + align256(chunks * s.r * s.N * 4);
     w.total = w.done + align256((grad_blocks(s.K) + grad_blocks(s.N)) * 4);
+    bwd_ws_wt(s, w);
     return w;
 }
 
@@ -228,9 +258,11 @@ int fwd_prep(const Shape& sh, const uint16_t* X, const uint16_t* A, float scale,
     return launch_lora_down(a, s);
 }
 
-// the register-fed fused product over the token operand's tiled copy `act` (forward or dX)
+// the register-fed product over the token operand's tiled copy `act` (forward or dX): with `wt`
+// (rt::wt_bytes of workspace) the weight decoded once into it, then the product over its tiles;
+// without, the fused kernel decoding in its main loop
 int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act, const uint16_t* P,
-            const uint16_t* Q, void* out, int32_t out_dtype, int32_t accumulate, hipStream_t s) {
+            const uint16_t* Q, void* out, int32_t out_dtype, int32_t accumulate, uint8_t* wt, hipStream_t s) {
     rt::Params p{};
     p.act = act;
     p.T = sh.T;
@@ -249,6 +281,19 @@ int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act,
     p.accumulate = accumulate != 0;
     p.mtiles = (int)((sh.T + rt::kBM - 1) / rt::kBM);
     p.otiles = (int)((fwd ? sh.N : sh.K) / rt::kBN);
+    p.wt = wt;
+    if (wt) {
+        switch (w->bits) {
+            case 3: rt::launch_predecode<3>(p, fwd, wt, s); break;
+            case 4: rt::launch_predecode<4>(p, fwd, wt, s); break;
+            case 5: rt::launch_predecode<5>(p, fwd, wt, s); break;
+            case 6: rt::launch_predecode<6>(p, fwd, wt, s); break;
+            default: rt::launch_predecode<R97Q_CODES8>(p, fwd, wt, s); break;
+        }
+        if (int e = launch_status("predecode_kernel")) return e;
+        rt::launch_pd(p, fwd, s);
+        return launch_status(fwd ? "qlinear_pd_kernel<fwd>" : "qlinear_pd_kernel<dx>");
+    }
     auto go = [&](auto fwd_fn, auto dx_fn) { fwd ? fwd_fn(p, s) : dx_fn(p, s); };
     switch (w->bits) {
         case 3: go(rt::launch_fwd<3>, rt::launch_dx<3>); break;
@@ -261,10 +306,11 @@ int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act,
 }
 
 int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* B, void* Y, int32_t y_dtype, uint8_t* wsb,
-             hipStream_t s) {
-    const FwdWs ws = fwd_ws(sh);
+             hipStream_t s, bool fused_only = false) {
+    const FwdWs ws = fwd_ws(sh, fused_only);
     return rt_base(w, true, sh, reinterpret_cast<const uint16_t*>(wsb + ws.Xt),
-                   reinterpret_cast<const uint16_t*>(wsb + ws.P), B, Y, y_dtype, 0, s);
+                   reinterpret_cast<const uint16_t*>(wsb + ws.P), B, Y, y_dtype, 0,
+                   ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s);
 }
 
 // B^T [rd, N] (zero rows past r), A^T [K, r]; dt = s.dY.B as P = [hi | lo](dt) for the fused dX
@@ -324,7 +370,7 @@ int dx_base(const R97qWeight* w, const Shape& sh, void* dX, int32_t dx_dtype, in
     const BwdWs ws = bwd_ws(sh);
     return rt_base(w, false, sh, reinterpret_cast<const uint16_t*>(wsb + ws.dYt),
                    reinterpret_cast<const uint16_t*>(wsb + ws.P), reinterpret_cast<const uint16_t*>(wsb + ws.At), dX,
-                   dx_dtype, accumulate, s);
+                   dx_dtype, accumulate, ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s);
 }
 
 // the LDS-staged dX kernel over row-major dY with the coded trunk's activation scale in its
@@ -408,6 +454,11 @@ int scratch_of_current_device(uint8_t** at, const char* who) {
 }  // namespace
 
 extern "C" {
+
+int32_t r97q_set_decode_once(int32_t mode) {
+    if (mode != R97Q_DECODE_AUTO && mode != R97Q_DECODE_ONCE && mode != R97Q_DECODE_FUSED) return -1;
+    return g_decode_once.exchange(mode);
+}
 
 int64_t r97q_fwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank) {
     return fwd_ws(Shape{T, N, K, rank}).total;
@@ -781,7 +832,7 @@ int r97q_qlinear_lora_fwd_noalloc(const R97qWeight* w, const uint16_t* X, int64_
         return R97Q_EINVAL;
     }
     const Shape sh{T, w->rows, w->cols, rank};
-    const int64_t need = fwd_ws(sh).total;
+    const int64_t need = fwd_ws(sh, true).total;
     if (need > kNoAllocScratchBytes) {
         set_error("%s: T %lld x K %lld at rank %d needs %lld workspace bytes, past the %lld this entry holds "
                   "(use r97q_qlinear_lora_fwd with a workspace)",
@@ -792,7 +843,7 @@ int r97q_qlinear_lora_fwd_noalloc(const R97qWeight* w, const uint16_t* X, int64_
     if (int e = scratch_of_current_device(&wsb, who)) return e;
     const hipStream_t s = (hipStream_t)stream;
     if (int e = fwd_prep(sh, X, A, scale, t_out, wsb, s)) return e;
-    return fwd_base(w, sh, B, Y, y_dtype, wsb, s);
+    return fwd_base(w, sh, B, Y, y_dtype, wsb, s, true);
 }
 
 }  // extern "C"

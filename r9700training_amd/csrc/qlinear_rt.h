@@ -29,12 +29,20 @@ struct Params {
     int out_f32;
     int accumulate;            // dX only: add into `out`
     int mtiles, otiles;
+    const uint8_t* wt;         // the weight decoded once a call (launch_predecode), for launch_pd
 };
 
 template <int BITS>
 void launch_fwd(const Params& p, hipStream_t s);
 template <int BITS>
 void launch_dx(const Params& p, hipStream_t s);
+
+// Every weight tile the product (forward when `fwd`, else dX) walks, decoded to bf16 in the LDS
+// tile format, into `out` (wt_bytes(N, K) bytes); then launch_pd runs the product over them.
+template <int BITS>
+void launch_predecode(const Params& p, bool fwd, uint8_t* out, hipStream_t s);
+void launch_pd(const Params& p, bool fwd, hipStream_t s);
+inline int64_t wt_bytes(int64_t N, int64_t K) { return N * K * 2; }
 
 }  // namespace rt
 }  // namespace r97q

@@ -39,9 +39,7 @@
 #include <cstdint>
 #include <type_traits>
 
-#include "act_tiles.h"
-#include "iqr_device.h"
-#include "qlinear_rt.h"
+#include "rt_core.h"
 
 #ifndef R97Q_BITS
 #error "compile with -DR97Q_BITS=<code width>"
@@ -55,64 +53,10 @@ namespace r97q {
 namespace rt {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((__vector_size__(16)));
-typedef __bf16 bf16x2 __attribute__((__vector_size__(4)));
-typedef float f32x16 __attribute__((__vector_size__(64)));
-
-constexpr int kNI = kBN / 32;               // 4 output blocks of 32
-constexpr int kTileBytes = kBN * kStep * 2; // one decoded bf16 tile: 128 rows x 128 bytes
-constexpr int kBlock = 32 * kStep;          // bf16 elements in one 32 x 64 block of the tiled operand
-
-// the geometry of a workgroup of W waves
-template <int W>
-struct Geo {
-    static constexpr int kWaveM = kBM / W;  // tokens a wave: 128 or 64
-    static constexpr int kMI = kWaveM / 32; // its token blocks of 32
-    static constexpr int kFRows = 32 / W;   // forward decode: rows a lane takes of each 32-row segment
-    static constexpr int kDRows = 64 / W;   // dX decode: rows a lane takes of the step's 64
-    static_assert(W == 4 || W == 8, "4 or 8 waves");
-};
-
-__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
-
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-    bf16x2 v = {(__bf16)a, (__bf16)b};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
 __device__ __forceinline__ uint32_t comp(const uint4& v, int c) {
     return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
 }
 __device__ __forceinline__ uint32_t comp(const uint2& v, int c) { return c == 0 ? v.x : v.y; }
-
-// XOR swizzle of a 128-byte LDS row's eight 16-byte chunks: 16 consecutive rows reading one
-// logical chunk land on 16 distinct 16-byte bank groups.
-__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
-
-__device__ __forceinline__ uint8_t* chunk_at(uint8_t* tile, int row, int chunk) {
-    return tile + row * 128 + ((chunk ^ swz(row)) << 4);
-}
-
-// The end of the decode of a tile: this wave's LDS writes (and fragment reads) are done, then the
-// workgroup barrier. Vector-memory loads (the wave's own token rows, the stream words) are not
-// waited for: nothing another wave reads depends on them.
-__device__ __forceinline__ void tile_barrier() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited
-    asm volatile("s_barrier" ::: "memory");
-}
-
-// XCD-aware tile order: consecutive workgroup ids are dealt round-robin over the 8 XCDs;
-// renumber so each XCD's workgroups take one contiguous run of tiles (tokens outer, outputs
-// inner), which keeps a token panel in that XCD's L2.
-__device__ __forceinline__ int xcd_tile(int bid, int nwg) {
-    const int xcd = bid & 7, local = bid >> 3;
-    const int base = nwg >> 3, rem = nwg & 7;
-    return xcd * base + (xcd < rem ? xcd : rem) + local;
-}
 
 // ---------------------------------------------------------------- one lane's slice of a tile
 // ROWS consecutive rows ROWS*SLICE.. of a 32-row segment. Their trellis states are the 16-bit
@@ -345,48 +289,6 @@ struct Wave {
         }
     }
 
-    // ------------------------------------------------ the token fragments of step s, round j
-    // blk[mi]: element offset of the wave's token block mi in step 0 (clamped to the operand's
-    // last block)
-    __device__ __forceinline__ void tokens(const uint16_t* act, const int64_t (&blk)[kMI], int s, int j,
-                                           uint4 (&t)[kMI][4]) const {
-#pragma unroll
-        for (int mi = 0; mi < kMI; ++mi)
-            t[mi][j] = *reinterpret_cast<const uint4*>(act + blk[mi] + (int64_t)s * sstride + 512 * j);
-    }
-
-    __device__ __forceinline__ void frags(const uint8_t* tile, int j, bf16x8 (&b)[kNI]) const {
-        const int half = lane >> 5, l32 = lane & 31;
-#pragma unroll
-        for (int ni = 0; ni < kNI; ++ni)
-            b[ni] = as_bf16x8(*reinterpret_cast<const uint4*>(
-                chunk_at(const_cast<uint8_t*>(tile), 32 * ni + l32, 4 * half + j)));
-    }
-
-    __device__ __forceinline__ void round(const uint4 (&t)[kMI][4], int j, const bf16x8 (&b)[kNI],
-                                          f32x16 (&acc)[kMI][kNI]) const {
-#pragma unroll
-        for (int mi = 0; mi < kMI; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = mfma32(as_bf16x8(t[mi][j]), b[ni], acc[mi][ni]);
-    }
-
-    // The issue order of one round: its MFMAs, each followed by a share of the round's other work --
-    // the next round's fragment reads first (they are needed a round later), then the
-    // vector-memory loads, NVALU decode operations spread evenly, the decode's LDS writes last.
-    template <int NDSR, int NVMEM, int NVALU, int NDSW>
-    __device__ __forceinline__ static void interleave() {
-        constexpr int M = kMI * kNI;
-#pragma unroll
-        for (int i = 0; i < M; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            if (i < NDSR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-            if (i >= 1 && i - 1 < NVMEM) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-            if (NVALU > 0) __builtin_amdgcn_sched_group_barrier(0x002, (NVALU + M - 1) / M, 0);  // VALU
-            if (i >= M - NDSW) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-        }
-    }
-
     static constexpr int kWordLoads = C8 ? (FWD ? 2 : ROWS / 8) + (ROWS + 7) / 8
                                          : Span<C8 ? 5 : BITS, ROWS, SLICE>::NW + (ROWS + 7) / 8;
     static constexpr int kValuPart = (FWD ? 4 * ROWS : 2 * ROWS) * 7 / 3 + 8;  // decode operations of a part
@@ -403,45 +305,38 @@ struct Wave {
         const int sn = s + 1 < nsteps ? s + 1 : nsteps - 1;
         const int sf = s + 2 < nsteps ? s + 2 : nsteps - 1;
         __builtin_amdgcn_sched_barrier(0);
-        tokens(act, blk, s, 3, t);
+        constexpr int M = kMI * kNI;
+        tokens(act, blk, sstride, s, 3, t);
         words(sf, fetch);
-        frags(cur, 1, b1);
+        frags(cur, lane, 1, b1);
         round(t, 0, b0, acc);
         decode<0>(dec, nxt);
-        interleave<4, kMI + kWordLoads, kValuPart, kWrites(0)>();
+        interleave<M, 4, kMI + kWordLoads, kValuPart, kWrites(0)>();
         __builtin_amdgcn_sched_barrier(0);
-        tokens(act, blk, sn, 0, t);
-        frags(cur, 2, b0);
+        tokens(act, blk, sstride, sn, 0, t);
+        frags(cur, lane, 2, b0);
         round(t, 1, b1, acc);
         decode<1>(dec, nxt);
-        interleave<4, kMI, kValuPart, kWrites(1)>();
+        interleave<M, 4, kMI, kValuPart, kWrites(1)>();
         __builtin_amdgcn_sched_barrier(0);
-        tokens(act, blk, sn, 1, t);
-        frags(cur, 3, b1);
+        tokens(act, blk, sstride, sn, 1, t);
+        frags(cur, lane, 3, b1);
         round(t, 2, b0, acc);
         decode<2>(dec, nxt);
-        interleave<4, kMI, kValuPart, kWrites(2)>();
+        interleave<M, 4, kMI, kValuPart, kWrites(2)>();
         __builtin_amdgcn_sched_barrier(0);
         tile_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        tokens(act, blk, sn, 2, t);
-        frags(nxt, 0, b0);
+        tokens(act, blk, sstride, sn, 2, t);
+        frags(nxt, lane, 0, b0);
         round(t, 3, b1, acc);
-        interleave<4, kMI, 0, 0>();
+        interleave<M, 4, kMI, 0, 0>();
         __builtin_amdgcn_sched_barrier(0);
     }
 
     __device__ __forceinline__ void run(const uint16_t* act, uint8_t* t0, uint8_t* t1, f32x16 (&acc)[kMI][kNI]) const {
-        // the wave's token blocks; rows past the operand's last block read that block again (their
-        // products land in rows that are never stored)
-        const int64_t nblk = act_tile_blocks(p.T);
         int64_t blk[kMI];
-#pragma unroll
-        for (int mi = 0; mi < kMI; ++mi) {
-            int64_t rb = (m0 >> 5) + mi;
-            if (rb > nblk - 1) rb = nblk - 1;
-            blk[mi] = rb * kBlock + 8 * lane;
-        }
+        token_blocks<kMI>(m0, p.T, lane, blk);
         uint4 t[kMI][4];
         LW wa, wb;
         bf16x8 b0[kNI], b1[kNI];
@@ -455,10 +350,10 @@ struct Wave {
         words(nsteps > 1 ? 1 : 0, wb);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 3; ++j) tokens(act, blk, 0, j, t);
+        for (int j = 0; j < 3; ++j) tokens(act, blk, sstride, 0, j, t);
         __builtin_amdgcn_sched_barrier(0);
         tile_barrier();
-        frags(t0, 0, b0);
+        frags(t0, lane, 0, b0);
         // step s decodes tile s+1 from the words of step s+1 and fetches those of step s+2 into
         // the set step s+1 decoded from; unrolled by two so the sets keep fixed names
         for (int s = 0; s < nsteps; s += 2) {
@@ -467,58 +362,6 @@ struct Wave {
         }
     }
 };
-
-// ---------------------------------------------------------------- epilogue
-// acc += [hi | lo](P)[m, :] . [Q | Q][o, :]^T over 2r: P [T, 2r] bf16; Q [outputs, r] bf16
-template <int MI>
-__device__ __forceinline__ void adapter(const uint16_t* P, const uint16_t* Q, int r, int64_t m0, int64_t o0,
-                                        int64_t T, int lane, f32x16 (&acc)[MI][kNI]) {
-    const int half = lane >> 5, l32 = lane & 31;
-    for (int kk = 0; kk < 2 * r; kk += 16) {
-        const int kq = kk + 8 * half;
-        bf16x8 pa[MI], qb[kNI];
-#pragma unroll
-        for (int mi = 0; mi < MI; ++mi) {
-            int64_t row = m0 + 32 * mi + l32;
-            if (row > T - 1) row = T - 1;
-            pa[mi] = as_bf16x8(*reinterpret_cast<const uint4*>(P + row * 2 * r + kq));
-        }
-#pragma unroll
-        for (int ni = 0; ni < kNI; ++ni)
-            qb[ni] = as_bf16x8(*reinterpret_cast<const uint4*>(Q + (o0 + 32 * ni + l32) * r + (kq % r)));
-#pragma unroll
-        for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = mfma32(pa[mi], qb[ni], acc[mi][ni]);
-    }
-}
-
-// accumulator element e of tile (mi, ni) is row 32*mi + 8*(e/4) + 4*half + e%4, column 32*ni + l32
-template <int MI>
-__device__ __forceinline__ void store(const f32x16 (&acc)[MI][kNI], void* out, int64_t ld, int64_t m0, int64_t o0,
-                                      int64_t T, int lane, int f32, int accumulate) {
-    const int half = lane >> 5, l32 = lane & 31;
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int64_t row = m0 + 32 * mi + 8 * (e >> 2) + 4 * half + (e & 3);
-            if (row >= T) continue;
-#pragma unroll
-            for (int ni = 0; ni < kNI; ++ni) {
-                const int64_t col = o0 + 32 * ni + l32;
-                float v = acc[mi][ni][e];
-                if (f32) {
-                    float* d = reinterpret_cast<float*>(out) + row * ld + col;
-                    *d = accumulate ? *d + v : v;
-                } else {
-                    uint16_t* d = reinterpret_cast<uint16_t*>(out) + row * ld + col;
-                    if (accumulate) v += bf16_to_f32(*d);
-                    *d = f32_to_bf16(v);
-                }
-            }
-        }
-}
 
 template <bool FWD, int WAVES, int WAVE>
 __device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t* t1, int mt, int ot) {
@@ -561,7 +404,89 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qlinear_rt_kernel(const Params 
     }
 }
 
+// ---------------------------------------------------------------- the weight decoded once a call
+// Every tile a product walks, decoded to bf16 in the LDS tile format (rt_core.h) and stored in
+// walk order: tile (o, s) -- outputs 128o.. (features n, or columns k for dX), reduction values
+// 64s.. -- at byte (o * nsteps + s) * kTileBytes of `out`. The lanes and the arithmetic are the
+// main loop's (Wave::words, Wave::decode): a tile is decoded into LDS exactly as the fused kernel
+// decodes it, then copied out whole, each wave a contiguous 2 KiB (one 1 KiB store a piece), so a
+// tile holds the bits the fused kernel multiplies. A workgroup takes one output tile and kPreSteps
+// consecutive steps, two LDS tiles in turn, the next step's words in flight while it decodes one.
+constexpr int kPreSteps = 8;
+
+template <int WAVES, int WAVE>
+__device__ __forceinline__ void copy_out(const uint8_t* tile, uint8_t* g, int lane) {
+    constexpr int kShare = kTileBytes / WAVES;
+#pragma unroll
+    for (int q = 0; q < kShare / 1024; ++q) {
+        const int off = kShare * WAVE + 1024 * q + 16 * lane;
+        *reinterpret_cast<uint4*>(g + off) = *reinterpret_cast<const uint4*>(tile + off);
+    }
+}
+
+template <bool FWD, int WAVES, int WAVE>
+__device__ __forceinline__ void wave_predecode(const Params& p, uint8_t* out, uint8_t* t0, uint8_t* t1, int ot,
+                                               int s0) {
+    using WV = Wave<FWD, WAVES, WAVE>;
+    const int lane = threadIdx.x & 63;
+    const int64_t red = FWD ? p.K : p.N;
+    const int nsteps = (int)(red / kStep);
+    WV w{p, red, 0, (int64_t)ot * kBN, 0, lane, nsteps};
+    w.setup();
+    const int s1 = s0 + kPreSteps < nsteps ? s0 + kPreSteps : nsteps;
+    uint8_t* base = out + (int64_t)ot * nsteps * kTileBytes;
+    typename WV::LW wa, wb;
+    w.words(s0, wa);
+    for (int s = s0; s < s1; s += 2) {
+        w.words(s + 1 < s1 ? s + 1 : s, wb);
+        w.template decode<0>(wa, t0);
+        w.template decode<1>(wa, t0);
+        w.template decode<2>(wa, t0);
+        __syncthreads();
+        copy_out<WAVES, WAVE>(t0, base + (int64_t)s * kTileBytes, lane);
+        if (s + 1 >= s1) break;
+        w.words(s + 2 < s1 ? s + 2 : s + 1, wa);
+        w.template decode<0>(wb, t1);
+        w.template decode<1>(wb, t1);
+        w.template decode<2>(wb, t1);
+        __syncthreads();
+        copy_out<WAVES, WAVE>(t1, base + (int64_t)(s + 1) * kTileBytes, lane);
+    }
+}
+
+template <bool FWD, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void predecode_kernel(const Params p, uint8_t* out) {
+    __shared__ __attribute__((aligned(16))) uint8_t t0[kTileBytes], t1[kTileBytes];
+    const int ot = blockIdx.x, s0 = blockIdx.y * kPreSteps;
+    switch (threadIdx.x >> 6) {
+        case 0: wave_predecode<FWD, WAVES, 0>(p, out, t0, t1, ot, s0); break;
+        case 1: wave_predecode<FWD, WAVES, 1>(p, out, t0, t1, ot, s0); break;
+        case 2: wave_predecode<FWD, WAVES, 2>(p, out, t0, t1, ot, s0); break;
+        case 3: wave_predecode<FWD, WAVES, 3>(p, out, t0, t1, ot, s0); break;
+        default:
+            if constexpr (WAVES == 8) {
+                switch (threadIdx.x >> 6) {
+                    case 4: wave_predecode<FWD, WAVES, 4>(p, out, t0, t1, ot, s0); break;
+                    case 5: wave_predecode<FWD, WAVES, 5>(p, out, t0, t1, ot, s0); break;
+                    case 6: wave_predecode<FWD, WAVES, 6>(p, out, t0, t1, ot, s0); break;
+                    default: wave_predecode<FWD, WAVES, 7>(p, out, t0, t1, ot, s0); break;
+                }
+            }
+            break;
+    }
+}
+
 }  // namespace
+
+template <>
+void launch_predecode<R97Q_BITS>(const Params& p, bool fwd, uint8_t* out, hipStream_t s) {
+    const int64_t nsteps = (fwd ? p.K : p.N) / kStep;
+    const dim3 grid((unsigned)p.otiles, (unsigned)((nsteps + kPreSteps - 1) / kPreSteps));
+    if (fwd)
+        hipLaunchKernelGGL((predecode_kernel<true, R97Q_RT_WAVES>), grid, dim3(64 * R97Q_RT_WAVES), 0, s, p, out);
+    else
+        hipLaunchKernelGGL((predecode_kernel<false, R97Q_RT_WAVES>), grid, dim3(64 * R97Q_RT_WAVES), 0, s, p, out);
+}
 
 template <>
 void launch_fwd<R97Q_BITS>(const Params& p, hipStream_t s) {
