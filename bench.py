@@ -44,6 +44,27 @@ DECODE_MODES = {"auto": 0, "once": 1, "fused": 2}  # R97Q_DECODE_AUTO / _ONCE / 
 DECODE_ONCE_MIN_T = 16384  # the library's automatic choice (csrc/qlinear.hip, kDecodeOnceMinT)
 
 
+def mfma_ceiling(L, torch, iters=24000, reps=3):
+    """The card's sustained bf16 MFMA rate with nothing else to do (r97q_mfma_probe): median of
+    `reps` launches of about 40 ms each, random operands and zero operands, in TFLOP/s."""
+    from r9700training_amd import _ptr, _stream, check
+
+    out = torch.empty(256 * 512, dtype=torch.float32, device="cuda")
+    st = _stream(torch.cuda.current_stream())
+    res = {}
+    for zero in (0, 1):
+        rates = []
+        for _ in range(reps + 1):  # the first launch ramps the clock
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            check(L.r97q_mfma_probe(iters, zero, _ptr(out), st), "r97q_mfma_probe")
+            b.record()
+            b.synchronize()
+            rates.append(L.r97q_mfma_probe_flops(iters) / (a.elapsed_time(b) * 1e-3) / 1e12)
+        res["zero_operands" if zero else "random_operands"] = round(sorted(rates[1:])[len(rates[1:]) // 2], 1)
+    return res
+
+
 def decodes_once(mode, T):
     return mode == "once" or (mode == "auto" and T >= DECODE_ONCE_MIN_T)
 
@@ -588,6 +609,13 @@ def main():
                                            f"of the {panels} token panels' workgroups"},
         "quantizer_rel_err": round(inp["q"]["rel_err"], 4),
     }
+    # the rate the card sustains on MFMAs alone (power-limited: its clock falls well below the peak's
+    # 2.4 GHz under a full matrix load): the nearer bar for the fused kernels
+    ceil = mfma_ceiling(L, torch)
+    line["roofline"]["ceiling_measured"] = dict(
+        ceil, unit="TFLOP/s",
+        what="v_mfma_f32_32x32x16_bf16 alone, operands in registers, 256 workgroups x 8 waves, ~40 ms a launch")
+    line["roofline"]["frac_of_measured_ceiling"] = round(achieved / ceil["random_operands"], 4)
     if args.cpu_seconds > 0:
         line["cpu_baseline"] = cpu_baseline(inp, T, N, K, r, s, args.cpu_seconds, min(8, host_cores()))
         line["cpu_baseline_all_cores"] = (cpu_baseline(inp, T, N, K, r, s, args.cpu_seconds, host_cores())

@@ -169,6 +169,8 @@ SIGNATURES = {
     "r97q_vocab_head_workspace_bytes": (_I, [C.POINTER(VocabPlan), _I]),
     "r97q_vocab_head_transpose": (C.c_int, [C.POINTER(VocabPlan), _P, _I, _P, _P, _I, _P]),
     "r97q_vocab_head_cast": (C.c_int, [_P, _P, _I, _P]),
+    "r97q_mfma_probe_flops": (_I, [_i]),
+    "r97q_mfma_probe": (C.c_int, [_i, _i, _P, _P]),
 }
 
 _lib = None
