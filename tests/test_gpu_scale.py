@@ -14,7 +14,11 @@ What is checked:
 * t (all T x r), dA and dB (whole) against f64 products of the same bf16 inputs (float64 GEMMs
   in torch, an implementation independent of this library's kernels), within 1e-4. The oracle's
   own adapter loops walk dY with stride N and take minutes at these sizes; at small sizes
-  test_gpu_qlinear.py holds t, dA and dB to the oracle itself.
+  test_gpu_qlinear.py holds t, dA and dB to the oracle itself;
+* every element of Y and dX against the host rows' arithmetic done in float64 GEMMs on the card:
+  the weight is the oracle's decode (code * scale in f64, the reference's weight value,
+  src/adjoint/host/linear.cpp:118-190), Y = X.W^T + s.t.B^T and dX = dY.W + dt.A with t and dt the
+  f64 products above; the whole tensor within relative L2 2e-3 and its worst row within 3e-3.
 """
 import numpy as np
 import pytest
@@ -69,6 +73,26 @@ def test_full_shape(name, T, N, K, r):
 
     Y, t = qlinear_lora_fwd(w, Xd, Ad, Bd, s, y_dtype=torch.float32)
     dX, dA, dB = qlinear_lora_bwd(w, Xd, dYd, Ad, Bd, t, s, dx_dtype=torch.float32)
+    torch.cuda.synchronize()
+
+    # every element, against float64 GEMMs on the card over the oracle's decoded weight
+    W64 = torch.from_numpy(codes).cuda().double() * torch.from_numpy(
+        S.bf16_bits_to_f32(scale).astype(np.float64)).cuda().repeat_interleave(128, dim=1)
+    X64, dY64, A64, B64 = Xd.double(), dYd.double(), Ad.double(), Bd.double()
+    t64 = X64 @ A64.T.contiguous()
+    dt64 = s * (dY64 @ B64)
+
+    def whole(got, ref, what):
+        err = got.double() - ref
+        e = float(torch.linalg.vector_norm(err) / torch.linalg.vector_norm(ref))
+        er = float((torch.linalg.vector_norm(err, dim=1) / torch.linalg.vector_norm(ref, dim=1)).max())
+        print(f"  every element of {what}: rel L2 {e:.3e}, worst row {er:.3e}", flush=True)
+        assert e <= TOL_BASE and er <= 1.5 * TOL_BASE, what
+
+    whole(Y, X64 @ W64.T.contiguous() + s * (t64 @ B64.T.contiguous()), "Y")
+    whole(dX, dY64 @ W64 + dt64 @ A64, "dX")
+    del W64, X64, dY64, A64, B64, t64, dt64
+    torch.cuda.empty_cache()
     rows = sample_rows(T, rng)
     ridx = torch.from_numpy(rows).cuda()
     got_y, got_dx = f64(Y.index_select(0, ridx)), f64(dX.index_select(0, ridx))
