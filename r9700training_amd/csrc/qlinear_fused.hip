@@ -285,7 +285,9 @@ struct Loop {
                     const int byte = FWD ? 8 * (c >> 1) + 2 * i + (c & 1) : 2 * i + c;
                     const uint32_t w = comp(wd.c, byte >> 2) ^ 0x80808080u;
                     const float v = code8_value(w, byte & 3, sc[i], off[i]);
-                    if constexpr (LO) return v - bf16_to_f32(f32_to_bf16(v));
+                    // the high half rounded by the hardware's RNE conversion (the one that packs
+                    // the high tile), so the two halves are exactly the split of v
+                    if constexpr (LO) return v - (float)(__bf16)v;
                     return v;
                 } else {
                     return slice_value<BITS, ROWS, COLS, SLICE>(wd, c, i, a24, b, sc[i], off[i]);
