@@ -7,7 +7,8 @@
 namespace r97q {
 
 // v[m][j] = sum_k In[m][k] W[j][k] for m < T, j < r (W row-major [down_rank(r), Kin], rows past r
-// zero; Kin a multiple of 128). Writes, each when non-null:
+// zero; or, with w_kmajor, W row-major [Kin, r]: the factor as B is held; Kin a multiple of 128).
+// Writes, each when non-null:
 //   tiled              the fused kernels' tiled copy of In (act_tiles.h), rows T..32*ceil(T/32) zero
 //   out [T, r] f32    = sa * v   (+= when out_add)
 //   P   [T, 2r] bf16  = [hi | lo](sb * v)                    (row-major)
@@ -30,6 +31,12 @@ struct DownArgs {
     uint16_t* tiled;
     int* zero;
     int nzero;
+    int w_kmajor;  // W is [Kin, r] (k-major) instead of [down_rank(r), Kin]
+    // a side job, when tr_out is non-null: tr_out [tr_cols, r] = tr_in^T, tr_in [r, tr_cols] (the
+    // dX epilogue's A^T, written by the backward's launch instead of a launch of its own)
+    const uint16_t* tr_in;
+    uint16_t* tr_out;
+    int64_t tr_cols;
 };
 
 // out += scale * sum_m (Pt[j][m] + Pt[r+j][m]) V[m][c]: V bf16 [T, C] (C a multiple of 128), out

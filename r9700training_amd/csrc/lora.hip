@@ -71,23 +71,59 @@ __device__ __forceinline__ bf16x8 tr_pair(s16x4 lo4, s16x4 hi4) {
 // ---------------------------------------------------------------- down
 // One workgroup = 16 token rows; its nw waves (8, or 4 when Kin is not a multiple of 256) each
 // reduce a contiguous nw-th of Kin, then the partial sums are added in wave order through LDS.
+//
+// KM (the factor k-major, W [Kin, r] row-major: the backward's B as the caller holds it): the MFMA's
+// B operand needs 8 consecutive k of one factor column, which that layout keeps r apart. Each wave
+// stages its chunk of factor rows -- contiguous in memory, one coalesced 16-byte piece a lane a
+// load -- into its own LDS region (rows padded to RD columns, the columns past r zero), then reads
+// the operand back transposed with ds_read_b64_tr_b16, as the gradient kernel reads its token
+// tile. The chunk's loads are issued with the token rows', a chunk ahead; no transpose launch.
 constexpr int kDownWavesMax = 8;
 
 template <int RD>
+struct DownStage {
+    static constexpr int S = 2 * RD + 16;              // LDS bytes a staged factor row (16-aligned)
+    static constexpr int NB = RD / 16;
+    static constexpr int CH = 32 * (8 / NB);           // factor rows a chunk
+    static constexpr int BYTES = CH * S;               // a wave's stage
+};
+
+template <int RD, bool KM>
 __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
     __shared__ float red[kDownWavesMax][16][RD];
+    __shared__ __attribute__((aligned(16))) uint8_t stage_lds[KM ? kDownWavesMax * DownStage<RD>::BYTES : 16];
     const int nw = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row16 = lane & 15, grp = lane >> 4;
     const int64_t m0 = (int64_t)blockIdx.x * 16;
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i < a.nzero; i += blockDim.x) a.zero[i] = 0;
+    if (a.tr_out) {
+        // this workgroup's share of the side transpose: columns [c0, c1) of tr_in
+        const int64_t per = (a.tr_cols + gridDim.x - 1) / gridDim.x;
+        const int64_t c0 = (int64_t)blockIdx.x * per, c1 = c0 + per < a.tr_cols ? c0 + per : a.tr_cols;
+        for (int64_t i = threadIdx.x; i < (c1 - c0) * a.r; i += blockDim.x) {
+            const int64_t c = c0 + i / a.r;
+            const int j = (int)(i % a.r);
+            a.tr_out[c * a.r + j] = a.tr_in[(int64_t)j * a.tr_cols + c];
+        }
+    }
     int64_t row = m0 + row16;
     if (row > a.T - 1) row = a.T - 1;
     const int64_t kq = a.Kin / nw;  // a multiple of 32
     const uint16_t* ap = a.In + row * a.Kin + wave * kq + 8 * grp;
     const uint16_t* wp = a.W + (int64_t)row16 * a.Kin + wave * kq + 8 * grp;
     constexpr int NB = RD / 16;
+    // KM: the wave's stage, its factor rows from wave * kq on, and the pieces of a full chunk
+    using St = DownStage<RD>;
+    uint8_t* stage = stage_lds + (KM ? wave * St::BYTES : 0);
+    const uint16_t* wk = a.W + (int64_t)wave * kq * a.r;
+    const int rb = 2 * a.r;                             // bytes a factor row in memory
+    if constexpr (KM) {
+        // the columns past r stay zero (never written again)
+        if (a.r < RD)
+            for (int i = lane; i < St::BYTES / 16; i += 64) reinterpret_cast<u32x4*>(stage)[i] = u32x4{0u, 0u, 0u, 0u};
+    }
     f32x4 acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = (f32x4){};
@@ -102,26 +138,63 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
     // copy's 32-row padding, is written as zeros)
     const int64_t mt = m0 + row16;
     const bool tile_row = a.tiled != nullptr && mt < (a.T + 31) / 32 * 32;
-    auto tile = [&](int64_t k, const uint4& v) {
+    auto tile = [&](int64_t k, const u32x4& v) {
         if (tile_row)
-            *reinterpret_cast<uint4*>(a.tiled + act_tile_index(mt, wave * kq + 8 * grp + k, a.T)) =
-                mt < a.T ? v : uint4{0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(a.tiled + act_tile_index(mt, wave * kq + 8 * grp + k, a.T)) =
+                mt < a.T ? v : u32x4{0u, 0u, 0u, 0u};
     };
-    uint4 xv[2][U], fv[2][U][NB];
-    auto load = [&](int64_t k, uint4 (&x)[U], uint4 (&f)[U][NB]) {
+    u32x4 xv[2][U], fv[2][U][NB];
+    // KM: piece q of a lane (16 bytes) is piece lane + 64 q of the chunk's rows k .. k + rows, in
+    // f's flattened slots; it lands at row (16 p) / rb, byte (16 p) % rb of the stage
+    // (pieces past the chunk's rows load piece 0 again and are not stored: no predicated loads,
+    // so the registers stay registers)
+    auto km_load = [&](int64_t k, int rows, u32x4 (&f)[U][NB]) {
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(wk + k * a.r);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            x[u] = *reinterpret_cast<const uint4*>(ap + k + 32 * u);
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                f[u][nb] = *reinterpret_cast<const uint4*>(wp + (int64_t)16 * nb * a.Kin + k + 32 * u);
+        for (int q = 0; q < U * NB; ++q) {
+            const int p = lane + 64 * q;
+            f[q / NB][q % NB] = *reinterpret_cast<const u32x4*>(src + (16 * p < rows * rb ? 16 * p : 0));
         }
     };
-    auto mult = [&](int64_t k, const uint4 (&x)[U], const uint4 (&f)[U][NB]) {
+    auto km_store = [&](int rows, const u32x4 (&f)[U][NB]) {
+#pragma unroll
+        for (int q = 0; q < U * NB; ++q) {
+            const int p = lane + 64 * q;
+            if (16 * p < rows * rb)
+                *reinterpret_cast<u32x4*>(stage + (16 * p) / rb * St::S + (16 * p) % rb) = f[q / NB][q % NB];
+        }
+    };
+    // KM: the B operand of slice u, column block nb: rows 32u + 8grp .. +8 of the stage at column
+    // 16nb + row16, read transposed
+    auto km_frag = [&](int u, int nb) {
+        const int e = row16 >> 2, q = row16 & 3;
+        const int r0 = 32 * u + 8 * grp + e;
+        const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(stage + r0 * St::S + (16 * nb + 4 * q) * 2));
+        const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(stage + (r0 + 4) * St::S + (16 * nb + 4 * q) * 2));
+        return tr_pair(lo4, hi4);
+    };
+    auto load = [&](int64_t k, u32x4 (&x)[U], u32x4 (&f)[U][NB]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) x[u] = *reinterpret_cast<const u32x4*>(ap + k + 32 * u);
+        if constexpr (KM) {
+            km_load(k, CH, f);
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    f[u][nb] = *reinterpret_cast<const u32x4*>(wp + (int64_t)16 * nb * a.Kin + k + 32 * u);
+        }
+    };
+    auto mult = [&](int64_t k, const u32x4 (&x)[U], const u32x4 (&f)[U][NB]) {
+        if constexpr (KM) km_store(CH, f);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16(as_bf16x8(x[u]), as_bf16x8(f[u][nb]), acc[nb]);
+            for (int nb = 0; nb < NB; ++nb) {
+                const bf16x8 bv = KM ? km_frag(u, nb) : __builtin_bit_cast(bf16x8, f[u][nb]);
+                acc[nb] = mfma16(__builtin_bit_cast(bf16x8, x[u]), bv, acc[nb]);
+            }
             tile(k + 32 * u, x[u]);
         }
     };
@@ -135,12 +208,19 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
     }
     if (c < nch) mult(c * CH, xv[0], fv[0]);  // an odd chunk count: the last one sits in set 0
     for (int64_t k = nch * CH; k < kq; k += 32) {
-        const uint4 xr = *reinterpret_cast<const uint4*>(ap + k);
+        const u32x4 xr = *reinterpret_cast<const u32x4*>(ap + k);
         tile(k, xr);
-        const bf16x8 av = as_bf16x8(xr);
+        const bf16x8 av = __builtin_bit_cast(bf16x8, xr);
+        if constexpr (KM) {
+            km_load(k, 32, fv[0]);
+            km_store(32, fv[0]);
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-            acc[nb] = mfma16(av, as_bf16x8(*reinterpret_cast<const uint4*>(wp + (int64_t)16 * nb * a.Kin + k)), acc[nb]);
+            for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16(av, km_frag(0, nb), acc[nb]);
+        } else {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                acc[nb] = mfma16(av, __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(wp + (int64_t)16 * nb * a.Kin + k)), acc[nb]);
+        }
     }
     // 16x16 accumulator: element e is row 4*grp + e, column row16
 #pragma unroll
@@ -569,7 +649,11 @@ int down_r(const DownArgs& a, hipStream_t s) {
     const int nw = a.Kin % 256 == 0 ? kDownWavesMax : 4;
     // the workgroups cover the splits' ldt rows and, when the tiled copy is written, its 32-row padding
     const int64_t rows = a.tiled && (a.T + 31) / 32 * 32 > a.ldt ? (a.T + 31) / 32 * 32 : a.ldt;
-    hipLaunchKernelGGL(lora_down_kernel<RD>, dim3((unsigned)((rows + 15) / 16)), dim3(64 * nw), 0, s, a);
+    const dim3 grid((unsigned)((rows + 15) / 16)), block(64 * nw);
+    if (a.w_kmajor)
+        hipLaunchKernelGGL((lora_down_kernel<RD, true>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((lora_down_kernel<RD, false>), grid, block, 0, s, a);
     return launch_status("lora_down_kernel");
 }
 

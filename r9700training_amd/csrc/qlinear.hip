@@ -55,7 +55,7 @@ bool decode_once(int64_t T) {
 
 // Workspace layout. Forward: Xt (X's tiled copy, act_tiles.h) | P [T, 2r] | Apad [rd, K] (when r
 // is not a multiple of 16) | Wt (the weight's decoded tiles, rt::wt_bytes, when decode_once).
-// Backward: dYt (dY's tiled copy) | Bt [rd, N] | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt]
+// Backward: dYt (dY's tiled copy) | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt]
 // | partA [chunks, r, K] | partB [chunks, r, N] (f32 partial sums of the factor gradients) | done
 // (the gradient launch's column-block counters, dA's then dB's) | Wt (as the forward's).
 // Wt is -1 where the layout has none.
@@ -80,7 +80,7 @@ FwdWs fwd_ws(const Shape& s, bool fused_only = false) {
     return w;
 }
 struct BwdWs {
-    int64_t dYt, Bt, At, P, PtA, PtB, partA, partB, done, Wt, total;
+    int64_t dYt, At, P, PtA, PtB, partA, partB, done, Wt, total;
 };
 void bwd_ws_wt(const Shape& s, BwdWs& w) {
     w.Wt = -1;
@@ -92,15 +92,13 @@ void bwd_ws_wt(const Shape& s, BwdWs& w) {
 BwdWs bwd_ws(const Shape& s) {
     BwdWs w{};
     w.dYt = 0;
-    w.Bt = w.dYt + align256(act_tile_bytes(s.T, s.N));
+    w.At = w.dYt + align256(act_tile_bytes(s.T, s.N));
     if (s.r == 0) {
-        w.total = w.Bt;
+        w.total = w.At;
         bwd_ws_wt(s, w);
         return w;
     }
-    const int rd = down_rank(s.r);
     const int64_t ldt = grad_ld(s.T);
-    w.At = w.Bt + align256((int64_t)rd * s.N * 2);
     w.P = w.At + align256(s.K * s.r * 2);
     w.PtA = w.P + align256(s.T * 2 * s.r * 2);
     w.PtB = w.PtA + align256(2 * s.r * ldt * 2);
@@ -320,12 +318,13 @@ int bwd_prep(const Shape& sh, const uint16_t* dY, const uint16_t* A, const uint1
     const BwdWs ws = bwd_ws(sh);
     uint16_t* dYt = reinterpret_cast<uint16_t*>(wsb + ws.dYt);
     if (sh.r == 0) return launch_act_tile(dY, sh.T, sh.N, dYt, s);
-    uint16_t* Bt = reinterpret_cast<uint16_t*>(wsb + ws.Bt);
-    uint16_t* At = reinterpret_cast<uint16_t*>(wsb + ws.At);
-    if (int e = launch_transpose2(B, Bt, sh.N, A, At, sh.K, sh.r, s)) return e;
     DownArgs a{};
     a.In = dY;
-    a.W = Bt;
+    a.W = B;
+    a.w_kmajor = 1;
+    a.tr_in = A;
+    a.tr_out = reinterpret_cast<uint16_t*>(wsb + ws.At);
+    a.tr_cols = sh.K;
     a.T = sh.T;
     a.Kin = sh.N;
     a.ldt = grad_ld(sh.T);
