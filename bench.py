@@ -4,15 +4,19 @@
 One step = one forward and one backward of the adapted linear on one batch of synthetic input:
   forward   t = X.A^T, Y = X.W^T + s.t.B^T                 (r97q_lora_fwd_prep, r97q_qlinear_fwd_base)
   backward  dt = s.dY.B, dA += dt^T.X, dB += s.dY^T.t,
-            dX = dY.W + dt.A                               (r97q_lora_bwd_prep, _grads, r97q_qlinear_dx_base)
+            dX = dY.W + dt.A                               (r97q_qlinear_lora_bwd: the down product, the
+                                                            factor gradients' chunk sums, the dX product
+                                                            that then adds those sums in)
 W is an IQR trunk-form weight (b5 trellis.mad, L 16, 256-row runs, f32 row scale + scale.col)
 quantized from W ~ N(0, 0.02) by this repo's quantizer; X, dY bf16 N(0,1); A, B bf16 N(0, 0.01).
 Default workload: C2, 4096 x 4096, T 4096, rank 16, alpha 32.
 
 Prints ONE JSON line (rank 0): the step's whole-job TFLOP/s over the timed steps (nothing else on
-the stream between them), the dominant kernel's roofline (HIP events around the fused kernels'
-launches, over a second run of as many steps: a timing event between two kernels costs several
-microseconds of GPU time, so the events stay out of the steps `value` is timed on), its HBM
+the stream between them), the dominant kernel's roofline (HIP events around the base products'
+launches -- the forward's in a second run of as many steps, the dX product's in as many backwards
+through the stand-alone stages, where its launch holds the product alone: a timing event between
+two kernels costs several microseconds of GPU time, so the events stay out of the steps `value` is
+timed on), its HBM
 traffic per launch from the
 committed FETCH_SIZE / WRITE_SIZE profile of the same sources (null when the sources changed since)
 and a CPU baseline (the reference's own host rows, oracle/_ref, on the box's host cores, over a
@@ -415,12 +419,8 @@ def c5_stack_bench(args):
         for i in reversed(range(len(weights))):
             N, K = C5_PROJ[i % 4]
             w = weights[i]
-            check(L.r97q_lora_bwd_prep(T, N, K, P(dY[N]), P(A[i]), P(B[i]), P(tt[i]), r, s, P(wsb), wsb.numel(), st),
-                  "bwd_prep")
-            check(L.r97q_lora_bwd_grads(T, N, K, P(X[K]), P(dY[N]), r, P(dA[i]), P(dB[i]), P(wsb), wsb.numel(), st),
-                  "grads")
-            check(L.r97q_qlinear_dx_base(C.byref(w.w), P(dY[N]), T, r, P(dX[K]), R97Q_F32, 0, P(wsb), wsb.numel(), st),
-                  "dx")
+            check(L.r97q_qlinear_lora_bwd(C.byref(w.w), P(X[K]), P(dY[N]), T, P(A[i]), P(B[i]), r, s, P(tt[i]),
+                                          P(dX[K]), R97Q_F32, 0, P(dA[i]), P(dB[i]), P(wsb), wsb.numel(), st), "bwd")
         opt.step(dA + dB, stream=stream, staged=True)
 
     steps, warmup = max(1, min(args.steps, 5)), max(1, min(args.warmup, 2))
@@ -499,22 +499,33 @@ def main():
     stream = torch.cuda.current_stream()
     st = _stream(stream)
     P = lambda x: _ptr(x)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
 
+    # The step: the forward's two stages, then the fused backward (r97q_qlinear_lora_bwd: the down
+    # product, dA's chunk sums, and the dX launch that also takes dB and adds dA's sums). With e,
+    # events around the forward's product and the whole backward.
     def step(e=None):
         check(L.r97q_lora_fwd_prep(T, N, K, P(inp["X"]), P(inp["A"]), r, s, P(t), P(wsf), wsf.numel(), st), "fwd_prep")
         if e: e[0].record(stream)
         check(L.r97q_qlinear_fwd_base(C.byref(w.w), P(inp["X"]), T, P(inp["B"]), r, P(Y), code, P(wsf),
                                       wsf.numel(), st), "fwd_base")
         if e: e[1].record(stream)
+        check(L.r97q_qlinear_lora_bwd(C.byref(w.w), P(inp["X"]), P(inp["dY"]), T, P(inp["A"]), P(inp["B"]), r, s,
+                                      P(t), P(dX), code, 0, P(dA), P(dB), P(wsb), wsb.numel(), st), "bwd")
+        if e: e[4].record(stream)
+
+    # The backward in its stages (the down product, both factor gradients in one launch, the dX
+    # product alone), with events around the dX product: its launch duration with no other work.
+    def staged_bwd(e):
+        e[5].record(stream)
         check(L.r97q_lora_bwd_prep(T, N, K, P(inp["dY"]), P(inp["A"]), P(inp["B"]), P(t), r, s, P(wsb),
                                    wsb.numel(), st), "bwd_prep")
         check(L.r97q_lora_bwd_grads(T, N, K, P(inp["X"]), P(inp["dY"]), r, P(dA), P(dB), P(wsb), wsb.numel(), st),
               "bwd_grads")
-        if e: e[2].record(stream)
+        e[2].record(stream)
         check(L.r97q_qlinear_dx_base(C.byref(w.w), P(inp["dY"]), T, r, P(dX), code, 0, P(wsb), wsb.numel(), st),
               "dx_base")
-        if e: e[3].record(stream)
+        e[3].record(stream)
 
     for _ in range(args.warmup):
         step()
@@ -525,14 +536,20 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_step = elapsed * 1e3 / args.steps
-    # the same steps again with events around the fused kernels, for their launch durations
+    # the same steps again with events around the forward's product and the backward, and the staged
+    # backward with events around the dX product, for their launch durations
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(ev[i])
     torch.cuda.synchronize()
     ms_step_ev = (time.perf_counter() - t0) * 1e3 / args.steps
+    for i in range(args.steps):
+        staged_bwd(ev[i])
+    torch.cuda.synchronize()
     fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    bwd_ms = sum(e[1].elapsed_time(e[4]) for e in ev) / args.steps
     dx_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / args.steps
+    staged_ms = sum(e[5].elapsed_time(e[3]) for e in ev) / args.steps
     # The whole LoRA step: the same steps, then the factors' AdamW on the card (f32 master weights,
     # the reference Optimiser's update) taking dA, dB as the step's staged gradients (the grad-stage
     # flush's bf16 rounding, the buffers cleared for the next step) and writing the bf16 copies the
@@ -598,8 +615,9 @@ def main():
         "lora_step": {"tokens_per_s": round(T / (ms_lora_step * 1e-3), 1), "ms": round(ms_lora_step, 4),
                       "what": "fwd+bwd + the staged dA/dB flushed into AdamW on A, B (device, f32 masters) + their bf16 copies"},
         "flops_per_step": total_flops,
-        "kernels_ms": {kf: round(fwd_ms, 4), kd: round(dx_ms, 4),
-                       "other": round(ms_step_ev - fwd_ms - dx_ms, 4), "ms_per_step_with_events": round(ms_step_ev, 4)},
+        "kernels_ms": {kf: round(fwd_ms, 4), kd + " (staged, alone)": round(dx_ms, 4),
+                       "bwd (r97q_qlinear_lora_bwd)": round(bwd_ms, 4), "bwd (staged entries)": round(staged_ms, 4),
+                       "other": round(ms_step_ev - fwd_ms - bwd_ms, 4), "ms_per_step_with_events": round(ms_step_ev, 4)},
         "roofline": {"bound": "mfma", "kernel": name, "achieved": round(achieved, 3),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic,

@@ -43,7 +43,8 @@ struct DownArgs {
 // [r, C] row-major or, `transposed`, [C, r]; Pt bf16 [2r, ldt]. The token chunks' partial sums go
 // to `part` (f32 [grad_chunks, r, C]) and are added into out in chunk order by the last chunk of
 // each column block to finish, counted on `done` (grad_blocks(C) counters, zero at the launch --
-// the launch before it clears them -- and zero again after it).
+// the launch before it clears them -- and zero again after it). With GradArgs::defer the launch
+// only writes the partial sums: a later launch adds them into out (the fused dX launch does).
 struct GradOne {
     const uint16_t* Pt;
     const uint16_t* V;
@@ -58,6 +59,7 @@ struct GradArgs {
     GradOne one[2];
     int64_t T, ldt;
     int64_t chunk;  // tokens a chunk: grad_chunk_rows(T, K, N), the size the partial buffers assume
+    int defer;      // write the chunks' partial sums only (no counters, no sum into out)
 };
 
 int down_rank(int r);          // r rounded up to a multiple of 16

@@ -417,7 +417,14 @@ __global__ __launch_bounds__(512) void lora_grads_kernel(GradArgs ga) {
     // Row j (< R) pairs with row R + j: the same lane and element VB/2 blocks on, or, for R = 8
     // (one block), the lane 32 on. The partial sums are stored at device scope (through to the
     // memory every XCD reads; no cache write-back or invalidation of the whole L2).
+    // Deferred (ga.defer): plain stores, which the launch's end makes visible to the next launch.
     float* part = g.part + (int64_t)blockIdx.y * R * C;
+    auto put = [&](float* p, float v) {
+        if (ga.defer)
+            *p = v;
+        else
+            device_store(p, v);
+    };
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
         const int64_t c = c0 + 32 * wave + 16 * cb + i16;
@@ -427,15 +434,16 @@ __global__ __launch_bounds__(512) void lora_grads_kernel(GradArgs ga) {
 #pragma unroll
                 for (int vb = 0; vb < VB / 2; ++vb) {
                     const int j = 16 * vb + 4 * grp + e;
-                    if (c < C) device_store(part + (int64_t)j * C + c, g.scale * (acc[vb][cb][e] + acc[vb + VB / 2][cb][e]));
+                    if (c < C) put(part + (int64_t)j * C + c, g.scale * (acc[vb][cb][e] + acc[vb + VB / 2][cb][e]));
                 }
             } else {
                 const float other = __shfl_xor(acc[0][cb][e], 32);
                 const int j = 4 * grp + e;
-                if (grp < 2 && c < C) device_store(part + (int64_t)j * C + c, g.scale * (acc[0][cb][e] + other));
+                if (grp < 2 && c < C) put(part + (int64_t)j * C + c, g.scale * (acc[0][cb][e] + other));
             }
         }
     }
+    if (ga.defer) return;
     // every store of the workgroup acknowledged, then the chunk counted done; the last of the
     // column block's chunks reads the others' sums at device scope
     __builtin_amdgcn_s_waitcnt(0);

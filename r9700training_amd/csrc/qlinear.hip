@@ -8,7 +8,9 @@
 //
 // Kernels: the fused decode + MFMA base products (qlinear_rt.hip, fed the token operand from
 // its tiled copy in the workspace) carry the adapter's up-projection in their epilogue; the
-// adapter's down products, factor gradients and the token operand's tiled copy are lora.hip's.
+// adapter's down products, factor gradients and the token operand's tiled copy are lora.hip's; in
+// the fused backward the gradient launch leaves its chunk sums for the dX launch to add (the
+// stand-alone gradient entry adds them in its own launch).
 // The coded trunk's dX (the activation's group scale in the epilogue) and the vocabulary head run
 // the LDS-staged kernels of qlinear_fused.hip on the row-major operand.
 #include <hip/hip_runtime.h>
@@ -57,7 +59,7 @@ bool decode_once(int64_t T) {
 // is not a multiple of 16) | Wt (the weight's decoded tiles, rt::wt_bytes, when decode_once).
 // Backward: dYt (dY's tiled copy) | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt]
 // | partA [chunks, r, K] | partB [chunks, r, N] (f32 partial sums of the factor gradients) | done
-// (the gradient launch's column-block counters, dA's then dB's) | Wt (as the forward's).
+// (bwd_counters) | Wt (as the forward's).
 // Wt is -1 where the layout has none.
 struct FwdWs {
     int64_t Xt, P, Apad, Wt, total;
@@ -82,6 +84,9 @@ FwdWs fwd_ws(const Shape& s, bool fused_only = false) {
 struct BwdWs {
     int64_t dYt, At, P, PtA, PtB, partA, partB, done, Wt, total;
 };
+// the backward's counters, zeroed by its down product: the gradient launch's column blocks (dA's,
+// then dB's)
+int64_t bwd_counters(const Shape& s) { return grad_blocks(s.K) + grad_blocks(s.N); }
 void bwd_ws_wt(const Shape& s, BwdWs& w) {
     w.Wt = -1;
     if (decode_once(s.T)) {
@@ -102,11 +107,13 @@ BwdWs bwd_ws(const Shape& s) {
     w.P = w.At + align256(s.K * s.r * 2);
     w.PtA = w.P + align256(s.T * 2 * s.r * 2);
     w.PtB = w.PtA + align256(2 * s.r * ldt * 2);
-    const int64_t chunks = grad_chunks(s.T, s.K, s.N);
+    // the chunk partials of either factor's gradient: as many as its launch alone takes (the most)
+    const int64_t chunksA = grad_chunks(s.T, s.K, 0);
+    const int64_t chunksB = grad_chunks(s.T, 0, s.N);
     w.partA = w.PtB + align256(2 * s.r * ldt * 2);
-    w.partB = w.partA + align256(chunks * s.r * s.K * 4);
-    w.done = w.partB + align256(chunks * s.r * s.N * 4);
-    w.total = w.done + align256((grad_blocks(s.K) + grad_blocks(s.N)) * 4);
+    w.partB = w.partA + align256(chunksA * s.r * s.K * 4);
+    w.done = w.partB + align256(chunksB * s.r * s.N * 4);
+    w.total = w.done + align256(bwd_counters(s) * 4);
     bwd_ws_wt(s, w);
     return w;
 }
@@ -260,7 +267,8 @@ int fwd_prep(const Shape& sh, const uint16_t* X, const uint16_t* A, float scale,
 // (rt::wt_bytes of workspace) the weight decoded once into it, then the product over its tiles;
 // without, the fused kernel decoding in its main loop
 int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act, const uint16_t* P,
-            const uint16_t* Q, void* out, int32_t out_dtype, int32_t accumulate, uint8_t* wt, hipStream_t s) {
+            const uint16_t* Q, void* out, int32_t out_dtype, int32_t accumulate, uint8_t* wt, hipStream_t s,
+            const rt::Params::Sums* sums = nullptr) {
     rt::Params p{};
     p.act = act;
     p.T = sh.T;
@@ -280,6 +288,10 @@ int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act,
     p.mtiles = (int)((sh.T + rt::kBM - 1) / rt::kBM);
     p.otiles = (int)((fwd ? sh.N : sh.K) / rt::kBN);
     p.wt = wt;
+    if (sums && !fwd) {
+        p.sums[0] = sums[0];
+        p.sums[1] = sums[1];
+    }
     if (wt) {
         switch (w->bits) {
             case 3: rt::launch_predecode<3>(p, fwd, wt, s); break;
@@ -335,7 +347,7 @@ int bwd_prep(const Shape& sh, const uint16_t* dY, const uint16_t* A, const uint1
     a.Pt = reinterpret_cast<uint16_t*>(wsb + ws.PtA);
     a.tiled = dYt;
     a.zero = reinterpret_cast<int*>(wsb + ws.done);
-    a.nzero = (int)(grad_blocks(sh.K) + grad_blocks(sh.N));
+    a.nzero = (int)bwd_counters(sh);
     if (t) {
         a.U2 = t;
         a.s2 = scale;
@@ -344,14 +356,22 @@ int bwd_prep(const Shape& sh, const uint16_t* dY, const uint16_t* A, const uint1
     return launch_lora_down(a, s);
 }
 
-// dA[j][k] += sum_m dt[m][j] X[m][k];  dB[n][j] += s . sum_m dY[m][n] t[m][j]
+// the token chunks of the gradient launch for the factor gradients asked for
+int64_t grad_launch_chunks(const Shape& sh, bool dA, bool dB) {
+    const int64_t chunk = grad_chunk_rows(sh.T, dA ? sh.K : 0, dB ? sh.N : 0);
+    return (grad_ld(sh.T) + chunk - 1) / chunk;
+}
+
+// dA[j][k] += sum_m dt[m][j] X[m][k];  dB[n][j] += s . sum_m dY[m][n] t[m][j]. With `defer` the
+// launch leaves its chunk sums in partA / partB for the dX launch to add (dx_base's dA, dB).
 int bwd_grads(const Shape& sh, const uint16_t* X, const uint16_t* dY, float* dA, float* dB, uint8_t* wsb,
-              hipStream_t s) {
+              hipStream_t s, bool defer = false) {
     const BwdWs ws = bwd_ws(sh);
     GradArgs g{};
     g.T = sh.T;
     g.ldt = grad_ld(sh.T);
-    g.chunk = grad_chunk_rows(sh.T, sh.K, sh.N);
+    g.chunk = grad_chunk_rows(sh.T, dA ? sh.K : 0, dB ? sh.N : 0);
+    g.defer = defer;
     int nz = 0;
     int* done = reinterpret_cast<int*>(wsb + ws.done);
     if (dA)
@@ -364,12 +384,21 @@ int bwd_grads(const Shape& sh, const uint16_t* X, const uint16_t* dY, float* dA,
     return launch_lora_grads(sh.r, g, nz, s);
 }
 
+// dX; with dA / dB (rank > 0, after a deferred bwd_grads for the same factors) the same launch
+// then adds the gradient launch's chunk sums into them
 int dx_base(const R97qWeight* w, const Shape& sh, void* dX, int32_t dx_dtype, int32_t accumulate, uint8_t* wsb,
-            hipStream_t s) {
+            hipStream_t s, float* dA = nullptr, float* dB = nullptr) {
     const BwdWs ws = bwd_ws(sh);
+    rt::Params::Sums sums[2] = {};
+    if (sh.r > 0 && (dA || dB)) {
+        const int chunks = (int)grad_launch_chunks(sh, dA != nullptr, dB != nullptr);
+        if (dA) sums[0] = {reinterpret_cast<const float*>(wsb + ws.partA), sh.K, chunks, 0, dA};
+        if (dB) sums[1] = {reinterpret_cast<const float*>(wsb + ws.partB), sh.N, chunks, 1, dB};
+    }
     return rt_base(w, false, sh, reinterpret_cast<const uint16_t*>(wsb + ws.dYt),
                    reinterpret_cast<const uint16_t*>(wsb + ws.P), reinterpret_cast<const uint16_t*>(wsb + ws.At), dX,
-                   dx_dtype, accumulate, ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s);
+                   dx_dtype, accumulate, ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s,
+                   sums[0].part || sums[1].part ? sums : nullptr);
 }
 
 // the LDS-staged dX kernel over row-major dY with the coded trunk's activation scale in its
@@ -596,9 +625,11 @@ int r97q_qlinear_lora_bwd(const R97qWeight* w, const uint16_t* X, const uint16_t
     uint8_t* wsb = static_cast<uint8_t*>(workspace);
     const hipStream_t s = (hipStream_t)stream;
     if (int e = bwd_prep(sh, dY, A, B, t, scale, wsb, s)) return e;
+    // the factor gradients' chunk sums by the gradient launch, added into dA and dB by the dX
+    // launch (spread over its workgroups, in chunk order)
     if (rank > 0)
-        if (int e = bwd_grads(sh, X, dY, dA, dB, wsb, s)) return e;
-    return dx_base(w, sh, dX, dx_dtype, dx_accumulate, wsb, s);
+        if (int e = bwd_grads(sh, X, dY, dA, dB, wsb, s, true)) return e;
+    return dx_base(w, sh, dX, dx_dtype, dx_accumulate, wsb, s, rank > 0 ? dA : nullptr, rank > 0 ? dB : nullptr);
 }
 
 int r97q_gemm_nt_q_dx(const R97qWeight* w, const uint16_t* dY, int64_t T, const float* a_scale, void* dA,

@@ -138,6 +138,8 @@ __device__ __forceinline__ void wave_main(const Params& p, uint8_t* l0, uint8_t*
     w.run(m0, p.T, l0, l1, acc);
     if (p.rank > 0) adapter<G::kMI>(p.P, p.Q, p.rank, m0, o0, p.T, lane, acc);
     store<G::kMI>(acc, p.out, FWD ? p.N : p.K, m0, o0, p.T, lane, p.out_f32, FWD ? 0 : p.accumulate);
+    if constexpr (!FWD)
+        if (p.sums[0].part || p.sums[1].part) sum_chunks<kPdWaves>(p);
 }
 
 template <bool FWD>

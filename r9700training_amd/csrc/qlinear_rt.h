@@ -30,6 +30,15 @@ struct Params {
     int accumulate;            // dX only: add into `out`
     int mtiles, otiles;
     const uint8_t* wt;         // the weight decoded once a call (launch_predecode), for launch_pd
+    // dX only: the factor gradients' deferred chunk sums of the gradient launch before this one,
+    // added into their outputs in chunk order, the elements spread over the launch's workgroups
+    struct Sums {
+        const float* part;     // [chunks, r, cols] f32; null: none
+        int64_t cols;
+        int chunks;
+        int transposed;        // out is [cols, r] (dB) instead of [r, cols] (dA)
+        float* out;
+    } sums[2];
 };
 
 template <int BITS>

@@ -379,6 +379,8 @@ __device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t*
     w.run(p.act, t0, t1, acc);
     if (p.rank > 0) adapter<G::kMI>(p.P, p.Q, p.rank, w.m0, w.o0, p.T, lane, acc);
     store<G::kMI>(acc, p.out, FWD ? p.N : p.K, w.m0, w.o0, p.T, lane, p.out_f32, FWD ? 0 : p.accumulate);
+    if constexpr (!FWD)
+        if (p.sums[0].part || p.sums[1].part) sum_chunks<WAVES>(p);
 }
 
 template <bool FWD, int WAVES>

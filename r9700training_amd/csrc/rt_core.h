@@ -180,5 +180,39 @@ __device__ __forceinline__ void store(const f32x16 (&acc)[MI][kNI], void* out, i
         }
 }
 
+// ---------------------------------------------------------------- the factor gradients' sums
+// out (+)= the deferred chunk sums of the gradient launch before this one, for dA and dB:
+// workgroup b of the launch takes elements [b per, (b+1) per) of each; an element's chunks are
+// added in chunk order (the order the gradient launch's own last chunk adds them in), so the
+// factor gradients are the same bits either way. Every wave calls it.
+template <int W>
+__device__ __forceinline__ void sum_chunks(const Params& p) {
+    const int64_t nwg = gridDim.x;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const Params::Sums& g = p.sums[q];
+        if (!g.part) continue;
+        const int64_t n = (int64_t)p.rank * g.cols;
+        const int64_t per = (n + nwg - 1) / nwg;
+        const int64_t e0 = (int64_t)blockIdx.x * per;
+        const int64_t e1 = e0 + per < n ? e0 + per : n;
+        for (int64_t e = e0 + threadIdx.x; e < e1; e += 64 * W) {
+            const float* src = g.part + e;
+            float sum = 0.0f;
+            int ch = 0;
+            for (; ch + 8 <= g.chunks; ch += 8) {
+                float x[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) x[u] = src[(int64_t)(ch + u) * n];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) sum += x[u];
+            }
+            for (; ch < g.chunks; ++ch) sum += src[(int64_t)ch * n];
+            const int64_t j = e / g.cols, c = e % g.cols;
+            g.out[g.transposed ? c * p.rank + j : e] += sum;
+        }
+    }
+}
+
 }  // namespace rt
 }  // namespace r97q

@@ -160,6 +160,41 @@ def test_grads_are_deterministic():
         assert torch.equal(dX, runs[0][0]) and torch.equal(dA, runs[0][1]) and torch.equal(dB, runs[0][2])
 
 
+@pytest.mark.parametrize("T,N,K,r", [(1100, 384, 512, 16), (700, 256, 640, 64), (300, 512, 256, 8)])
+def test_fused_backward_equals_stages(T, N, K, r):
+    """r97q_qlinear_lora_bwd hands the factor gradients' chunk sums to its dX launch, which adds them
+    in chunk order; the stand-alone stages (bwd_prep, bwd_grads adding them in its own launch,
+    dx_base) give the same dX, dA and dB bit for bit."""
+    import ctypes as C
+    from r9700training_amd import R97Q_F32, _ptr, _stream, check, lib
+    from r9700training_amd.qlinear import bwd_workspace, qlinear_lora_bwd, qlinear_lora_fwd
+
+    print(f"case fused vs staged T={T} N={N} K={K} r={r}", flush=True)
+    rng = np.random.default_rng(T + r)
+    keep = []
+    w = prepared(weight_planes(N, K, seed=T), keep)
+    X = bf16_tensor(rng.standard_normal((T, K)))
+    dY = bf16_tensor(rng.standard_normal((T, N)))
+    A = bf16_tensor(0.01 * rng.standard_normal((r, K)))
+    B = bf16_tensor(0.01 * rng.standard_normal((N, r)))
+    _, t = qlinear_lora_fwd(w, X, A, B, 2.0)
+    dA0 = torch.randn((r, K), dtype=torch.float32, device="cuda")  # added into, both ways
+    dB0 = torch.randn((N, r), dtype=torch.float32, device="cuda")
+    dX1, dA1, dB1 = qlinear_lora_bwd(w, X, dY, A, B, t, 2.0, dx_dtype=torch.float32, dA=dA0.clone(), dB=dB0.clone())
+    L = lib()
+    ws = bwd_workspace(T, N, K, r)
+    st = _stream(None)
+    dX2 = torch.empty((T, K), dtype=torch.float32, device="cuda")
+    dA2, dB2 = dA0.clone(), dB0.clone()
+    P = _ptr
+    check(L.r97q_lora_bwd_prep(T, N, K, P(dY), P(A), P(B), P(t), r, 2.0, P(ws), ws.numel(), st), "bwd_prep")
+    check(L.r97q_lora_bwd_grads(T, N, K, P(X), P(dY), r, P(dA2), P(dB2), P(ws), ws.numel(), st), "bwd_grads")
+    check(L.r97q_qlinear_dx_base(C.byref(w.w), P(dY), T, r, P(dX2), R97Q_F32, 0, P(ws), ws.numel(), st), "dx_base")
+    torch.cuda.synchronize()
+    assert torch.equal(dX1, dX2) and torch.equal(dA1, dA2) and torch.equal(dB1, dB2)
+    assert not torch.equal(dA1, dA0) and not torch.equal(dB1, dB0)
+
+
 def test_refusals():
     from r9700training_amd import R97qError
     from r9700training_amd.qlinear import QWeight, fwd_workspace, qlinear_lora_fwd
