@@ -48,7 +48,7 @@ int batch_of(int64_t rows, int64_t K) {
 }
 
 struct VocabWs {
-    int64_t codes, scale, gather, part, cf, total;
+    int64_t codes, scale, gather, part, part_lo, cf, total;
 };
 
 VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
@@ -69,6 +69,7 @@ VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
     w.scale = take(Z * nkb * Np * 2);
     w.gather = take(Z * rows * Np * 2);
     w.part = take(Z * rows * K * 4);
+    w.part_lo = take(Z * rows * K * 4);
     w.cf = take(nkb * 4);
     w.total = off;
     return w;
@@ -112,13 +113,14 @@ __global__ __launch_bounds__(256) void vocab_gather_kernel(const uint16_t* __res
     }
 }
 
-// d_x[i] += part[0][i] + part[1][i] + ... (the ranges in order)
-__global__ __launch_bounds__(256) void vocab_reduce_kernel(float* __restrict__ d_x, const float* __restrict__ part,
-                                                           int64_t n, int Z) {
+// d_x[i] += (hi[0][i] + lo[0][i]) + (hi[1][i] + lo[1][i]) + ... (the ranges in order; a range's
+// product over the weights' high halves plus its product over their low halves)
+__global__ __launch_bounds__(256) void vocab_reduce_kernel(float* __restrict__ d_x, const float* __restrict__ hi,
+                                                           const float* __restrict__ lo, int64_t n, int Z) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     float v = d_x[i];
-    for (int z = 0; z < Z; ++z) v += part[z * n + i];
+    for (int z = 0; z < Z; ++z) v += hi[z * n + i] + lo[z * n + i];
     d_x[i] = v;
 }
 
@@ -207,6 +209,7 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
     uint16_t* scale_t = reinterpret_cast<uint16_t*>(wsb + ws.scale);
     uint16_t* gathered = reinterpret_cast<uint16_t*>(wsb + ws.gather);
     float* part = reinterpret_cast<float*>(wsb + ws.part);
+    float* part_lo = reinterpret_cast<float*>(wsb + ws.part_lo);
     float* cf = reinterpret_cast<float*>(wsb + ws.cf);
     const hipStream_t s = (hipStream_t)stream;
     const int64_t K = plan->n_embd, nkb = K / 128;
@@ -278,15 +281,16 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
             p.z_scale = nkb * Np;
             p.z_out = rows * K;
             // each weight as the exact sum of two bf16 values: the product over the high halves,
-            // then over the low halves added in (f32 products of bf16 values are exact)
+            // then over the low halves into partials of their own (f32 products of bf16 values are
+            // exact); the reduction adds each range's two
             launch_dx<R97Q_CODES8>(p, s);
             if (int e = launch_status("qlinear_dx_kernel (vocab head)")) return e;
             p.lo = 1;
-            p.accumulate = 1;
+            p.dX = part_lo;
             launch_dx<R97Q_CODES8>(p, s);
             if (int e = launch_status("qlinear_dx_kernel (vocab head, low halves)")) return e;
-            hipLaunchKernelGGL(vocab_reduce_kernel, dim3(blocks(rows * K, 256)), dim3(256), 0, s, d_x, part, rows * K,
-                               Z);
+            hipLaunchKernelGGL(vocab_reduce_kernel, dim3(blocks(rows * K, 256)), dim3(256), 0, s, d_x, part, part_lo,
+                               rows * K, Z);
             if (int e = launch_status("vocab_reduce_kernel")) return e;
         }
     }
