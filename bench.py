@@ -87,10 +87,13 @@ def parse():
     ap.add_argument("--weight-form", default="trellis", choices=["trellis", "codes8"],
                     help="the prepared weight the kernels read: the trellis stream (decoded inside the "
                          "kernels), or the same weight in the int8-code form")
-    ap.add_argument("--workload", default="qlinear", choices=["qlinear", "vocab_head", "c5_stack", "coded_fwd"],
+    ap.add_argument("--workload", default="qlinear",
+                    choices=["qlinear", "vocab_head", "c3_block", "c4_attn", "c5_stack", "coded_fwd"],
                     help="qlinear: the C2 fwd+bwd step (the headline); vocab_head: the vocabulary head's "
                          "transposed product at a 248320-row head, n_embd 2048, --vocab-rows token rows; "
-                         "c5_stack: one whole LoRA step of the 24-layer stack (T=32768, rank 16 on every projection); "
+                         "c3_block / c4_attn / c5_stack: one whole LoRA step of BASELINE's MLP block (T=8192, "
+                         "rank 32), attention projections (T=16384, rank 64) or 24-layer stack (T=32768, rank 16 "
+                         "on every projection); "
                          "coded_fwd: gemm_nt_q's twin (int8 codes x the int8-code weight) at C2's square layer")
     ap.add_argument("--decode", default="auto", choices=sorted(DECODE_MODES),
                     help="how the base products meet the weight (r97q_set_decode_once): fused (each tile "
@@ -308,6 +311,23 @@ def vocab_head_bench(args):
 # 6144->2048; 24 layers; LoRA rank 16 alpha 32 on every projection; T = 32768 tokens
 C5_PROJ = [(8192, 2048), (2048, 4096), (6144, 2048), (2048, 6144)]  # (N, K)
 C5_LAYERS, C5_T, C5_R, C5_ALPHA = 24, 32768, 16, 32.0
+# BASELINE's configs of several projections, each one whole LoRA step:
+# name: (projections (N, K) of a layer, layers, T, rank, alpha, metric, description)
+STACKS = {
+    "c3_block": ([(12288, 4096), (12288, 4096), (4096, 12288)], 1, 8192, 32, 64.0,
+                 "C3 LoRA-step tokens/s (one MLP block: gate, up, down; fwd + bwd + AdamW on the adapters)",
+                 "C3: MLP block, hidden 4096, intermediate 12288: gate and up (4096->12288), down (12288->4096), "
+                 "b5 trellis.mad, LoRA r32 alpha 64 on all three, T=8192, Y/dX f32 (the SiLU gate between "
+                 "them is not this path)"),
+    "c4_attn": ([(8192, 2048), (2048, 4096)], 1, 16384, 64, 128.0,
+                "C4 LoRA-step tokens/s (attention projections: qkv+gate in, out; fwd + bwd + AdamW on the adapters)",
+                "C4: attention projections, hidden 2048: qkv+gate 2048->8192, out 4096->2048, b5 trellis.mad, "
+                "LoRA r64 alpha 128 on both, T=16384, Y/dX f32"),
+    "c5_stack": (C5_PROJ, C5_LAYERS, C5_T, C5_R, C5_ALPHA,
+                 "C5 LoRA-step tokens/s (24-layer stack, fwd + bwd + AdamW on the adapters)",
+                 "C5: 24 layers x (2048->8192, 4096->2048, 2048->6144, 6144->2048) b5 trellis.mad, "
+                 "LoRA r16 alpha 32 on every projection, T=32768, Y/dX f32"),
+}
 
 
 def coded_fwd_bench(args):
@@ -356,10 +376,10 @@ def coded_fwd_bench(args):
     }), flush=True)
 
 
-def c5_stack_bench(args):
-    """One complete LoRA step of the 24-layer stack on one GPU: the forward of every projection,
-    layer by layer, then the backward in reverse (dX, dA, dB, the adapters' gradients staged), then
-    AdamW on all 192 factors with their bf16 copies refreshed. Synthetic: the 96 weights are random
+def stack_bench(args):
+    """One complete LoRA step of a STACKS workload (C5: the 24-layer stack) on one GPU: the forward
+    of every projection, layer by layer, then the backward in reverse (dX, dA, dB, the adapters'
+    gradients staged), then AdamW on every factor with its bf16 copy refreshed. Synthetic: the weights are random
     b5 trellis.mad codes (any bytes are valid codes) with an f32 row scale and scale.col, prepared
     on the card; each projection's X and dY are shared random bf16 buffers of its shape (the
     projections between them -- norms, attention, the gated product -- are not this path)."""
@@ -372,16 +392,17 @@ def c5_stack_bench(args):
     from r9700training_amd.optim import DeviceAdamW, config
     from r9700training_amd.qlinear import QWeight, bwd_workspace, device_desc, fwd_workspace
 
+    proj, layers, T, r, alpha, metric, what = STACKS[args.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    T, r, s = C5_T, C5_R, C5_ALPHA / C5_R
+    s = alpha / r
     L = lib()
     L.r97q_set_decode_once(DECODE_MODES[args.decode])
     g = torch.Generator(device="cuda").manual_seed(args.seed)
     rng = np.random.default_rng(args.seed)
     weights, keep = [], []
-    for _layer in range(C5_LAYERS):
-        for N, K in C5_PROJ:
+    for _layer in range(layers):
+        for N, K in proj:
             codes = torch.randint(0, 256, (N, K * 5 // 8), dtype=torch.uint8, device=dev, generator=g)
             scale = torch.from_numpy((0.0005 + 0.01 * rng.random(N)).astype(np.float32).view(np.uint8)).to(dev)
             cf = torch.from_numpy((0.5 + rng.random(K // 128)).astype(np.float32)).to(dev)
@@ -390,19 +411,19 @@ def c5_stack_bench(args):
                 mad_b=0x9E3779B9, codes_row_bytes=K * 5 // 8, scale_dtype=0, scale_block_cols=0, scale_row_bytes=4))
             weights.append(QWeight(d, scale_col=cf))
             keep += [codes, scale, cf]
-    X = {K: torch.randn((T, K), dtype=torch.bfloat16, device=dev, generator=g) for _, K in C5_PROJ}
-    dY = {N: torch.randn((T, N), dtype=torch.bfloat16, device=dev, generator=g) for N, _ in C5_PROJ}
-    Y = {N: torch.empty((T, N), dtype=torch.float32, device=dev) for N, _ in C5_PROJ}
-    dX = {K: torch.empty((T, K), dtype=torch.float32, device=dev) for _, K in C5_PROJ}
+    X = {K: torch.randn((T, K), dtype=torch.bfloat16, device=dev, generator=g) for _, K in proj}
+    dY = {N: torch.randn((T, N), dtype=torch.bfloat16, device=dev, generator=g) for N, _ in proj}
+    Y = {N: torch.empty((T, N), dtype=torch.float32, device=dev) for N, _ in proj}
+    dX = {K: torch.empty((T, K), dtype=torch.float32, device=dev) for _, K in proj}
     A = [(0.01 * torch.randn((r, K), generator=g, device=dev)).to(torch.bfloat16)
-         for _ in range(C5_LAYERS) for _, K in C5_PROJ]
+         for _ in range(layers) for _, K in proj]
     B = [(0.01 * torch.randn((N, r), generator=g, device=dev)).to(torch.bfloat16)
-         for _ in range(C5_LAYERS) for N, _ in C5_PROJ]
+         for _ in range(layers) for N, _ in proj]
     tt = [torch.empty((T, r), dtype=torch.float32, device=dev) for _ in A]
     dA = [torch.zeros((r, a.shape[1]), dtype=torch.float32, device=dev) for a in A]
     dB = [torch.zeros((b.shape[0], r), dtype=torch.float32, device=dev) for b in B]
-    wsf = max((fwd_workspace(T, N, K, r, dev) for N, K in C5_PROJ), key=lambda x: x.numel())
-    wsb = max((bwd_workspace(T, N, K, r, dev) for N, K in C5_PROJ), key=lambda x: x.numel())
+    wsf = max((fwd_workspace(T, N, K, r, dev) for N, K in proj), key=lambda x: x.numel())
+    wsb = max((bwd_workspace(T, N, K, r, dev) for N, K in proj), key=lambda x: x.numel())
     masters = [a.float().contiguous() for a in A] + [b.float().contiguous() for b in B]
     copies = A + B
     opt = DeviceAdamW(masters, config(lr=1e-4), bf16_out=copies)
@@ -412,12 +433,12 @@ def c5_stack_bench(args):
 
     def lora_step():
         for i, w in enumerate(weights):
-            N, K = C5_PROJ[i % 4]
+            N, K = proj[i % len(proj)]
             check(L.r97q_lora_fwd_prep(T, N, K, P(X[K]), P(A[i]), r, s, P(tt[i]), P(wsf), wsf.numel(), st), "prep")
             check(L.r97q_qlinear_fwd_base(C.byref(w.w), P(X[K]), T, P(B[i]), r, P(Y[N]), R97Q_F32, P(wsf),
                                           wsf.numel(), st), "fwd")
         for i in reversed(range(len(weights))):
-            N, K = C5_PROJ[i % 4]
+            N, K = proj[i % len(proj)]
             w = weights[i]
             check(L.r97q_qlinear_lora_bwd(C.byref(w.w), P(X[K]), P(dY[N]), T, P(A[i]), P(B[i]), r, s, P(tt[i]),
                                           P(dX[K]), R97Q_F32, 0, P(dA[i]), P(dB[i]), P(wsb), wsb.numel(), st), "bwd")
@@ -432,16 +453,14 @@ def c5_stack_bench(args):
         lora_step()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
-    total = C5_LAYERS * sum(flops(T, N, K, r) for N, K in C5_PROJ)
+    total = layers * sum(flops(T, N, K, r) for N, K in proj)
     tf = total / (ms * 1e-3) / 1e12
     print(json.dumps({
-        "metric": "C5 LoRA-step tokens/s (24-layer stack, fwd + bwd + AdamW on the adapters)",
+        "metric": metric,
         "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
         "tflops": round(tf, 3),
-        "config": {"workload": "C5: 24 layers x (2048->8192, 4096->2048, 2048->6144, 6144->2048) b5 trellis.mad, "
-                               "LoRA r16 alpha 32 on every projection, T=32768, Y/dX f32",
-                   "T": T, "layers": C5_LAYERS, "rank": r, "decode": "once" if decodes_once(args.decode, T) else "fused"},
+        "config": {"workload": what, "T": T, "layers": layers, "rank": r, "decode": "once" if decodes_once(args.decode, T) else "fused"},
         "roofline": {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
         "memory_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 2),
@@ -471,8 +490,8 @@ def main():
 
     if args.workload == "vocab_head":
         return vocab_head_bench(args)
-    if args.workload == "c5_stack":
-        return c5_stack_bench(args)
+    if args.workload in STACKS:
+        return stack_bench(args)
     if args.workload == "coded_fwd":
         return coded_fwd_bench(args)
 

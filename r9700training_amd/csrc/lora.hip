@@ -7,7 +7,8 @@
 // [hi | lo] pair of bf16 (hi = bf16(v), lo = bf16(v - hi)) wherever they enter an MFMA, so the
 // adapter path keeps ~16 significant bits.
 //
-//   lora_down_kernel   one workgroup = 16 token rows x the whole reduction, its 8 (or 4) waves an
+//   lora_down_kernel   one workgroup = 16 token rows (32 at ranks 32 and 64) x the whole
+//                      reduction, its 8 (or 4) waves an
 //                      eighth (quarter) each (v_mfma_f32_16x16x32_bf16), reduced through LDS in a
 //                      fixed order; it writes the f32 result and its [hi | lo] splits for the
 //                      fused kernels' epilogues (row-major) and for the gradient kernel
@@ -69,8 +70,10 @@ __device__ __forceinline__ bf16x8 tr_pair(s16x4 lo4, s16x4 hi4) {
 }
 
 // ---------------------------------------------------------------- down
-// One workgroup = 16 token rows; its nw waves (8, or 4 when Kin is not a multiple of 256) each
-// reduce a contiguous nw-th of Kin, then the partial sums are added in wave order through LDS.
+// One workgroup = 16 token rows (two blocks of 16 at ranks 32 and 64); its nw waves (8, or 4 when
+// Kin is not a multiple of 256) each reduce a contiguous nw-th of Kin, then the partial sums are
+// added in wave order through LDS. A 16-row block's products are the same whatever the workgroup's
+// other block, so the results do not depend on the blocking.
 //
 // KM (the factor k-major, W [Kin, r] row-major: the backward's B as the caller holds it): the MFMA's
 // B operand needs 8 consecutive k of one factor column, which that layout keeps r apart. Each wave
@@ -88,14 +91,20 @@ struct DownStage {
     static constexpr int BYTES = CH * S;               // a wave's stage
 };
 
+// token blocks of 16 rows a workgroup: two at the larger ranks, so each factor value a wave loads
+// feeds 32 token rows (at rank 64 the factor is four times the token rows' bytes a chunk)
+template <int RD>
+constexpr int down_blocks() { return RD >= 32 ? 2 : 1; }
+
 template <int RD, bool KM>
 __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
-    __shared__ float red[kDownWavesMax][16][RD];
+    constexpr int MB = down_blocks<RD>();
+    __shared__ float red[kDownWavesMax][16 * MB][RD];
     __shared__ __attribute__((aligned(16))) uint8_t stage_lds[KM ? kDownWavesMax * DownStage<RD>::BYTES : 16];
     const int nw = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row16 = lane & 15, grp = lane >> 4;
-    const int64_t m0 = (int64_t)blockIdx.x * 16;
+    const int64_t m0 = (int64_t)blockIdx.x * 16 * MB;
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i < a.nzero; i += blockDim.x) a.zero[i] = 0;
     if (a.tr_out) {
@@ -108,10 +117,14 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
             a.tr_out[c * a.r + j] = a.tr_in[(int64_t)j * a.tr_cols + c];
         }
     }
-    int64_t row = m0 + row16;
-    if (row > a.T - 1) row = a.T - 1;
     const int64_t kq = a.Kin / nw;  // a multiple of 32
-    const uint16_t* ap = a.In + row * a.Kin + wave * kq + 8 * grp;
+    const uint16_t* ap[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+        int64_t row = m0 + 16 * b + row16;
+        if (row > a.T - 1) row = a.T - 1;
+        ap[b] = a.In + row * a.Kin + wave * kq + 8 * grp;
+    }
     const uint16_t* wp = a.W + (int64_t)row16 * a.Kin + wave * kq + 8 * grp;
     constexpr int NB = RD / 16;
     // KM: the wave's stage, its factor rows from wave * kq on, and the pieces of a full chunk
@@ -124,9 +137,11 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
         if (a.r < RD)
             for (int i = lane; i < St::BYTES / 16; i += 64) reinterpret_cast<u32x4*>(stage)[i] = u32x4{0u, 0u, 0u, 0u};
     }
-    f32x4 acc[NB];
+    f32x4 acc[MB][NB];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = (f32x4){};
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[b][nb] = (f32x4){};
     // Chunks of U 32-deep slices (U loads of the token rows and U*NB of the factor a lane, 32
     // registers a set), two register sets: the loads of chunk c+1 are in flight while chunk c
     // multiplies, so a wave's whole share (two chunks at the common sizes) is requested at once
@@ -136,14 +151,13 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
     const int64_t nch = kq / CH;
     // the tiled copy: every value this lane loads, at the lane's true row (a row past T, up to the
     // copy's 32-row padding, is written as zeros)
-    const int64_t mt = m0 + row16;
-    const bool tile_row = a.tiled != nullptr && mt < (a.T + 31) / 32 * 32;
-    auto tile = [&](int64_t k, const u32x4& v) {
-        if (tile_row)
+    auto tile = [&](int b, int64_t k, const u32x4& v) {
+        const int64_t mt = m0 + 16 * b + row16;
+        if (a.tiled != nullptr && mt < (a.T + 31) / 32 * 32)
             *reinterpret_cast<u32x4*>(a.tiled + act_tile_index(mt, wave * kq + 8 * grp + k, a.T)) =
                 mt < a.T ? v : u32x4{0u, 0u, 0u, 0u};
     };
-    u32x4 xv[2][U], fv[2][U][NB];
+    u32x4 xv[2][MB][U], fv[2][U][NB];
     // KM: piece q of a lane (16 bytes) is piece lane + 64 q of the chunk's rows k .. k + rows, in
     // f's flattened slots; it lands at row (16 p) / rb, byte (16 p) % rb of the stage
     // (pieces past the chunk's rows load piece 0 again and are not stored: no predicated loads,
@@ -173,9 +187,11 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
         const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(stage + (r0 + 4) * St::S + (16 * nb + 4 * q) * 2));
         return tr_pair(lo4, hi4);
     };
-    auto load = [&](int64_t k, u32x4 (&x)[U], u32x4 (&f)[U][NB]) {
+    auto load = [&](int64_t k, u32x4 (&x)[MB][U], u32x4 (&f)[U][NB]) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) x[u] = *reinterpret_cast<const u32x4*>(ap + k + 32 * u);
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int u = 0; u < U; ++u) x[b][u] = *reinterpret_cast<const u32x4*>(ap[b] + k + 32 * u);
         if constexpr (KM) {
             km_load(k, CH, f);
         } else {
@@ -186,16 +202,18 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
                     f[u][nb] = *reinterpret_cast<const u32x4*>(wp + (int64_t)16 * nb * a.Kin + k + 32 * u);
         }
     };
-    auto mult = [&](int64_t k, const u32x4 (&x)[U], const u32x4 (&f)[U][NB]) {
+    auto mult = [&](int64_t k, const u32x4 (&x)[MB][U], const u32x4 (&f)[U][NB]) {
         if constexpr (KM) km_store(CH, f);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 const bf16x8 bv = KM ? km_frag(u, nb) : __builtin_bit_cast(bf16x8, f[u][nb]);
-                acc[nb] = mfma16(__builtin_bit_cast(bf16x8, x[u]), bv, acc[nb]);
+#pragma unroll
+                for (int b = 0; b < MB; ++b) acc[b][nb] = mfma16(__builtin_bit_cast(bf16x8, x[b][u]), bv, acc[b][nb]);
             }
-            tile(k + 32 * u, x[u]);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) tile(b, k + 32 * u, x[b][u]);
         }
     };
     int64_t c = 0;
@@ -208,27 +226,41 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
     }
     if (c < nch) mult(c * CH, xv[0], fv[0]);  // an odd chunk count: the last one sits in set 0
     for (int64_t k = nch * CH; k < kq; k += 32) {
-        const u32x4 xr = *reinterpret_cast<const u32x4*>(ap + k);
-        tile(k, xr);
-        const bf16x8 av = __builtin_bit_cast(bf16x8, xr);
+        bf16x8 av[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            const u32x4 xr = *reinterpret_cast<const u32x4*>(ap[b] + k);
+            tile(b, k, xr);
+            av[b] = __builtin_bit_cast(bf16x8, xr);
+        }
         if constexpr (KM) {
             km_load(k, 32, fv[0]);
             km_store(32, fv[0]);
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) acc[nb] = mfma16(av, km_frag(0, nb), acc[nb]);
+            for (int nb = 0; nb < NB; ++nb) {
+                const bf16x8 bv = km_frag(0, nb);
+#pragma unroll
+                for (int b = 0; b < MB; ++b) acc[b][nb] = mfma16(av[b], bv, acc[b][nb]);
+            }
         } else {
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                acc[nb] = mfma16(av, __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(wp + (int64_t)16 * nb * a.Kin + k)), acc[nb]);
+            for (int nb = 0; nb < NB; ++nb) {
+                const bf16x8 bv =
+                    __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(wp + (int64_t)16 * nb * a.Kin + k));
+#pragma unroll
+                for (int b = 0; b < MB; ++b) acc[b][nb] = mfma16(av[b], bv, acc[b][nb]);
+            }
         }
     }
     // 16x16 accumulator: element e is row 4*grp + e, column row16
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int b = 0; b < MB; ++b)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) red[wave][4 * grp + e][16 * nb + row16] = acc[nb][e];
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[wave][16 * b + 4 * grp + e][16 * nb + row16] = acc[b][nb][e];
     __syncthreads();
-    for (int i = threadIdx.x; i < 16 * RD; i += blockDim.x) {
+    for (int i = threadIdx.x; i < 16 * MB * RD; i += blockDim.x) {
         const int ml = i / RD, j = i % RD;
         const int64_t m = m0 + ml;
         if (j >= a.r || m >= a.ldt) continue;
@@ -657,7 +689,8 @@ int down_r(const DownArgs& a, hipStream_t s) {
     const int nw = a.Kin % 256 == 0 ? kDownWavesMax : 4;
     // the workgroups cover the splits' ldt rows and, when the tiled copy is written, its 32-row padding
     const int64_t rows = a.tiled && (a.T + 31) / 32 * 32 > a.ldt ? (a.T + 31) / 32 * 32 : a.ldt;
-    const dim3 grid((unsigned)((rows + 15) / 16)), block(64 * nw);
+    constexpr int M = 16 * down_blocks<RD>();
+    const dim3 grid((unsigned)((rows + M - 1) / M)), block(64 * nw);
     if (a.w_kmajor)
         hipLaunchKernelGGL((lora_down_kernel<RD, true>), grid, block, 0, s, a);
     else
