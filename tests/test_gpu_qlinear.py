@@ -195,6 +195,47 @@ def test_fused_backward_equals_stages(T, N, K, r):
     assert not torch.equal(dA1, dA0) and not torch.equal(dB1, dB0)
 
 
+@pytest.mark.parametrize("want", ["dA", "dB"])
+def test_fused_backward_one_factor(want):
+    """The fused backward asked for one factor's gradient (the other pointer null) takes that
+    factor's own chunking, as the stand-alone gradient entry does: the same bits as the stages
+    called the same way, and the other factor untouched."""
+    import ctypes as C
+    from r9700training_amd import R97Q_F32, _ptr, _stream, check, lib
+    from r9700training_amd.qlinear import bwd_workspace, qlinear_lora_fwd
+
+    T, N, K, r = 1000, 384, 640, 16
+    print(f"case fused one factor {want} T={T} N={N} K={K} r={r}", flush=True)
+    rng = np.random.default_rng(77)
+    keep = []
+    w = prepared(weight_planes(N, K, seed=5), keep)
+    X = bf16_tensor(rng.standard_normal((T, K)))
+    dY = bf16_tensor(rng.standard_normal((T, N)))
+    A = bf16_tensor(0.01 * rng.standard_normal((r, K)))
+    B = bf16_tensor(0.01 * rng.standard_normal((N, r)))
+    _, t = qlinear_lora_fwd(w, X, A, B, 2.0)
+    L = lib()
+    P = _ptr
+    st = _stream(None)
+    out = {}
+    for path in ("fused", "stages"):
+        ws = bwd_workspace(T, N, K, r)
+        dX = torch.empty((T, K), dtype=torch.float32, device="cuda")
+        g = torch.zeros((r, K) if want == "dA" else (N, r), dtype=torch.float32, device="cuda")
+        dA, dB = (g, None) if want == "dA" else (None, g)
+        if path == "fused":
+            check(L.r97q_qlinear_lora_bwd(C.byref(w.w), P(X), P(dY), T, P(A), P(B), r, 2.0, P(t), P(dX), R97Q_F32, 0,
+                                          P(dA), P(dB), P(ws), ws.numel(), st), "bwd")
+        else:
+            check(L.r97q_lora_bwd_prep(T, N, K, P(dY), P(A), P(B), P(t), r, 2.0, P(ws), ws.numel(), st), "prep")
+            check(L.r97q_lora_bwd_grads(T, N, K, P(X), P(dY), r, P(dA), P(dB), P(ws), ws.numel(), st), "grads")
+            check(L.r97q_qlinear_dx_base(C.byref(w.w), P(dY), T, r, P(dX), R97Q_F32, 0, P(ws), ws.numel(), st), "dx")
+        torch.cuda.synchronize()
+        out[path] = (dX, g)
+    assert torch.equal(out["fused"][0], out["stages"][0]) and torch.equal(out["fused"][1], out["stages"][1])
+    assert out["fused"][1].abs().max().item() > 0
+
+
 def test_refusals():
     from r9700training_amd import R97qError
     from r9700training_amd.qlinear import QWeight, fwd_workspace, qlinear_lora_fwd
