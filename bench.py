@@ -45,7 +45,9 @@ CONFIGS = {
 
 
 DECODE_MODES = {"auto": 0, "once": 1, "fused": 2}  # R97Q_DECODE_AUTO / _ONCE / _FUSED (include/r97q.h)
-DECODE_ONCE_MIN_T = 16384  # the library's automatic choice (csrc/qlinear.hip, kDecodeOnceMinT)
+# the library's automatic choice (csrc/qlinear.hip, decode_once): the weight decoded once from
+# 16384 tokens on, and from 8192 for weights of 2^23 values or more
+DECODE_ONCE_MIN_T, DECODE_ONCE_MIN_T_LARGE, DECODE_ONCE_LARGE = 16384, 8192, 1 << 23
 
 
 def mfma_ceiling(L, torch, iters=24000, reps=3):
@@ -69,8 +71,14 @@ def mfma_ceiling(L, torch, iters=24000, reps=3):
     return res
 
 
-def decodes_once(mode, T):
-    return mode == "once" or (mode == "auto" and T >= DECODE_ONCE_MIN_T)
+def decode_label(once):
+    """once / fused / mixed over the projections of a workload"""
+    return "once" if all(once) else "fused" if not any(once) else "mixed"
+
+
+def decodes_once(mode, T, N, K):
+    return mode == "once" or (mode == "auto" and (T >= DECODE_ONCE_MIN_T or
+                                                  (T >= DECODE_ONCE_MIN_T_LARGE and N * K >= DECODE_ONCE_LARGE)))
 
 
 def parse():
@@ -99,7 +107,8 @@ def parse():
                     help="how the base products meet the weight (r97q_set_decode_once): fused (each tile "
                          "decoded in the product's main loop, once a 512-token panel), once (the whole weight "
                          "decoded once a call into the workspace, then the product over the decoded tiles), "
-                         "auto (the library's choice: once from 16384 tokens on)")
+                         "auto (the library's choice: once from 16384 tokens on, from 8192 for weights of "
+                         "2^23 values or more)")
     ap.add_argument("--vocab-rows", type=int, default=4096)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (3 launches), the known-size "
@@ -460,7 +469,8 @@ def stack_bench(args):
         "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms, 3), "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
         "tflops": round(tf, 3),
-        "config": {"workload": what, "T": T, "layers": layers, "rank": r, "decode": "once" if decodes_once(args.decode, T) else "fused"},
+        "config": {"workload": what, "T": T, "layers": layers, "rank": r,
+                   "decode": decode_label([decodes_once(args.decode, T, N, K) for N, K in proj])},
         "roofline": {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
         "memory_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 2),
@@ -597,7 +607,7 @@ def main():
     value = total_flops / (ms_step * 1e-3) / 1e12
     # the dominant kernel and its algorithmic work per launch (with the weight decoded once a call,
     # the event pair holds the decode launch and the product over its tiles)
-    once = decodes_once(args.decode, T)
+    once = decodes_once(args.decode, T, N, K)
     kf, kd = ("predecode+qlinear_pd_kernel<fwd>", "predecode+qlinear_pd_kernel<dx>") if once else \
         ("qlinear_rt_kernel<fwd>", "qlinear_rt_kernel<dx>")
     kern = {kf: (fwd_ms, 2 * T * N * K + 2 * T * N * r),

@@ -242,7 +242,8 @@ int r97q_weight_from_decoded(const int8_t* codes, const uint16_t* scale, int64_t
  * loop, once for every 512-token panel; R97Q_DECODE_ONCE decodes the whole weight once a call into
  * the workspace (N*K*2 more bytes) and runs the product over the decoded tiles, the same values in
  * the same order (the results are the same bits); R97Q_DECODE_AUTO (the default) takes the second
- * from 16384 tokens on. Process-wide; returns the previous mode, or -1 for an unknown one. The
+ * from 16384 tokens on, and from 8192 for weights of 8M (2^23) values or more. Process-wide;
+ * returns the previous mode, or -1 for an unknown one. The
  * workspace sizes below follow the mode in force when they are asked. */
 #define R97Q_DECODE_AUTO 0
 #define R97Q_DECODE_ONCE 1

@@ -44,15 +44,24 @@ struct Shape {
 // The base products either decode each weight tile in the main loop, once for every 512-token
 // panel (the fused kernel), or decode the whole weight once a call into the workspace and run the
 // product over the decoded tiles (rt::launch_predecode, then rt::launch_pd). The second saves the
-// repeated decode's VALU work and power, but costs a launch that writes and re-reads N*K*2 bytes:
-// measured on the card, it wins at 64 panels (C5's 32768 tokens: the 24-layer step 182 ms against
-// 191 ms) and loses at 8 (C2's 4096: 328 us a step against 313). r97q_set_decode_once overrides
-// the choice; the entry that allocates nothing always runs the fused kernel.
-constexpr int64_t kDecodeOnceMinT = 32 * rt::kBM;
+// repeated decode's VALU work and power, but costs a launch that writes and re-reads N*K*2 bytes.
+// Measured on the card (one whole LoRA step each):
+//   - it loses at 8 panels (C2's 4096 tokens: 328 us a step against 313);
+//   - at 16 panels (8192 tokens) it wins for weights of 8M values and more (4096 x 4096: 0.64 ms
+//     against 0.70; C3's MLP block: 4.99 ms against 5.11; a C5 layer: 2.02 against 2.13) and loses
+//     for 2048 x 2048 (0.229 ms against 0.214);
+//   - it wins at 32 and 64 panels (4096 x 4096 at 16384 tokens: 1.21 ms against 1.27; C5's 32768
+//     tokens: the 24-layer step 182 ms against 191).
+// r97q_set_decode_once overrides the choice; the entry that allocates nothing always runs the
+// fused kernel.
+constexpr int64_t kDecodeOnceMinT = 32 * rt::kBM;          // any weight from 16384 tokens
+constexpr int64_t kDecodeOnceMinTLarge = 16 * rt::kBM;     // weights of kDecodeOnceLarge values from 8192
+constexpr int64_t kDecodeOnceLarge = int64_t(1) << 23;
 std::atomic<int> g_decode_once{R97Q_DECODE_AUTO};
-bool decode_once(int64_t T) {
+bool decode_once(const Shape& s) {
     const int m = g_decode_once.load(std::memory_order_relaxed);
-    return m == R97Q_DECODE_ONCE || (m == R97Q_DECODE_AUTO && T >= kDecodeOnceMinT);
+    if (m != R97Q_DECODE_AUTO) return m == R97Q_DECODE_ONCE;
+    return s.T >= kDecodeOnceMinT || (s.T >= kDecodeOnceMinTLarge && s.N * s.K >= kDecodeOnceLarge);
 }
 
 // Workspace layout. Forward: Xt (X's tiled copy, act_tiles.h) | P [T, 2r] | Apad [rd, K] (when r
@@ -75,7 +84,7 @@ FwdWs fwd_ws(const Shape& s, bool fused_only = false) {
         w.total = w.Apad + (rd != s.r ? align256((int64_t)rd * s.K * 2) : 0);
     }
     w.Wt = -1;
-    if (!fused_only && decode_once(s.T)) {
+    if (!fused_only && decode_once(s)) {
         w.Wt = w.total;
         w.total += align256(rt::wt_bytes(s.N, s.K));
     }
@@ -89,7 +98,7 @@ struct BwdWs {
 int64_t bwd_counters(const Shape& s) { return grad_blocks(s.K) + grad_blocks(s.N); }
 void bwd_ws_wt(const Shape& s, BwdWs& w) {
     w.Wt = -1;
-    if (decode_once(s.T)) {
+    if (decode_once(s)) {
         w.Wt = w.total;
         w.total += align256(rt::wt_bytes(s.N, s.K));
     }
