@@ -51,6 +51,10 @@ struct DxParams {
     // batched int8-code form with a_scale: the tile holds the low half of each weight's split,
     // bf16(w - bf16(w)) (a second pass completing the exact weight)
     int lo;
+    // batched int8-code form with a_scale, both halves in one launch: gridDim.z = 2 * batch, slices
+    // z >= batch the low halves of slice z - batch, into dX_lo (+ (z - batch) * z_out)
+    int both;
+    void* dX_lo;
 };
 
 template <int BITS>

@@ -541,6 +541,33 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_dx_kernel(const DxParams 
     R97Q_WAVE_SWITCH(dx_wave, R97Q_COMMA_SCALED_LO, p, lds, lane, mt, kt)
 }
 
+// both halves of the int8-code weight's split in one batched launch: slices z < batch over the
+// high halves into dX, slices z >= batch over the low halves of slice z - batch into dX_lo
+template <bool SCALED>
+__global__ __launch_bounds__(kThreads, 1) void qlinear_dx_both_kernel(const DxParams pb) {
+    __shared__ __attribute__((aligned(16))) uint8_t w0[kTileBytes], w1[kTileBytes], x0[kActBytes], x1[kActBytes];
+    const Lds lds{{w0, w1}, {x0, x1}};
+    DxParams p = pb;
+    const bool low = (int)blockIdx.z >= pb.batch;
+    const int64_t z = low ? (int64_t)blockIdx.z - pb.batch : (int64_t)blockIdx.z;
+    p.dY += z * pb.z_dy;
+    p.stream += z * pb.z_w;
+    p.scale_t += z * pb.z_scale;
+    void* base = low ? pb.dX_lo : pb.dX;
+    p.dX = p.dx_f32 ? static_cast<void*>(static_cast<float*>(base) + z * pb.z_out)
+                    : static_cast<void*>(static_cast<uint16_t*>(base) + z * pb.z_out);
+    const int tile = xcd_tile(blockIdx.x, p.mtiles * p.ktiles);
+    const int mt = tile / p.ktiles, kt = tile % p.ktiles;
+    const int lane = threadIdx.x & 63;
+    if (low) {
+        constexpr bool LO = true;
+        R97Q_WAVE_SWITCH(dx_wave, R97Q_COMMA_SCALED_LO, p, lds, lane, mt, kt)
+    } else {
+        constexpr bool LO = false;
+        R97Q_WAVE_SWITCH(dx_wave, R97Q_COMMA_SCALED_LO, p, lds, lane, mt, kt)
+    }
+}
+
 }  // namespace
 
 template <>
@@ -551,6 +578,14 @@ void launch_fwd<R97Q_BITS>(const FwdParams& p, hipStream_t s) {
 template <>
 void launch_dx<R97Q_BITS>(const DxParams& p, hipStream_t s) {
     if constexpr (R97Q_BITS == R97Q_CODES8) {
+        if (p.both) {
+            const dim3 grid((unsigned)(p.mtiles * p.ktiles), 1, (unsigned)(2 * (p.batch > 1 ? p.batch : 1)));
+            if (p.a_scale)
+                hipLaunchKernelGGL(qlinear_dx_both_kernel<true>, grid, dim3(kThreads), 0, s, p);
+            else
+                hipLaunchKernelGGL(qlinear_dx_both_kernel<false>, grid, dim3(kThreads), 0, s, p);
+            return;
+        }
         if (p.batch > 1 || p.lo) {
             const dim3 grid((unsigned)(p.mtiles * p.ktiles), 1, (unsigned)(p.batch > 1 ? p.batch : 1));
             if (p.lo && p.a_scale)

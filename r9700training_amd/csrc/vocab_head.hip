@@ -280,15 +280,13 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
             p.z_w = Np * K / 4;
             p.z_scale = nkb * Np;
             p.z_out = rows * K;
-            // each weight as the exact sum of two bf16 values: the product over the high halves,
-            // then over the low halves into partials of their own (f32 products of bf16 values are
-            // exact); the reduction adds each range's two
+            // each weight as the exact sum of two bf16 values: one launch runs the product over the
+            // high halves and, in slices of its own, over the low halves into partials of their own
+            // (f32 products of bf16 values are exact); the reduction adds each range's two
+            p.both = 1;
+            p.dX_lo = part_lo;
             launch_dx<R97Q_CODES8>(p, s);
-            if (int e = launch_status("qlinear_dx_kernel (vocab head)")) return e;
-            p.lo = 1;
-            p.dX = part_lo;
-            launch_dx<R97Q_CODES8>(p, s);
-            if (int e = launch_status("qlinear_dx_kernel (vocab head, low halves)")) return e;
+            if (int e = launch_status("qlinear_dx_both_kernel (vocab head)")) return e;
             hipLaunchKernelGGL(vocab_reduce_kernel, dim3(blocks(rows * K, 256)), dim3(256), 0, s, d_x, part, part_lo,
                                rows * K, Z);
             if (int e = launch_status("vocab_reduce_kernel")) return e;
