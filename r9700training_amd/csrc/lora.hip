@@ -7,7 +7,7 @@
 // [hi | lo] pair of bf16 (hi = bf16(v), lo = bf16(v - hi)) wherever they enter an MFMA, so the
 // adapter path keeps ~16 significant bits.
 //
-//   lora_down_kernel   one workgroup = 16 token rows (32 at ranks 32 and 64) x the whole
+//   lora_down_kernel   one workgroup = 16 token rows (32 at ranks 32 and 64 on long runs) x the whole
 //                      reduction, its 8 (or 4) waves an
 //                      eighth (quarter) each (v_mfma_f32_16x16x32_bf16), reduced through LDS in a
 //                      fixed order; it writes the f32 result and its [hi | lo] splits for the
@@ -70,10 +70,11 @@ __device__ __forceinline__ bf16x8 tr_pair(s16x4 lo4, s16x4 hi4) {
 }
 
 // ---------------------------------------------------------------- down
-// One workgroup = 16 token rows (two blocks of 16 at ranks 32 and 64); its nw waves (8, or 4 when
-// Kin is not a multiple of 256) each reduce a contiguous nw-th of Kin, then the partial sums are
-// added in wave order through LDS. A 16-row block's products are the same whatever the workgroup's
-// other block, so the results do not depend on the blocking.
+// One workgroup = 16 token rows (two blocks of 16 at ranks 32 and 64 when that still gives 256
+// workgroups); its nw waves (8, or 4 when Kin is not a multiple of 256) each reduce a contiguous
+// nw-th of Kin, then the partial sums are added in wave order through LDS. A 16-row block's
+// products are the same whatever the workgroup's other block, so the results do not depend on
+// the blocking.
 //
 // KM (the factor k-major, W [Kin, r] row-major: the backward's B as the caller holds it): the MFMA's
 // B operand needs 8 consecutive k of one factor column, which that layout keeps r apart. Each wave
@@ -91,14 +92,11 @@ struct DownStage {
     static constexpr int BYTES = CH * S;               // a wave's stage
 };
 
-// token blocks of 16 rows a workgroup: two at the larger ranks, so each factor value a wave loads
-// feeds 32 token rows (at rank 64 the factor is four times the token rows' bytes a chunk)
-template <int RD>
-constexpr int down_blocks() { return RD >= 32 ? 2 : 1; }
-
-template <int RD, bool KM>
+// MB token blocks of 16 rows a workgroup: two at the larger ranks when that still gives a workgroup
+// to every CU (down_r), so each factor value a wave loads feeds 32 token rows (at rank 64 the
+// factor is four times the token rows' bytes a chunk)
+template <int RD, bool KM, int MB>
 __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
-    constexpr int MB = down_blocks<RD>();
     __shared__ float red[kDownWavesMax][16 * MB][RD];
     __shared__ __attribute__((aligned(16))) uint8_t stage_lds[KM ? kDownWavesMax * DownStage<RD>::BYTES : 16];
     const int nw = blockDim.x >> 6;
@@ -689,12 +687,24 @@ int down_r(const DownArgs& a, hipStream_t s) {
     const int nw = a.Kin % 256 == 0 ? kDownWavesMax : 4;
     // the workgroups cover the splits' ldt rows and, when the tiled copy is written, its 32-row padding
     const int64_t rows = a.tiled && (a.T + 31) / 32 * 32 > a.ldt ? (a.T + 31) / 32 * 32 : a.ldt;
-    constexpr int M = 16 * down_blocks<RD>();
-    const dim3 grid((unsigned)((rows + M - 1) / M)), block(64 * nw);
+    // two 16-row blocks a workgroup at ranks 32 and 64 when that leaves at least 256 workgroups
+    // (one a CU; with fewer, the launch is short of memory parallelism)
+    const dim3 block(64 * nw);
+    if constexpr (RD >= 32) {
+        if ((rows + 31) / 32 >= 256) {
+            const dim3 grid((unsigned)((rows + 31) / 32));
+            if (a.w_kmajor)
+                hipLaunchKernelGGL((lora_down_kernel<RD, true, 2>), grid, block, 0, s, a);
+            else
+                hipLaunchKernelGGL((lora_down_kernel<RD, false, 2>), grid, block, 0, s, a);
+            return launch_status("lora_down_kernel");
+        }
+    }
+    const dim3 grid((unsigned)((rows + 15) / 16));
     if (a.w_kmajor)
-        hipLaunchKernelGGL((lora_down_kernel<RD, true>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((lora_down_kernel<RD, true, 1>), grid, block, 0, s, a);
     else
-        hipLaunchKernelGGL((lora_down_kernel<RD, false>), grid, block, 0, s, a);
+        hipLaunchKernelGGL((lora_down_kernel<RD, false, 1>), grid, block, 0, s, a);
     return launch_status("lora_down_kernel");
 }
 
