@@ -63,7 +63,7 @@ def mfma_ceiling(L, torch, iters=24000, reps=3):
         for _ in range(reps + 1):  # the first launch ramps the clock
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            check(L.r97q_mfma_probe(iters, zero, _ptr(out), st), "r97q_mfma_probe")
+            check(L.r97q_mfma_probe(iters, zero, _ptr(out), out.numel(), st), "r97q_mfma_probe")
             b.record()
             b.synchronize()
             rates.append(L.r97q_mfma_probe_flops(iters) / (a.elapsed_time(b) * 1e-3) / 1e12)
@@ -110,6 +110,9 @@ def parse():
                          "auto (the library's choice: once from 16384 tokens on, from 8192 for weights of "
                          "2^23 values or more)")
     ap.add_argument("--vocab-rows", type=int, default=4096)
+    ap.add_argument("--settle-s", type=float, default=1.5,
+                    help="untimed steps for this long before the warmup steps, so the GPU's clocks leave their "
+                         "idle state before anything is timed (declared in the line as clock_settle)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (3 launches), the known-size "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
@@ -185,11 +188,49 @@ def host_cores():
     return max(1, min(16, n))
 
 
-def cpu_baseline(inp, T, N, K, r, s, target_s, nthreads):
-    """The reference's own host path (oracle/_ref: its r97_iqr_decode_host, gemm_nt twin and
-    adjoint, float lora_shrink / lora_expand twins and adjoints, f64 with its parallel_for) on
-    `nthreads` threads, on a row sample of the same workload, extrapolated linearly in tokens to the
-    whole step."""
+def ref_decode(codes_p, rs, col_factor, N, K, mad_a, mad_b):
+    """The stored weight the host rows read: the reference's r97_iqr_decode_host (oracle/_ref, else the
+    oracle's restatement) over a b5 trellis.mad weight with an f32 row scale, then scale.col folded
+    in. Returns (codes, scale, seconds)."""
+    import numpy as np
+
+    from oracle import oracle as O
+    from oracle.oracle import Desc
+
+    codes_p = np.ascontiguousarray(codes_p)
+    rs = np.ascontiguousarray(rs, dtype=np.float32)
+    d = Desc()
+    d.rows_all, d.cols, d.row0, d.rows = N, K, 0, N
+    d.bits, d.state_bits, d.run_rows, d.rb, d.mad, d.round_mad = 5, 16, 256, 1, 1, 1
+    d.mad_a, d.mad_b = mad_a, mad_b
+    d.codes, d.codes_row_bytes = codes_p.ctypes.data, codes_p.shape[1]
+    d.scale, d.scale_dtype, d.scale_block_cols, d.scale_row_bytes = rs.ctypes.data, 0, 0, 4
+    t0 = time.perf_counter()
+    codes, _ = O.decode(d, use_ref=O.ref() is not None)
+    scale = O.fold_scale_col(rs, np.asarray(col_factor, np.float32))
+    return codes, scale, time.perf_counter() - t0
+
+
+def settle(step, seconds, torch, chunk=20):
+    """Run `step` (untimed) for about `seconds`, synchronising every `chunk` steps: the GPU's clocks
+    ramp from idle over the first few hundred milliseconds of work. Returns the line's clock_settle."""
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(chunk):
+            step()
+        n += chunk
+        torch.cuda.synchronize()
+    return {"s": round(time.perf_counter() - t0, 3), "steps": n,
+            "what": "untimed steps run before the warmup steps, so the clocks leave their idle state first"}
+
+
+def cpu_baseline(projs, T, r, s, target_s, nthreads, layers=1, reps=3, what="", unit="TFLOP/s"):
+    """The reference's own host path (oracle/_ref: its r97_iqr_decode_host, gemm_nt twin and adjoint,
+    float lora_shrink / lora_expand twins and adjoints, f64 with its parallel_for) on `nthreads`
+    threads, over an evenly spaced sample of token rows of every projection in `projs`, timed `reps`
+    times (the median taken) and extrapolated linearly in tokens (and in layers) to the whole step.
+    Each projection is a dict: N, K, codes / scale (the decoded stored weight), decode_s, A [r, K],
+    B [N, r] (f64), rows(idx) -> (x [m, K], dy [m, N]) f64."""
     import numpy as np
 
     from oracle import oracle as O
@@ -197,62 +238,66 @@ def cpu_baseline(inp, T, N, K, r, s, target_s, nthreads):
     use_ref = O.ref() is not None
     os.environ["R97_THREADS"] = str(nthreads)
     O.set_threads(nthreads)
-    q = inp["q"]
-    # the decode (once): the stored planes to the int8 grid + folded scale
-    import ctypes as C
-    from oracle.oracle import Desc
-
-    codes_p = np.ascontiguousarray(q["codes"])
-    rs = np.ascontiguousarray(q["row_scale"])
-    d = Desc()
-    d.rows_all, d.cols, d.row0, d.rows = N, K, 0, N
-    d.bits, d.state_bits, d.run_rows, d.rb, d.mad, d.round_mad = 5, 16, 256, 1, 1, 1
-    d.mad_a, d.mad_b = q["mad_a"], q["mad_b"]
-    d.codes, d.codes_row_bytes = codes_p.ctypes.data, codes_p.shape[1]
-    d.scale, d.scale_dtype, d.scale_block_cols, d.scale_row_bytes = rs.ctypes.data, 0, 0, 4
-    t0 = time.perf_counter()
-    codes, _ = O.decode(d, use_ref=use_ref)
-    scale = O.fold_scale_col(rs, q["col_factor"])
-    t_decode = time.perf_counter() - t0
-
-    X = inp["X"].float().cpu().numpy().astype(np.float64)
-    dY = inp["dY"].float().cpu().numpy().astype(np.float64)
-    A = inp["A"].float().cpu().numpy().astype(np.float64)
-    B = inp["B"].float().cpu().numpy().astype(np.float64)
 
     def path(rows):
-        x, dy = X[rows], dY[rows]
-        M = len(rows)
-        slot = np.zeros(M)
-        sc = np.full((1, N), s)
-        O.gemm_nt_twin(x, codes, scale, use_ref=use_ref)
-        t = O.lora_shrink_twin(x, slot, A.reshape(1, r, K), use_ref=use_ref)
-        O.lora_expand_twin(t, slot, B.reshape(1, N, r), sc, use_ref=use_ref)
-        dt, _ = O.lora_expand_adjoint(t, slot, B.reshape(1, N, r), sc, dy, use_ref=use_ref)
-        O.lora_shrink_adjoint(x, slot, A.reshape(1, r, K), dt, use_ref=use_ref)
-        O.gemm_nt_adjoint(dy, codes, scale, use_ref=use_ref)
+        for pj in projs:
+            N, K = pj["N"], pj["K"]
+            x, dy = pj["rows"](rows)
+            M = len(rows)
+            slot = np.zeros(M)
+            sc = np.full((1, N), s)
+            codes, scale, A, B = pj["codes"], pj["scale"], pj["A"], pj["B"]
+            O.gemm_nt_twin(x, codes, scale, use_ref=use_ref)
+            t = O.lora_shrink_twin(x, slot, A.reshape(1, r, K), use_ref=use_ref)
+            O.lora_expand_twin(t, slot, B.reshape(1, N, r), sc, use_ref=use_ref)
+            dt, _ = O.lora_expand_adjoint(t, slot, B.reshape(1, N, r), sc, dy, use_ref=use_ref)
+            O.lora_shrink_adjoint(x, slot, A.reshape(1, r, K), dt, use_ref=use_ref)
+            O.gemm_nt_adjoint(dy, codes, scale, use_ref=use_ref)
 
-    probe = list(range(min(T, 2 * nthreads)))
+    probe = np.arange(min(T, 2 * nthreads))
     t0 = time.perf_counter()
     path(probe)
     per_row = (time.perf_counter() - t0) / len(probe)
-    n = int(max(len(probe), min(T, target_s / max(per_row, 1e-9))))
+    n = int(max(len(probe), min(T, target_s / reps / max(per_row, 1e-9))))
     n = max(2 * nthreads, (n // (2 * nthreads)) * (2 * nthreads))
     rows = np.linspace(0, T - 1, n).astype(np.int64)
-    t0 = time.perf_counter()
-    path(rows)
-    t_rows = time.perf_counter() - t0
-    step_s = t_decode + t_rows * (T / n)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        path(rows)
+        times.append(time.perf_counter() - t0)
+    t_rows = sorted(times)[len(times) // 2]
+    decode_s = sum(pj["decode_s"] for pj in projs)
+    step_s = (decode_s + t_rows * (T / n)) * layers
+    total = layers * sum(flops(T, pj["N"], pj["K"], r) for pj in projs)
     return {
-        "value": round(flops(T, N, K, r) / step_s / 1e12, 6),
-        "unit": "TFLOP/s",
+        "value": round(total / step_s / 1e12, 6) if unit == "TFLOP/s" else round(T / step_s, 3),
+        "unit": unit,
+        "tflops": round(total / step_s / 1e12, 6),
+        "s_per_step": round(step_s, 2),
         "cores": nthreads,
         "kind": "reference" if use_ref else "port",
-        "sample": f"{n} of {T} token rows (evenly spaced) through decode + gemm_nt twin/adjoint + "
-                  f"lora shrink/expand twins/adjoints, f64, {nthreads} threads; extrapolated "
-                  f"linearly in tokens ({t_rows:.1f} s sampled + {t_decode:.2f} s decode; "
-                  f"{step_s:.1f} s per full step; nproc {os.cpu_count()}, affinity {host_cores()})",
+        "sample": f"{n} of {T} token rows (evenly spaced) of {len(projs)} projection(s){what} through decode + "
+                  f"gemm_nt twin/adjoint + lora shrink/expand twins/adjoints, f64, {nthreads} threads; the "
+                  f"median of {reps} passes ({', '.join(f'{x:.1f}' for x in times)} s) extrapolated linearly "
+                  f"in tokens" + (f" and in layers (x{layers})" if layers > 1 else "") +
+                  f" ({decode_s:.2f} s decode; {step_s:.1f} s per full step; nproc {os.cpu_count()}, "
+                  f"affinity {host_cores()})",
     }
+
+
+def c2_projection(inp, T, N, K, r):
+    """The C2 layer as cpu_baseline's projection: the decoded stored weight and the step's inputs."""
+    import numpy as np
+
+    q = inp["q"]
+    codes, scale, dec_s = ref_decode(q["codes"], q["row_scale"], q["col_factor"], N, K, q["mad_a"], q["mad_b"])
+    X = inp["X"].float().cpu().numpy().astype(np.float64)
+    dY = inp["dY"].float().cpu().numpy().astype(np.float64)
+    return dict(N=N, K=K, codes=codes, scale=scale, decode_s=dec_s,
+                A=inp["A"].float().cpu().numpy().astype(np.float64),
+                B=inp["B"].float().cpu().numpy().astype(np.float64),
+                rows=lambda idx: (X[idx], dY[idx]))
 
 
 VOCAB_CLASSES = [32768, 65536, 98304, 51712]  # rows a class (one trellis width each): 248320 in all
@@ -454,6 +499,7 @@ def stack_bench(args):
         opt.step(dA + dB, stream=stream, staged=True)
 
     steps, warmup = max(1, min(args.steps, 5)), max(1, min(args.warmup, 2))
+    clock_settle = settle(lora_step, args.settle_s, torch, chunk=1) if args.settle_s > 0 else None
     for _ in range(warmup):
         lora_step()
     torch.cuda.synchronize()
@@ -464,6 +510,31 @@ def stack_bench(args):
     ms = (time.perf_counter() - t0) * 1e3 / steps
     total = layers * sum(flops(T, N, K, r) for N, K in proj)
     tf = total / (ms * 1e-3) / 1e12
+    cpu = None
+    if args.cpu_seconds > 0:
+        # the reference's host rows over the first layer's projections (the same weights and inputs),
+        # extrapolated to every layer
+        projs = []
+        for i, (N, K) in enumerate(proj):
+            c_d, s_d, f_d = keep[3 * i], keep[3 * i + 1], keep[3 * i + 2]
+            codes, scale, dec_s = ref_decode(c_d.cpu().numpy(), s_d.cpu().numpy().view(np.float32),
+                                             f_d.cpu().numpy(), N, K, 0x2F1E3D | 1, 0x9E3779B9)
+            cache = {}
+
+            def rows(idx, K=K, N=N, cache=cache):
+                key = (int(idx[0]), len(idx), int(idx[-1]))
+                if key not in cache:
+                    it = torch.from_numpy(np.asarray(idx)).to(dev)
+                    cache.clear()
+                    cache[key] = (X[K][it].float().cpu().numpy().astype(np.float64),
+                                  dY[N][it].float().cpu().numpy().astype(np.float64))
+                return cache[key]
+
+            projs.append(dict(N=N, K=K, codes=codes, scale=scale, decode_s=dec_s,
+                              A=A[i].float().cpu().numpy().astype(np.float64),
+                              B=B[i].float().cpu().numpy().astype(np.float64), rows=rows))
+        cpu = cpu_baseline(projs, T, r, s, args.cpu_seconds, min(8, host_cores()), layers=layers,
+                           what=" (one layer)" if layers > 1 else "", unit="tokens/s")
     print(json.dumps({
         "metric": metric,
         "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -474,6 +545,8 @@ def stack_bench(args):
         "roofline": {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
         "memory_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 2),
+        "clock_settle": clock_settle,
+        **({"cpu_baseline": cpu} if cpu else {}),
     }), flush=True)
 
 
@@ -556,6 +629,7 @@ def main():
               "dx_base")
         e[3].record(stream)
 
+    clock_settle = settle(step, args.settle_s, torch) if args.settle_s > 0 else None
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -655,6 +729,7 @@ def main():
                      "weight_stream_note": f"the {packed_bytes / 1e6:.1f} MB packed weight fetched once by each "
                                            f"of the {panels} token panels' workgroups"},
         "quantizer_rel_err": round(inp["q"]["rel_err"], 4),
+        "clock_settle": clock_settle,
     }
     # the rate the card sustains on MFMAs alone (power-limited: its clock falls well below the peak's
     # 2.4 GHz under a full matrix load): the nearer bar for the fused kernels
@@ -664,8 +739,9 @@ def main():
         what="v_mfma_f32_32x32x16_bf16 alone, operands in registers, 256 workgroups x 8 waves, ~40 ms a launch")
     line["roofline"]["frac_of_measured_ceiling"] = round(achieved / ceil["random_operands"], 4)
     if args.cpu_seconds > 0:
-        line["cpu_baseline"] = cpu_baseline(inp, T, N, K, r, s, args.cpu_seconds, min(8, host_cores()))
-        line["cpu_baseline_all_cores"] = (cpu_baseline(inp, T, N, K, r, s, args.cpu_seconds, host_cores())
+        pj = [c2_projection(inp, T, N, K, r)]
+        line["cpu_baseline"] = cpu_baseline(pj, T, r, s, args.cpu_seconds, min(8, host_cores()))
+        line["cpu_baseline_all_cores"] = (cpu_baseline(pj, T, r, s, args.cpu_seconds, host_cores())
                                           if host_cores() > 8 else line["cpu_baseline"])
     print(json.dumps(line), flush=True)
 

@@ -504,10 +504,11 @@ int r97q_vocab_head_cast(uint16_t* dst, const float* src, int64_t values, R97Iqr
  * The card's sustained bf16 MFMA rate with nothing else to do (no counterpart in the reference; for
  * bench.py's roofline): 256 workgroups x 8 waves each issuing `iters` x 32
  * v_mfma_f32_32x32x16_bf16 over operands held in registers, random bf16 values or, with
- * zero_operands, zeros. out: 256 * 512 floats (the sums, so nothing is optimised away). The FLOPs of
+ * zero_operands, zeros. out: out_count floats, at least 256 * 512 (the sums, so nothing is optimised
+ * away); a smaller out_count is refused with R97Q_EINVAL before anything is launched. The FLOPs of
  * one launch: r97q_mfma_probe_flops(iters). */
 int64_t r97q_mfma_probe_flops(int32_t iters);
-int r97q_mfma_probe(int32_t iters, int32_t zero_operands, float* out, R97IqrStream stream);
+int r97q_mfma_probe(int32_t iters, int32_t zero_operands, float* out, int64_t out_count, R97IqrStream stream);
 
 #ifdef __cplusplus
 }

@@ -170,7 +170,7 @@ SIGNATURES = {
     "r97q_vocab_head_transpose": (C.c_int, [C.POINTER(VocabPlan), _P, _I, _P, _P, _I, _P]),
     "r97q_vocab_head_cast": (C.c_int, [_P, _P, _I, _P]),
     "r97q_mfma_probe_flops": (_I, [_i]),
-    "r97q_mfma_probe": (C.c_int, [_i, _i, _P, _P]),
+    "r97q_mfma_probe": (C.c_int, [_i, _i, _P, _I, _P]),
 }
 
 _lib = None

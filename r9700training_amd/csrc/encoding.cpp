@@ -121,8 +121,10 @@ int r97_iqr_desc_from_encoding(const R97Encoding* enc, const R97IqrStoredPlane* 
         // the affine grid: a zero a block beside the scale, no trellis; every row its own run
         if (it >= 0) return 0;
         const R97EncPlane& zp = enc->plane[iz];
+        // any plane dtype of 1-8 bits (an unsigned packed width, or an 8-bit one such as i8): the
+        // decode reads the zero as that many unsigned bits
         d.zero_bits = r97_enc_dtype_bits(zp.dtype);
-        if (zp.dtype < R97_DT_U1 || zp.dtype > R97_DT_U12 || d.zero_bits > 8) return 0;
+        if (d.zero_bits < 1 || d.zero_bits > 8) return 0;
         if (zp.block[0] != sp.block[0] || zp.block[1] != sp.block[1]) return 0;
         d.affine = 1;
         d.run_rows = 1;

@@ -474,15 +474,19 @@ __global__ __launch_bounds__(512) void lora_grads_kernel(GradArgs ga) {
         }
     }
     if (ga.defer) return;
-    // every store of the workgroup acknowledged, then the chunk counted done; the last of the
-    // column block's chunks reads the others' sums at device scope
+    // every store of the workgroup complete (its device-scope stores acknowledged, then the
+    // workgroup barrier), then the chunk counted done by one acquire-release increment at device
+    // scope, whose release covers the workgroup's stores ordered before it by the barrier; the last
+    // of the column block's chunks acquires the others' sums (a device-scope fence in every thread)
+    // before it reads them
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(g.done + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        last = __hip_atomic_fetch_add(g.done + blockIdx.x, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
                (int)gridDim.y - 1;
     __syncthreads();
     if (!last) return;
+    __threadfence();
     // out (+)= the chunks' sums in chunk order; out is [r, C] row-major or, `transposed`, [C, r].
     // A thread takes PAIRS (j, c) pairs; their loads are issued U chunks at a time (32 in flight).
     constexpr int PAIRS = R * kGradCols / 512;

@@ -72,10 +72,12 @@ extern "C" int64_t r97q_mfma_probe_flops(int32_t iters) {
     return (int64_t)2 * 32 * 32 * 16 * 32 * iters * 8 * 256;
 }
 
-extern "C" int r97q_mfma_probe(int32_t iters, int32_t zero_operands, float* out, R97IqrStream stream) {
+extern "C" int r97q_mfma_probe(int32_t iters, int32_t zero_operands, float* out, int64_t out_count,
+                               R97IqrStream stream) {
     r97q::clear_error();
-    if (iters <= 0 || !out) {
-        r97q::set_error("r97q_mfma_probe: iters > 0 and an out buffer of 256 * 512 floats");
+    if (iters <= 0 || !out || out_count < (int64_t)256 * 512) {
+        r97q::set_error("r97q_mfma_probe: iters %d, out_count %lld (iters > 0 and an out buffer of at least 256 * 512 "
+                        "floats)", (int)iters, (long long)out_count);
         return R97Q_EINVAL;
     }
     hipLaunchKernelGGL(mfma_probe_kernel, dim3(256), dim3(512), 0, (hipStream_t)stream, (int)iters,

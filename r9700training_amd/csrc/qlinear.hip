@@ -36,9 +36,13 @@ int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
 
 bool rank_ok(int r) { return r == 0 || r == 8 || r == 16 || r == 32 || r == 64; }
 
+// One call's shape. `once` is the decode-once choice, read once when the entry builds its shape:
+// every workspace layout and launch of that call follows the same choice, whatever another
+// thread sets meanwhile.
 struct Shape {
     int64_t T, N, K;
     int r;
+    bool once;
 };
 
 // The base products either decode each weight tile in the main loop, once for every 512-token
@@ -58,10 +62,11 @@ constexpr int64_t kDecodeOnceMinT = 32 * rt::kBM;          // any weight from 16
 constexpr int64_t kDecodeOnceMinTLarge = 16 * rt::kBM;     // weights of kDecodeOnceLarge values from 8192
 constexpr int64_t kDecodeOnceLarge = int64_t(1) << 23;
 std::atomic<int> g_decode_once{R97Q_DECODE_AUTO};
-bool decode_once(const Shape& s) {
+Shape shape(int64_t T, int64_t N, int64_t K, int r) {
     const int m = g_decode_once.load(std::memory_order_relaxed);
-    if (m != R97Q_DECODE_AUTO) return m == R97Q_DECODE_ONCE;
-    return s.T >= kDecodeOnceMinT || (s.T >= kDecodeOnceMinTLarge && s.N * s.K >= kDecodeOnceLarge);
+    const bool once = m != R97Q_DECODE_AUTO ? m == R97Q_DECODE_ONCE
+                                            : T >= kDecodeOnceMinT || (T >= kDecodeOnceMinTLarge && N * K >= kDecodeOnceLarge);
+    return Shape{T, N, K, r, once};
 }
 
 // Workspace layout. Forward: Xt (X's tiled copy, act_tiles.h) | P [T, 2r] | Apad [rd, K] (when r
@@ -84,7 +89,7 @@ FwdWs fwd_ws(const Shape& s, bool fused_only = false) {
         w.total = w.Apad + (rd != s.r ? align256((int64_t)rd * s.K * 2) : 0);
     }
     w.Wt = -1;
-    if (!fused_only && decode_once(s)) {
+    if (!fused_only && s.once) {
         w.Wt = w.total;
         w.total += align256(rt::wt_bytes(s.N, s.K));
     }
@@ -98,7 +103,7 @@ struct BwdWs {
 int64_t bwd_counters(const Shape& s) { return grad_blocks(s.K) + grad_blocks(s.N); }
 void bwd_ws_wt(const Shape& s, BwdWs& w) {
     w.Wt = -1;
-    if (decode_once(s)) {
+    if (s.once) {
         w.Wt = w.total;
         w.total += align256(rt::wt_bytes(s.N, s.K));
     }
@@ -498,11 +503,11 @@ int32_t r97q_set_decode_once(int32_t mode) {
 }
 
 int64_t r97q_fwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank) {
-    return fwd_ws(Shape{T, N, K, rank}).total;
+    return fwd_ws(shape(T, N, K, rank)).total;
 }
 
 int64_t r97q_bwd_workspace_bytes(int64_t T, int64_t N, int64_t K, int32_t rank) {
-    return bwd_ws(Shape{T, N, K, rank}).total;
+    return bwd_ws(shape(T, N, K, rank)).total;
 }
 
 int r97q_lora_fwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* X, const uint16_t* A,
@@ -516,7 +521,7 @@ int r97q_lora_fwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* X, const
         set_error("%s: null X, or A or t_out with rank > 0", who);
         return R97Q_EINVAL;
     }
-    const Shape sh{T, N, K, rank};
+    const Shape sh = shape(T, N, K, rank);
     if (int e = check_ws(workspace_bytes, fwd_ws(sh).total, workspace, who)) return e;
     return fwd_prep(sh, X, A, scale, t_out, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
 }
@@ -532,7 +537,7 @@ int r97q_qlinear_fwd_base(const R97qWeight* w, const uint16_t* X, int64_t T, con
         set_error("%s: null X / Y (or B with rank > 0), or T <= 0", who);
         return R97Q_EINVAL;
     }
-    const Shape sh{T, w->rows, w->cols, rank};
+    const Shape sh = shape(T, w->rows, w->cols, rank);
     if (int e = check_ws(workspace_bytes, fwd_ws(sh).total, workspace, who)) return e;
     return fwd_base(w, sh, B, Y, y_dtype, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
 }
@@ -553,7 +558,7 @@ int r97q_qlinear_lora_fwd(const R97qWeight* w, const uint16_t* X, int64_t T, con
         set_error("%s: rank %d needs A, B and t_out", who, (int)rank);
         return R97Q_EINVAL;
     }
-    const Shape sh{T, w->rows, w->cols, rank};
+    const Shape sh = shape(T, w->rows, w->cols, rank);
     if (int e = check_ws(workspace_bytes, fwd_ws(sh).total, workspace, who)) return e;
     uint8_t* wsb = static_cast<uint8_t*>(workspace);
     const hipStream_t s = (hipStream_t)stream;
@@ -574,7 +579,7 @@ int r97q_lora_bwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* dY, cons
         set_error("%s: null dY, or A, B or t with rank > 0", who);
         return R97Q_EINVAL;
     }
-    const Shape sh{T, N, K, rank};
+    const Shape sh = shape(T, N, K, rank);
     if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
     return bwd_prep(sh, dY, A, B, t, scale, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
 }
@@ -591,7 +596,7 @@ int r97q_lora_bwd_grads(int64_t T, int64_t N, int64_t K, const uint16_t* X, cons
         set_error("%s: dA needs X, dB needs dY", who);
         return R97Q_EINVAL;
     }
-    const Shape sh{T, N, K, rank};
+    const Shape sh = shape(T, N, K, rank);
     if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
     return bwd_grads(sh, X, dY, dA, dB, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
 }
@@ -607,7 +612,7 @@ int r97q_qlinear_dx_base(const R97qWeight* w, const uint16_t* dY, int64_t T, int
         set_error("%s: null dY / dX or T <= 0", who);
         return R97Q_EINVAL;
     }
-    const Shape sh{T, w->rows, w->cols, rank};
+    const Shape sh = shape(T, w->rows, w->cols, rank);
     if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
     return dx_base(w, sh, dX, dx_dtype, dx_accumulate, static_cast<uint8_t*>(workspace), (hipStream_t)stream);
 }
@@ -629,7 +634,7 @@ int r97q_qlinear_lora_bwd(const R97qWeight* w, const uint16_t* X, const uint16_t
         set_error("%s: rank %d needs X, A, B and t", who, (int)rank);
         return R97Q_EINVAL;
     }
-    const Shape sh{T, w->rows, w->cols, rank};
+    const Shape sh = shape(T, w->rows, w->cols, rank);
     if (int e = check_ws(workspace_bytes, bwd_ws(sh).total, workspace, who)) return e;
     uint8_t* wsb = static_cast<uint8_t*>(workspace);
     const hipStream_t s = (hipStream_t)stream;
@@ -650,7 +655,7 @@ int r97q_gemm_nt_q_dx(const R97qWeight* w, const uint16_t* dY, int64_t T, const 
         set_error("%s: null dY / dA / a_scale or T <= 0", who);
         return R97Q_EINVAL;
     }
-    const Shape sh{T, w->rows, w->cols, 0};
+    const Shape sh = shape(T, w->rows, w->cols, 0);
     return dx_scaled(w, sh, dY, dA, da_dtype, accumulate, (hipStream_t)stream, a_scale);
 }
 
@@ -870,7 +875,7 @@ int r97q_qlinear_lora_fwd_noalloc(const R97qWeight* w, const uint16_t* X, int64_
         set_error("%s: rank %d needs A, B and t_out", who, (int)rank);
         return R97Q_EINVAL;
     }
-    const Shape sh{T, w->rows, w->cols, rank};
+    const Shape sh = shape(T, w->rows, w->cols, rank);
     const int64_t need = fwd_ws(sh, true).total;
     if (need > kNoAllocScratchBytes) {
         set_error("%s: T %lld x K %lld at rank %d needs %lld workspace bytes, past the %lld this entry holds "

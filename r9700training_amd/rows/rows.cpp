@@ -20,10 +20,13 @@
 // overwrites, never writes a frozen slot, and returns with its results host-visible (one
 // process-wide stream, synchronised before return). The factor gradients (lora_A, lora_B) are
 // added into the step's f32 accumulators on the card (r97/grad_stage.h), named and shaped as the
-// leaves, as the reference's device rows do; the walk's grad_stage_flush puts them in `grads`. A record whose layout is malformed is left
-// untouched, as the reference's rows do; a well-formed record this build's kernels cannot serve
-// (a rank outside 8/16/32/64, a K or N not a multiple of 128, a stored form the fused kernels do not
-// decode) throws std::runtime_error naming the op and the shape, instead of dropping a gradient.
+// leaves, as the reference's device rows do; the walk's grad_stage_flush puts them in `grads`. A
+// record whose layout is malformed is left untouched, as the reference's rows do. Any rank, and
+// any K or N of an activation, a factor or a cotangent, is served through zero padding (the served
+// shapes below). A well-formed record this build cannot serve throws std::runtime_error naming the
+// op and the shape, instead of dropping a gradient: a stored weight whose N or K is not a multiple
+// of 128 (its planes are laid out for those dims), or whose encoding is not a form the decode
+// reads.
 //
 // Numerics: activations and weights arrive as f64 copies of bf16 values and are uploaded exactly;
 // a cotangent (an arbitrary f64) is split into a bf16 [hi | lo] pair and both halves are

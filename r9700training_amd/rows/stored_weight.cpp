@@ -32,6 +32,7 @@ using Key = std::tuple<const void*, const void*, int64_t, int64_t>;
 struct Store {
     std::mutex mu;
     std::map<Key, Entry> weights;
+    uint8_t* pinned = nullptr;  // the print's staging buffer (pinned host memory, sizeof(Print))
 };
 
 Store& store() {
@@ -93,10 +94,15 @@ R97IqrDecodeDesc describe(const R97Encoding* enc, const void* raw, int64_t rows,
     return d;
 }
 
-Print print_of(const R97Encoding* enc, const void* raw, int64_t rows, int64_t cols) {
+// The print of the weight's planes as they are on `stream`: every piece copied on the stream into
+// the store's pinned buffer, then one synchronisation (a lookup costs one round trip, not four
+// blocking copies).
+Print print_of(const R97Encoding* enc, const void* raw, int64_t rows, int64_t cols, hipStream_t stream,
+               uint8_t* pinned) {
     Print p{};
     int64_t off[R97_ENC_MAX_PLANES] = {};
     if (r97_enc_plane_offsets(enc, rows, cols, off) < 0) return p;
+    std::memset(pinned, 0, sizeof p);
     int at = 0;
     for (int i = 0; i < enc->n_planes && at < 4; ++i) {
         const char* role = enc->plane[i].role;
@@ -104,10 +110,12 @@ Print print_of(const R97Encoding* enc, const void* raw, int64_t rows, int64_t co
         const int64_t bytes = r97_enc_plane_bytes(&enc->plane[i], rows, cols);
         const int64_t n = bytes < 64 ? bytes : 64;
         const uint8_t* base = static_cast<const uint8_t*>(raw) + off[i];
-        if (hipMemcpy(p.b[at++], base, (size_t)n, hipMemcpyDeviceToHost) != hipSuccess ||
-            hipMemcpy(p.b[at++], base + bytes - n, (size_t)n, hipMemcpyDeviceToHost) != hipSuccess)
+        if (hipMemcpyAsync(pinned + 64 * at++, base, (size_t)n, hipMemcpyDeviceToHost, stream) != hipSuccess ||
+            hipMemcpyAsync(pinned + 64 * at++, base + bytes - n, (size_t)n, hipMemcpyDeviceToHost, stream) != hipSuccess)
             fail("reading the planes failed", rows, cols);
     }
+    if (hipStreamSynchronize(stream) != hipSuccess) fail("reading the planes failed", rows, cols);
+    std::memcpy(&p, pinned, sizeof p);
     return p;
 }
 
@@ -120,7 +128,11 @@ const R97qWeight* device_weight_get(const R97Encoding* enc, const void* raw, int
     Store& s = store();
     std::lock_guard<std::mutex> lock(s.mu);
     const Key key{enc, raw, rows, cols};
-    const Print print = print_of(enc, raw, rows, cols);
+    if (!s.pinned && hipHostMalloc(reinterpret_cast<void**>(&s.pinned), sizeof(Print)) != hipSuccess) {
+        s.pinned = nullptr;
+        fail("pinned staging allocation failed", rows, cols);
+    }
+    const Print print = print_of(enc, raw, rows, cols, static_cast<hipStream_t>(stream), s.pinned);
     const auto it = s.weights.find(key);
     if (it != s.weights.end()) {
         if (same(it->second.enc, *enc) && std::memcmp(&it->second.print, &print, sizeof print) == 0)

@@ -170,6 +170,27 @@ def test_affine_form():
     assert np.array_equal(codes.astype(np.int32), vals.astype(np.int32) - zero)
 
 
+def test_affine_zero_i8():
+    """src/iqr_form.h:110-124: the zero plane may be any dtype of 1-8 bits (rad_dtype_bits), so an i8
+    zero plane is the same grid as the u8 one, read as 8 unsigned bits; a 12-bit or f32 zero is
+    refused."""
+    rows, cols = 256, 256
+    e, planes, vals = affine_form(rows, cols)
+    iz = role_index(e, "zero")
+    e.plane[iz].dtype = R.R97_DT_I8
+    d = derive(e, planes, rows, cols)
+    assert d is not None, "an i8 zero plane is an affine description"
+    assert d.affine == 1 and d.zero_bits == 8 and d.zero_row_bytes == cols // 128
+    codes, _ = oracle_decode(d)
+    zero = (np.arange(cols)[None, :] // 128 + 1).astype(np.int32)
+    assert np.array_equal(codes.astype(np.int32), vals.astype(np.int32) - zero)
+    for dt in (R.R97_DT_U[12], R.R97_DT_F32):
+        e, planes, _ = affine_form(rows, cols)
+        e.plane[role_index(e, "zero")].dtype = dt
+        planes[iz] = np.zeros(plane_bytes(e, iz, rows, cols), np.uint8)
+        assert derive(e, planes, rows, cols) is None, dt
+
+
 def test_refusals():
     """tests/host/iqr_form.cpp:320-342 (check_refusals)."""
     rows, cols = 256, 256

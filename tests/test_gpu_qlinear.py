@@ -116,6 +116,67 @@ def test_bf16_outputs_and_teeth():
     assert rel_l2(got["Y"], ref["y"] + 0.02 * np.abs(ref["y"]).mean()) > TOL_BASE
 
 
+# Weights whose last trellis run is short (rows_all % run_rows != 0): its tail-biting seam wraps to
+# that short run's own top segment (src/iqr_decode.h:278-315; the reference pins the case in
+# tests/host/iqr_decode.cpp:311-338). The fused kernels read the seam in both walks.
+SHORT_RUNS = [
+    # bits, run, N, K
+    (3, 256, 640, 256),  # runs 256, 256, 128
+    (4, 96, 256, 128),   # runs 96, 96, 64
+    (5, 256, 384, 256),  # runs 256, 128
+    (6, 96, 128, 256),   # runs 96, 32: the shortest run
+]
+
+
+def _decode_mode(mode):
+    from r9700training_amd import R97Q_DECODE_AUTO, R97Q_DECODE_FUSED, R97Q_DECODE_ONCE, lib
+
+    return lib(), {"fused": R97Q_DECODE_FUSED, "once": R97Q_DECODE_ONCE}[mode], R97Q_DECODE_AUTO
+
+
+@pytest.mark.parametrize("mode", ["fused", "once"])
+@pytest.mark.parametrize("bits,run,N,K", SHORT_RUNS)
+def test_short_last_run_decode_is_exact(bits, run, N, K, mode):
+    """The identity read-back of test_fused_decode_is_exact over weights with a short last run, on the
+    fused kernels (the decode in the main loop) and on the decode-once path (the same lanes into the
+    workspace): both walks give bf16(code * scale) bit for bit, the seam rows included."""
+    print(f"case bits={bits} run={run} N={N} K={K} mode={mode}", flush=True)
+    from r9700training_amd.qlinear import qlinear_lora_bwd, qlinear_lora_fwd
+
+    L, m, auto = _decode_mode(mode)
+    p = weight_planes(N, K, bits, run, seed=bits * 11 + run + N)
+    keep = []
+    w = prepared(p, keep)
+    assert w.w.bits == bits, "the trellis form itself, not the int8-code form"
+    codes, scale = host_weight(p)
+    Wb = S.bf16_bits_to_f32(S.f32_to_bf16_bits(
+        (codes.astype(np.float32) * np.repeat(S.bf16_bits_to_f32(scale), 128, axis=1))))
+    L.r97q_set_decode_once(m)
+    try:
+        Y, _ = qlinear_lora_fwd(w, torch.eye(K, dtype=torch.bfloat16, device="cuda"), y_dtype=torch.float32)
+        dX, _, _ = qlinear_lora_bwd(w, None, torch.eye(N, dtype=torch.bfloat16, device="cuda"),
+                                    dx_dtype=torch.float32)
+        torch.cuda.synchronize()
+    finally:
+        L.r97q_set_decode_once(auto)
+    assert np.array_equal(Y.cpu().numpy().T.view(np.uint32), Wb.view(np.uint32))
+    assert np.array_equal(dX.cpu().numpy().view(np.uint32), Wb.view(np.uint32))
+
+
+@pytest.mark.parametrize("bits,run,N,K", SHORT_RUNS)
+def test_short_last_run_parity(bits, run, N, K):
+    """Y, dX within 2e-3 and t, dA, dB within 1e-4 of the host rows over the same weights, at a token
+    count that is not a multiple of the 512-token tile."""
+    T, r = 300, 16
+    print(f"case T={T} N={N} K={K} r={r} bits={bits} run={run}", flush=True)
+    got, ref = run_case(T, N, K, r, bits, run, seed=N + K + bits)
+    ey, edx = rel_l2(got["Y"], ref["y"]), rel_l2(got["dX"], ref["dx"])
+    et, eA, eB = rel_l2(got["t"], ref["t"]), rel_l2(got["dA"], ref["dA"]), rel_l2(got["dB"], ref["dB"])
+    print(f"  rel L2  Y {ey:.3e}  dX {edx:.3e}  t {et:.3e}  dA {eA:.3e}  dB {eB:.3e}", flush=True)
+    assert ey <= TOL_BASE and edx <= TOL_BASE
+    assert et <= TOL_ADAPTER and eA <= TOL_ADAPTER and eB <= TOL_ADAPTER
+
+
 def test_dx_accumulate_and_grad_accumulate():
     from r9700training_amd.qlinear import qlinear_lora_bwd, qlinear_lora_fwd
 

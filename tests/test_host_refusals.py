@@ -20,3 +20,16 @@ def test_bwd_prep_needs_t_with_a_rank():
     rc = f(256, 256, 256, fake, fake, fake, None, 16, 2.0, fake, 1 << 30, None)
     assert rc == R97Q_EINVAL
     assert b"t" in lib.r97q_last_error()
+
+
+def test_mfma_probe_refuses_a_short_out_buffer():
+    """r97q_mfma_probe writes 256 * 512 floats: an out_count below that is refused before the launch."""
+    lib = C.CDLL(os.path.join(ROOT, "r9700training_amd", "libr97q.so"))
+    f = lib.r97q_mfma_probe
+    f.restype = C.c_int
+    f.argtypes = [C.c_int32, C.c_int32, C.c_void_p, C.c_int64, C.c_void_p]
+    lib.r97q_last_error.restype = C.c_char_p
+    fake = C.c_void_p(0x1000)  # never dereferenced: the refusal comes first
+    assert f(100, 0, fake, 256 * 512 - 1, None) == R97Q_EINVAL
+    assert b"out_count" in lib.r97q_last_error()
+    assert f(0, 0, fake, 256 * 512, None) == R97Q_EINVAL
