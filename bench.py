@@ -96,13 +96,15 @@ def parse():
                     help="the prepared weight the kernels read: the trellis stream (decoded inside the "
                          "kernels), or the same weight in the int8-code form")
     ap.add_argument("--workload", default="qlinear",
-                    choices=["qlinear", "vocab_head", "c3_block", "c4_attn", "c5_stack", "coded_fwd"],
+                    choices=["qlinear", "vocab_head", "c3_block", "c4_attn", "c5_stack", "coded_fwd", "ref_shapes"],
                     help="qlinear: the C2 fwd+bwd step (the headline); vocab_head: the vocabulary head's "
                          "transposed product at a 248320-row head, n_embd 2048, --vocab-rows token rows; "
                          "c3_block / c4_attn / c5_stack: one whole LoRA step of BASELINE's MLP block (T=8192, "
                          "rank 32), attention projections (T=16384, rank 64) or 24-layer stack (T=32768, rank 16 "
                          "on every projection); "
-                         "coded_fwd: gemm_nt_q's twin (int8 codes x the int8-code weight) at C2's square layer")
+                         "coded_fwd: gemm_nt_q's twin (int8 codes x the int8-code weight) at C2's square layer; "
+                         "ref_shapes: the stored-weight gemm_nt twin and adjoint alone at the shapes the reference "
+                         "publishes its device adjoint at (docs/kernels/linear.md:261-268)")
     ap.add_argument("--decode", default="auto", choices=sorted(DECODE_MODES),
                     help="how the base products meet the weight (r97q_set_decode_once): fused (each tile "
                          "decoded in the product's main loop, once a 512-token panel), once (the whole weight "
@@ -430,6 +432,98 @@ def coded_fwd_bench(args):
     }), flush=True)
 
 
+# The shapes the reference publishes its gemm_nt device adjoint at (docs/kernels/linear.md:261-268):
+# name, tokens M, outputs N, inputs K (dX[M, K] = dY[M, N] . W[N, K]; the twin Y[M, N] = X . W^T), and
+# the reference's R9700 kernel time for the adjoint in ms (context only: another card and kernel).
+REF_SHAPES = [
+    ("attn_k/v", 4096, 1024, 5120, 1.06),
+    ("attn_output", 4096, 5120, 6144, 5.73),
+    ("attn_qg", 1024, 12288, 5120, 3.39),
+    ("attn_qg", 4096, 12288, 5120, 21.34),
+    ("ssm_inz", 4096, 16384, 5120, 35.00),
+    ("ffn_down", 4096, 5120, 17408, 18.47),
+    ("ffn_gate_up", 1024, 34816, 5120, 11.38),
+    ("ffn_gate_up", 4096, 34816, 5120, 53.91),
+]
+
+
+def ref_shapes_bench(args):
+    """The stored-weight gemm_nt twin (Y = X . W^T) and adjoint (dX = dY . W) alone, no adapter, at
+    the reference's published shapes: each product timed by HIP events around `steps` launches after
+    a clock settle, over a b5 trellis.mad weight with an f32 row scale and scale.col (random packed
+    codes; every byte pattern is a valid code), X and dY bf16 N(0,1), outputs f32."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    from r9700training_amd import R97Q_F32, _ptr, _stream, check, lib
+    from r9700training_amd.qlinear import QWeight, bwd_workspace, device_desc, fwd_workspace
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = lib()
+    L.r97q_set_decode_once(DECODE_MODES[args.decode])
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    rng = np.random.default_rng(args.seed)
+    st = _stream(torch.cuda.current_stream())
+    P = _ptr
+    out = []
+    for name, M, N, K, ref_ms in REF_SHAPES:
+        codes = torch.randint(0, 256, (N, K * 5 // 8), dtype=torch.uint8, device=dev, generator=g)
+        scale = torch.from_numpy((0.0005 + 0.01 * rng.random(N)).astype(np.float32).view(np.uint8)).to(dev)
+        cf = torch.from_numpy((0.5 + rng.random(K // 128)).astype(np.float32)).to(dev)
+        d = device_desc(dict(codes=codes, scale=scale), N, K, dict(
+            bits=5, state_bits=16, run_rows=256, rb=1, mad=1, round_mad=1, mad_a=0x2F1E3D | 1,
+            mad_b=0x9E3779B9, codes_row_bytes=K * 5 // 8, scale_dtype=0, scale_block_cols=0, scale_row_bytes=4))
+        w = QWeight(d, scale_col=cf)
+        X = torch.randn((M, K), dtype=torch.bfloat16, device=dev, generator=g)
+        dY = torch.randn((M, N), dtype=torch.bfloat16, device=dev, generator=g)
+        Y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        dX = torch.empty((M, K), dtype=torch.float32, device=dev)
+        wsf, wsb = fwd_workspace(M, N, K, 0, dev), bwd_workspace(M, N, K, 0, dev)
+        check(L.r97q_lora_fwd_prep(M, N, K, P(X), None, 0, 1.0, None, P(wsf), wsf.numel(), st), "fwd_prep")
+        check(L.r97q_lora_bwd_prep(M, N, K, P(dY), None, None, None, 0, 1.0, P(wsb), wsb.numel(), st), "bwd_prep")
+
+        def fwd():
+            check(L.r97q_qlinear_fwd_base(C.byref(w.w), P(X), M, None, 0, P(Y), R97Q_F32, P(wsf), wsf.numel(), st),
+                  "fwd_base")
+
+        def dx():
+            check(L.r97q_qlinear_dx_base(C.byref(w.w), P(dY), M, 0, P(dX), R97Q_F32, 0, P(wsb), wsb.numel(), st),
+                  "dx_base")
+
+        res = {"shape": f"{name} {M} x {N} x {K}", "M": M, "N": N, "K": K}
+        for tag, f, out_cols in (("twin", fwd, N), ("adjoint", dx, K)):
+            settle(f, 0.3, torch)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                f()
+            e1.record()
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / args.steps
+            tf = 2 * M * N * K / (ms * 1e-3) / 1e12
+            tiles = ((M + 511) // 512) * (out_cols // 128)
+            res[tag] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                        "tiles_512x128": tiles}
+        res["reference_r9700_adjoint_kernel_ms"] = ref_ms
+        out.append(res)
+        print(json.dumps(res), file=sys.stderr, flush=True)
+        del w, codes, scale, cf, X, dY, Y, dX, wsf, wsb
+        torch.cuda.empty_cache()
+    print(json.dumps({
+        "metric": "stored-weight gemm_nt twin / adjoint TFLOP/s at the reference's published shapes",
+        "value": round(sum(2 * r["M"] * r["N"] * r["K"] * 2 for r in out) /
+                       sum((r["twin"]["ms"] + r["adjoint"]["ms"]) * 1e-3 for r in out) / 1e12, 3),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic: random b5 trellis.mad codes, f32 row scale + scale.col; X, dY ~ N(0,1) bf16",
+        "config": {"workload": "ref_shapes: docs/kernels/linear.md:261-268, M x N x K, no adapter, outputs f32",
+                   "decode": args.decode},
+        "shapes": out,
+    }), flush=True)
+
+
 def stack_bench(args):
     """One complete LoRA step of a STACKS workload (C5: the 24-layer stack) on one GPU: the forward
     of every projection, layer by layer, then the backward in reverse (dX, dA, dB, the adapters'
@@ -577,6 +671,8 @@ def main():
         return stack_bench(args)
     if args.workload == "coded_fwd":
         return coded_fwd_bench(args)
+    if args.workload == "ref_shapes":
+        return ref_shapes_bench(args)
 
     from r9700training_amd import R97Q_BF16, R97Q_F32, _ptr, _stream, check, lib
     from r9700training_amd.qlinear import bwd_workspace, fwd_workspace

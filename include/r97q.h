@@ -301,7 +301,8 @@ int r97q_iqr_encode_trellis(const float* W, int64_t N, int64_t K, int32_t bits, 
  * of the reference rows named beside it.
  *
  * Forward: t = X.A^T (f32 into t_out) and the adapter operand of the fused kernel
- *          (lora_shrink_twin, src/adjoint/host/lora.cpp:226-244). rank 0: a no-op. */
+ *          (lora_shrink_twin, src/adjoint/host/lora.cpp:226-244), and X's tiled copy in the workspace
+ *          (the fused kernel's token operand). rank 0: only the tiled copy of X. */
 int r97q_lora_fwd_prep(int64_t T, int64_t N, int64_t K, const uint16_t* X, const uint16_t* A,
                        int32_t rank, float scale, float* t_out, void* workspace,
                        int64_t workspace_bytes, R97IqrStream stream);

@@ -15,6 +15,7 @@
 // the LDS-staged kernels of qlinear_fused.hip on the row-major operand.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 
@@ -69,14 +70,54 @@ Shape shape(int64_t T, int64_t N, int64_t K, int r) {
     return Shape{T, N, K, r, once};
 }
 
+// Split-K of the fused kernel (rt::Params::ksplit). A launch holds tiles = ceil(T/512) x outputs/128
+// workgroups, one a CU at a time over the card's 256 CUs; when the tiles leave much of the last
+// round of CUs idle and the reduction is long, the reduction is dealt over S ranges (S x tiles
+// workgroups), each range's f32 partial product written to the workspace and added in range order
+// by a second launch. The choice minimises a model of the launch's time in microseconds, measured
+// at C2 and at the reference's published shapes: a 64-deep step of a full round of tiles takes
+// ~1.9 us, a partial last round with a fraction f of the CUs busy runs at a higher clock and takes
+// (0.4 + 0.6 f) of a full round's time, a round's prologue and epilogue ~3 us, and the partials
+// cost S x T x outputs x 8 bytes (written, then read) at ~5 TB/s plus ~4 us for the added launch.
+// A split needs at least 16 steps a range and must beat no split by 10%. Deterministic in the
+// shape, so a call's bits never depend on anything else.
+constexpr int kSplitMax = 8;
+int ksplit_for(int64_t T, int64_t outputs, int64_t red) {
+    const int64_t tiles = ((T + rt::kBM - 1) / rt::kBM) * (outputs / rt::kBN);
+    const int64_t nsteps = red / rt::kStep;
+    auto cost = [&](int S) {
+        const double u = (double)(tiles * S) / 256.0;
+        const double full = std::floor(u), frac = u - full;
+        const double rounds = full + (frac > 0 ? 0.4 + 0.6 * frac : 0.0);
+        double t = rounds * ((double)nsteps / S * 1.9 + 3.0);
+        if (S > 1) t += (double)S * (double)T * (double)outputs * 8.0 / 5.0e6 + 4.0;
+        return t;
+    };
+    const double t1 = cost(1);
+    int best = 1;
+    double best_t = t1;
+    for (int S = 2; S <= kSplitMax; ++S) {
+        if (nsteps / S < 16) break;
+        const double t = cost(S);
+        if (t < 0.9 * t1 && t < best_t) {
+            best = S;
+            best_t = t;
+        }
+    }
+    return best;
+}
+
 // Workspace layout. Forward: Xt (X's tiled copy, act_tiles.h) | P [T, 2r] | Apad [rd, K] (when r
 // is not a multiple of 16) | Wt (the weight's decoded tiles, rt::wt_bytes, when decode_once).
 // Backward: dYt (dY's tiled copy) | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt]
 // | partA [chunks, r, K] | partB [chunks, r, N] (f32 partial sums of the factor gradients) | done
 // (bwd_counters) | Wt (as the forward's).
-// Wt is -1 where the layout has none.
+// Either direction then holds Sp [S, T, outputs] f32: the split-K partials, when the fused kernel
+// splits (ksplit > 1; never on the decode-once path, nor for the entry that allocates nothing).
+// Wt and Sp are -1 where the layout has none.
 struct FwdWs {
-    int64_t Xt, P, Apad, Wt, total;
+    int64_t Xt, P, Apad, Wt, Sp, total;
+    int ksplit;
 };
 FwdWs fwd_ws(const Shape& s, bool fused_only = false) {
     FwdWs w{};
@@ -88,24 +129,39 @@ FwdWs fwd_ws(const Shape& s, bool fused_only = false) {
         w.Apad = w.P + align256(s.T * 2 * s.r * 2);
         w.total = w.Apad + (rd != s.r ? align256((int64_t)rd * s.K * 2) : 0);
     }
-    w.Wt = -1;
+    w.Wt = w.Sp = -1;
+    w.ksplit = 1;
     if (!fused_only && s.once) {
         w.Wt = w.total;
         w.total += align256(rt::wt_bytes(s.N, s.K));
+    } else if (!fused_only) {
+        w.ksplit = ksplit_for(s.T, s.N, s.K);
+        if (w.ksplit > 1) {
+            w.Sp = w.total;
+            w.total += align256((int64_t)w.ksplit * s.T * s.N * 4);
+        }
     }
     return w;
 }
 struct BwdWs {
-    int64_t dYt, At, P, PtA, PtB, partA, partB, done, Wt, total;
+    int64_t dYt, At, P, PtA, PtB, partA, partB, done, Wt, Sp, total;
+    int ksplit;
 };
 // the backward's counters, zeroed by its down product: the gradient launch's column blocks (dA's,
 // then dB's)
 int64_t bwd_counters(const Shape& s) { return grad_blocks(s.K) + grad_blocks(s.N); }
 void bwd_ws_wt(const Shape& s, BwdWs& w) {
-    w.Wt = -1;
+    w.Wt = w.Sp = -1;
+    w.ksplit = 1;
     if (s.once) {
         w.Wt = w.total;
         w.total += align256(rt::wt_bytes(s.N, s.K));
+    } else {
+        w.ksplit = ksplit_for(s.T, s.K, s.N);
+        if (w.ksplit > 1) {
+            w.Sp = w.total;
+            w.total += align256((int64_t)w.ksplit * s.T * s.K * 4);
+        }
     }
 }
 BwdWs bwd_ws(const Shape& s) {
@@ -282,7 +338,7 @@ int fwd_prep(const Shape& sh, const uint16_t* X, const uint16_t* A, float scale,
 // without, the fused kernel decoding in its main loop
 int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act, const uint16_t* P,
             const uint16_t* Q, void* out, int32_t out_dtype, int32_t accumulate, uint8_t* wt, hipStream_t s,
-            const rt::Params::Sums* sums = nullptr) {
+            const rt::Params::Sums* sums = nullptr, int ksplit = 1, float* part = nullptr) {
     rt::Params p{};
     p.act = act;
     p.T = sh.T;
@@ -302,6 +358,8 @@ int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act,
     p.mtiles = (int)((sh.T + rt::kBM - 1) / rt::kBM);
     p.otiles = (int)((fwd ? sh.N : sh.K) / rt::kBN);
     p.wt = wt;
+    p.ksplit = wt || !part ? 1 : ksplit;
+    p.part = p.ksplit > 1 ? part : nullptr;
     if (sums && !fwd) {
         p.sums[0] = sums[0];
         p.sums[1] = sums[1];
@@ -326,7 +384,12 @@ int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act,
         case 6: go(rt::launch_fwd<6>, rt::launch_dx<6>); break;
         default: go(rt::launch_fwd<R97Q_CODES8>, rt::launch_dx<R97Q_CODES8>); break;
     }
-    return launch_status(fwd ? "qlinear_rt_kernel<fwd>" : "qlinear_rt_kernel<dx>");
+    if (int e = launch_status(fwd ? "qlinear_rt_kernel<fwd>" : "qlinear_rt_kernel<dx>")) return e;
+    if (p.ksplit > 1) {
+        rt::launch_split_reduce(p, fwd, s);
+        return launch_status("split_reduce_kernel");
+    }
+    return R97Q_OK;
 }
 
 int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* B, void* Y, int32_t y_dtype, uint8_t* wsb,
@@ -334,7 +397,8 @@ int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* B, void* Y, i
     const FwdWs ws = fwd_ws(sh, fused_only);
     return rt_base(w, true, sh, reinterpret_cast<const uint16_t*>(wsb + ws.Xt),
                    reinterpret_cast<const uint16_t*>(wsb + ws.P), B, Y, y_dtype, 0,
-                   ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s);
+                   ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s, nullptr, ws.ksplit,
+                   ws.Sp >= 0 ? reinterpret_cast<float*>(wsb + ws.Sp) : nullptr);
 }
 
 // B^T [rd, N] (zero rows past r), A^T [K, r]; dt = s.dY.B as P = [hi | lo](dt) for the fused dX
@@ -412,7 +476,8 @@ int dx_base(const R97qWeight* w, const Shape& sh, void* dX, int32_t dx_dtype, in
     return rt_base(w, false, sh, reinterpret_cast<const uint16_t*>(wsb + ws.dYt),
                    reinterpret_cast<const uint16_t*>(wsb + ws.P), reinterpret_cast<const uint16_t*>(wsb + ws.At), dX,
                    dx_dtype, accumulate, ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s,
-                   sums[0].part || sums[1].part ? sums : nullptr);
+                   sums[0].part || sums[1].part ? sums : nullptr, ws.ksplit,
+                   ws.Sp >= 0 ? reinterpret_cast<float*>(wsb + ws.Sp) : nullptr);
 }
 
 // the LDS-staged dX kernel over row-major dY with the coded trunk's activation scale in its

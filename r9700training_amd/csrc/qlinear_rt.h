@@ -29,6 +29,12 @@ struct Params {
     int out_f32;
     int accumulate;            // dX only: add into `out`
     int mtiles, otiles;
+    // split-K (fused kernel only): the reduction's steps are dealt over `ksplit` ranges, each a
+    // workgroup per output tile, each writing its f32 partial product into part[z] [T, outputs]
+    // (the adapter's epilogue in range 0 only); launch_split_reduce then adds them, in range
+    // order, into `out`. ksplit 1: no split, the product written into `out` directly.
+    int ksplit;
+    float* part;
     const uint8_t* wt;         // the weight decoded once a call (launch_predecode), for launch_pd
     // dX only: the factor gradients' deferred chunk sums of the gradient launch before this one,
     // added into their outputs in chunk order, the elements spread over the launch's workgroups
@@ -51,6 +57,8 @@ void launch_dx(const Params& p, hipStream_t s);
 template <int BITS>
 void launch_predecode(const Params& p, bool fwd, uint8_t* out, hipStream_t s);
 void launch_pd(const Params& p, bool fwd, hipStream_t s);
+// out (+)= part[0] + part[1] + ... + part[ksplit-1], in that order (the split product's partials)
+void launch_split_reduce(const Params& p, bool fwd, hipStream_t s);
 inline int64_t wt_bytes(int64_t N, int64_t K) { return N * K * 2; }
 
 }  // namespace rt

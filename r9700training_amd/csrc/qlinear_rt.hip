@@ -133,7 +133,8 @@ struct Wave {
     int64_t o0;      // the tile's first output
     int64_t sstride; // elements between consecutive steps of the tiled operand
     int lane;
-    int nsteps;
+    int nsteps;      // the walk's end: steps s0 .. nsteps-1 (an even count)
+    int s0 = 0;      // the walk's first step (split-K: the range's first)
     // forward, trellis forms: the stream offsets of the lane's 32-row segment g and of its halo (the
     // segment below, or the run's top one at the tail-biting seam)
     int64_t fwd_seg = 0, fwd_halo = 0;
@@ -342,21 +343,21 @@ struct Wave {
         bf16x8 b0[kNI], b1[kNI];
         // the loads outstanding at the loop's head are, in order, the words of step 1 and the
         // token fragments of step 0's rounds 0-2: the order every later step leaves them in
-        words(0, wa);
+        words(s0, wa);
         decode<0>(wa, t0);
         decode<1>(wa, t0);
         decode<2>(wa, t0);
         __builtin_amdgcn_sched_barrier(0);
-        words(nsteps > 1 ? 1 : 0, wb);
+        words(s0 + 1 < nsteps ? s0 + 1 : s0, wb);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 3; ++j) tokens(act, blk, sstride, 0, j, t);
+        for (int j = 0; j < 3; ++j) tokens(act, blk, sstride, s0, j, t);
         __builtin_amdgcn_sched_barrier(0);
         tile_barrier();
         frags(t0, lane, 0, b0);
         // step s decodes tile s+1 from the words of step s+1 and fetches those of step s+2 into
         // the set step s+1 decoded from; unrolled by two so the sets keep fixed names
-        for (int s = 0; s < nsteps; s += 2) {
+        for (int s = s0; s < nsteps; s += 2) {
             step(s, act, blk, t, t0, t1, wb, wa, b0, b1, acc);
             step(s + 1, act, blk, t, t1, t0, wa, wb, b0, b1, acc);
         }
@@ -364,7 +365,7 @@ struct Wave {
 };
 
 template <bool FWD, int WAVES, int WAVE>
-__device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t* t1, int mt, int ot) {
+__device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t* t1, int mt, int ot, int z) {
     using G = Geo<WAVES>;
     f32x16 acc[G::kMI][kNI];
 #pragma unroll
@@ -373,12 +374,18 @@ __device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t*
         for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = (f32x16){};
     const int lane = threadIdx.x & 63;
     const int64_t red = FWD ? p.K : p.N;
+    const int pairs = (int)(red / kStep) / 2;  // the steps go in pairs: a range holds whole pairs
     Wave<FWD, WAVES, WAVE> w{p, red, (int64_t)mt * kBM + G::kWaveM * WAVE, (int64_t)ot * kBN,
-                             act_tile_blocks(p.T) * kBlock, lane, (int)(red / kStep)};
+                             act_tile_blocks(p.T) * kBlock, lane, 2 * (int)((int64_t)(z + 1) * pairs / p.ksplit)};
+    w.s0 = 2 * (int)((int64_t)z * pairs / p.ksplit);
     w.setup();
     w.run(p.act, t0, t1, acc);
-    if (p.rank > 0) adapter<G::kMI>(p.P, p.Q, p.rank, w.m0, w.o0, p.T, lane, acc);
-    store<G::kMI>(acc, p.out, FWD ? p.N : p.K, w.m0, w.o0, p.T, lane, p.out_f32, FWD ? 0 : p.accumulate);
+    const int64_t ld = FWD ? p.N : p.K;
+    if (p.rank > 0 && z == 0) adapter<G::kMI>(p.P, p.Q, p.rank, w.m0, w.o0, p.T, lane, acc);
+    if (p.ksplit > 1)
+        store<G::kMI>(acc, p.part + (int64_t)z * p.T * ld, ld, w.m0, w.o0, p.T, lane, 1, 0);
+    else
+        store<G::kMI>(acc, p.out, ld, w.m0, w.o0, p.T, lane, p.out_f32, FWD ? 0 : p.accumulate);
     if constexpr (!FWD)
         if (p.sums[0].part || p.sums[1].part) sum_chunks<WAVES>(p);
 }
@@ -386,20 +393,23 @@ __device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t*
 template <bool FWD, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, 1) void qlinear_rt_kernel(const Params p) {
     __shared__ __attribute__((aligned(16))) uint8_t t0[kTileBytes], t1[kTileBytes];
-    const int tile = xcd_tile(blockIdx.x, p.mtiles * p.otiles);
+    // split-K: the grid is ksplit x tiles workgroups, numbered (range, tile) with the tiles inner
+    const int ntiles = p.mtiles * p.otiles;
+    const int lin = xcd_tile(blockIdx.x, ntiles * p.ksplit);
+    const int z = lin / ntiles, tile = lin % ntiles;
     const int mt = tile / p.otiles, ot = tile % p.otiles;
     switch (threadIdx.x >> 6) {
-        case 0: wave_main<FWD, WAVES, 0>(p, t0, t1, mt, ot); break;
-        case 1: wave_main<FWD, WAVES, 1>(p, t0, t1, mt, ot); break;
-        case 2: wave_main<FWD, WAVES, 2>(p, t0, t1, mt, ot); break;
-        case 3: wave_main<FWD, WAVES, 3>(p, t0, t1, mt, ot); break;
+        case 0: wave_main<FWD, WAVES, 0>(p, t0, t1, mt, ot, z); break;
+        case 1: wave_main<FWD, WAVES, 1>(p, t0, t1, mt, ot, z); break;
+        case 2: wave_main<FWD, WAVES, 2>(p, t0, t1, mt, ot, z); break;
+        case 3: wave_main<FWD, WAVES, 3>(p, t0, t1, mt, ot, z); break;
         default:
             if constexpr (WAVES == 8) {
                 switch (threadIdx.x >> 6) {
-                    case 4: wave_main<FWD, WAVES, 4>(p, t0, t1, mt, ot); break;
-                    case 5: wave_main<FWD, WAVES, 5>(p, t0, t1, mt, ot); break;
-                    case 6: wave_main<FWD, WAVES, 6>(p, t0, t1, mt, ot); break;
-                    default: wave_main<FWD, WAVES, 7>(p, t0, t1, mt, ot); break;
+                    case 4: wave_main<FWD, WAVES, 4>(p, t0, t1, mt, ot, z); break;
+                    case 5: wave_main<FWD, WAVES, 5>(p, t0, t1, mt, ot, z); break;
+                    case 6: wave_main<FWD, WAVES, 6>(p, t0, t1, mt, ot, z); break;
+                    default: wave_main<FWD, WAVES, 7>(p, t0, t1, mt, ot, z); break;
                 }
             }
             break;
@@ -492,13 +502,13 @@ void launch_predecode<R97Q_BITS>(const Params& p, bool fwd, uint8_t* out, hipStr
 
 template <>
 void launch_fwd<R97Q_BITS>(const Params& p, hipStream_t s) {
-    hipLaunchKernelGGL((qlinear_rt_kernel<true, R97Q_RT_WAVES>), dim3((unsigned)(p.mtiles * p.otiles)),
+    hipLaunchKernelGGL((qlinear_rt_kernel<true, R97Q_RT_WAVES>), dim3((unsigned)(p.mtiles * p.otiles * p.ksplit)),
                        dim3(64 * R97Q_RT_WAVES), 0, s, p);
 }
 
 template <>
 void launch_dx<R97Q_BITS>(const Params& p, hipStream_t s) {
-    hipLaunchKernelGGL((qlinear_rt_kernel<false, R97Q_RT_WAVES>), dim3((unsigned)(p.mtiles * p.otiles)),
+    hipLaunchKernelGGL((qlinear_rt_kernel<false, R97Q_RT_WAVES>), dim3((unsigned)(p.mtiles * p.otiles * p.ksplit)),
                        dim3(64 * R97Q_RT_WAVES), 0, s, p);
 }
 

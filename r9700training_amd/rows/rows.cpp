@@ -764,10 +764,13 @@ R97_REGISTER_ADJOINT_IF_F("gemm_nt", device, gemm_nt_device, serves_bf16, 1)
 R97_REGISTER_ADJOINT_IF("had_quant_act_i8g", device, had_quant_device, serves_rotated)
 R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_device, float_act, 1, 2, 3)
 R97_REGISTER_ADJOINT_F("lora_expand", device, lora_expand_device, 1, 2, 3)
+// lora_expand_mm is lora_expand with t rounded to bf16 in its twin only (src/adjoint/host/lora.cpp:
+// 33-35, 420): the rounding has no derivative, so its adjoint is the expand's row
+R97_REGISTER_ADJOINT_F("lora_expand_mm", device, lora_expand_device, 1, 2, 3)
 R97_REGISTER_ADJOINT_IF_F("gemm_nt_q", device, gemm_nt_q_device, serves_i8a8h, 1, 2, 3)
 R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_q_device, coded_act, 2, 3)
 
 R97_REGISTER_ADJOINT_FAMILY(Linear, "gemm_nt", "gemm_nt_q");
-R97_REGISTER_ADJOINT_FAMILY(Lora, "lora_shrink", "lora_expand");
+R97_REGISTER_ADJOINT_FAMILY(Lora, "lora_shrink", "lora_expand", "lora_expand_mm");
 
 }  // namespace r97

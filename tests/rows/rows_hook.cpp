@@ -150,6 +150,10 @@ int rh_registry_selftest() {
     CHECK(adjoint_frozen("lora_expand", Side::device, f32) == (std::vector<int>{1, 2, 3}));
     CHECK(family_find("gemm_nt") == AdjointFamily::Linear);
     CHECK(family_find("lora_shrink") == AdjointFamily::Lora && family_find("lora_expand") == AdjointFamily::Lora);
+    CHECK(adjoint_find("lora_expand_mm", Side::device, bf16, nullptr) ==
+          adjoint_find("lora_expand", Side::device, bf16, nullptr));
+    CHECK(adjoint_frozen("lora_expand_mm", Side::device, f32) == (std::vector<int>{1, 2, 3}));
+    CHECK(family_find("lora_expand_mm") == AdjointFamily::Lora);
 #undef CHECK
     return 0;
 }
@@ -234,12 +238,14 @@ int rh_lora_shrink(int64_t M, int64_t K, int64_t R, int64_t S, const double* x, 
 // the expand's row: t_cot[M, R] += ..., dB: the lora_B leaves written as [S, N, R] (fused: the one
 // [N, S*R] leaf, copied as is), scale [S, N] or null (a 4-operand record), in_place: y is an
 // in-place write whose own slot gets y_cot (returned in d_base[M, N])
-int rh_lora_expand(int64_t M, int64_t N, int64_t R, int64_t S, const double* t, const double* slot, const double* lb,
-                   const double* scale, const double* y_cot, double* t_cot, float* dB, int fused, int in_place,
-                   double* d_base) {
+// the expand's record under `op`: lora_expand, or lora_expand_mm (the same adjoint: the mm form's
+// bf16 rounding of t is in its twin only)
+int rh_lora_expand_op(const char* op, int64_t M, int64_t N, int64_t R, int64_t S, const double* t, const double* slot,
+                      const double* lb, const double* scale, const double* y_cot, double* t_cot, float* dB, int fused,
+                      int in_place, double* d_base) {
     try {
         OpRecord rec;
-        rec.op = "lora_expand";
+        rec.op = op;
         rec.params = {{"dtype", std::string("bf16")}};
         rec.operands = {opd("t", "f32", {M, R}), opd("slot", "i32", {M}), opd("lora_b", "bf16", {S, N, R})};
         std::vector<AdValue> fwd = {val("f32", {M, R}, t), val("i32", {M}, slot), val("bf16", {S, N, R}, lb)};
@@ -256,7 +262,7 @@ int rh_lora_expand(int64_t M, int64_t N, int64_t R, int64_t S, const double* t, 
         ParamSet grads;
         AdjointCall call{rec, fwd, cot, &dc, dB ? &grads : nullptr, "layers.0.q", {}, fused != 0, nullptr, nullptr};
         if (!fused) call.slot_prefix = [](int64_t s) { return "adapter" + std::to_string(s); };
-        row("lora_expand", rec.params)(call);
+        row(op, rec.params)(call);
         std::memcpy(t_cot, dc[0].value.data(), sizeof(double) * (size_t)(M * R));
         if (in_place && d_base) std::memcpy(d_base, dc.back().value.data(), sizeof(double) * (size_t)(M * N));
         if (dB) {
@@ -278,6 +284,12 @@ int rh_lora_expand(int64_t M, int64_t N, int64_t R, int64_t S, const double* t, 
         g_err = e.what();
         return -1;
     }
+}
+
+int rh_lora_expand(int64_t M, int64_t N, int64_t R, int64_t S, const double* t, const double* slot, const double* lb,
+                   const double* scale, const double* y_cot, double* t_cot, float* dB, int fused, int in_place,
+                   double* d_base) {
+    return rh_lora_expand_op("lora_expand", M, N, R, S, t, slot, lb, scale, y_cot, t_cot, dB, fused, in_place, d_base);
 }
 
 // gemm_nt_q's row (the coded trunk): da[M, K] += ..., a codes (values unused by the adjoint),

@@ -44,6 +44,11 @@ SHAPES = [
     ("c5-attn-out", 32768, 2048, 4096, 16),
     ("c5-gate-up", 32768, 6144, 2048, 16),
     ("c5-down", 32768, 2048, 6144, 16),
+    # two of the reference's published shapes (docs/kernels/linear.md:261-268) whose tile counts
+    # leave the CUs mostly idle, so the fused kernel splits their reductions (split-K): attn_k/v's
+    # twin (64 tiles) and attn_qg's adjoint at 1024 tokens (80 tiles)
+    ("ref-attn-kv", 4096, 1024, 5120, 16),
+    ("ref-attn-qg-1024", 1024, 12288, 5120, 16),
 ]
 
 

@@ -46,6 +46,7 @@ def frozen(op, dev, dt, g):
 
 for op, dev, dt, g in [("gemm_nt", 1, "bf16", 0), ("lora_shrink", 1, "bf16", 0), ("lora_shrink", 1, "i8", 128),
                        ("lora_shrink", 1, "fp8_e4m3", 128), ("lora_expand", 1, "bf16", 0),
+                       ("lora_expand_mm", 1, "bf16", 0), ("lora_expand_mm", 0, "bf16", 0),
                        ("gemm_nt_q", 1, "i8a8h", 128), ("gemm_nt", 0, "bf16", 0), ("lora_shrink", 0, "bf16", 0),
                        ("lora_expand", 0, "bf16", 0)]:
     print(op, dev, dt, where(ref.ref_adjoint_find(op.encode(), dev, dt.encode(), g)), frozen(op, dev, dt, g))
@@ -66,7 +67,8 @@ def test_rows_register_into_the_reference_registry():
     assert got[("lora_shrink", "1", "i8")] == "libr97rows.so [2, 3]"
     assert got[("lora_shrink", "1", "fp8_e4m3")] == "libr97rows.so [2, 3]"
     assert got[("lora_expand", "1", "bf16")] == "libr97rows.so [1, 2, 3]"
+    assert got[("lora_expand_mm", "1", "bf16")] == "libr97rows.so [1, 2, 3]"
     assert got[("gemm_nt_q", "1", "i8a8h")] == "libr97rows.so [1, 2, 3]"
     # host rows: still the reference's own
-    for op in ("gemm_nt", "lora_shrink", "lora_expand"):
+    for op in ("gemm_nt", "lora_shrink", "lora_expand", "lora_expand_mm"):
         assert got[(op, "0", "bf16")].startswith("libr97ref.so"), got[(op, "0", "bf16")]

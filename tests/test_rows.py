@@ -33,6 +33,7 @@ def hook():
     L.rh_gemm_nt.argtypes = [C.c_int64, C.c_int64, C.c_int64, _P, _P, _P, _P, _P]
     L.rh_lora_shrink.argtypes = [C.c_int64] * 4 + [_P] * 6 + [C.c_int]
     L.rh_lora_expand.argtypes = [C.c_int64] * 4 + [_P] * 7 + [C.c_int, C.c_int, _P]
+    L.rh_lora_expand_op.argtypes = [C.c_char_p] + [C.c_int64] * 4 + [_P] * 7 + [C.c_int, C.c_int, _P]
     L.rh_weights_prepared.restype = C.c_int64
     return L
 
@@ -149,13 +150,18 @@ def test_lora_shrink_row(M, K, R, S, fused):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,N,R,S,scaled,fused,in_place",
-                         [(128, 256, 16, 1, True, False, True), (200, 384, 8, 2, True, False, False),
-                          (96, 256, 64, 2, False, True, False)])
-def test_lora_expand_row(M, N, R, S, scaled, fused, in_place):
+@pytest.mark.parametrize("op,M,N,R,S,scaled,fused,in_place",
+                         [("lora_expand", 128, 256, 16, 1, True, False, True),
+                          ("lora_expand", 200, 384, 8, 2, True, False, False),
+                          ("lora_expand", 96, 256, 64, 2, False, True, False),
+                          ("lora_expand_mm", 200, 384, 8, 2, True, False, True),
+                          ("lora_expand_mm", 96, 256, 64, 2, False, True, False)])
+def test_lora_expand_row(op, M, N, R, S, scaled, fused, in_place):
+    """The expand's device row, and lora_expand_mm's (the same adjoint: the mm form rounds t to bf16
+    in its twin only, src/adjoint/host/lora.cpp:33-35), against the oracle's host adjoint."""
     from oracle import oracle as O
 
-    print(f"case lora_expand M={M} N={N} R={R} S={S} scaled={scaled} fused={fused} in_place={in_place}", flush=True)
+    print(f"case {op} M={M} N={N} R={R} S={S} scaled={scaled} fused={fused} in_place={in_place}", flush=True)
     L = hook()
     rng = np.random.default_rng(M + N + R + S + 7)
     t = rng.standard_normal((M, R)).astype(np.float32).astype(np.float64)
@@ -167,8 +173,8 @@ def test_lora_expand_row(M, N, R, S, scaled, fused, in_place):
     tc = tc0.copy()
     dB = np.zeros(S * N * R, np.float32)
     base = np.zeros((M, N))
-    check(L, L.rh_lora_expand(M, N, R, S, p(t), p(slot), p(lb), p(scale), p(cy), p(tc), p(dB), int(fused),
-                              int(in_place), p(base)))
+    check(L, L.rh_lora_expand_op(op.encode(), M, N, R, S, p(t), p(slot), p(lb), p(scale), p(cy), p(tc), p(dB),
+                                 int(fused), int(in_place), p(base)))
     ref_dt, ref_db = O.lora_expand_adjoint(t, slot, lb, scale if scaled else np.ones((S, N)), cy, dt=tc0,
                                            fused=True)
     e_dt = rel_l2(tc - tc0, ref_dt - tc0)
