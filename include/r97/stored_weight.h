@@ -15,10 +15,14 @@
 // An entry is keyed by (enc, raw, rows, cols) and keeps a copy of the encoding it was prepared from
 // and a print of its planes (the first and last 64 bytes of the codes and scale planes): a lookup
 // whose encoding or print no longer matches (an encoding rebuilt, or another weight written, at
-// reused addresses) prepares the weight again. Bytes changed elsewhere in the planes are not seen:
-// a frozen weight keeps its planes while the entry lives, and the walk clears the store at every
-// step's end, as the reference's does (stored_weight_clear, src/step_device.cpp:1621). Pointers the store returns stay valid until the
-// entry is replaced or cleared; a mutex guards the map.
+// reused addresses) prepares the weight again; the print costs one pinned round trip a lookup (its
+// pieces copied on the row's stream, one synchronisation). Bytes changed elsewhere in the planes
+// are not seen: a frozen weight keeps its planes, so entries persist across steps and a walk needs
+// no clear at a step's end (the reference's walk clears its host store there, stored_weight_clear,
+// src/step_device.cpp:1621; device_weight_clear is for a caller that wants the memory back).
+// The functions are this build's own (device_weight_*), not the reference's host-store API: its
+// store holds host grids for host rows, this one the card's prepared form. Pointers the store
+// returns stay valid until the entry is replaced or cleared; a mutex guards the map.
 #pragma once
 
 #include <cstdint>

@@ -188,27 +188,46 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
 }
 
 // ---------------------------------------------------------------- preparation
-// One thread per (segment g, column): the segment's 32 codes of the column, assembled into its
-// `bits` stream dwords (row 32g+i's code at bit bits*(31-i)).
-__global__ __launch_bounds__(256) void prepare_stream_kernel(const R97IqrDecodeDesc d,
-                                                             uint32_t* __restrict__ stream) {
-    const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// One workgroup per (segment g, 256 columns): the segment's 32 packed rows over those columns are
+// staged in LDS (every byte load of the workgroup in flight at once, each row's bytes contiguous),
+// then each thread assembles its column's 32 codes into the `BITS` stream dwords (row 32g+i's
+// code at bit BITS*(31-i)), written coalesced: consecutive columns are consecutive dwords.
+constexpr int kPrepCols = 256;
+template <int BITS>
+__global__ __launch_bounds__(kPrepCols) void prepare_stream_kernel(const R97IqrDecodeDesc d,
+                                                                   uint32_t* __restrict__ stream) {
+    constexpr int kSpan = kPrepCols * BITS / 8 + 1;  // a row's bytes over the block's columns (+ a straddle)
+    __shared__ uint8_t rows[32][kSpan + 3];
+    const int64_t c0 = (int64_t)blockIdx.x * kPrepCols;
     const int64_t g = blockIdx.y;
-    if (col >= d.cols) return;
-    uint32_t w[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = 0;
-    for (int i = 0; i < 32; ++i) {
-        const uint32_t code = load_bits(d.codes + (g * 32 + i) * d.codes_row_bytes, d.bits, col);
-        const int pos = d.bits * (31 - i);
-        const int wi = pos >> 5, sh = pos & 31;
-        // a code may straddle two dwords
-        for (int q = 0; q < 16; ++q) {
-            if (q == wi) w[q] |= code << sh;
-            if (q == wi + 1 && sh + d.bits > 32) w[q] |= code >> (32 - sh);
-        }
+    const int64_t byte0 = c0 * BITS / 8;  // c0 is a multiple of 8: the block starts on a byte
+    const int64_t avail = d.codes_row_bytes - byte0;
+    const int span = (int)(avail < kSpan ? avail : kSpan);
+    for (int idx = threadIdx.x; idx < 32 * span; idx += kPrepCols) {
+        const int i = idx / span, b = idx - i * span;
+        rows[i][b] = d.codes[(g * 32 + i) * d.codes_row_bytes + byte0 + b];
     }
-    for (int q = 0; q < d.bits; ++q) stream[stream_index(g, d.bits, q, d.cols, col)] = w[q];
+    __syncthreads();
+    const int64_t col = c0 + threadIdx.x;
+    if (col >= d.cols) return;
+    const int o = (int)threadIdx.x * BITS;  // the column's bit offset in the staged rows
+    const int byte = o >> 3, sh = o & 7;
+    uint32_t w[BITS];
+#pragma unroll
+    for (int q = 0; q < BITS; ++q) w[q] = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        // a code spans at most two bytes (sh + BITS <= 13); the second is read only when it holds bits
+        uint32_t v = rows[i][byte];
+        if (sh + BITS > 8) v |= (uint32_t)rows[i][byte + 1] << 8;
+        const uint32_t code = (v >> sh) & ((1u << BITS) - 1u);
+        const int pos = BITS * (31 - i);
+        const int wi = pos >> 5, bs = pos & 31;
+        w[wi] |= code << bs;
+        if (bs + BITS > 32) w[wi + 1] |= code >> (32 - bs);
+    }
+#pragma unroll
+    for (int q = 0; q < BITS; ++q) stream[stream_index(g, BITS, q, d.cols, col)] = w[q];
 }
 
 // One thread per 32-byte unit (8 rows x 4 columns) of a decoded int8 grid [rows, cols]: the unit in
@@ -401,9 +420,13 @@ int r97q_weight_prepare(const R97IqrDecodeDesc* desc, const float* scale_col,
                                           stream);
     }
     const hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(prepare_stream_kernel,
-                       dim3((unsigned)((d.cols + 255) / 256), (unsigned)(d.rows_all / 32)), dim3(256),
-                       0, s, d, stream_out);
+    const dim3 pgrid((unsigned)((d.cols + kPrepCols - 1) / kPrepCols), (unsigned)(d.rows_all / 32));
+    switch (d.bits) {
+        case 3: hipLaunchKernelGGL(prepare_stream_kernel<3>, pgrid, dim3(kPrepCols), 0, s, d, stream_out); break;
+        case 4: hipLaunchKernelGGL(prepare_stream_kernel<4>, pgrid, dim3(kPrepCols), 0, s, d, stream_out); break;
+        case 5: hipLaunchKernelGGL(prepare_stream_kernel<5>, pgrid, dim3(kPrepCols), 0, s, d, stream_out); break;
+        default: hipLaunchKernelGGL(prepare_stream_kernel<6>, pgrid, dim3(kPrepCols), 0, s, d, stream_out); break;
+    }
     if (int e = launch_status("prepare_stream_kernel")) return e;
     hipLaunchKernelGGL(prepare_scale_kernel,
                        dim3((unsigned)((d.rows_all + 255) / 256), (unsigned)(d.cols / 128)),

@@ -245,3 +245,56 @@ def test_every_decode_form_derives_its_description(name, kw):
     assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1]), name
     ok, f = scale_col(e, planes, p.rows, p.cols)
     assert ok and (f is None) == (p.scale_col is None)
+
+
+# radiance's plane dtypes by name -> this build's codes: the mapping INTEGRATION.md gives for the
+# copy of a RadEncoding into an R97Encoding (radiance's own numeric values are not in this tree)
+RAD_TO_R97 = dict({f"RAD_U{b}": R.R97_DT_U[b] for b in range(1, 13)},
+                  RAD_I8=R.R97_DT_I8, RAD_U32=R.R97_DT_U32, RAD_F32=R.R97_DT_F32, RAD_BF16=R.R97_DT_BF16,
+                  RAD_F16=R.R97_DT_F16, RAD_F8E4M3=R.R97_DT_F8E4M3)
+
+
+def from_rad(scheme, planes):
+    """An R97Encoding copied field for field from a RadEncoding written as (role, kind, RAD dtype
+    name, block, extent) tuples, the dtype mapped by name."""
+    e = R.Encoding()
+    e.scheme = scheme.encode()
+    for role, kind, dt, block, extent in planes:
+        e.add(role, R.R97_PLANE_TILED if kind == "tiled" else R.R97_PLANE_TABLE, RAD_TO_R97[dt], block=block,
+              extent=extent)
+    return e
+
+
+@pytest.mark.parametrize("form", ["f32-row+scale.col", "bf16-128", "f16-128", "e4m3-128", "bf16-128+scale.1"])
+def test_rad_mapping_scale_forms(form):
+    """Each scale form a stored weight's RadEncoding can carry, copied through the name mapping,
+    derives the description the synthetic builder states for the same planes (scale dtype, block,
+    row bytes, scale.1, the scale.col factor) and decodes to the same bytes."""
+    rows, cols = 256, 256
+    kind = {"f32-row+scale.col": dict(rowf=True, scale_col=np.linspace(0.5, 1.5, cols // 128).astype(np.float32)),
+            "bf16-128": dict(scale_dtype=S.BF16), "f16-128": dict(scale_dtype=S.F16),
+            "e4m3-128": dict(scale_dtype=S.E4M3), "bf16-128+scale.1": dict(scale_dtype=S.BF16, second=True)}[form]
+    p = S.trellis(rows=rows, cols=cols, bits=4, run_rows=128, seed=3, **kind)
+    rad_scale = {S.F32: "RAD_F32", S.BF16: "RAD_BF16", S.F16: "RAD_F16", S.E4M3: "RAD_F8E4M3"}[p.scale_dtype]
+    planes = [("codes", "tiled", "RAD_U4", (1, 1), (0, 0)),
+              ("scale", "tiled", rad_scale, (1, p.scale_block_cols), (0, 0)),
+              ("trellis", "table", "RAD_I8", (p.run_rows, p.rb), (1 << p.state_bits, 1)),
+              ("trellis.mad", "table", "RAD_U32", (0, 0), (2, 1))]
+    data = [p.codes, p.scale, p.lut.view(np.uint8), np.array([p.mad_a, p.mad_b], np.uint32).view(np.uint8)]
+    if p.scale2 is not None:
+        planes.append(("scale.1", "tiled", "RAD_F32", (0, 0), (0, 0)))
+        data.append(p.scale2)
+    if p.scale_col is not None:
+        planes.append(("scale.col", "tiled", "RAD_F32", (0, 128), (0, 0)))
+        data.append(p.scale_col.view(np.uint8))
+    e = from_rad("trellis", planes)
+    data = [np.ascontiguousarray(a).view(np.uint8).reshape(-1) for a in data]
+    d = derive(e, data, rows, cols)
+    assert d is not None, form
+    want = p.desc()
+    for f in FIELDS:
+        assert getattr(d, f) == getattr(want, f), (form, f, getattr(d, f), getattr(want, f))
+    got, ref = oracle_decode(d), O.decode(want)
+    assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1]), form
+    ok, fcol = scale_col(e, data, rows, cols)
+    assert ok and (fcol is None) == (p.scale_col is None), form
