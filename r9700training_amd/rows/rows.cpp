@@ -37,11 +37,13 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "r97/adjoint.h"
@@ -122,6 +124,46 @@ int64_t group_width(int64_t k, int64_t groups) {
     return (k + b - 1) / b == groups ? b : lo;
 }
 
+// ---------------------------------------------------------------- host threads
+// The host side of a row (conversions, staging copies, the adds into the f64 slots) runs on the
+// worker count the reference's host loops use (src/parallel.h:39-90): R97_THREADS when it holds an
+// integer of at least 1, else min(8, hardware threads). [0, n) is cut into one contiguous range a
+// worker; below `serial` items the caller's thread does it all.
+int host_threads() {
+    if (const char* e = std::getenv("R97_THREADS")) {
+        char* end = nullptr;
+        const long v = std::strtol(e, &end, 10);
+        if (*e && end != e && *end == '\0' && v >= 1) return (int)v;
+    }
+    const unsigned hw = std::thread::hardware_concurrency();
+    return hw == 0 ? 1 : (int)std::min(hw, 8u);
+}
+
+template <class F>
+void par_ranges(int64_t n, F&& fn, int64_t serial = 1 << 16) {
+    const int nt = host_threads();
+    if (n <= 0) return;
+    if (nt < 2 || n < serial) {
+        fn((int64_t)0, n);
+        return;
+    }
+    std::vector<std::thread> workers;
+    const int64_t per = (n + nt - 1) / nt;
+    for (int t = 1; t < nt; ++t) {
+        const int64_t lo = t * per, hi = std::min(n, lo + per);
+        if (lo < hi) workers.emplace_back([&fn, lo, hi] { fn(lo, hi); });
+    }
+    fn((int64_t)0, std::min(n, per));
+    for (auto& w : workers) w.join();
+}
+
+// dst[i] += src[i] (f32 results into an f64 slot)
+void add_into(double* dst, const float* src, int64_t n) {
+    par_ranges(n, [&](int64_t lo, int64_t hi) {
+        for (int64_t i = lo; i < hi; ++i) dst[i] += (double)src[i];
+    });
+}
+
 // ---------------------------------------------------------------- served shapes
 // The kernels serve ranks 8, 16, 32 and 64 and widths (K of a shrink, N of an expand) that are
 // multiples of 128. Every other shape a record carries is served exactly through zero padding: the
@@ -148,8 +190,10 @@ template <class T, class F>
 std::vector<T> padded(const double* src, int64_t ld, int64_t rows, int64_t cols, int64_t rows_p, int64_t cols_p,
                       F cvt) {
     std::vector<T> out((size_t)(rows_p * cols_p), T{});
-    for (int64_t r = 0; r < rows; ++r)
-        for (int64_t c = 0; c < cols; ++c) out[(size_t)(r * cols_p + c)] = cvt(src[r * ld + c]);
+    par_ranges(rows, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; ++r)
+            for (int64_t c = 0; c < cols; ++c) out[(size_t)(r * cols_p + c)] = cvt(src[r * ld + c]);
+    }, cols > 0 ? std::max<int64_t>(1, (int64_t(1) << 16) / cols) : 1);
     return out;
 }
 
@@ -244,27 +288,35 @@ float from_bf16(uint16_t b) {
 
 void to_bf16(const double* v, size_t n, std::vector<uint16_t>& out) {
     out.resize(n);
-    for (size_t i = 0; i < n; ++i) out[i] = to_bf16((float)v[i]);
+    par_ranges((int64_t)n, [&](int64_t lo, int64_t hi) {
+        for (int64_t i = lo; i < hi; ++i) out[(size_t)i] = to_bf16((float)v[i]);
+    });
 }
 
 // v ~ hi + lo, both bf16 (~16 significant bits)
 void split_bf16(const std::vector<double>& v, std::vector<uint16_t>& hi, std::vector<uint16_t>& lo) {
     hi.resize(v.size());
     lo.resize(v.size());
-    for (size_t i = 0; i < v.size(); ++i) {
-        hi[i] = to_bf16((float)v[i]);
-        lo[i] = to_bf16((float)(v[i] - (double)from_bf16(hi[i])));
-    }
+    par_ranges((int64_t)v.size(), [&](int64_t a, int64_t b) {
+        for (int64_t i = a; i < b; ++i) {
+            hi[(size_t)i] = to_bf16((float)v[(size_t)i]);
+            lo[(size_t)i] = to_bf16((float)(v[(size_t)i] - (double)from_bf16(hi[(size_t)i])));
+        }
+    });
 }
 
 // ---------------------------------------------------------------- the card
-// One stream, grow-only buffers by role, one rocBLAS handle; created on first use, kept for the
-// process. A mutex serialises rows called from more than one thread.
+// One stream, buffers by role (device, and pinned host memory for the staging copies), one rocBLAS
+// handle; created on first use. A buffer grows when a call needs more; when a row returns with more
+// than kHeldBytes held on either side, every buffer is freed, so a huge call's buffers do not stay
+// for the process. A mutex serialises rows called from more than one thread.
+constexpr size_t kHeldBytes = size_t(1) << 30;
 struct Card {
     std::mutex mu;
     hipStream_t stream = nullptr;
     rocblas_handle blas = nullptr;
     std::map<std::string, std::pair<void*, size_t>> bufs;
+    std::map<std::string, std::pair<void*, size_t>> pinned;
 };
 
 Card& card() {
@@ -296,11 +348,53 @@ void* buffer(Card& c, const std::string& role, size_t bytes) {
     return b.first;
 }
 
-// uploads complete before return: the host vectors are temporaries of the row
+// the pinned host buffer of a role (grow-only within a call)
+void* pinned(Card& c, const std::string& role, size_t bytes) {
+    auto& b = c.pinned[role];
+    if (b.second < bytes || !b.first) {
+        if (b.first) hip_ok(hipHostFree(b.first), "hipHostFree");
+        b = {nullptr, 0};
+        hip_ok(hipHostMalloc(&b.first, bytes ? bytes : 1, hipHostMallocDefault), "hipHostMalloc");
+        b.second = bytes;
+    }
+    return b.first;
+}
+
+// a row's end: every buffer freed when either side holds more than kHeldBytes (the card's work is
+// done: the row synchronised its stream before it read its results back)
+void trim(Card& c) {
+    size_t dev = 0, host = 0;
+    for (const auto& kv : c.bufs) dev += kv.second.second;
+    for (const auto& kv : c.pinned) host += kv.second.second;
+    if (dev > kHeldBytes) {
+        for (auto& kv : c.bufs)
+            if (kv.second.first) (void)hipFree(kv.second.first);
+        c.bufs.clear();
+    }
+    if (host > kHeldBytes) {
+        for (auto& kv : c.pinned)
+            if (kv.second.first) (void)hipHostFree(kv.second.first);
+        c.pinned.clear();
+    }
+}
+
+// held for the length of one row call, after its lock: trims the card's buffers on the way out
+struct RowScope {
+    Card& c;
+    ~RowScope() { trim(c); }
+};
+
+// uploads complete before return: the host vectors are temporaries of the row. The values go
+// through the role's pinned buffer (copied in by the host threads), then one DMA copy.
 template <class T>
 T* upload(Card& c, const std::string& role, const std::vector<T>& h) {
-    void* d = buffer(c, role, h.size() * sizeof(T));
-    hip_ok(hipMemcpyAsync(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice, stream_of(c)), "upload");
+    const size_t bytes = h.size() * sizeof(T);
+    void* d = buffer(c, role, bytes);
+    uint8_t* p = static_cast<uint8_t*>(pinned(c, role, bytes));
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(h.data());
+    par_ranges((int64_t)bytes, [&](int64_t lo, int64_t hi) { std::memcpy(p + lo, src + lo, (size_t)(hi - lo)); },
+               int64_t(1) << 20);
+    hip_ok(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, stream_of(c)), "upload");
     hip_ok(hipStreamSynchronize(stream_of(c)), "hipStreamSynchronize");
     return static_cast<T*>(d);
 }
@@ -311,9 +405,24 @@ float* zeros(Card& c, const std::string& role, size_t n) {
     return static_cast<float*>(d);
 }
 
-std::vector<float> download(Card& c, const float* d, size_t n) {
-    std::vector<float> h(n);
-    hip_ok(hipMemcpyAsync(h.data(), d, n * sizeof(float), hipMemcpyDeviceToHost, stream_of(c)), "download");
+// `count` values of T written into the role's pinned buffer by fill(p, lo, hi) over parts [lo, hi)
+// of [0, parts) on the host threads (a part: a row, say), then one DMA copy to the role's device
+// buffer (no intermediate host vector)
+template <class T, class F>
+T* upload_fill(Card& c, const std::string& role, int64_t count, int64_t parts, int64_t serial, F&& fill) {
+    const size_t bytes = (size_t)count * sizeof(T);
+    void* d = buffer(c, role, bytes);
+    T* p = static_cast<T*>(pinned(c, role, bytes));
+    par_ranges(parts, [&](int64_t lo, int64_t hi) { fill(p, lo, hi); }, serial);
+    hip_ok(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, stream_of(c)), "upload");
+    hip_ok(hipStreamSynchronize(stream_of(c)), "hipStreamSynchronize");
+    return static_cast<T*>(d);
+}
+
+// the n f32 results at `d`, in the download's pinned buffer: valid until the next download
+const float* download(Card& c, const float* d, size_t n) {
+    float* h = static_cast<float*>(pinned(c, "download", n * sizeof(float)));
+    hip_ok(hipMemcpyAsync(h, d, n * sizeof(float), hipMemcpyDeviceToHost, stream_of(c)), "download");
     hip_ok(hipStreamSynchronize(stream_of(c)), "hipStreamSynchronize");
     return h;
 }
@@ -326,9 +435,11 @@ void add_block(hipStream_t s, float* dst, int64_t ld_dst, const float* src, int6
 
 // a [rows, cols] block of host f64 values, added into the f64 slot `dst` (row stride ld_dst) from a
 // downloaded f32 block of row stride ld_src
-void add_host(double* dst, int64_t ld_dst, const std::vector<float>& src, int64_t ld_src, int64_t rows, int64_t cols) {
-    for (int64_t r = 0; r < rows; ++r)
-        for (int64_t c = 0; c < cols; ++c) dst[r * ld_dst + c] += (double)src[(size_t)(r * ld_src + c)];
+void add_host(double* dst, int64_t ld_dst, const float* src, int64_t ld_src, int64_t rows, int64_t cols) {
+    par_ranges(rows, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; ++r)
+            for (int64_t c = 0; c < cols; ++c) dst[r * ld_dst + c] += (double)src[r * ld_src + c];
+    }, cols > 0 ? std::max<int64_t>(1, (int64_t(1) << 16) / cols) : 1);
 }
 
 // The prepared weight of a stored operand: its encoding (AdValue::enc, an R97Encoding) over its
@@ -357,6 +468,7 @@ void gemm_nt_device(const AdjointCall& call) {
 
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
+    RowScope scope{c};
     const hipStream_t s = stream_of(c);
     std::vector<uint16_t> hi, lo;
     split_bf16(dy.value, hi, lo);
@@ -395,8 +507,7 @@ void gemm_nt_device(const AdjointCall& call) {
             if (st != rocblas_status_success) refuse(rec.op, std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(st));
         }
     }
-    const std::vector<float> h = download(c, d_dx, (size_t)(M * K));
-    for (size_t i = 0; i < h.size(); ++i) dx.value[i] += (double)h[i];
+    add_into(dx.value.data(), download(c, d_dx, (size_t)(M * K)), M * K);
 }
 
 // ---------------------------------------------------------------- lora_shrink
@@ -430,6 +541,7 @@ void lora_shrink_device(const AdjointCall& call) {
 
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
+    RowScope scope{c};
     const hipStream_t s = stream_of(c);
     const int64_t Kp = pad128(K);
     const std::vector<RankChunk> chunks = rank_chunks(R);
@@ -491,7 +603,9 @@ void lora_expand_device(const AdjointCall& call) {
         if (rec.operands[i].written && rec.operands[i].in_place) {
             AdValue& d = call.dc->at(i);
             if (d.value.size() == y_cot.value.size())
-                for (size_t e = 0; e < y_cot.value.size(); ++e) d.value[e] += y_cot.value[e];
+                par_ranges((int64_t)d.value.size(), [&](int64_t lo, int64_t hi) {
+                    for (int64_t e = lo; e < hi; ++e) d.value[(size_t)e] += y_cot.value[(size_t)e];
+                });
         }
     std::vector<char> used((size_t)S, 0);
     for (int64_t m = 0; m < M; ++m) {
@@ -508,6 +622,7 @@ void lora_expand_device(const AdjointCall& call) {
 
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
+    RowScope scope{c};
     const hipStream_t s = stream_of(c);
     const int64_t Np = pad128(N);
     const std::vector<RankChunk> chunks = rank_chunks(R);
@@ -515,21 +630,28 @@ void lora_expand_device(const AdjointCall& call) {
     void* d_ws = buffer(c, "ws", (size_t)wsb);
     for (int64_t sl = 0; sl < S; ++sl) {
         if (!used[(size_t)sl]) continue;
-        std::vector<double> dys((size_t)(M * N), 0.0);
-        for (int64_t m = 0; m < M; ++m) {
-            if (row_slot(slot, m, S) != sl) continue;
-            for (int64_t k = 0; k < N; ++k)
-                dys[(size_t)(m * N + k)] = y_cot.value[(size_t)(m * N + k)] * (sc ? sc->value[(size_t)(sl * N + k)] : 1.0);
-        }
-        std::vector<uint16_t> hi, lo;
-        split_bf16(dys, hi, lo);
-        const auto widen = [&](const std::vector<uint16_t>& h) {
-            std::vector<uint16_t> out((size_t)(M * Np), 0);
-            for (int64_t m = 0; m < M; ++m) std::memcpy(&out[(size_t)(m * Np)], &h[(size_t)(m * N)], (size_t)N * 2);
-            return out;
+        // the slot's rows of y_cot times the slot's scale, as [hi | lo] bf16 halves [M, Np] (other
+        // slots' rows and the padded columns zero), written straight into the staging buffers
+        const auto half = [&](bool low) {
+            return [&, low](uint16_t* p, int64_t lo_m, int64_t hi_m) {
+                for (int64_t m = lo_m; m < hi_m; ++m) {
+                    uint16_t* row = p + m * Np;
+                    if (row_slot(slot, m, S) != sl) {
+                        std::memset(row, 0, (size_t)Np * 2);
+                        continue;
+                    }
+                    for (int64_t k = 0; k < N; ++k) {
+                        const double v = y_cot.value[(size_t)(m * N + k)] * (sc ? sc->value[(size_t)(sl * N + k)] : 1.0);
+                        const uint16_t h = to_bf16((float)v);
+                        row[k] = low ? to_bf16((float)(v - (double)from_bf16(h))) : h;
+                    }
+                    for (int64_t k = N; k < Np; ++k) row[k] = 0;
+                }
+            };
         };
-        const uint16_t* d_hi = upload(c, "dy_hi", widen(hi));
-        const uint16_t* d_lo = upload(c, "dy_lo", widen(lo));
+        const int64_t rows_serial = std::max<int64_t>(1, (int64_t(1) << 16) / Np);
+        const uint16_t* d_hi = upload_fill<uint16_t>(c, "dy_hi", M * Np, M, rows_serial, half(false));
+        const uint16_t* d_lo = upload_fill<uint16_t>(c, "dy_lo", M * Np, M, rows_serial, half(true));
         for (const RankChunk& ch : chunks) {
             const uint16_t* d_b = upload(c, "b_s", padded<uint16_t>(lb.value.data() + sl * N * R + ch.j0, R, N, ch.rc, Np,
                                                                     ch.rp, [](double d) { return to_bf16((float)d); }));
@@ -583,6 +705,7 @@ void gemm_nt_q_device(const AdjointCall& call) {
 
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
+    RowScope scope{c};
     const hipStream_t s = stream_of(c);
     std::vector<uint16_t> hi, lo;
     split_bf16(dy.value, hi, lo);
@@ -663,6 +786,7 @@ void lora_shrink_q_device(const AdjointCall& call) {
 
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
+    RowScope scope{c};
     const hipStream_t s = stream_of(c);
     const int64_t Kp = pad128(K);
     const std::vector<RankChunk> chunks = rank_chunks(R);
@@ -745,14 +869,14 @@ void had_quant_device(const AdjointCall& call) {
         gf(g.value.begin(), g.value.end());
     Card& c = card();
     std::lock_guard<std::mutex> lock(c.mu);
+    RowScope scope{c};
     const hipStream_t s = stream_of(c);
     const float* d_x = upload(c, "q_x", xf);
     const float* d_s = upload(c, "q_scale", sf);
     const float* d_g = upload(c, "q_g", gf);
     float* d_dx = zeros(c, "q_dx", xf.size());
     r97q_ok(r97q_quant_act_i8g_bwd(d_x, R97Q_F32, rows, n, group, 1, d_s, d_g, d_dx, s), "had_quant_act_i8g adjoint");
-    const std::vector<float> h = download(c, d_dx, xf.size());
-    for (size_t i = 0; i < h.size(); ++i) dx.value[i] += (double)h[i];
+    add_into(dx.value.data(), download(c, d_dx, xf.size()), (int64_t)xf.size());
 }
 
 }  // namespace

@@ -3,6 +3,7 @@
 // reference's backward walk builds them (schema-ordered operands, f64 forward values, the stored
 // weight as raw + enc, dc pre-sized), looks the row up through the registry (adjoint_find on the
 // device side) and runs it. Also a self-test of the registry's lookup rules.
+#include <chrono>
 #include <cstdint>
 #include <cstring>
 #include <map>
@@ -22,6 +23,16 @@ using namespace r97;
 namespace {
 
 thread_local std::string g_err;
+// the wall time of the last row invocation alone (the row's own staging, kernels and adds; not the
+// hook's building of the record's f64 values around it), in ms
+thread_local double g_row_ms = 0.0;
+
+template <class F>
+void timed_row(F&& f) {
+    const auto t0 = std::chrono::steady_clock::now();
+    f();
+    g_row_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
 
 Operand opd(const char* name, const char* dtype, std::vector<int64_t> shape, bool written = false,
             bool in_place = false) {
@@ -80,6 +91,7 @@ bool is_x(const std::vector<OpParam>& p) {
 extern "C" {
 
 const char* rh_last_error() { return g_err.c_str(); }
+double rh_last_row_ms() { return g_row_ms; }
 
 // 0, or the line of the first failed check
 int rh_registry_selftest() {
@@ -183,7 +195,7 @@ int rh_gemm_nt(int64_t M, int64_t N, int64_t K, const double* dy, const R97Encod
         const std::vector<AdValue> cot = {val("bf16", {M, N}, dy)};
         std::vector<AdValue> dc = {val("bf16", {M, K}, dx), AdValue{}, AdValue{}};
         const AdjointCall call{rec, fwd, cot, &dc, nullptr, "", {}, false, nullptr, nullptr};
-        row("gemm_nt", rec.params)(call);
+        timed_row([&] { row("gemm_nt", rec.params)(call); });
         std::memcpy(dx, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
         return 0;
     } catch (const std::exception& e) {
@@ -211,7 +223,7 @@ int rh_lora_shrink(int64_t M, int64_t K, int64_t R, int64_t S, const double* x, 
         ParamSet grads;
         AdjointCall call{rec, fwd, cot, &dc, dA ? &grads : nullptr, "layers.0.q", {}, fused != 0, nullptr, nullptr};
         if (!fused) call.slot_prefix = [](int64_t s) { return "adapter" + std::to_string(s); };
-        row("lora_shrink", rec.params)(call);
+        timed_row([&] { row("lora_shrink", rec.params)(call); });
         std::memcpy(dx, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
         if (dA) {
             // the leaves wait in the step's staging; nothing reached `grads`
@@ -262,7 +274,7 @@ int rh_lora_expand_op(const char* op, int64_t M, int64_t N, int64_t R, int64_t S
         ParamSet grads;
         AdjointCall call{rec, fwd, cot, &dc, dB ? &grads : nullptr, "layers.0.q", {}, fused != 0, nullptr, nullptr};
         if (!fused) call.slot_prefix = [](int64_t s) { return "adapter" + std::to_string(s); };
-        row(op, rec.params)(call);
+        timed_row([&] { row(op, rec.params)(call); });
         std::memcpy(t_cot, dc[0].value.data(), sizeof(double) * (size_t)(M * R));
         if (in_place && d_base) std::memcpy(d_base, dc.back().value.data(), sizeof(double) * (size_t)(M * N));
         if (dB) {
@@ -345,7 +357,7 @@ int rh_lora_shrink_q(int64_t M, int64_t K, int64_t R, int64_t S, int64_t groups,
         ParamSet grads;
         AdjointCall call{rec, fwd, cot, &dc, dA ? &grads : nullptr, "layers.1.q", {}, fused != 0, nullptr, nullptr};
         if (!fused) call.slot_prefix = [](int64_t s) { return "adapter" + std::to_string(s); };
-        row("lora_shrink", rec.params)(call);
+        timed_row([&] { row("lora_shrink", rec.params)(call); });
         std::memcpy(da, dc[0].value.data(), sizeof(double) * (size_t)(M * K));
         std::memcpy(ds, dc[1].value.data(), sizeof(double) * (size_t)(M * groups));
         if (dA) {

@@ -32,23 +32,27 @@ _P = C.c_void_p
 def hook():
     L = C.CDLL(os.path.join(HERE, "librowshook.so"))
     L.rh_last_error.restype = C.c_char_p
+    L.rh_last_row_ms.restype = C.c_double
     L.rh_gemm_nt.argtypes = [C.c_int64, C.c_int64, C.c_int64, _P, _P, _P, _P, _P]
     L.rh_lora_shrink.argtypes = [C.c_int64] * 4 + [_P] * 6 + [C.c_int]
     L.rh_lora_expand.argtypes = [C.c_int64] * 4 + [_P] * 7 + [C.c_int, C.c_int, _P]
     return L
 
 
-def timed(fn, reps=3):
-    """Median wall time (ms) of `fn` over `reps` calls after one warm call."""
+def timed(fn, H, reps=3):
+    """Median wall time (ms) of `fn` over `reps` calls after one warm call, and the median time of
+    the row invocation alone inside it (rh_last_row_ms: without the hook building the record's f64
+    values and copying the results out, which a walk does not do)."""
     fn()
-    out = []
+    out, row = [], []
     for _ in range(reps):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         fn()
         torch.cuda.synchronize()
         out.append((time.perf_counter() - t0) * 1e3)
-    return statistics.median(out)
+        row.append(H.rh_last_row_ms())
+    return statistics.median(out), statistics.median(row)
 
 
 def events(fn, reps=20):
@@ -103,7 +107,7 @@ def main():
             T, N, r, 1, t.ctypes.data, slot.ctypes.data, lb.ctypes.data, scale.ctypes.data, dy.ctypes.data,
             tc.ctypes.data, dB.ctypes.data, 1, 0, None)),
     }
-    row_ms = {k: timed(f) for k, f in rows.items()}
+    row_ms = {k: timed(f, H) for k, f in rows.items()}
 
     # the C ABI on resident operands: the fused dX product, and the whole fwd + bwd step
     dev = torch.device("cuda:0")
@@ -135,14 +139,15 @@ def main():
     abi = {"dX product, C ABI (dY tiled copy + fused kernel)": events(dx_base),
            "whole fwd + bwd step, C ABI (all five entries)": events(step)}
 
-    print("| call at C2 (T = N = K = 4096, rank 16) | ms a call |")
-    print("|---|---:|")
-    for k, v in row_ms.items():
-        print(f"| registry row `{k}`, f64 host in / out | {v:.1f} |")
+    print("| call at C2 (T = N = K = 4096, rank 16) | ms a call (the row) | ms a call (with the hook's record building) |")
+    print("|---|---:|---:|")
+    for k, (v, rv) in row_ms.items():
+        print(f"| registry row `{k}`, f64 host in / out | {rv:.1f} | {v:.1f} |")
     for k, v in abi.items():
-        print(f"| {k}, device-resident | {v:.3f} |")
-    print(f"\nrow calls: median of 3 after a warm call (wall clock, synchronised); C ABI: HIP events over "
-          f"20 calls; torch {torch.__version__}, nproc {os.cpu_count()}")
+        print(f"| {k}, device-resident | {v:.3f} | |")
+    print(f"\nrow calls: median of 3 after a warm call (wall clock, synchronised; the row alone timed inside "
+          f"the hook around the registry's function); C ABI: HIP events over 20 calls; torch {torch.__version__}, "
+          f"nproc {os.cpu_count()}, host threads {os.environ.get('R97_THREADS', 'min(8, nproc)')}")
 
 
 if __name__ == "__main__":
