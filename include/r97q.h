@@ -464,6 +464,39 @@ int r97q_quant_act_i8g(const void* x, int32_t x_dtype, int64_t rows, int64_t n, 
 int r97q_quant_act_i8g_bwd(const void* x, int32_t x_dtype, int64_t rows, int64_t n, int64_t group, int32_t rotated,
                            const float* scale, const float* g, float* dx, R97IqrStream stream);
 
+/* ------------------------------------------------------------------ the fused quantiser producers
+ *
+ * rmsnorm_had_quant_i8g, gated_had_quant_i8g and gate_had_quant_i8g: an elementwise part, then
+ * had_quant_act_i8g (above, rotated) over its output y [rows, n]. The reference composes them on the
+ * host (src/adjoint/host/quant.cpp:896-935, fused_twin; its card forward is radiance's, absent from
+ * the reference tree) from the parts' rows (src/adjoint/host/elementwise.cpp):
+ *   R97Q_PART_RMSNORM     x0 = x [rows, n], x1 = w [n]: y = x * rs * (w + wadd) * mult,
+ *                         rs = 1 / sqrt(mean over the row of x^2 + eps)               (:459-541)
+ *   R97Q_PART_SILU_MUL    x0 = gate_up [rows, 2n], x1 unused: y = silu(gate) * up     (:278-293)
+ *   R97Q_PART_SIGMOID_MUL x0 = a, x1 = b [rows, n]: y = sigmoid(a) * b (act_mul, act=sigmoid) (:316-327)
+ * x_dtype (bf16, f32 or f64) is that of x0 and x1. y is formed in f64 as the host twins form it;
+ * group is a power of two of at most 1024 dividing n (the reference rows' predicate,
+ * src/adjoint/device/quant.hip:129-159). codes int8 [rows, n], scale f32 [rows, n / group]; y_out
+ * (may be NULL) receives y rounded to f32 and then to bf16, the output the live records write beside
+ * the codes. eps, wadd and mult are the norm's (ignored by the other parts). */
+#define R97Q_F64 3
+#define R97Q_PART_RMSNORM 0
+#define R97Q_PART_SILU_MUL 1
+#define R97Q_PART_SIGMOID_MUL 2
+int r97q_fused_had_quant_i8g(int32_t part, const void* x0, const void* x1, int32_t x_dtype, int64_t rows, int64_t n,
+                             int64_t group, double eps, double wadd, double mult, int8_t* codes, float* scale,
+                             uint16_t* y_out, R97IqrStream stream);
+/* The adjoint (the reference's device rows src/adjoint/device/quant.hip:959-961, host rows
+ * src/adjoint/host/quant.cpp:1008-1405): e = W^T(live * g_codes / scale) at y with the forward's
+ * scale (f32 [rows, n / group]), plus g_out (the output write's cotangent f32 [rows, n]; may be
+ * NULL), then the part's adjoint of e added into dx0 f32 (x0's shape: [rows, 2n] for silu_mul) and,
+ * for the sigmoid part, dx1 f32 [rows, n] (b's). The norm's gain is frozen, as the reference
+ * registers it: no gain cotangent. */
+int r97q_fused_had_quant_i8g_bwd(int32_t part, const void* x0, const void* x1, int32_t x_dtype, int64_t rows,
+                                 int64_t n, int64_t group, double eps, double wadd, double mult, const float* scale,
+                                 const float* g_codes, const float* g_out, float* dx0, float* dx1,
+                                 R97IqrStream stream);
+
 /* ------------------------------------------------------------------ the vocabulary head
  *
  * The vocabulary head's transposed product (src/vocab_head.h:27-99, its kernels

@@ -34,6 +34,20 @@
  *                                  scipy's Sylvester Hadamard for the rotation; the codes against a
  *                                  numpy rint/clip; ties to even on exact halves; the adjoint as the
  *                                  transpose of the straight-through linearisation (dot products).
+ *   orc_part_twin, orc_part_adjoint
+ *                                  the reference's own elementwise rows (oracle/_ref, src/adjoint/host/
+ *                                  elementwise.cpp: rmsnorm, silu_mul, act_mul) on seeded inputs;
+ *                                  central finite differences of the twin for the adjoint; closed
+ *                                  forms (the norm's unit rms, silu(0) = 0, sigmoid(0) = 1/2).
+ *   orc_fused_quant, orc_fused_quant_adjoint
+ *                                  the reference's fused rows (src/adjoint/host/quant.cpp) need
+ *                                  radiance's rad_plugin.h, absent here, so they are not built: the
+ *                                  forward is pinned as the _ref part followed by the pinned
+ *                                  quantiser; the adjoint by central finite differences of the
+ *                                  straight-through surrogate sum(g . live . H part(x) / s) +
+ *                                  sum(g_out . part(x)), which a dropped rotation, a missing mask,
+ *                                  the output term left out or the part's adjoint applied before
+ *                                  the quantiser's each fail.
  *   orc_vocab_class_product, orc_fwht128
  *                                  the reference test's own known answer (tests/gpu/vocab_head.cpp:
  *                                  a one-hot cotangent row selects one weight row, scaled by its
@@ -922,5 +936,108 @@ int32_t orc_quant_act_i8g_adjoint(const double* x, int64_t rows, int64_t n, int6
     }
     free(v);
     free(d);
+    return rc;
+}
+
+/* ------------------------------------------------------------------ the fused quantiser producers */
+
+/* src/adjoint/host/elementwise.cpp:121 */
+static double part_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+/* the rms factor of one row, src/adjoint/host/elementwise.cpp:526-529 */
+static double part_rs(const double* x, int64_t n, double eps) {
+    double ss = 0.0;
+    for (int64_t i = 0; i < n; ++i) ss += x[i] * x[i];
+    return 1.0 / sqrt(ss / (double)n + eps);
+}
+
+/* rmsnorm :459-541, silu_mul :278-293 (act_value(silu) :124), act_mul with act = sigmoid :316-327 */
+int32_t orc_part_twin(int32_t part, int64_t rows, int64_t n, const double* x0, const double* x1, double eps,
+                      double wadd, double mult, double* y) {
+    if (rows <= 0 || n <= 0 || part < 0 || part > 2) return 1;
+    if (part == ORC_PART_RMSNORM && !x1 && wadd != 0.0) return 1; /* a gain offset with no gain */
+    for (int64_t r = 0; r < rows; ++r) {
+        double* yr = y + r * n;
+        if (part == ORC_PART_RMSNORM) {
+            const double* xr = x0 + r * n;
+            const double s = part_rs(xr, n, eps);
+            for (int64_t i = 0; i < n; ++i) yr[i] = xr[i] * s * (x1 ? x1[i] + wadd : 1.0) * mult;
+        } else if (part == ORC_PART_SILU_MUL) {
+            const double* g = x0 + r * 2 * n;
+            for (int64_t i = 0; i < n; ++i) yr[i] = g[i] * part_sigmoid(g[i]) * g[n + i];
+        } else {
+            const double *a = x0 + r * n, *b = x1 + r * n;
+            for (int64_t i = 0; i < n; ++i) yr[i] = part_sigmoid(a[i]) * b[i];
+        }
+    }
+    return 0;
+}
+
+/* rmsnorm :543-641 (the gain frozen: dx1 untouched), silu_mul :295-313 (act_slope(silu) :142-145),
+ * act_mul sigmoid :329-347 (act_slope(sigmoid) :155-158) */
+int32_t orc_part_adjoint(int32_t part, int64_t rows, int64_t n, const double* x0, const double* x1, const double* dy,
+                         double eps, double wadd, double mult, double* dx0, double* dx1) {
+    if (rows <= 0 || n <= 0 || part < 0 || part > 2) return 1;
+    if (part == ORC_PART_RMSNORM && !x1 && wadd != 0.0) return 1;
+    for (int64_t r = 0; r < rows; ++r) {
+        const double* d = dy + r * n;
+        if (part == ORC_PART_RMSNORM) {
+            const double* xr = x0 + r * n;
+            double* o = dx0 + r * n;
+            const double s = part_rs(xr, n, eps);
+            double t = 0.0;
+            for (int64_t i = 0; i < n; ++i) t += d[i] * xr[i] * (x1 ? x1[i] + wadd : 1.0);
+            for (int64_t i = 0; i < n; ++i) {
+                const double c = x1 ? x1[i] + wadd : 1.0;
+                const double shared = s * s * s * xr[i] * t / (double)n;
+                o[i] += mult * (s * c * d[i] - shared);
+            }
+        } else if (part == ORC_PART_SILU_MUL) {
+            const double* gu = x0 + r * 2 * n;
+            double* o = dx0 + r * 2 * n;
+            for (int64_t i = 0; i < n; ++i) {
+                const double g = gu[i], u = gu[n + i], sg = part_sigmoid(g);
+                o[i] += d[i] * u * (sg * (1.0 + g * (1.0 - sg)));
+                o[n + i] += d[i] * (g * part_sigmoid(g));
+            }
+        } else {
+            const double *a = x0 + r * n, *b = x1 + r * n;
+            for (int64_t i = 0; i < n; ++i) {
+                const double sa = part_sigmoid(a[i]);
+                dx0[r * n + i] += d[i] * (sa * (1.0 - sa)) * b[i];
+                dx1[r * n + i] += d[i] * part_sigmoid(a[i]);
+            }
+        }
+    }
+    return 0;
+}
+
+/* src/adjoint/host/quant.cpp:896-935 (fused_twin): the part's twin, then had_quant_act_i8g over its
+ * output */
+int32_t orc_fused_quant(int32_t part, int64_t rows, int64_t n, int64_t group, const double* x0, const double* x1,
+                        double eps, double wadd, double mult, double* y, double* codes, double* scale) {
+    if (quant_group(n, group, 1) == 0) return 1;
+    if (orc_part_twin(part, rows, n, x0, x1, eps, wadd, mult, y)) return 1;
+    return orc_quant_act_i8g(y, rows, n, group, 1, codes, scale, NULL);
+}
+
+/* src/adjoint/host/quant.cpp:1008-1117 and :1321-1405 (fused_adjoint): the intermediate y rebuilt
+ * by the part's twin; the quantiser's adjoint of the codes' cotangent at y with the forward's scale,
+ * from zero; the output write's cotangent (g_out, may be NULL) added to it; then the part's adjoint
+ * of that sum into dx0 (and dx1 for act_mul). Returns 0, 1 for a refused geometry, 2 for a
+ * non-positive scale. */
+int32_t orc_fused_quant_adjoint(int32_t part, int64_t rows, int64_t n, int64_t group, const double* x0,
+                                const double* x1, double eps, double wadd, double mult, const double* scale,
+                                const double* g_codes, const double* g_out, double* dx0, double* dx1) {
+    if (quant_group(n, group, 1) == 0 || rows <= 0) return 1;
+    double* y = (double*)malloc((size_t)(rows * n) * sizeof(double));
+    double* e = (double*)calloc((size_t)(rows * n), sizeof(double));
+    int32_t rc = orc_part_twin(part, rows, n, x0, x1, eps, wadd, mult, y);
+    if (rc == 0) rc = orc_quant_act_i8g_adjoint(y, rows, n, group, 1, scale, g_codes, e);
+    if (rc == 0 && g_out)
+        for (int64_t i = 0; i < rows * n; ++i) e[i] += g_out[i];
+    if (rc == 0) rc = orc_part_adjoint(part, rows, n, x0, x1, e, eps, wadd, mult, dx0, dx1);
+    free(y);
+    free(e);
     return rc;
 }

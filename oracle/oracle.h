@@ -135,6 +135,31 @@ int32_t orc_quant_act_i8g(const double* x, int64_t rows, int64_t n, int64_t grou
 int32_t orc_quant_act_i8g_adjoint(const double* x, int64_t rows, int64_t n, int64_t group, int32_t rotated,
                                   const double* scale, const double* g, double* dx);
 
+/* The elementwise parts of the fused quantiser producers (src/adjoint/host/elementwise.cpp), in f64:
+ *   ORC_PART_RMSNORM   x0 = x [rows, n], x1 = w [n] (NULL: no gain; wadd must then be 0):
+ *                      y = x * rs * (w + wadd) * mult, rs = 1 / sqrt(mean(x^2) + eps)      (:459-541)
+ *   ORC_PART_SILU_MUL  x0 = gate_up [rows, 2n]: y = silu(gate) * up                       (:278-293)
+ *   ORC_PART_SIGMOID_MUL x0 = a, x1 = b [rows, n]: y = sigmoid(a) * b (act_mul, act=sigmoid) (:316-327)
+ * The adjoint adds dy's cotangent into dx0 (x0's shape) and, for the sigmoid part, dx1 (b's); the
+ * norm's gain is frozen (dx1 untouched). Both return 0, or 1 for an argument outside the rules. */
+#define ORC_PART_RMSNORM 0
+#define ORC_PART_SILU_MUL 1
+#define ORC_PART_SIGMOID_MUL 2
+int32_t orc_part_twin(int32_t part, int64_t rows, int64_t n, const double* x0, const double* x1, double eps,
+                      double wadd, double mult, double* y);
+int32_t orc_part_adjoint(int32_t part, int64_t rows, int64_t n, const double* x0, const double* x1, const double* dy,
+                         double eps, double wadd, double mult, double* dx0, double* dx1);
+/* rmsnorm_had_quant_i8g / gated_had_quant_i8g / gate_had_quant_i8g (src/adjoint/host/quant.cpp:
+ * 896-935, 1008-1405): y = part(x) (f64 [rows, n]), then had_quant_act_i8g over y (codes, scale as
+ * orc_quant_act_i8g with rotated = 1). The adjoint: e = W^T(live * g_codes / scale) at y with the
+ * forward's scale, plus g_out (the output write's cotangent; may be NULL), then the part's adjoint
+ * of e into dx0 / dx1. 0, 1 for a refused geometry, 2 for a non-positive scale. */
+int32_t orc_fused_quant(int32_t part, int64_t rows, int64_t n, int64_t group, const double* x0, const double* x1,
+                        double eps, double wadd, double mult, double* y, double* codes, double* scale);
+int32_t orc_fused_quant_adjoint(int32_t part, int64_t rows, int64_t n, int64_t group, const double* x0,
+                                const double* x1, double eps, double wadd, double mult, const double* scale,
+                                const double* g_codes, const double* g_out, double* dx0, double* dx1);
+
 /* The vocabulary head's transposed product for one class (src/adjoint/device/vocab_head.hip:88-143,
  * the gather and the GEMV; f64 here): for every token row m and column k,
  *   d_x[m, k] += cf[k/128] * sum_n dy[m, ids[n] - vocab_offset] * gscale[n, k/128] * codes[n, k]

@@ -103,6 +103,15 @@ def lib():
         L.orc_quant_act_i8g.argtypes = [_P, _I, _I, _I, C.c_int32, _P, _P, _P]
         L.orc_quant_act_i8g_adjoint.restype = C.c_int32
         L.orc_quant_act_i8g_adjoint.argtypes = [_P, _I, _I, _I, C.c_int32, _P, _P, _P]
+        L.orc_part_twin.restype = C.c_int32
+        L.orc_part_twin.argtypes = [C.c_int32, _I, _I, _P, _P, C.c_double, C.c_double, C.c_double, _P]
+        L.orc_part_adjoint.restype = C.c_int32
+        L.orc_part_adjoint.argtypes = [C.c_int32, _I, _I, _P, _P, _P, C.c_double, C.c_double, C.c_double, _P, _P]
+        L.orc_fused_quant.restype = C.c_int32
+        L.orc_fused_quant.argtypes = [C.c_int32, _I, _I, _I, _P, _P, C.c_double, C.c_double, C.c_double, _P, _P, _P]
+        L.orc_fused_quant_adjoint.restype = C.c_int32
+        L.orc_fused_quant_adjoint.argtypes = [C.c_int32, _I, _I, _I, _P, _P, C.c_double, C.c_double, C.c_double,
+                                              _P, _P, _P, _P, _P]
         L.orc_rounded_bf16.restype = C.c_double
         L.orc_rounded_bf16.argtypes = [C.c_double]
         L.orc_thread_count.restype = C.c_int
@@ -133,6 +142,8 @@ def ref():
         R.ref_scheduled_lr.argtypes = [C.POINTER(AdamWConfig), C.c_int32]
         R.ref_clip_global_norm.restype = C.c_float
         R.ref_clip_global_norm.argtypes = [_P, _I, C.c_float]
+        R.ref_part_twin.argtypes = [C.c_int32, _I, _I, _P, _P, C.c_double, C.c_double, C.c_double, _P]
+        R.ref_part_adjoint.argtypes = [C.c_int32, _I, _I, _P, _P, _P, C.c_double, C.c_double, C.c_double, _P, _P]
         R.ref_adamw_run.argtypes = [C.POINTER(AdamWConfig), _P, _P, C.c_int32, _P, _P, C.c_int32, _P, _P, _P, _P, _P]
         _ref = R
     return _ref
@@ -522,3 +533,72 @@ def quant_act_i8g_adjoint(x, scale, g, group, rotated=False, dx=None):
     if rc:
         raise ValueError("quant adjoint: geometry refused" if rc == 1 else "quant adjoint: non-positive scale")
     return out
+
+
+# The fused quantiser producers' elementwise parts (src/adjoint/host/elementwise.cpp) and the
+# producers themselves (src/adjoint/host/quant.cpp:896-1405). part: "rmsnorm" (x0 = x [rows, n],
+# x1 = w [n] or None), "silu_mul" (x0 = gate_up [rows, 2n]), "sigmoid_mul" (x0 = a, x1 = b [rows, n]).
+PARTS = {"rmsnorm": 0, "silu_mul": 1, "sigmoid_mul": 2}
+
+
+def _part_args(part, x0, x1):
+    x0 = np.ascontiguousarray(x0, np.float64)
+    x1 = None if x1 is None else np.ascontiguousarray(x1, np.float64)
+    rows = x0.shape[0]
+    n = x0.shape[1] // 2 if part == "silu_mul" else x0.shape[1]
+    return PARTS[part], rows, n, x0, x1
+
+
+def _opt(a):
+    return None if a is None else _ptr(a)
+
+
+def part_twin(part, x0, x1=None, eps=1e-6, wadd=0.0, mult=1.0, use_ref=False):
+    """y [rows, n] = the part over its inputs (f64)."""
+    k, rows, n, x0, x1 = _part_args(part, x0, x1)
+    y = np.zeros((rows, n))
+    if use_ref:
+        _check_ref(ref().ref_part_twin(k, rows, n, _ptr(x0), _opt(x1), eps, wadd, mult, _ptr(y)))
+    elif lib().orc_part_twin(k, rows, n, _ptr(x0), _opt(x1), eps, wadd, mult, _ptr(y)):
+        raise ValueError(f"{part}: arguments refused")
+    return y
+
+
+def part_adjoint(part, x0, x1, dy, eps=1e-6, wadd=0.0, mult=1.0, use_ref=False):
+    """(dx0, dx1): the part's adjoint of dy [rows, n] (dx1 None unless sigmoid_mul)."""
+    k, rows, n, x0, x1 = _part_args(part, x0, x1)
+    dy = np.ascontiguousarray(dy, np.float64)
+    dx0 = np.zeros(x0.shape)
+    dx1 = np.zeros((rows, n)) if part == "sigmoid_mul" else None
+    if use_ref:
+        _check_ref(ref().ref_part_adjoint(k, rows, n, _ptr(x0), _opt(x1), _ptr(dy), eps, wadd, mult, _ptr(dx0),
+                                          _opt(dx1)))
+    elif lib().orc_part_adjoint(k, rows, n, _ptr(x0), _opt(x1), _ptr(dy), eps, wadd, mult, _ptr(dx0), _opt(dx1)):
+        raise ValueError(f"{part}: arguments refused")
+    return dx0, dx1
+
+
+def fused_quant(part, x0, x1, group, eps=1e-6, wadd=0.0, mult=1.0):
+    """(y f64 [rows, n], codes f64, scale f64 [rows, n/group]) of the fused producer."""
+    k, rows, n, x0, x1 = _part_args(part, x0, x1)
+    y, codes, scale = np.zeros((rows, n)), np.zeros((rows, n)), np.zeros((rows, n // max(group, 1)))
+    if lib().orc_fused_quant(k, rows, n, group, _ptr(x0), _opt(x1), eps, wadd, mult, _ptr(y), _ptr(codes),
+                             _ptr(scale)):
+        raise ValueError(f"fused {part}: geometry refused")
+    return y, codes, scale
+
+
+def fused_quant_adjoint(part, x0, x1, group, scale, g_codes, g_out=None, eps=1e-6, wadd=0.0, mult=1.0):
+    """(dx0, dx1) of the fused producer: the codes' cotangent through the quantiser at part(x) with
+    the forward's scale, plus the output write's cotangent, then through the part."""
+    k, rows, n, x0, x1 = _part_args(part, x0, x1)
+    dx0 = np.zeros(x0.shape)
+    dx1 = np.zeros((rows, n)) if part == "sigmoid_mul" else None
+    g_out = None if g_out is None else np.ascontiguousarray(g_out, np.float64)
+    rc = lib().orc_fused_quant_adjoint(k, rows, n, group, _ptr(x0), _opt(x1), eps, wadd, mult,
+                                       _ptr(np.ascontiguousarray(scale, np.float64)),
+                                       _ptr(np.ascontiguousarray(g_codes, np.float64)), _opt(g_out), _ptr(dx0),
+                                       _opt(dx1))
+    if rc:
+        raise ValueError(f"fused {part} adjoint: " + ("geometry refused" if rc == 1 else "non-positive scale"))
+    return dx0, dx1

@@ -15,6 +15,7 @@
 #include "r97/optim.h"
 #include "stored_weight.h"
 
+#include <cstdio>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -121,6 +122,63 @@ OpRecord shrink_q_rec(int64_t M, int64_t K, int64_t R, int64_t S, int64_t group)
 }
 
 thread_local std::string g_err;
+
+// The elementwise parts of the fused quantiser producers (src/adjoint/host/elementwise.cpp's rows,
+// found through the registry): part 0 rmsnorm (x [rows, n], w [n]; params n, eps, wadd, mult),
+// 1 silu_mul (gate_up [rows, 2n]; param n), 2 act_mul with act = sigmoid (a, b [rows, n]).
+OpRecord part_rec(int32_t part, int64_t rows, int64_t n, double eps, double wadd, double mult) {
+    OpRecord rec;
+    auto spell = [](double v) {
+        char b[64];
+        std::snprintf(b, sizeof b, "%.17g", v);
+        return std::string(b);
+    };
+    if (part == 0) {
+        rec.op = "rmsnorm";
+        rec.params = {{"n", n}, {"eps", spell(eps)}, {"wadd", spell(wadd)}, {"mult", spell(mult)}};
+        rec.operands = {{"x", "bf16", {rows, n}, 0, rows, false},
+                        {"w", "bf16", {n}, 0, 1, false},
+                        {"y", "bf16", {rows, n}, 0, rows, true}};
+    } else if (part == 1) {
+        rec.op = "silu_mul";
+        rec.params = {{"n", n}};
+        rec.operands = {{"gate_up", "bf16", {rows, 2 * n}, 0, rows, false},
+                        {"y", "bf16", {rows, n}, 0, rows, true}};
+    } else {
+        rec.op = "act_mul";
+        rec.params = {{"act", std::string("sigmoid")}};
+        rec.operands = {{"a", "bf16", {rows, n}, 0, rows, false},
+                        {"b", "bf16", {rows, n}, 0, rows, false},
+                        {"y", "bf16", {rows, n}, 0, rows, true}};
+    }
+    return rec;
+}
+
+std::vector<OpParam> spec_params(const char* spec) {
+    std::vector<OpParam> params;
+    std::string s(spec ? spec : "");
+    size_t at = 0;
+    while (at < s.size()) {
+        size_t end = s.find(';', at);
+        if (end == std::string::npos) end = s.size();
+        const std::string kv = s.substr(at, end - at);
+        const size_t eq = kv.find('=');
+        if (eq != std::string::npos) {
+            const std::string k = kv.substr(0, eq), v = kv.substr(eq + 1);
+            const bool digits = !v.empty() && v.find_first_not_of("0123456789") == std::string::npos;
+            if (digits) params.push_back({k, (int64_t)std::stoll(v)});
+            else params.push_back({k, v});
+        }
+        at = end + 1;
+    }
+    return params;
+}
+
+std::vector<AdValue> part_inputs(int32_t part, int64_t rows, int64_t n, const double* x0, const double* x1) {
+    if (part == 0) return {values("bf16", {rows, n}, x0), values("bf16", {n}, x1)};
+    if (part == 1) return {values("bf16", {rows, 2 * n}, x0)};
+    return {values("bf16", {rows, n}, x0), values("bf16", {rows, n}, x1)};
+}
 
 }  // namespace
 
@@ -487,6 +545,69 @@ int32_t ref_adjoint_frozen(const char* op, int32_t device, const char* dtype, in
     const std::vector<int> f = adjoint_frozen(op, device ? Side::device : Side::host, params);
     for (size_t i = 0; i < f.size() && i < 4; ++i) first4[i] = f[i];
     return (int32_t)f.size();
+}
+
+// The same for a record with parameters spelled "key=value;key=value" (a value of digits only is an
+// int, anything else a string), for rows whose predicates read more than the dtype and the group.
+const void* ref_adjoint_find_spec(const char* op, int32_t device, const char* spec) {
+    std::string err;
+    AdjointFn fn = adjoint_find(op, device ? Side::device : Side::host, spec_params(spec), &err);
+    return reinterpret_cast<const void*>(fn);
+}
+
+int32_t ref_adjoint_frozen_spec(const char* op, int32_t device, const char* spec, int32_t* first4) {
+    const std::vector<int> f = adjoint_frozen(op, device ? Side::device : Side::host, spec_params(spec));
+    for (size_t i = 0; i < f.size() && i < 4; ++i) first4[i] = f[i];
+    return (int32_t)f.size();
+}
+
+// y [rows, n] = the part's twin over its inputs
+int ref_part_twin(int32_t part, int64_t rows, int64_t n, const double* x0, const double* x1, double eps, double wadd,
+                  double mult, double* y) {
+    try {
+        const OpRecord rec = part_rec(part, rows, n, eps, wadd, mult);
+        TwinFn tw = twin_find(rec.op, rec.params, nullptr);
+        if (!tw) throw std::runtime_error("no twin for " + rec.op);
+        std::vector<AdValue> out;
+        tw(rec, part_inputs(part, rows, n, x0, x1), &out);
+        if (out.empty() || (int64_t)out[0].value.size() != rows * n) throw std::runtime_error(rec.op + ": no output");
+        std::memcpy(y, out[0].value.data(), sizeof(double) * (size_t)(rows * n));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
+// dx0 (+)= and dx1 (+)= the part's host adjoint of dy [rows, n]: dx0 has x0's shape; dx1 b's for
+// act_mul (the rmsnorm gain is frozen: dx1 untouched)
+int ref_part_adjoint(int32_t part, int64_t rows, int64_t n, const double* x0, const double* x1, const double* dy,
+                     double eps, double wadd, double mult, double* dx0, double* dx1) {
+    try {
+        const OpRecord rec = part_rec(part, rows, n, eps, wadd, mult);
+        AdjointFn fn = adjoint_find(rec.op, Side::host, rec.params, nullptr);
+        if (!fn) throw std::runtime_error("no host adjoint for " + rec.op);
+        std::vector<AdValue> fwd = part_inputs(part, rows, n, x0, x1);
+        std::vector<AdValue> y;
+        TwinFn tw = twin_find(rec.op, rec.params, nullptr);
+        tw(rec, fwd, &y);
+        fwd.push_back(y[0]);
+        const std::vector<AdValue> cot = {values("f32", {rows, n}, dy)};
+        const int64_t n0 = part == 1 ? rows * 2 * n : rows * n;
+        std::vector<AdValue> dc;
+        dc.push_back(values("f32", part == 1 ? std::vector<int64_t>{rows, 2 * n} : std::vector<int64_t>{rows, n}, dx0));
+        if (part == 0) dc.push_back(values("f32", {n}, nullptr));
+        if (part == 2) dc.push_back(values("f32", {rows, n}, dx1));
+        dc.push_back(values("f32", {rows, n}, nullptr));
+        AdjointCall call{rec, fwd, cot, &dc, nullptr, ""};
+        fn(call);
+        std::memcpy(dx0, dc[0].value.data(), sizeof(double) * (size_t)n0);
+        if (part == 2) std::memcpy(dx1, dc[1].value.data(), sizeof(double) * (size_t)(rows * n));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
 }
 
 }  // extern "C"

@@ -15,6 +15,8 @@ LIB_PATH = os.path.join(HERE, "libr97q.so")
 R97Q_F32 = 0
 R97Q_BF16 = 1
 R97Q_I8 = 2
+R97Q_F64 = 3
+R97Q_PART_RMSNORM, R97Q_PART_SILU_MUL, R97Q_PART_SIGMOID_MUL = 0, 1, 2  # the fused quantisers' parts
 R97Q_CODES8 = 8  # R97qWeight.bits of the int8-code form (include/r97q.h)
 R97Q_DECODE_AUTO, R97Q_DECODE_ONCE, R97Q_DECODE_FUSED = 0, 1, 2  # r97q_set_decode_once modes
 R97Q_ADAMW_GRADS_STAGED = 1  # r97q_adamw_step flags: the gradients are staging buffers (include/r97q.h)
@@ -166,6 +168,10 @@ SIGNATURES = {
     "r97q_f32_to_bf16": (C.c_int, [_P, _P, _I, _P]),
     "r97q_quant_act_i8g": (C.c_int, [_P, _i, _I, _I, _I, _i, _P, _P, _P]),
     "r97q_quant_act_i8g_bwd": (C.c_int, [_P, _i, _I, _I, _I, _i, _P, _P, _P, _P]),
+    "r97q_fused_had_quant_i8g": (C.c_int, [_i, _P, _P, _i, _I, _I, _I, C.c_double, C.c_double, C.c_double, _P,
+                                           _P, _P, _P]),
+    "r97q_fused_had_quant_i8g_bwd": (C.c_int, [_i, _P, _P, _i, _I, _I, _I, C.c_double, C.c_double, C.c_double,
+                                               _P, _P, _P, _P, _P, _P]),
     "r97q_vocab_head_workspace_bytes": (_I, [C.POINTER(VocabPlan), _I]),
     "r97q_vocab_head_transpose": (C.c_int, [C.POINTER(VocabPlan), _P, _I, _P, _P, _I, _P]),
     "r97q_vocab_head_cast": (C.c_int, [_P, _P, _I, _P]),

@@ -829,19 +829,39 @@ void lora_shrink_q_device(const AdjointCall& call) {
 }
 
 // ---------------------------------------------------------------- the activation quantiser
+// A numeric parameter as the reference's rows read one (src/adjoint/device/quant.hip:95-118): an
+// int, or a string that is a whole decimal number; false otherwise.
+bool num_param(const std::vector<OpParam>& params, const char* name, double* out) {
+    const OpParam* p = find_param(params, name);
+    if (!p) return false;
+    if (const int64_t* i = std::get_if<int64_t>(&p->second)) {
+        *out = (double)*i;
+        return true;
+    }
+    const std::string* s = std::get_if<std::string>(&p->second);
+    if (!s || s->empty()) return false;
+    char* end = nullptr;
+    const double v = std::strtod(s->c_str(), &end);
+    if (!end || *end != '\0') return false;
+    *out = v;
+    return true;
+}
+
+double param_num(const OpRecord& rec, const char* name, double fallback) {
+    double v = 0.0;
+    return num_param(rec.params, name, &v) ? v : fallback;
+}
+
 // had_quant_act_i8g's straight-through adjoint on the card (the reference's device row
 // src/adjoint/device/quant.hip:951-958 with its predicate :129-137; the rule
 // src/adjoint/host/quant.cpp:318-372): schema x (read); codes, scale (written). dc[x] += W^T (live
 // * cot[codes] / scale); the scale's cotangent is dropped.
 bool serves_rotated(const std::vector<OpParam>& params) {
-    int64_t n = 0, group = 0;
-    for (const OpParam& p : params) {
-        if (const int64_t* v = std::get_if<int64_t>(&p.second)) {
-            if (p.first == "n") n = *v;
-            if (p.first == "group") group = *v;
-        }
-    }
-    return n > 0 && group > 0 && group <= 1024 && (group & (group - 1)) == 0 && n % group == 0;
+    double n = 0.0, group = 0.0;
+    if (!num_param(params, "n", &n) || !num_param(params, "group", &group)) return false;
+    if (n <= 0.0 || n != std::floor(n) || group <= 0.0 || group != std::floor(group) || group > 1024.0) return false;
+    const int64_t g = (int64_t)group;
+    return (g & (g - 1)) == 0 && (int64_t)n % g == 0;
 }
 
 void had_quant_device(const AdjointCall& call) {
@@ -879,6 +899,210 @@ void had_quant_device(const AdjointCall& call) {
     add_into(dx.value.data(), download(c, d_dx, xf.size()), (int64_t)xf.size());
 }
 
+
+// ---------------------------------------------------------------- the fused quantiser producers
+// rmsnorm_had_quant_i8g, gated_had_quant_i8g and gate_had_quant_i8g on the card: the reference's
+// device rows src/adjoint/device/quant.hip:959-961 (predicates :129-159, the record's roles
+// :540-700, the output write's cotangent :817-880) over the composition of its host rows
+// src/adjoint/host/quant.cpp:1008-1405. The roles come from the operands, never from positions or
+// the `n` / `group` parameters: the codes are the written int8 [rows, n] operand, the scale the
+// written float [rows, k] operand with k < n dividing n (group = n / k), a written operand with
+// no dtype or shape is a phantom; the layouts served are the schema's two writes, the live tape's
+// three (the part's output beside the codes) and, with at most one phantom, four. A write of the
+// part's width adds its cotangent to the quantiser's before the part's adjoint; a write over a
+// buffer the record also reads, of that read's size, is the direct path and adds its cotangent
+// into that read's slot. The norm's gain is frozen (no cotangent), and a norm row no consumer reads
+// (the two-way rule, AdjointCall::read_rows) is left out of the result. The intermediate is formed
+// on the card from the inputs uploaded at f64, so the clamp decisions are the host twin's.
+bool serves_gated(const std::vector<OpParam>& params) {
+    if (!serves_rotated(params)) return false;
+    const OpParam* a = find_param(params, "act");
+    return !a || param_is(params, "act", "silu");
+}
+
+bool serves_gate(const std::vector<OpParam>& params) {
+    return serves_rotated(params) && param_is(params, "act", "sigmoid");
+}
+
+int64_t write_slot(const OpRecord& rec, int64_t operand) {
+    int64_t at = 0;
+    for (int64_t j = 0; j < (int64_t)rec.operands.size(); ++j) {
+        if (!rec.operands[(size_t)j].written) continue;
+        if (j == operand) return at;
+        ++at;
+    }
+    return -1;
+}
+
+void fused_quant_device(const AdjointCall& call, int32_t part) {
+    const OpRecord& rec = call.rec;
+    const int64_t operands = (int64_t)rec.operands.size();
+    if (!call.dc) refuse(rec.op, "the walk handed no gradient slots");
+    if (call.cot.size() < 2) refuse(rec.op, "a record that writes the codes and the scale has two cotangents at least");
+    if ((int64_t)call.fwd.size() != operands || (int64_t)call.dc->size() < operands)
+        refuse(rec.op, std::to_string(call.fwd.size()) + " forward values and " + std::to_string(call.dc->size()) +
+                           " gradient slots for a record of " + std::to_string(operands) + " operands");
+    int64_t codes_at = -1, scale_at = -1, reads = 0, writes = 0, phantom = 0;
+    std::string listed;
+    for (int64_t j = 0; j < operands; ++j) {
+        const Operand& o = rec.operands[(size_t)j];
+        if (!o.written) {
+            ++reads;
+            continue;
+        }
+        ++writes;
+        listed += " [" + o.buffer + " " + o.dtype;
+        for (int64_t d : o.shape) listed += " " + std::to_string(d);
+        listed += "]";
+        if (o.dtype.empty() || o.dtype == "invalid" || o.shape.empty()) {
+            ++phantom;
+            continue;
+        }
+        if (codes_at < 0 && o.shape.size() == 2 && (o.dtype == "i8" || o.dtype == "fp8_e4m3" || o.dtype == "fp8_e5m2"))
+            codes_at = j;
+    }
+    if (codes_at < 0) refuse(rec.op, "its writes carry no codes operand:" + listed);
+    if (rec.operands[(size_t)codes_at].dtype != "i8")
+        refuse(rec.op, "fp8 codes are not served by this row (int8 only)");
+    const int64_t rows = rec.operands[(size_t)codes_at].shape[0], n = rec.operands[(size_t)codes_at].shape[1];
+    for (int64_t j = 0; j < operands && scale_at < 0; ++j) {
+        const Operand& o = rec.operands[(size_t)j];
+        if (!o.written || j == codes_at || o.shape.size() != 2 || o.shape[0] != rows) continue;
+        if (o.dtype != "f32" && o.dtype != "f16" && o.dtype != "bf16") continue;
+        if (o.shape[1] > 0 && o.shape[1] < n && n % o.shape[1] == 0) scale_at = j;
+    }
+    if (rows <= 0 || n <= 0 || scale_at < 0) refuse(rec.op, "its writes carry no group scale over the codes:" + listed);
+    const int64_t ngrp = rec.operands[(size_t)scale_at].shape[1], group = n / ngrp;
+    if (group > 1024 || (group & (group - 1)) != 0)
+        refuse(rec.op, "codes " + std::to_string(n) + " wide over " + std::to_string(ngrp) + " groups is not a group size");
+    const int64_t part_reads = part == R97Q_PART_SILU_MUL ? 1 : 2;
+    if (reads != part_reads || !(writes == 2 || writes == 3 || (writes == 4 && phantom <= 1)))
+        refuse(rec.op, "a record of " + std::to_string(reads) + " reads and " + std::to_string(writes) + " writes (" +
+                           std::to_string(phantom) + " phantom) is not a layout this row serves; its writes:" + listed);
+    int64_t second_at = -1;
+    for (int64_t k = 1; k < operands && second_at < 0; ++k)
+        if (!rec.operands[(size_t)k].written) second_at = k;
+    if (rec.operands[0].written) refuse(rec.op, "its first operand is a write, not the part's input");
+    const int64_t total = rows * n;
+    const int64_t in0 = part == R97Q_PART_SILU_MUL ? 2 * total : total;
+    const AdValue& x0 = call.fwd[0];
+    if ((int64_t)x0.value.size() != in0)
+        refuse(rec.op, "its input holds " + std::to_string(x0.value.size()) + " values, the codes need " + std::to_string(in0));
+    const AdValue* x1 = second_at >= 0 ? &call.fwd[(size_t)second_at] : nullptr;
+    if (part == R97Q_PART_RMSNORM && (int64_t)x1->value.size() < n)
+        refuse(rec.op, "the gain holds " + std::to_string(x1->value.size()) + " values for " + std::to_string(n) + " columns");
+    if (part == R97Q_PART_SIGMOID_MUL && (int64_t)x1->value.size() != total)
+        refuse(rec.op, "the gate's second input holds " + std::to_string(x1->value.size()) + " values, not " +
+                           std::to_string(total));
+    const AdValue& scale = call.fwd[(size_t)scale_at];
+    if ((int64_t)scale.value.size() < rows * ngrp) refuse(rec.op, "the scale holds fewer values than its shape");
+    for (int64_t i = 0; i < rows * ngrp; ++i)
+        if (!(scale.value[(size_t)i] > 0.0)) refuse(rec.op, "the scale of a group must be positive");
+    const int64_t codes_cot = write_slot(rec, codes_at);
+    if (codes_cot < 0 || (size_t)codes_cot >= call.cot.size() || (int64_t)call.cot[(size_t)codes_cot].value.size() < total)
+        refuse(rec.op, "the codes' cotangent is missing or short");
+    AdValue& dc0 = call.dc->at(0);
+    if ((int64_t)dc0.value.size() < in0) refuse(rec.op, "the input's gradient slot is short");
+    if (part == R97Q_PART_SIGMOID_MUL && (int64_t)call.dc->at((size_t)second_at).value.size() < total)
+        refuse(rec.op, "the second input's gradient slot is short");
+    const double eps = param_num(rec, "eps", 1e-6), wadd = param_num(rec, "wadd", 0.0),
+                 mult = param_num(rec, "mult", 1.0);
+    // the norm's live rows: a non-finite activation in a read row refuses (elementwise.cpp:587-603)
+    std::vector<char> live_row((size_t)rows, 1);
+    if (part == R97Q_PART_RMSNORM) {
+        int64_t zeroed = 0, admitted = 0, refused = 0;
+        for (int64_t r = 0; r < rows; ++r) {
+            if (!row_readable(call, r)) {
+                live_row[(size_t)r] = 0;
+                ++zeroed;
+                continue;
+            }
+            ++admitted;
+            double ss = 0.0;
+            for (int64_t i = 0; i < n && std::isfinite(ss); ++i) ss += x0.value[(size_t)(r * n + i)] * x0.value[(size_t)(r * n + i)];
+            if (!std::isfinite(ss)) ++refused;
+        }
+        count_read_rows(call.row_count, call.read_rows, zeroed, admitted, refused);
+        if (refused > 0)
+            refuse(rec.op, std::to_string(refused) + " of " + std::to_string(admitted) +
+                               " rows a consumer reads have a non-finite activation");
+    }
+    // the output writes' cotangents: the part's width joins the quantiser's, a read's size over the
+    // read's buffer is the direct path (quant.cpp:1340-1380)
+    std::vector<const AdValue*> outs;
+    for (int64_t j = 0; j < operands; ++j) {
+        const Operand& o = rec.operands[(size_t)j];
+        if (!o.written || j == codes_at || j == scale_at) continue;
+        const int64_t at = write_slot(rec, j);
+        if (at < 0 || (size_t)at >= call.cot.size()) refuse(rec.op, "the write '" + o.buffer + "' has no cotangent slot");
+        const AdValue& oc = call.cot[(size_t)at];
+        const int64_t count = (int64_t)oc.value.size();
+        if (count == 0 || count == 1) continue;
+        if (count == total) {
+            outs.push_back(&oc);
+            continue;
+        }
+        int64_t read_at = -1;
+        for (int64_t k = 0; k < operands && read_at < 0; ++k)
+            if (!rec.operands[(size_t)k].written && rec.operands[(size_t)k].buffer == o.buffer) read_at = k;
+        if (read_at < 0 || count != in0)
+            refuse(rec.op, "the write '" + o.buffer + "' carries " + std::to_string(count) + " values, not the part's " +
+                               std::to_string(total) + " or the direct path's " + std::to_string(in0));
+        AdValue& into = call.dc->at((size_t)read_at);
+        if ((int64_t)into.value.size() != count) refuse(rec.op, "the direct path's slot is not its cotangent's size");
+        for (int64_t i = 0; i < count; ++i) into.value[(size_t)i] += oc.value[(size_t)i];
+    }
+
+    Card& c = card();
+    std::lock_guard<std::mutex> lock(c.mu);
+    RowScope scope{c};
+    const hipStream_t s = stream_of(c);
+    const double* d_x0 = upload_fill<double>(c, "fq_x0", in0, rows, 64, [&](double* p, int64_t lo, int64_t hi) {
+        const int64_t w = in0 / rows;
+        std::memcpy(p + lo * w, x0.value.data() + lo * w, sizeof(double) * (size_t)((hi - lo) * w));
+    });
+    const double* d_x1 = nullptr;
+    if (part == R97Q_PART_RMSNORM)
+        d_x1 = upload(c, "fq_x1", std::vector<double>(x1->value.begin(), x1->value.begin() + n));
+    else if (part == R97Q_PART_SIGMOID_MUL)
+        d_x1 = upload_fill<double>(c, "fq_x1", total, rows, 64, [&](double* p, int64_t lo, int64_t hi) {
+            std::memcpy(p + lo * n, x1->value.data() + lo * n, sizeof(double) * (size_t)((hi - lo) * n));
+        });
+    const float* d_s = upload_fill<float>(c, "fq_scale", rows * ngrp, rows, 256, [&](float* p, int64_t lo, int64_t hi) {
+        for (int64_t i = lo * ngrp; i < hi * ngrp; ++i) p[i] = (float)scale.value[(size_t)i];
+    });
+    const AdValue& gc = call.cot[(size_t)codes_cot];
+    const float* d_g = upload_fill<float>(c, "fq_g", total, rows, 64, [&](float* p, int64_t lo, int64_t hi) {
+        for (int64_t i = lo * n; i < hi * n; ++i) p[i] = (float)gc.value[(size_t)i];
+    });
+    const float* d_go = nullptr;
+    if (!outs.empty())
+        d_go = upload_fill<float>(c, "fq_gout", total, rows, 64, [&](float* p, int64_t lo, int64_t hi) {
+            for (int64_t i = lo * n; i < hi * n; ++i) {
+                double v = 0.0;
+                for (const AdValue* o : outs) v += o->value[(size_t)i];
+                p[i] = (float)v;
+            }
+        });
+    float* d_dx0 = zeros(c, "fq_dx0", (size_t)in0);
+    float* d_dx1 = part == R97Q_PART_SIGMOID_MUL ? zeros(c, "fq_dx1", (size_t)total) : nullptr;
+    r97q_ok(r97q_fused_had_quant_i8g_bwd(part, d_x0, d_x1, R97Q_F64, rows, n, group, eps, wadd, mult, d_s, d_g, d_go,
+                                         d_dx0, d_dx1, s),
+            rec.op.c_str());
+    const float* h0 = download(c, d_dx0, (size_t)in0);
+    const int64_t w0 = in0 / rows;
+    par_ranges(rows, [&](int64_t lo, int64_t hi) {
+        for (int64_t r = lo; r < hi; ++r)
+            if (live_row[(size_t)r])
+                for (int64_t i = r * w0; i < (r + 1) * w0; ++i) dc0.value[(size_t)i] += (double)h0[i];
+    }, 64);
+    if (d_dx1) add_into(call.dc->at((size_t)second_at).value.data(), download(c, d_dx1, (size_t)total), total);
+}
+
+void rmsnorm_quant_device(const AdjointCall& call) { fused_quant_device(call, R97Q_PART_RMSNORM); }
+void gated_quant_device(const AdjointCall& call) { fused_quant_device(call, R97Q_PART_SILU_MUL); }
+void gate_quant_device(const AdjointCall& call) { fused_quant_device(call, R97Q_PART_SIGMOID_MUL); }
+
 }  // namespace
 
 // The frozen positions are the reference's (the weight for gemm_nt; slot, factor and scale for
@@ -886,6 +1110,9 @@ void had_quant_device(const AdjointCall& call) {
 // shrink on the host only).
 R97_REGISTER_ADJOINT_IF_F("gemm_nt", device, gemm_nt_device, serves_bf16, 1)
 R97_REGISTER_ADJOINT_IF("had_quant_act_i8g", device, had_quant_device, serves_rotated)
+R97_REGISTER_ADJOINT_IF_F("rmsnorm_had_quant_i8g", device, rmsnorm_quant_device, serves_rotated, 1)
+R97_REGISTER_ADJOINT_IF("gated_had_quant_i8g", device, gated_quant_device, serves_gated)
+R97_REGISTER_ADJOINT_IF("gate_had_quant_i8g", device, gate_quant_device, serves_gate)
 R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_device, float_act, 1, 2, 3)
 R97_REGISTER_ADJOINT_F("lora_expand", device, lora_expand_device, 1, 2, 3)
 // lora_expand_mm is lora_expand with t rounded to bf16 in its twin only (src/adjoint/host/lora.cpp:
@@ -896,5 +1123,7 @@ R97_REGISTER_ADJOINT_IF_F("lora_shrink", device, lora_shrink_q_device, coded_act
 
 R97_REGISTER_ADJOINT_FAMILY(Linear, "gemm_nt", "gemm_nt_q");
 R97_REGISTER_ADJOINT_FAMILY(Lora, "lora_shrink", "lora_expand", "lora_expand_mm");
+R97_REGISTER_ADJOINT_FAMILY(Quant, "had_quant_act_i8g", "rmsnorm_had_quant_i8g", "gated_had_quant_i8g",
+                            "gate_had_quant_i8g");
 
 }  // namespace r97

@@ -261,6 +261,36 @@ def c1_fixture():
     print("c1 reference")
 
 
+PART_CASES = [
+    # name, part, rows, n, eps, wadd, mult (the fused producers' parts; wadd 1 is Qwen3.5's w + 1 norm)
+    ("rmsnorm_wadd1", "rmsnorm", 6, 256, 1e-6, 1.0, 1.0),
+    ("rmsnorm_scaled", "rmsnorm", 3, 160, 1e-5, 0.5, 1.25),
+    ("silu_mul", "silu_mul", 5, 192, 0.0, 0.0, 1.0),
+    ("sigmoid_mul", "sigmoid_mul", 7, 128, 0.0, 0.0, 1.0),
+]
+
+
+def part_fixtures():
+    """The elementwise parts of the fused quantiser producers: the reference's rmsnorm, silu_mul and
+    act_mul (act = sigmoid) twins and host adjoints (src/adjoint/host/elementwise.cpp:278-347,
+    459-641) on seeded bf16 inputs and an f32 cotangent."""
+    for name, part, rows, n, eps, wadd, mult in PART_CASES:
+        rng = np.random.default_rng(len(name) * 7919 + rows)
+        w0 = 2 * n if part == "silu_mul" else n
+        x0 = bf16r(rng.standard_normal((rows, w0)) * 1.5)
+        x1 = {"rmsnorm": bf16r(rng.standard_normal(n) * 0.3), "silu_mul": None,
+              "sigmoid_mul": bf16r(rng.standard_normal((rows, n)))}[part]
+        dy = rng.standard_normal((rows, n)).astype(np.float32).astype(np.float64)
+        y = O.part_twin(part, x0, x1, eps, wadd, mult, use_ref=True)
+        dx0, dx1 = O.part_adjoint(part, x0, x1, dy, eps, wadd, mult, use_ref=True)
+        d = dict(part=part, eps=eps, wadd=wadd, mult=mult, x0=x0, dy=dy, y=y, dx0=dx0)
+        if x1 is not None:
+            d["x1"] = x1
+        if dx1 is not None:
+            d["dx1"] = dx1
+        np.savez_compressed(os.path.join(OUT, f"part_{name}.npz"), **d)
+
+
 if __name__ == "__main__":
     if O.ref() is None:
         sys.exit("oracle/_ref/libr97ref.so is not built (make -C oracle, needs /root/reference)")
@@ -270,4 +300,5 @@ if __name__ == "__main__":
     linear_q_fixtures()
     lora_q_fixtures()
     adamw_fixture()
+    part_fixtures()
     c1_fixture()

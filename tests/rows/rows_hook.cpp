@@ -436,6 +436,85 @@ int rh_had_quant(int64_t rows, int64_t n, int64_t group, const double* x, const 
     }
 }
 
+// The fused quantiser producers' device rows (rmsnorm_had_quant_i8g, gated_had_quant_i8g,
+// gate_had_quant_i8g). part 0 rmsnorm (x0 [rows, n], x1 w [n]), 1 silu_mul (x0 gate_up [rows, 2n]),
+// 2 sigmoid_mul (x0 gate, x1 x [rows, n]). layout 0: the schema's record (reads, codes, scale);
+// 1: the live tape's (the part's output written beside the codes, its cotangent gout, and for the
+// norm a phantom write ahead of them, tests/gpu/adjoint_quant.cpp:128-175 of the reference);
+// 2: the output write and a write over the first input's buffer (the direct path, cotangent gdir
+// of x0's size), no phantom: four writes; 3: layout 2 with the norm's phantom, five writes, which
+// no row serves. read_rows (count >= 0) is the two-way rule's read set. dx0 / dx1 are added to. Returns
+// -2 when no device row serves the parameters.
+int rh_fused_quant(int32_t part, int64_t rows, int64_t n, int64_t group, int32_t layout, const double* x0,
+                   const double* x1, const double* scale, const double* g, const double* gout, const double* gdir,
+                   double eps, double wadd, double mult, const int64_t* read_rows, int64_t read_count, double* dx0,
+                   double* dx1) {
+    try {
+        static const char* ops[] = {"rmsnorm_had_quant_i8g", "gated_had_quant_i8g", "gate_had_quant_i8g"};
+        OpRecord rec;
+        rec.op = ops[part];
+        rec.params = {{"M", rows}, {"n", n}, {"group", group}, {"dtype", std::string("bf16")}};
+        char b[3][64];
+        std::snprintf(b[0], sizeof b[0], "%.17g", eps);
+        std::snprintf(b[1], sizeof b[1], "%.17g", wadd);
+        std::snprintf(b[2], sizeof b[2], "%.17g", mult);
+        if (part == 0) rec.params.insert(rec.params.end(), {{"eps", std::string(b[0])}, {"wadd", std::string(b[1])},
+                                                           {"mult", std::string(b[2])}});
+        if (part == 2) rec.params.push_back({"act", std::string("sigmoid")});
+        const int64_t w0 = part == 1 ? 2 * n : n, ngrp = n / group;
+        std::vector<AdValue> fwd, cot;
+        const char* in0 = part == 0 ? "x" : part == 1 ? "gate_up" : "gate";
+        rec.operands.push_back(opd(in0, "bf16", {rows, w0}));
+        fwd.push_back(val("bf16", {rows, w0}, x0));
+        const bool phantom = part == 0 && (layout == 1 || layout == 3);
+        if (phantom) {
+            rec.operands.push_back(opd("none:1", "invalid", {}, true));
+            fwd.emplace_back();
+            cot.emplace_back();
+        }
+        if (part == 0) {
+            rec.operands.push_back(opd("w", "bf16", {n}));
+            fwd.push_back(val("bf16", {n}, x1));
+        } else if (part == 2) {
+            rec.operands.push_back(opd("x", "bf16", {rows, n}));
+            fwd.push_back(val("bf16", {rows, n}, x1));
+        }
+        rec.operands.push_back(opd("q", "i8", {rows, n}, true));
+        fwd.push_back(val("i8", {rows, n}, nullptr));
+        cot.push_back(val("f32", {rows, n}, g));
+        rec.operands.push_back(opd("scale", "f32", {rows, ngrp}, true));
+        fwd.push_back(val("f32", {rows, ngrp}, scale));
+        cot.push_back(val("f32", {rows, ngrp}, nullptr));
+        if (layout >= 1) {
+            rec.operands.push_back(opd("out_bf16", "bf16", {rows, n}, true));
+            fwd.push_back(val("bf16", {rows, n}, nullptr));
+            cot.push_back(val("f32", {rows, n}, gout));
+        }
+        if (layout >= 2) {
+            rec.operands.push_back(opd(in0, "bf16", {rows, w0}, true));
+            fwd.push_back(val("bf16", {rows, w0}, nullptr));
+            cot.push_back(val("f32", {rows, w0}, gdir));
+        }
+        std::vector<AdValue> dc;
+        for (size_t j = 0; j < rec.operands.size(); ++j) dc.push_back(val("f32", fwd[j].shape, nullptr));
+        dc[0].value.assign(dx0, dx0 + rows * w0);
+        const size_t second = phantom ? 2 : 1;
+        if (part == 2) dc[second].value.assign(dx1, dx1 + rows * n);
+        AdjointFn fn = adjoint_find(rec.op, Side::device, rec.params, nullptr);
+        if (!fn) return -2;
+        std::vector<int64_t> rr;
+        if (read_count >= 0) rr.assign(read_rows, read_rows + read_count);
+        AdjointCall call{rec, fwd, cot, &dc, nullptr, "", {}, false, read_count >= 0 ? &rr : nullptr, nullptr};
+        timed_row([&] { fn(call); });
+        std::memcpy(dx0, dc[0].value.data(), sizeof(double) * (size_t)(rows * w0));
+        if (part == 2) std::memcpy(dx1, dc[second].value.data(), sizeof(double) * (size_t)(rows * n));
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+
 int64_t rh_weights_prepared() { return device_weight_count(); }
 void rh_weights_clear() { device_weight_clear(); }
 

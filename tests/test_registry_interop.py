@@ -44,6 +44,22 @@ def frozen(op, dev, dt, g):
     n = ref.ref_adjoint_frozen(op.encode(), dev, dt.encode(), g, f)
     return list(f[:min(n, 4)])
 
+ref.ref_adjoint_find_spec.restype = C.c_void_p
+ref.ref_adjoint_find_spec.argtypes = [C.c_char_p, C.c_int32, C.c_char_p]
+ref.ref_adjoint_frozen_spec.restype = C.c_int32
+ref.ref_adjoint_frozen_spec.argtypes = [C.c_char_p, C.c_int32, C.c_char_p, C.POINTER(C.c_int32)]
+
+def frozen_spec(op, dev, spec):
+    f = (C.c_int32 * 4)()
+    n = ref.ref_adjoint_frozen_spec(op.encode(), dev, spec.encode(), f)
+    return list(f[:min(n, 4)])
+
+for op, spec in [("had_quant_act_i8g", "n=256;group=128"), ("rmsnorm_had_quant_i8g", "n=5120;group=128;eps=1e-6"),
+                 ("gated_had_quant_i8g", "n=256;group=128"), ("gated_had_quant_i8g", "n=256;group=128;act=silu"),
+                 ("gate_had_quant_i8g", "n=256;group=128;act=sigmoid"), ("gate_had_quant_i8g", "n=256;group=128"),
+                 ("gated_had_quant_i8g", "n=256;group=128;act=sigmoid"), ("rmsnorm_had_quant_i8g", "n=4096;group=2048")]:
+    print("spec", op, spec, where(ref.ref_adjoint_find_spec(op.encode(), 1, spec.encode())), frozen_spec(op, 1, spec))
+
 for op, dev, dt, g in [("gemm_nt", 1, "bf16", 0), ("lora_shrink", 1, "bf16", 0), ("lora_shrink", 1, "i8", 128),
                        ("lora_shrink", 1, "fp8_e4m3", 128), ("lora_expand", 1, "bf16", 0),
                        ("lora_expand_mm", 1, "bf16", 0), ("lora_expand_mm", 0, "bf16", 0),
@@ -60,7 +76,20 @@ def test_rows_register_into_the_reference_registry():
         pytest.fail(f"{ROWS} is not built (run __graft_entry__.build())")
     out = subprocess.run([sys.executable, "-c", CHILD, REF, ROWS], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr
-    got = {tuple(line.split(" ", 3)[:3]): line.split(" ", 3)[3] for line in out.stdout.strip().splitlines()}
+    lines = out.stdout.strip().splitlines()
+    spec = {tuple(line.split(" ", 3)[1:3]): line.split(" ", 3)[3] for line in lines if line.startswith("spec ")}
+    got = {tuple(line.split(" ", 3)[:3]): line.split(" ", 3)[3] for line in lines if not line.startswith("spec ")}
+    # the quantiser's rows: this build's on the device side, keyed by the reference's predicates
+    # (src/adjoint/device/quant.hip:129-159): the gated row for silu or no act, the gate for sigmoid
+    # only, no row for a group wider than 1024; the norm's gain frozen
+    assert spec[("had_quant_act_i8g", "n=256;group=128")].startswith("libr97rows.so")
+    assert spec[("rmsnorm_had_quant_i8g", "n=5120;group=128;eps=1e-6")] == "libr97rows.so [1]"
+    assert spec[("gated_had_quant_i8g", "n=256;group=128")] == "libr97rows.so []"
+    assert spec[("gated_had_quant_i8g", "n=256;group=128;act=silu")] == "libr97rows.so []"
+    assert spec[("gate_had_quant_i8g", "n=256;group=128;act=sigmoid")] == "libr97rows.so []"
+    assert spec[("gate_had_quant_i8g", "n=256;group=128")].startswith("none")
+    assert spec[("gated_had_quant_i8g", "n=256;group=128;act=sigmoid")].startswith("none")
+    assert spec[("rmsnorm_had_quant_i8g", "n=4096;group=2048")].startswith("none")
     # device rows: this build's, with this build's (the reference's) frozen positions
     assert got[("gemm_nt", "1", "bf16")] == "libr97rows.so [1]"
     assert got[("lora_shrink", "1", "bf16")] == "libr97rows.so [1, 2, 3]"
