@@ -96,7 +96,8 @@ def parse():
                     help="the prepared weight the kernels read: the trellis stream (decoded inside the "
                          "kernels), or the same weight in the int8-code form")
     ap.add_argument("--workload", default="qlinear",
-                    choices=["qlinear", "vocab_head", "c3_block", "c4_attn", "c5_stack", "coded_fwd", "ref_shapes"],
+                    choices=["qlinear", "vocab_head", "c3_block", "c4_attn", "c5_stack", "coded_fwd", "ref_shapes",
+                             "fused_quant"],
                     help="qlinear: the C2 fwd+bwd step (the headline); vocab_head: the vocabulary head's "
                          "transposed product at a 248320-row head, n_embd 2048, --vocab-rows token rows; "
                          "c3_block / c4_attn / c5_stack: one whole LoRA step of BASELINE's MLP block (T=8192, "
@@ -104,7 +105,8 @@ def parse():
                          "on every projection); "
                          "coded_fwd: gemm_nt_q's twin (int8 codes x the int8-code weight) at C2's square layer; "
                          "ref_shapes: the stored-weight gemm_nt twin and adjoint alone at the shapes the reference "
-                         "publishes its device adjoint at (docs/kernels/linear.md:261-268)")
+                         "publishes its device adjoint at (docs/kernels/linear.md:261-268); "
+                         "fused_quant: the fused quantiser producers' forward and adjoint at the live widths")
     ap.add_argument("--decode", default="auto", choices=sorted(DECODE_MODES),
                     help="how the base products meet the weight (r97q_set_decode_once): fused (each tile "
                          "decoded in the product's main loop, once a 512-token panel), once (the whole weight "
@@ -524,6 +526,87 @@ def ref_shapes_bench(args):
     }), flush=True)
 
 
+# The fused quantiser producers at the live tape's widths (tests/gpu/adjoint_quant.cpp:61-67 and the
+# projections around them): name, part, rows, n (the part's output width), group.
+FUSED_SHAPES = [
+    ("rmsnorm_had_quant_i8g", "rmsnorm", 4096, 5120, 128),
+    ("gated_had_quant_i8g", "silu_mul", 4096, 17408, 128),
+    ("gate_had_quant_i8g", "sigmoid_mul", 4096, 6144, 128),
+]
+
+
+def fused_quant_bytes(part, rows, n, group, bwd):
+    """The algorithmic HBM bytes of one launch: every input, output and cotangent once (bf16
+    inputs, int8 codes, f32 scales, a bf16 output beside the codes, f32 cotangents, f32 dx read and
+    written)."""
+    total = rows * n
+    in0 = 2 * total if part == "silu_mul" else total
+    in1 = n if part == "rmsnorm" else total if part == "sigmoid_mul" else 0
+    scale = 4 * total // group
+    if not bwd:
+        return 2 * (in0 + in1) + total + scale + 2 * total
+    dx = 8 * in0 + (8 * total if part == "sigmoid_mul" else 0)
+    return 2 * (in0 + in1) + scale + 4 * total + 4 * total + dx
+
+
+def fused_quant_bench(args):
+    """rmsnorm_had_quant_i8g, gated_had_quant_i8g and gate_had_quant_i8g (r97q_fused_had_quant_i8g and
+    its adjoint) at the live widths: each launch timed by HIP events around `steps` launches after a
+    clock settle, bf16 inputs N(0,1), the part's output written beside the codes, the adjoint with
+    the output's cotangent. Achieved = algorithmic bytes / launch time against HBM's 8 TB/s."""
+    import torch
+
+    from r9700training_amd.quant import fused_had_quant_i8g, fused_had_quant_i8g_bwd
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    out = []
+    for name, part, rows, n, group in FUSED_SHAPES:
+        w0 = 2 * n if part == "silu_mul" else n
+        x0 = torch.randn((rows, w0), dtype=torch.bfloat16, device=dev, generator=g)
+        x1 = (torch.randn(n, dtype=torch.bfloat16, device=dev, generator=g) * 0.3 if part == "rmsnorm" else
+              torch.randn((rows, n), dtype=torch.bfloat16, device=dev, generator=g) if part == "sigmoid_mul" else None)
+        kw = dict(eps=1e-6, wadd=1.0) if part == "rmsnorm" else {}
+        codes, scale, y = fused_had_quant_i8g(part, x0, x1, group, want_y=True, **kw)
+        gc = torch.randn((rows, n), dtype=torch.float32, device=dev, generator=g)
+        go = torch.randn((rows, n), dtype=torch.float32, device=dev, generator=g)
+        dx0 = torch.zeros((rows, w0), dtype=torch.float32, device=dev)
+        dx1 = torch.zeros((rows, n), dtype=torch.float32, device=dev) if part == "sigmoid_mul" else None
+        res = {"op": name, "rows": rows, "n": n, "group": group}
+        for tag, f, bwd in (("forward", lambda: fused_had_quant_i8g(part, x0, x1, group, want_y=True, **kw), False),
+                            ("adjoint", lambda: fused_had_quant_i8g_bwd(part, x0, x1, group, scale, gc, go, dx0=dx0,
+                                                                        dx1=dx1, **kw), True)):
+            settle(f, 0.3, torch)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                f()
+            e1.record()
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / args.steps
+            gbs = fused_quant_bytes(part, rows, n, group, bwd) / (ms * 1e-3) / 1e9
+            res[tag] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                        "bytes": fused_quant_bytes(part, rows, n, group, bwd)}
+        out.append(res)
+        print(json.dumps(res), file=sys.stderr, flush=True)
+        del x0, x1, codes, scale, y, gc, go, dx0, dx1
+        torch.cuda.empty_cache()
+    total_bytes = sum(r[t]["bytes"] for r in out for t in ("forward", "adjoint"))
+    total_s = sum(r[t]["us"] * 1e-6 for r in out for t in ("forward", "adjoint"))
+    gbs = total_bytes / total_s / 1e9
+    print(json.dumps({
+        "metric": "fused quantiser producers (forward + adjoint) GB/s at the live widths",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(total_s * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f64", "data": "synthetic: bf16 inputs N(0,1), gain N(0,0.09); f32 cotangents N(0,1)",
+        "config": {"workload": "fused_quant: rmsnorm / gated / gate _had_quant_i8g, 4096 rows, group 128"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        "ops": out,
+    }), flush=True)
+
+
 def stack_bench(args):
     """One complete LoRA step of a STACKS workload (C5: the 24-layer stack) on one GPU: the forward
     of every projection, layer by layer, then the backward in reverse (dX, dA, dB, the adapters'
@@ -673,6 +756,8 @@ def main():
         return coded_fwd_bench(args)
     if args.workload == "ref_shapes":
         return ref_shapes_bench(args)
+    if args.workload == "fused_quant":
+        return fused_quant_bench(args)
 
     from r9700training_amd import R97Q_BF16, R97Q_F32, _ptr, _stream, check, lib
     from r9700training_amd.qlinear import bwd_workspace, fwd_workspace
