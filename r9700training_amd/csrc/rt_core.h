@@ -13,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "act_tiles.h"
 #include "iqr_device.h"
@@ -153,31 +154,65 @@ __device__ __forceinline__ void adapter(const uint16_t* P, const uint16_t* Q, in
     }
 }
 
-// accumulator element e of tile (mi, ni) is row 32*mi + 8*(e/4) + 4*half + e%4, column 32*ni + l32
-template <int MI>
-__device__ __forceinline__ void store(const f32x16 (&acc)[MI][kNI], void* out, int64_t ld, int64_t m0, int64_t o0,
-                                      int64_t T, int lane, int f32, int accumulate) {
+// accumulator element e of tile (mi, ni) is row 32*mi + 8*(e/4) + 4*half + e%4, column 32*ni + l32.
+// One instantiation per output mode, so the 64 x MI stores of a lane carry no per-element branch:
+// a row pointer a (mi, e) and four stores at immediate offsets 32 ni. FULL: every row of the wave
+// is below T (no row check). ACC: a token block's old values are all loaded before any is stored.
+template <int MI, bool F32, bool ACC, bool FULL>
+__device__ __forceinline__ void store_as(const f32x16 (&acc)[MI][kNI], void* out, int64_t ld, int64_t m0, int64_t o0,
+                                         int64_t T, int lane) {
+    using E = typename std::conditional<F32, float, uint16_t>::type;
     const int half = lane >> 5, l32 = lane & 31;
+    E* base = reinterpret_cast<E*>(out) + (m0 + 4 * half) * ld + o0 + l32;
+    const int64_t rows = T - (m0 + 4 * half);  // rows r < rows of this lane's column are stored
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
+    for (int mi = 0; mi < MI; ++mi) {
+        float old[16][kNI];
+        if constexpr (ACC) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int64_t row = m0 + 32 * mi + 8 * (e >> 2) + 4 * half + (e & 3);
-            if (row >= T) continue;
+            for (int e = 0; e < 16; ++e) {
+                const int r = 32 * mi + 8 * (e >> 2) + (e & 3);
+                const E* d = base + (int64_t)r * ld;
 #pragma unroll
-            for (int ni = 0; ni < kNI; ++ni) {
-                const int64_t col = o0 + 32 * ni + l32;
-                float v = acc[mi][ni][e];
-                if (f32) {
-                    float* d = reinterpret_cast<float*>(out) + row * ld + col;
-                    *d = accumulate ? *d + v : v;
-                } else {
-                    uint16_t* d = reinterpret_cast<uint16_t*>(out) + row * ld + col;
-                    if (accumulate) v += bf16_to_f32(*d);
-                    *d = f32_to_bf16(v);
+                for (int ni = 0; ni < kNI; ++ni) {
+                    if (!FULL && r >= rows) { old[e][ni] = 0.0f; continue; }
+                    if constexpr (F32) old[e][ni] = d[32 * ni];
+                    else old[e][ni] = bf16_to_f32(d[32 * ni]);
                 }
             }
         }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int r = 32 * mi + 8 * (e >> 2) + (e & 3);
+            if (!FULL && r >= rows) continue;
+            E* d = base + (int64_t)r * ld;
+#pragma unroll
+            for (int ni = 0; ni < kNI; ++ni) {
+                float v = acc[mi][ni][e];
+                if constexpr (ACC) v += old[e][ni];
+                if constexpr (F32) d[32 * ni] = v;
+                else d[32 * ni] = f32_to_bf16(v);
+            }
+        }
+    }
+}
+
+template <int MI>
+__device__ __forceinline__ void store(const f32x16 (&acc)[MI][kNI], void* out, int64_t ld, int64_t m0, int64_t o0,
+                                      int64_t T, int lane, int f32, int accumulate) {
+    const bool full = m0 + 32 * MI <= T;  // wave-uniform
+    if (f32) {
+        if (accumulate) {
+            if (full) store_as<MI, true, true, true>(acc, out, ld, m0, o0, T, lane);
+            else store_as<MI, true, true, false>(acc, out, ld, m0, o0, T, lane);
+        } else {
+            if (full) store_as<MI, true, false, true>(acc, out, ld, m0, o0, T, lane);
+            else store_as<MI, true, false, false>(acc, out, ld, m0, o0, T, lane);
+        }
+    } else {
+        if (accumulate) store_as<MI, false, true, false>(acc, out, ld, m0, o0, T, lane);
+        else store_as<MI, false, false, false>(acc, out, ld, m0, o0, T, lane);
+    }
 }
 
 // ---------------------------------------------------------------- the factor gradients' sums
