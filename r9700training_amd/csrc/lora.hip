@@ -10,9 +10,10 @@
 //   lora_down_kernel   one workgroup = 16 token rows (32 at ranks 32 and 64 on long runs) x the whole
 //                      reduction, its 8 (or 4) waves an
 //                      eighth (quarter) each (v_mfma_f32_16x16x32_bf16), reduced through LDS in a
-//                      fixed order; it writes the f32 result and its [hi | lo] splits for the
-//                      fused kernels' epilogues (row-major) and for the gradient kernel
-//                      (transposed).
+//                      fixed order; the token rows are read whole-row (coalesced) and turned into
+//                      MFMA fragments through the wave's LDS region; it writes the f32 result and
+//                      its [hi | lo] splits for the fused kernels' epilogues (row-major) and for the
+//                      gradient kernel (transposed).
 //   lora_grads_kernel  dA and dB in one launch: a workgroup = 256 output columns x a token
 //                      chunk; the token tile (X or dY) and the Pt rows stream through registers
 //                      into two LDS slots, loaded three tiles ahead; the token tile is read back
@@ -84,12 +85,35 @@ __device__ __forceinline__ bf16x8 tr_pair(s16x4 lo4, s16x4 hi4) {
 // tile. The chunk's loads are issued with the token rows', a chunk ahead; no transpose launch.
 constexpr int kDownWavesMax = 8;
 
-template <int RD>
+// A chunk is U 32-deep slices: 128 values at rank 16, and at rank 32 with one token block; 64 at
+// rank 32 with two and at rank 64 (the token rows' and the factor's registers of two chunks in
+// flight stay within the wave's budget)
+template <int RD, int MB>
 struct DownStage {
     static constexpr int S = 2 * RD + 16;              // LDS bytes a staged factor row (16-aligned)
     static constexpr int NB = RD / 16;
-    static constexpr int CH = 32 * (8 / NB);           // factor rows a chunk
+    static constexpr int U = RD == 16 || (RD == 32 && MB == 1) ? 4 : 2;
+    static constexpr int CH = 32 * U;                  // values (factor rows) a chunk
     static constexpr int BYTES = CH * S;               // a wave's stage
+};
+
+// The token rows of a chunk (16 MB rows x CH values) reach the MFMA layout through the wave's own
+// LDS region: each load instruction reads whole row segments (RPI rows of RB bytes, 16 bytes a
+// lane, every row's bytes contiguous), the wave writes them into its region and reads back the
+// A-operand fragments (16 rows x 4 16-byte pieces). A row's 16-byte chunk c sits at chunk
+// c ^ (row & 7): the 8 lanes an LDS cycle serves touch 8 distinct 16-byte bank groups on both
+// sides. After the loop the region holds the wave's partial sums for the cross-wave reduction.
+template <int RD, int MB>
+struct DownTok {
+    static constexpr int CH = DownStage<RD, MB>::CH;
+    static constexpr int RB = 2 * CH;                  // bytes a staged row
+    static constexpr int CPR = RB / 16;                // 16-byte chunks a row (32, 16 or 8)
+    static constexpr int RPI = 64 / CPR;               // rows one load instruction covers
+    static constexpr int NLD = 16 * MB / RPI;          // load instructions a chunk
+    static constexpr int TOK = 16 * MB * RB;           // a wave's staged rows
+    static constexpr int RED = 16 * MB * RD * 4;       // a wave's partial sums
+    static constexpr int BYTES = TOK > RED ? TOK : RED;
+    static_assert(CPR >= 8, "a staged row holds at least 8 chunks");
 };
 
 // MB token blocks of 16 rows a workgroup: two at the larger ranks when that still gives a workgroup
@@ -97,8 +121,9 @@ struct DownStage {
 // factor is four times the token rows' bytes a chunk)
 template <int RD, bool KM, int MB>
 __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
-    __shared__ float red[kDownWavesMax][16 * MB][RD];
-    __shared__ __attribute__((aligned(16))) uint8_t stage_lds[KM ? kDownWavesMax * DownStage<RD>::BYTES : 16];
+    using Tk = DownTok<RD, MB>;
+    __shared__ __attribute__((aligned(16))) uint8_t tok_lds[kDownWavesMax * Tk::BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t stage_lds[KM ? kDownWavesMax * DownStage<RD, MB>::BYTES : 16];
     const int nw = blockDim.x >> 6;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row16 = lane & 15, grp = lane >> 4;
@@ -123,10 +148,18 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
         if (row > a.T - 1) row = a.T - 1;
         ap[b] = a.In + row * a.Kin + wave * kq + 8 * grp;
     }
+    // the chunk loads: instruction i reads rows RPI i + lrow (clamped to T - 1), chunk lch
+    uint8_t* tok = tok_lds + wave * Tk::BYTES;
+    const int lrow = lane / Tk::CPR, lch = lane % Tk::CPR;
+    const uint16_t* cbase = a.In + wave * kq + 8 * lch;
+    auto crow = [&](int i) {
+        int64_t row = m0 + Tk::RPI * i + lrow;
+        return row > a.T - 1 ? a.T - 1 : row;
+    };
     const uint16_t* wp = a.W + (int64_t)row16 * a.Kin + wave * kq + 8 * grp;
     constexpr int NB = RD / 16;
     // KM: the wave's stage, its factor rows from wave * kq on, and the pieces of a full chunk
-    using St = DownStage<RD>;
+    using St = DownStage<RD, MB>;
     uint8_t* stage = stage_lds + (KM ? wave * St::BYTES : 0);
     const uint16_t* wk = a.W + (int64_t)wave * kq * a.r;
     const int rb = 2 * a.r;                             // bytes a factor row in memory
@@ -140,12 +173,11 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
     for (int b = 0; b < MB; ++b)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) acc[b][nb] = (f32x4){};
-    // Chunks of U 32-deep slices (U loads of the token rows and U*NB of the factor a lane, 32
-    // registers a set), two register sets: the loads of chunk c+1 are in flight while chunk c
-    // multiplies, so a wave's whole share (two chunks at the common sizes) is requested at once
-    // instead of one memory latency per 128 values.
-    constexpr int U = 8 / NB;
-    constexpr int CH = 32 * U;
+    // Chunks of U 32-deep slices (the chunk's token rows, read whole-row, and U*NB factor loads a
+    // lane), two register sets: the loads of chunk c+1 are in flight while chunk c is staged and
+    // multiplies.
+    constexpr int U = St::U;
+    constexpr int CH = St::CH;
     const int64_t nch = kq / CH;
     // the tiled copy: every value this lane loads, at the lane's true row (a row past T, up to the
     // copy's 32-row padding, is written as zeros)
@@ -155,7 +187,7 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
             *reinterpret_cast<u32x4*>(a.tiled + act_tile_index(mt, wave * kq + 8 * grp + k, a.T)) =
                 mt < a.T ? v : u32x4{0u, 0u, 0u, 0u};
     };
-    u32x4 xv[2][MB][U], fv[2][U][NB];
+    u32x4 rv[2][Tk::NLD], fv[2][U][NB];
     // KM: piece q of a lane (16 bytes) is piece lane + 64 q of the chunk's rows k .. k + rows, in
     // f's flattened slots; it lands at row (16 p) / rb, byte (16 p) % rb of the stage
     // (pieces past the chunk's rows load piece 0 again and are not stored: no predicated loads,
@@ -185,11 +217,9 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
         const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(stage + (r0 + 4) * St::S + (16 * nb + 4 * q) * 2));
         return tr_pair(lo4, hi4);
     };
-    auto load = [&](int64_t k, u32x4 (&x)[MB][U], u32x4 (&f)[U][NB]) {
+    auto load = [&](int64_t k, u32x4 (&x)[Tk::NLD], u32x4 (&f)[U][NB]) {
 #pragma unroll
-        for (int b = 0; b < MB; ++b)
-#pragma unroll
-            for (int u = 0; u < U; ++u) x[b][u] = *reinterpret_cast<const u32x4*>(ap[b] + k + 32 * u);
+        for (int i = 0; i < Tk::NLD; ++i) x[i] = *reinterpret_cast<const u32x4*>(cbase + crow(i) * a.Kin + k);
         if constexpr (KM) {
             km_load(k, CH, f);
         } else {
@@ -200,7 +230,21 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
                     f[u][nb] = *reinterpret_cast<const u32x4*>(wp + (int64_t)16 * nb * a.Kin + k + 32 * u);
         }
     };
-    auto mult = [&](int64_t k, const u32x4 (&x)[MB][U], const u32x4 (&f)[U][NB]) {
+    auto mult = [&](int64_t k, const u32x4 (&raw)[Tk::NLD], const u32x4 (&f)[U][NB]) {
+        // the chunk's rows into the wave's region, then the A-operand fragments out of it
+#pragma unroll
+        for (int i = 0; i < Tk::NLD; ++i) {
+            const int row = Tk::RPI * i + lrow;
+            *reinterpret_cast<u32x4*>(tok + row * Tk::RB + ((lch ^ (row & 7)) << 4)) = raw[i];
+        }
+        u32x4 x[MB][U];
+#pragma unroll
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int row = 16 * b + row16;
+                x[b][u] = *reinterpret_cast<const u32x4*>(tok + row * Tk::RB + (((4 * u + grp) ^ (row & 7)) << 4));
+            }
         if constexpr (KM) km_store(CH, f);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -215,14 +259,14 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
         }
     };
     int64_t c = 0;
-    if (nch > 0) load(0, xv[0], fv[0]);
+    if (nch > 0) load(0, rv[0], fv[0]);
     for (; c + 2 <= nch; c += 2) {
-        load((c + 1) * CH, xv[1], fv[1]);
-        mult(c * CH, xv[0], fv[0]);
-        if (c + 2 < nch) load((c + 2) * CH, xv[0], fv[0]);
-        mult((c + 1) * CH, xv[1], fv[1]);
+        load((c + 1) * CH, rv[1], fv[1]);
+        mult(c * CH, rv[0], fv[0]);
+        if (c + 2 < nch) load((c + 2) * CH, rv[0], fv[0]);
+        mult((c + 1) * CH, rv[1], fv[1]);
     }
-    if (c < nch) mult(c * CH, xv[0], fv[0]);  // an odd chunk count: the last one sits in set 0
+    if (c < nch) mult(c * CH, rv[0], fv[0]);  // an odd chunk count: the last one sits in set 0
     for (int64_t k = nch * CH; k < kq; k += 32) {
         bf16x8 av[MB];
 #pragma unroll
@@ -250,20 +294,25 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
             }
         }
     }
-    // 16x16 accumulator: element e is row 4*grp + e, column row16
+    // 16x16 accumulator: element e is row 4*grp + e, column row16. The partial sums go into the
+    // wave's own region: its last reads of staged rows were issued before these writes (one wave's
+    // LDS operations run in order), and no other wave touches the region
+    auto red = [&](int w, int ml, int j) -> float& {
+        return reinterpret_cast<float*>(tok_lds + w * Tk::BYTES)[ml * RD + j];
+    };
 #pragma unroll
     for (int b = 0; b < MB; ++b)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) red[wave][16 * b + 4 * grp + e][16 * nb + row16] = acc[b][nb][e];
+            for (int e = 0; e < 4; ++e) red(wave, 16 * b + 4 * grp + e, 16 * nb + row16) = acc[b][nb][e];
     __syncthreads();
     for (int i = threadIdx.x; i < 16 * MB * RD; i += blockDim.x) {
         const int ml = i / RD, j = i % RD;
         const int64_t m = m0 + ml;
         if (j >= a.r || m >= a.ldt) continue;
-        float v = red[0][ml][j];
-        for (int w = 1; w < nw; ++w) v += red[w][ml][j];
+        float v = red(0, ml, j);
+        for (int w = 1; w < nw; ++w) v += red(w, ml, j);
         uint16_t hi = 0, lo = 0;
         if (m < a.T) {
             if (a.out) a.out[m * a.r + j] = a.out_add ? a.out[m * a.r + j] + a.sa * v : a.sa * v;
