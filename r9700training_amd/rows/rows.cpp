@@ -49,6 +49,7 @@
 #include "r97/adjoint.h"
 #include "r97/adjoint_family.h"
 #include "r97/grad_stage.h"
+#include "r97/scratch.h"
 #include "r97/stored_weight.h"
 #include "r97q.h"
 
@@ -306,10 +307,12 @@ void split_bf16(const std::vector<double>& v, std::vector<uint16_t>& hi, std::ve
 }
 
 // ---------------------------------------------------------------- the card
-// One stream, buffers by role (device, and pinned host memory for the staging copies), one rocBLAS
-// handle; created on first use. A buffer grows when a call needs more; when a row returns with more
-// than kHeldBytes held on either side, every buffer is freed, so a huge call's buffers do not stay
-// for the process. A mutex serialises rows called from more than one thread.
+// One stream, buffers by role (device scratch, and pinned host memory for the staging copies), one
+// rocBLAS handle; created on first use. A row's device buffers are scratch of that call
+// (r97/scratch.h, as the reference's rows take theirs): taken from the ledger as the call needs them
+// and all returned when the row ends, so the ledger holds nothing between calls. The pinned buffers
+// stay for the next call unless more than kHeldBytes is held. A mutex serialises rows called from
+// more than one thread.
 constexpr size_t kHeldBytes = size_t(1) << 30;
 struct Card {
     std::mutex mu;
@@ -340,9 +343,11 @@ hipStream_t stream_of(Card& c) {
 void* buffer(Card& c, const std::string& role, size_t bytes) {
     auto& b = c.bufs[role];
     if (b.second < bytes || !b.first) {
-        if (b.first) hip_ok(hipFree(b.first), "hipFree");
+        device::scratch_free(b.first);
         b = {nullptr, 0};
-        hip_ok(hipMalloc(&b.first, bytes ? bytes : 1), "hipMalloc");
+        b.first = device::scratch_alloc(bytes ? (int64_t)bytes : 1);
+        if (!b.first)
+            throw std::runtime_error("device scratch: " + std::to_string(bytes) + " bytes refused (" + role + ")");
         b.second = bytes;
     }
     return b.first;
@@ -360,17 +365,15 @@ void* pinned(Card& c, const std::string& role, size_t bytes) {
     return b.first;
 }
 
-// a row's end: every buffer freed when either side holds more than kHeldBytes (the card's work is
-// done: the row synchronised its stream before it read its results back)
+// a row's end: every device buffer returned to the scratch ledger, the pinned buffers freed when
+// they hold more than kHeldBytes (the card's work is done: the row synchronised its stream before it
+// read its results back, and a row that throws midway returns its scratch through hipFree, which
+// waits for the card)
 void trim(Card& c) {
-    size_t dev = 0, host = 0;
-    for (const auto& kv : c.bufs) dev += kv.second.second;
+    for (auto& kv : c.bufs) device::scratch_free(kv.second.first);
+    c.bufs.clear();
+    size_t host = 0;
     for (const auto& kv : c.pinned) host += kv.second.second;
-    if (dev > kHeldBytes) {
-        for (auto& kv : c.bufs)
-            if (kv.second.first) (void)hipFree(kv.second.first);
-        c.bufs.clear();
-    }
     if (host > kHeldBytes) {
         for (auto& kv : c.pinned)
             if (kv.second.first) (void)hipHostFree(kv.second.first);

@@ -16,6 +16,7 @@
 #include "r97/adjoint.h"
 #include "r97/adjoint_family.h"
 #include "r97/grad_stage.h"
+#include "r97/scratch.h"
 #include "r97/stored_weight.h"
 
 using namespace r97;
@@ -517,5 +518,25 @@ int rh_fused_quant(int32_t part, int64_t rows, int64_t n, int64_t group, int32_t
 
 int64_t rh_weights_prepared() { return device_weight_count(); }
 void rh_weights_clear() { device_weight_clear(); }
+
+// the scratch ledger (r97/scratch.h): its counters, a reset (0, or -1 with the error when scratch is
+// still held), and a block taken and returned outside any row (a test's stand-in for a leak)
+void rh_scratch_stats(int64_t* live, int64_t* peak, int64_t* allocations) {
+    const device::ScratchStats s = device::scratch_stats();
+    *live = s.live_bytes;
+    *peak = s.peak_bytes;
+    *allocations = s.allocations;
+}
+int rh_scratch_reset() {
+    try {
+        device::scratch_reset();
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return -1;
+    }
+}
+void* rh_scratch_alloc(int64_t bytes) { return device::scratch_alloc(bytes); }
+void rh_scratch_free(void* p) { device::scratch_free(p); }
 
 }  // extern "C"

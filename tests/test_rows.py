@@ -35,7 +35,17 @@ def hook():
     L.rh_lora_expand.argtypes = [C.c_int64] * 4 + [_P] * 7 + [C.c_int, C.c_int, _P]
     L.rh_lora_expand_op.argtypes = [C.c_char_p] + [C.c_int64] * 4 + [_P] * 7 + [C.c_int, C.c_int, _P]
     L.rh_weights_prepared.restype = C.c_int64
+    L.rh_scratch_stats.argtypes = [C.POINTER(C.c_int64)] * 3
+    L.rh_scratch_alloc.restype = _P
+    L.rh_scratch_alloc.argtypes = [C.c_int64]
+    L.rh_scratch_free.argtypes = [_P]
     return L
+
+
+def scratch(L):
+    v = [C.c_int64() for _ in range(3)]
+    L.rh_scratch_stats(*[C.byref(x) for x in v])
+    return tuple(x.value for x in v)  # live, peak, allocations
 
 
 def p(a):
@@ -60,6 +70,47 @@ def rel_l2(got, want):
 def test_registry_rules_and_registrations():
     line = hook().rh_registry_selftest()
     assert line == 0, f"registry self-test failed at rows_hook.cpp:{line}"
+
+
+def test_scratch_ledger_without_a_card():
+    """The ledger's bookkeeping that needs no device memory (src/adjoint/device/scratch.h:15-48): a
+    request of no bytes, and a null or unknown block returned, change nothing."""
+    L = hook()
+    assert L.rh_scratch_reset() == 0
+    assert scratch(L) == (0, 0, 0)
+    assert L.rh_scratch_alloc(0) is None and L.rh_scratch_alloc(-8) is None
+    L.rh_scratch_free(None)
+    L.rh_scratch_free(C.c_void_p(0x1000))
+    assert scratch(L) == (0, 0, 0)
+
+
+@pytest.mark.gpu
+def test_scratch_ledger_rows_return_their_scratch():
+    """A row's device buffers are scratch of its call: the ledger reports the call's peak and holds
+    nothing once the row returns, as the reference's device tests read it
+    (tests/support/device_check.h:252-262); a block still held makes the reset throw, naming the bytes."""
+    from gpu_util import stored_operand
+
+    print("case scratch ledger over a gemm_nt row", flush=True)
+    L = hook()
+    M, N, K = 96, 256, 384
+    rng = np.random.default_rng(5)
+    planes = S.trellis(rows=N, cols=K, bits=5, state_bits=16, run_rows=128, rb=1, mad=1, scale_dtype=S.F32,
+                       rowf=True, seed=3)
+    keep = []
+    enc, raw = stored_operand(planes, keep)
+    dy, dx = rng.standard_normal((M, N)), np.zeros((M, K))
+    assert L.rh_scratch_reset() == 0
+    check(L, L.rh_gemm_nt(M, N, K, p(dy), C.addressof(enc), raw.data_ptr(), None, p(dx)))
+    live, peak, allocs = scratch(L)
+    print(f"  live {live} peak {peak} allocations {allocs}", flush=True)
+    # the row's uploads (dy as a bf16 [hi | lo] pair) and its f32 result at least
+    assert live == 0 and allocs >= 2 and peak >= M * N * 4 + M * K * 4
+    blk = L.rh_scratch_alloc(4096)
+    assert blk and scratch(L)[0] == 4096
+    assert L.rh_scratch_reset() == -1 and "4096 bytes" in L.rh_last_error().decode()
+    L.rh_scratch_free(blk)
+    assert L.rh_scratch_reset() == 0 and scratch(L) == (0, 0, 0)
 
 
 @pytest.mark.gpu
