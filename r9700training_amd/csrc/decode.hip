@@ -187,6 +187,91 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
     }
 }
 
+// The common form -- trellis.mad, L = 16, rb = 1, bits 3..6 -- with the code width a compile-time
+// constant. One thread: the 4 columns 4q..4q+3 (their codes are 4 BITS consecutive bits of a row:
+// one or two dword loads and a funnel shift) over the ROWS rows of chunk ch (8: the chunks never
+// straddle a run: the launch checks that runs, rows and row0 are whole chunks, and that code rows
+// are 4-byte aligned; 16-row chunks measured slower, 13.3 against 10.0 µs, with half the threads);
+// the state walk, the hash and the byte sum are a handful of VALU a value with no per-value form
+// branches. TILED: each 8 x 4 codes of the thread are one 32-byte unit of the
+// int8-code form, written as two 16-byte stores; canonical: one 4-byte store a row. The same values as
+// decode_kernel, bit for bit.
+template <int BITS, bool TILED, int ROWS>
+__global__ __launch_bounds__(kDecodeThreads) void decode_mad_kernel(const R97IqrDecodeDesc d, int64_t chunks,
+                                                                    int64_t scale_ld) {
+    using O = DecodeOut<TILED>;
+    constexpr int C = (16 + BITS - 1) / BITS;  // codes above a chunk that seed its state
+    const int64_t ch = blockIdx.y + (int64_t)blockIdx.z * gridDim.y;
+    const int64_t q4 = (int64_t)blockIdx.x * kDecodeThreads + threadIdx.x;
+    if (ch >= chunks || 4 * q4 >= d.cols) return;
+    const int64_t j = 4 * q4;  // the thread's first column
+    const int64_t r = d.row0 + ch * ROWS;
+    const int64_t run_start = (r / d.run_rows) * d.run_rows;
+    int64_t run_end = run_start + d.run_rows;
+    if (run_end > d.rows_all) run_end = d.rows_all;
+    const int64_t len = run_end - run_start;
+    const int64_t w = (j * BITS) >> 5;
+    const int sh = (int)((j * BITS) & 31);
+    const bool straddle = sh + 4 * BITS > 32;
+    // the 4 codes of row q, column 4q4 + c at bits BITS c
+    auto codes4 = [&](int64_t q) -> uint32_t {
+        const uint32_t* row = reinterpret_cast<const uint32_t*>(d.codes + (q - d.row0) * d.codes_row_bytes);
+        const uint32_t lo = row[w];
+        const uint32_t hi = straddle ? row[w + 1] : 0u;
+        return __builtin_amdgcn_alignbit(hi, lo, (uint32_t)sh);
+    };
+    constexpr uint32_t kMask = (1u << BITS) - 1u;
+    uint32_t st[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = C; q >= 1; --q) {
+        int64_t t = r - q;
+        if (t < run_start) t += len;
+        const uint32_t c4 = codes4(t);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) st[c] = ((st[c] << BITS) | ((c4 >> (BITS * c)) & kMask)) & 0xFFFFu;
+    }
+    const uint32_t a24 = d.mad_a & 0xFFFFFFu;
+#pragma unroll
+    for (int u = 0; u < ROWS / 8; ++u) {
+        const int64_t ru = r + 8 * u;
+        uint32_t v[8][4];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t c4 = codes4(ru + i);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                st[c] = ((st[c] << BITS) | ((c4 >> (BITS * c)) & kMask)) & 0xFFFFu;
+                v[i][c] = (uint32_t)mad_value(st[c], a24, d.mad_b) & 0xFFu;
+            }
+        }
+        if constexpr (TILED) {
+            // byte 16 (c >> 1) + 2 i + (c & 1) of the unit is row i, column c
+            uint32_t o[8];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    o[4 * h + k] = v[2 * k][2 * h] | (v[2 * k][2 * h + 1] << 8) | (v[2 * k + 1][2 * h] << 16) |
+                                   (v[2 * k + 1][2 * h + 1] << 24);
+            uint4* dst = reinterpret_cast<uint4*>(d.out_codes + O::code(d, ru, j));
+            dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+            dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                *reinterpret_cast<uint32_t*>(d.out_codes + O::code(d, ru + i, j)) =
+                    v[i][0] | (v[i][1] << 8) | (v[i][2] << 16) | (v[i][3] << 24);
+        }
+    }
+    // the chunk's scales of the thread's 128-column block: the block's first thread
+    if ((j & 127) == 0) {
+        const int64_t kb = j >> 7;
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i)
+            d.out_scale[O::scale(d, r + i, kb, scale_ld)] = f32_to_bf16(block_scale(d, r + i, kb));
+    }
+}
+
 // ---------------------------------------------------------------- preparation
 // One workgroup per (segment g, 256 columns): the segment's 32 packed rows over those columns are
 // staged in LDS (every byte load of the workgroup in flight at once, each row's bytes contiguous),
@@ -286,8 +371,31 @@ __global__ __launch_bounds__(256) void prepare_scale_kernel(const R97IqrDecodeDe
 
 }  // namespace
 
+// the common form on whole 8-row chunks and aligned rows: decode_mad_kernel
+template <bool TILED>
+bool mad_fast(const R97IqrDecodeDesc& d) {
+    return !d.affine && d.mad && d.rb == 1 && d.state_bits == 16 && d.bits >= 3 && d.bits <= 6 &&
+           d.run_rows % 8 == 0 && d.row0 % 8 == 0 && d.rows % 8 == 0 && d.codes_row_bytes % 4 == 0 &&
+           (reinterpret_cast<uintptr_t>(d.codes) & 3) == 0 &&
+           (reinterpret_cast<uintptr_t>(d.out_codes) & (TILED ? 15 : 3)) == 0;
+}
+
 template <bool TILED>
 void launch_decode(const R97IqrDecodeDesc& d, hipStream_t s, int64_t scale_ld = 0) {
+    if (mad_fast<TILED>(d)) {
+        const int64_t chunks = d.rows / 8;
+        const int64_t gy = chunks < 65535 ? chunks : 65535;
+        const int64_t gz = (chunks + gy - 1) / gy;
+        const dim3 grid((unsigned)((d.cols / 4 + kDecodeThreads - 1) / kDecodeThreads), (unsigned)gy, (unsigned)gz);
+        const dim3 block(kDecodeThreads);
+        switch (d.bits) {
+            case 3: hipLaunchKernelGGL((decode_mad_kernel<3, TILED, 8>), grid, block, 0, s, d, chunks, scale_ld); break;
+            case 4: hipLaunchKernelGGL((decode_mad_kernel<4, TILED, 8>), grid, block, 0, s, d, chunks, scale_ld); break;
+            case 5: hipLaunchKernelGGL((decode_mad_kernel<5, TILED, 8>), grid, block, 0, s, d, chunks, scale_ld); break;
+            default: hipLaunchKernelGGL((decode_mad_kernel<6, TILED, 8>), grid, block, 0, s, d, chunks, scale_ld); break;
+        }
+        return;
+    }
     const int64_t chunk_rows = (d.run_rows % 8 == 0) ? 8 : 1;
     // chunks never straddle a run: runs start at multiples of run_rows and chunk_rows divides it
     const int64_t chunks = (d.rows + chunk_rows - 1) / chunk_rows;
