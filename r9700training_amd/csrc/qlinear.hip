@@ -70,38 +70,55 @@ Shape shape(int64_t T, int64_t N, int64_t K, int r) {
     return Shape{T, N, K, r, once};
 }
 
-// Split-K of the fused kernel (rt::Params::ksplit). A launch holds tiles = ceil(T/512) x outputs/128
-// workgroups, one a CU at a time over the card's 256 CUs; when the tiles leave much of the last
-// round of CUs idle and the reduction is long, the reduction is dealt over S ranges (S x tiles
-// workgroups), each range's f32 partial product written to the workspace and added in range order
-// by a second launch. The choice minimises a model of the launch's time in microseconds, measured
-// at C2 and at the reference's published shapes: a 64-deep step of a full round of tiles takes
-// ~1.9 us, a partial last round with a fraction f of the CUs busy runs at a higher clock and takes
-// (0.4 + 0.6 f) of a full round's time, a round's prologue and epilogue ~3 us, and the partials
-// cost S x T x outputs x 8 bytes (written, then read) at ~5 TB/s plus ~4 us for the added launch.
-// A split needs at least 16 steps a range and must beat no split by 10%. Deterministic in the
-// shape, so a call's bits never depend on anything else.
+// Split-K of the fused kernel (rt::Params::ksplit, nfull). A launch holds tiles = ceil(T/512) x
+// outputs/128 workgroups, one a CU at a time over the card's 256 CUs. When the tiles leave much of
+// the last round of CUs idle and the reduction is long, the reductions of the tiles past nfull are
+// dealt over S ranges each (a workgroup a range), each range's f32 partial product written to the
+// workspace and added in range order by a second launch. Two forms: every tile split (nfull 0: a
+// launch of fewer tiles than CUs), or the whole rounds' tiles run whole and only the tiles of the
+// partial last round split (nfull = 256 x whole rounds), so the last round runs on every CU for
+// 1/S of a tile's time and only its tiles write partials. The choice minimises a model of the
+// launch's time in microseconds, measured at C2 and at the reference's published shapes: a 64-deep
+// step of a full round of tiles takes ~1.85 us, a partial last round with a fraction f of the CUs
+// busy runs at a higher clock and takes (0.4 + 0.6 f) of a full round's time, a round's prologue
+// and epilogue ~3 us, and the partials cost their bytes written and read (S x split tiles x
+// 512 x 128 x 8; the writes overlap other workgroups' products) at ~10 TB/s plus ~4 us for the
+// added launch. A split needs at least 16 steps a range and must beat no split by 7%.
+// Deterministic in the shape, so a call's bits never depend on anything else.
 constexpr int kSplitMax = 8;
-int ksplit_for(int64_t T, int64_t outputs, int64_t red) {
+struct Split {
+    int S;      // ranges a split tile's reduction is dealt over (1: no split)
+    int nfull;  // tiles run whole, before the split ones (every tile when S is 1)
+};
+Split split_for(int64_t T, int64_t outputs, int64_t red) {
     const int64_t tiles = ((T + rt::kBM - 1) / rt::kBM) * (outputs / rt::kBN);
     const int64_t nsteps = red / rt::kStep;
-    auto cost = [&](int S) {
-        const double u = (double)(tiles * S) / 256.0;
+    auto rounds = [](double u) {
         const double full = std::floor(u), frac = u - full;
-        const double rounds = full + (frac > 0 ? 0.4 + 0.6 * frac : 0.0);
-        double t = rounds * ((double)nsteps / S * 1.9 + 3.0);
-        if (S > 1) t += (double)S * (double)T * (double)outputs * 8.0 / 5.0e6 + 4.0;
+        return full + (frac > 0 ? 0.4 + 0.6 * frac : 0.0);
+    };
+    auto cost = [&](int64_t nfull, int S) {
+        double t = rounds((double)nfull / 256.0) * ((double)nsteps * 1.85 + 3.0);
+        if (S > 1) {
+            const int64_t rest = tiles - nfull;
+            t += rounds((double)(rest * S) / 256.0) * ((double)nsteps / S * 1.85 + 3.0);
+            t += (double)S * (double)rest * rt::kBM * rt::kBN * 8.0 / 1.0e7 + 4.0;
+        }
         return t;
     };
-    const double t1 = cost(1);
-    int best = 1;
+    const double t1 = cost(tiles, 1);
+    Split best{1, (int)tiles};
     double best_t = t1;
-    for (int S = 2; S <= kSplitMax; ++S) {
-        if (nsteps / S < 16) break;
-        const double t = cost(S);
-        if (t < 0.9 * t1 && t < best_t) {
-            best = S;
-            best_t = t;
+    const int64_t whole = tiles / 256 * 256;  // the whole rounds' tiles
+    for (int64_t nfull : {(int64_t)0, whole}) {
+        if (nfull > 0 && nfull == tiles) continue;
+        for (int S = 2; S <= kSplitMax; ++S) {
+            if (nsteps / S < 16) break;
+            const double t = cost(nfull, S);
+            if (t < 0.93 * t1 && t < best_t) {
+                best = Split{S, (int)nfull};
+                best_t = t;
+            }
         }
     }
     return best;
@@ -112,12 +129,13 @@ int ksplit_for(int64_t T, int64_t outputs, int64_t red) {
 // Backward: dYt (dY's tiled copy) | At [K, r] | P [T, 2r] | PtA [2r, ldt] | PtB [2r, ldt]
 // | partA [chunks, r, K] | partB [chunks, r, N] (f32 partial sums of the factor gradients) | done
 // (bwd_counters) | Wt (as the forward's).
-// Either direction then holds Sp [S, T, outputs] f32: the split-K partials, when the fused kernel
-// splits (ksplit > 1; never on the decode-once path, nor for the entry that allocates nothing).
+// Either direction then holds Sp [S, split tiles, 512, 128] f32: the split-K partials, when the fused
+// kernel splits (ksplit > 1; never on the decode-once path, nor for the entry that allocates
+// nothing).
 // Wt and Sp are -1 where the layout has none.
 struct FwdWs {
     int64_t Xt, P, Apad, Wt, Sp, total;
-    int ksplit;
+    int ksplit, nfull;
 };
 FwdWs fwd_ws(const Shape& s, bool fused_only = false) {
     FwdWs w{};
@@ -135,17 +153,19 @@ FwdWs fwd_ws(const Shape& s, bool fused_only = false) {
         w.Wt = w.total;
         w.total += align256(rt::wt_bytes(s.N, s.K));
     } else if (!fused_only) {
-        w.ksplit = ksplit_for(s.T, s.N, s.K);
+        const Split sp = split_for(s.T, s.N, s.K);
+        w.ksplit = sp.S;
+        w.nfull = sp.nfull;
         if (w.ksplit > 1) {
             w.Sp = w.total;
-            w.total += align256((int64_t)w.ksplit * s.T * s.N * 4);
+            w.total += align256(rt::split_bytes(sp.S, ((s.T + rt::kBM - 1) / rt::kBM) * (s.N / rt::kBN) - sp.nfull));
         }
     }
     return w;
 }
 struct BwdWs {
     int64_t dYt, At, P, PtA, PtB, partA, partB, done, Wt, Sp, total;
-    int ksplit;
+    int ksplit, nfull;
 };
 // the backward's counters, zeroed by its down product: the gradient launch's column blocks (dA's,
 // then dB's)
@@ -157,10 +177,12 @@ void bwd_ws_wt(const Shape& s, BwdWs& w) {
         w.Wt = w.total;
         w.total += align256(rt::wt_bytes(s.N, s.K));
     } else {
-        w.ksplit = ksplit_for(s.T, s.K, s.N);
+        const Split sp = split_for(s.T, s.K, s.N);
+        w.ksplit = sp.S;
+        w.nfull = sp.nfull;
         if (w.ksplit > 1) {
             w.Sp = w.total;
-            w.total += align256((int64_t)w.ksplit * s.T * s.K * 4);
+            w.total += align256(rt::split_bytes(sp.S, ((s.T + rt::kBM - 1) / rt::kBM) * (s.K / rt::kBN) - sp.nfull));
         }
     }
 }
@@ -338,7 +360,7 @@ int fwd_prep(const Shape& sh, const uint16_t* X, const uint16_t* A, float scale,
 // without, the fused kernel decoding in its main loop
 int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act, const uint16_t* P,
             const uint16_t* Q, void* out, int32_t out_dtype, int32_t accumulate, uint8_t* wt, hipStream_t s,
-            const rt::Params::Sums* sums = nullptr, int ksplit = 1, float* part = nullptr) {
+            const rt::Params::Sums* sums = nullptr, int ksplit = 1, int nfull = 0, float* part = nullptr) {
     rt::Params p{};
     p.act = act;
     p.T = sh.T;
@@ -359,6 +381,7 @@ int rt_base(const R97qWeight* w, bool fwd, const Shape& sh, const uint16_t* act,
     p.otiles = (int)((fwd ? sh.N : sh.K) / rt::kBN);
     p.wt = wt;
     p.ksplit = wt || !part ? 1 : ksplit;
+    p.nfull = p.ksplit > 1 ? nfull : p.mtiles * p.otiles;
     p.part = p.ksplit > 1 ? part : nullptr;
     if (sums && !fwd) {
         p.sums[0] = sums[0];
@@ -397,7 +420,7 @@ int fwd_base(const R97qWeight* w, const Shape& sh, const uint16_t* B, void* Y, i
     const FwdWs ws = fwd_ws(sh, fused_only);
     return rt_base(w, true, sh, reinterpret_cast<const uint16_t*>(wsb + ws.Xt),
                    reinterpret_cast<const uint16_t*>(wsb + ws.P), B, Y, y_dtype, 0,
-                   ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s, nullptr, ws.ksplit,
+                   ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s, nullptr, ws.ksplit, ws.nfull,
                    ws.Sp >= 0 ? reinterpret_cast<float*>(wsb + ws.Sp) : nullptr);
 }
 
@@ -476,7 +499,7 @@ int dx_base(const R97qWeight* w, const Shape& sh, void* dX, int32_t dx_dtype, in
     return rt_base(w, false, sh, reinterpret_cast<const uint16_t*>(wsb + ws.dYt),
                    reinterpret_cast<const uint16_t*>(wsb + ws.P), reinterpret_cast<const uint16_t*>(wsb + ws.At), dX,
                    dx_dtype, accumulate, ws.Wt >= 0 ? wsb + ws.Wt : nullptr, s,
-                   sums[0].part || sums[1].part ? sums : nullptr, ws.ksplit,
+                   sums[0].part || sums[1].part ? sums : nullptr, ws.ksplit, ws.nfull,
                    ws.Sp >= 0 ? reinterpret_cast<float*>(wsb + ws.Sp) : nullptr);
 }
 

@@ -159,13 +159,21 @@ __global__ __launch_bounds__(64 * kPdWaves, 1) void qlinear_pd_kernel(const Para
     }
 }
 
-// out[i] (+)= part[0][i] + ... + part[S-1][i] over n = T x outputs values, four a thread a pass
-// (outputs is a multiple of 128, so n is a multiple of 4): the split product's partials added in
-// range order, then into the f32 output (accumulate) or written as f32 / bf16
-__global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, int S, int64_t n, void* out,
-                                                           int out_f32, int accumulate) {
+// The split tiles' partials (part [S][nsplit][kBM][kBN]; slot lt holds tile nfull + lt) added in
+// range order, then into the f32 output (accumulate) or written as f32 / bf16; the slots' rows past
+// T (never written) are skipped. Four values a thread a pass: kBN is a multiple of 4, so the four
+// lie in one row of the tile.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, int S, int nsplit, int nfull,
+                                                           int otiles, int64_t T, int64_t ld, void* out, int out_f32,
+                                                           int accumulate) {
+    const int64_t n = (int64_t)nsplit * kBM * kBN;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x * 4;
     for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < n; i += stride) {
+        const int tile = nfull + (int)(i / (kBM * kBN));
+        const int e = (int)(i % (kBM * kBN));
+        const int64_t row = (int64_t)(tile / otiles) * kBM + e / kBN;
+        if (row >= T) continue;
+        const int64_t o = row * ld + (int64_t)(tile % otiles) * kBN + e % kBN;
         float4 v = *reinterpret_cast<const float4*>(part + i);
         for (int z = 1; z < S; ++z) {
             const float4 u = *reinterpret_cast<const float4*>(part + (int64_t)z * n + i);
@@ -175,23 +183,23 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, in
             v.w += u.w;
         }
         if (out_f32) {
-            float4* d = reinterpret_cast<float4*>(static_cast<float*>(out) + i);
+            float4* d = reinterpret_cast<float4*>(static_cast<float*>(out) + o);
             if (accumulate) {
-                const float4 o = *d;
-                v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+                const float4 old = *d;
+                v = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
             }
             *d = v;
         } else {
-            uint16_t* d = static_cast<uint16_t*>(out) + i;
+            uint16_t* d = static_cast<uint16_t*>(out) + o;
             if (accumulate) {
                 v.x += bf16_to_f32(d[0]);
                 v.y += bf16_to_f32(d[1]);
                 v.z += bf16_to_f32(d[2]);
                 v.w += bf16_to_f32(d[3]);
             }
-            const uint2 o = {(uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16),
+            const uint2 w = {(uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16),
                              (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16)};
-            *reinterpret_cast<uint2*>(d) = o;
+            *reinterpret_cast<uint2*>(d) = w;
         }
     }
 }
@@ -199,10 +207,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* part, in
 }  // namespace
 
 void launch_split_reduce(const Params& p, bool fwd, hipStream_t s) {
-    const int64_t n = p.T * (fwd ? p.N : p.K);
+    const int nsplit = p.mtiles * p.otiles - p.nfull;
+    const int64_t n = (int64_t)nsplit * kBM * kBN;
     const int64_t blocks = (n / 4 + 255) / 256;
     hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s,
-                       (const float*)p.part, p.ksplit, n, p.out, p.out_f32, fwd ? 0 : p.accumulate);
+                       (const float*)p.part, p.ksplit, nsplit, p.nfull, p.otiles, p.T, fwd ? p.N : p.K, p.out,
+                       p.out_f32, fwd ? 0 : p.accumulate);
 }
 
 void launch_pd(const Params& p, bool fwd, hipStream_t s) {

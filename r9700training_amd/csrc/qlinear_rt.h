@@ -29,11 +29,13 @@ struct Params {
     int out_f32;
     int accumulate;            // dX only: add into `out`
     int mtiles, otiles;
-    // split-K (fused kernel only): the reduction's steps are dealt over `ksplit` ranges, each a
-    // workgroup per output tile, each writing its f32 partial product into part[z] [T, outputs]
-    // (the adapter's epilogue in range 0 only); launch_split_reduce then adds them, in range
-    // order, into `out`. ksplit 1: no split, the product written into `out` directly.
+    // split-K (fused kernel only): tiles 0 .. nfull-1 (tokens outer, outputs inner) run whole; the
+    // reduction of each of the others is dealt over `ksplit` ranges, a workgroup each, each writing
+    // its f32 partial product into part [ksplit][tiles - nfull][kBM][kBN] (the adapter's epilogue
+    // in range 0 only); launch_split_reduce then adds them, in range order, into `out`. ksplit 1:
+    // no split (nfull = every tile), the product written into `out` directly.
     int ksplit;
+    int nfull;
     float* part;
     const uint8_t* wt;         // the weight decoded once a call (launch_predecode), for launch_pd
     // dX only: the factor gradients' deferred chunk sums of the gradient launch before this one,
@@ -57,9 +59,16 @@ void launch_dx(const Params& p, hipStream_t s);
 template <int BITS>
 void launch_predecode(const Params& p, bool fwd, uint8_t* out, hipStream_t s);
 void launch_pd(const Params& p, bool fwd, hipStream_t s);
-// out (+)= part[0] + part[1] + ... + part[ksplit-1], in that order (the split product's partials)
+// out (+)= part[0] + part[1] + ... + part[ksplit-1], in that order, over each split tile (the split
+// product's partials)
 void launch_split_reduce(const Params& p, bool fwd, hipStream_t s);
 inline int64_t wt_bytes(int64_t N, int64_t K) { return N * K * 2; }
+// the fused kernel's grid for `full` whole tiles and `items` split ranges: 8 x the largest share
+// of an XCD (each XCD's share of either kind rounded up; the workgroups past its share do no
+// product)
+inline int work_grid(int full, int items) { return 8 * ((full + 7) / 8 + (items + 7) / 8); }
+// bytes of the split partials: ksplit ranges of each of the tiles past nfull
+inline int64_t split_bytes(int ksplit, int64_t split_tiles) { return (int64_t)ksplit * split_tiles * kBM * kBN * 4; }
 
 }  // namespace rt
 }  // namespace r97q

@@ -364,28 +364,35 @@ struct Wave {
     }
 };
 
+// The wave's part of one work item: tile (mt, ot), range z of S over the reduction (S = 1: the whole
+// reduction, the product into `out`; S > 1: a split tile's range, its partial into the tile's slot
+// `sp` of the split partials). mt < 0: no tile (a workgroup past its XCD's share), only the
+// factor gradients' sums.
 template <bool FWD, int WAVES, int WAVE>
-__device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t* t1, int mt, int ot, int z) {
+__device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t* t1, int mt, int ot, int z, int S,
+                                          float* sp) {
     using G = Geo<WAVES>;
-    f32x16 acc[G::kMI][kNI];
+    if (mt >= 0) {
+        f32x16 acc[G::kMI][kNI];
 #pragma unroll
-    for (int mi = 0; mi < G::kMI; ++mi)
+        for (int mi = 0; mi < G::kMI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = (f32x16){};
-    const int lane = threadIdx.x & 63;
-    const int64_t red = FWD ? p.K : p.N;
-    const int pairs = (int)(red / kStep) / 2;  // the steps go in pairs: a range holds whole pairs
-    Wave<FWD, WAVES, WAVE> w{p, red, (int64_t)mt * kBM + G::kWaveM * WAVE, (int64_t)ot * kBN,
-                             act_tile_blocks(p.T) * kBlock, lane, 2 * (int)((int64_t)(z + 1) * pairs / p.ksplit)};
-    w.s0 = 2 * (int)((int64_t)z * pairs / p.ksplit);
-    w.setup();
-    w.run(p.act, t0, t1, acc);
-    const int64_t ld = FWD ? p.N : p.K;
-    if (p.rank > 0 && z == 0) adapter<G::kMI>(p.P, p.Q, p.rank, w.m0, w.o0, p.T, lane, acc);
-    if (p.ksplit > 1)
-        store<G::kMI>(acc, p.part + (int64_t)z * p.T * ld, ld, w.m0, w.o0, p.T, lane, 1, 0);
-    else
-        store<G::kMI>(acc, p.out, ld, w.m0, w.o0, p.T, lane, p.out_f32, FWD ? 0 : p.accumulate);
+            for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = (f32x16){};
+        const int lane = threadIdx.x & 63;
+        const int64_t red = FWD ? p.K : p.N;
+        const int pairs = (int)(red / kStep) / 2;  // the steps go in pairs: a range holds whole pairs
+        Wave<FWD, WAVES, WAVE> w{p, red, (int64_t)mt * kBM + G::kWaveM * WAVE, (int64_t)ot * kBN,
+                                 act_tile_blocks(p.T) * kBlock, lane, 2 * (int)((int64_t)(z + 1) * pairs / S)};
+        w.s0 = 2 * (int)((int64_t)z * pairs / S);
+        w.setup();
+        w.run(p.act, t0, t1, acc);
+        const int64_t ld = FWD ? p.N : p.K;
+        if (p.rank > 0 && z == 0) adapter<G::kMI>(p.P, p.Q, p.rank, w.m0, w.o0, p.T, lane, acc);
+        if (S > 1)  // the tile's [kBM][kBN] slot, its rows past T left unwritten
+            store<G::kMI>(acc, sp, kBN, G::kWaveM * WAVE, 0, p.T - (int64_t)mt * kBM, lane, 1, 0);
+        else
+            store<G::kMI>(acc, p.out, ld, w.m0, w.o0, p.T, lane, p.out_f32, FWD ? 0 : p.accumulate);
+    }
     if constexpr (!FWD)
         if (p.sums[0].part || p.sums[1].part) sum_chunks<WAVES>(p);
 }
@@ -393,23 +400,35 @@ __device__ __forceinline__ void wave_main(const Params& p, uint8_t* t0, uint8_t*
 template <bool FWD, int WAVES>
 __global__ __launch_bounds__(64 * WAVES, 1) void qlinear_rt_kernel(const Params p) {
     __shared__ __attribute__((aligned(16))) uint8_t t0[kTileBytes], t1[kTileBytes];
-    // split-K: the grid is ksplit x tiles workgroups, numbered (range, tile) with the tiles inner
+    // the work: tiles 0 .. nfull-1 whole, then ksplit ranges of each later tile (the tiles inner)
     const int ntiles = p.mtiles * p.otiles;
-    const int lin = xcd_tile(blockIdx.x, ntiles * p.ksplit);
-    const int z = lin / ntiles, tile = lin % ntiles;
-    const int mt = tile / p.otiles, ot = tile % p.otiles;
+    const int nfull = p.ksplit > 1 ? p.nfull : ntiles;
+    const int nsplit = ntiles - nfull;
+    const int w = xcd_work(blockIdx.x, nfull, p.ksplit > 1 ? p.ksplit * nsplit : 0);
+    int tile = -1, z = 0, S = 1;
+    float* sp = nullptr;
+    if (w >= 0 && w < nfull) {
+        tile = w;
+    } else if (w >= nfull) {
+        const int q = w - nfull;
+        z = q / nsplit;
+        tile = nfull + q % nsplit;
+        S = p.ksplit;
+        sp = p.part + ((int64_t)z * nsplit + (tile - nfull)) * kBM * kBN;
+    }
+    const int mt = tile >= 0 ? tile / p.otiles : -1, ot = tile >= 0 ? tile % p.otiles : 0;
     switch (threadIdx.x >> 6) {
-        case 0: wave_main<FWD, WAVES, 0>(p, t0, t1, mt, ot, z); break;
-        case 1: wave_main<FWD, WAVES, 1>(p, t0, t1, mt, ot, z); break;
-        case 2: wave_main<FWD, WAVES, 2>(p, t0, t1, mt, ot, z); break;
-        case 3: wave_main<FWD, WAVES, 3>(p, t0, t1, mt, ot, z); break;
+        case 0: wave_main<FWD, WAVES, 0>(p, t0, t1, mt, ot, z, S, sp); break;
+        case 1: wave_main<FWD, WAVES, 1>(p, t0, t1, mt, ot, z, S, sp); break;
+        case 2: wave_main<FWD, WAVES, 2>(p, t0, t1, mt, ot, z, S, sp); break;
+        case 3: wave_main<FWD, WAVES, 3>(p, t0, t1, mt, ot, z, S, sp); break;
         default:
             if constexpr (WAVES == 8) {
                 switch (threadIdx.x >> 6) {
-                    case 4: wave_main<FWD, WAVES, 4>(p, t0, t1, mt, ot, z); break;
-                    case 5: wave_main<FWD, WAVES, 5>(p, t0, t1, mt, ot, z); break;
-                    case 6: wave_main<FWD, WAVES, 6>(p, t0, t1, mt, ot, z); break;
-                    default: wave_main<FWD, WAVES, 7>(p, t0, t1, mt, ot, z); break;
+                    case 4: wave_main<FWD, WAVES, 4>(p, t0, t1, mt, ot, z, S, sp); break;
+                    case 5: wave_main<FWD, WAVES, 5>(p, t0, t1, mt, ot, z, S, sp); break;
+                    case 6: wave_main<FWD, WAVES, 6>(p, t0, t1, mt, ot, z, S, sp); break;
+                    default: wave_main<FWD, WAVES, 7>(p, t0, t1, mt, ot, z, S, sp); break;
                 }
             }
             break;
@@ -502,14 +521,16 @@ void launch_predecode<R97Q_BITS>(const Params& p, bool fwd, uint8_t* out, hipStr
 
 template <>
 void launch_fwd<R97Q_BITS>(const Params& p, hipStream_t s) {
-    hipLaunchKernelGGL((qlinear_rt_kernel<true, R97Q_RT_WAVES>), dim3((unsigned)(p.mtiles * p.otiles * p.ksplit)),
-                       dim3(64 * R97Q_RT_WAVES), 0, s, p);
+    const int ntiles = p.mtiles * p.otiles;
+    const int grid = p.ksplit > 1 ? work_grid(p.nfull, p.ksplit * (ntiles - p.nfull)) : ntiles;
+    hipLaunchKernelGGL((qlinear_rt_kernel<true, R97Q_RT_WAVES>), dim3((unsigned)grid), dim3(64 * R97Q_RT_WAVES), 0, s, p);
 }
 
 template <>
 void launch_dx<R97Q_BITS>(const Params& p, hipStream_t s) {
-    hipLaunchKernelGGL((qlinear_rt_kernel<false, R97Q_RT_WAVES>), dim3((unsigned)(p.mtiles * p.otiles * p.ksplit)),
-                       dim3(64 * R97Q_RT_WAVES), 0, s, p);
+    const int ntiles = p.mtiles * p.otiles;
+    const int grid = p.ksplit > 1 ? work_grid(p.nfull, p.ksplit * (ntiles - p.nfull)) : ntiles;
+    hipLaunchKernelGGL((qlinear_rt_kernel<false, R97Q_RT_WAVES>), dim3((unsigned)grid), dim3(64 * R97Q_RT_WAVES), 0, s, p);
 }
 
 }  // namespace rt

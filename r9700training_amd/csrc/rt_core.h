@@ -74,6 +74,21 @@ __device__ __forceinline__ int xcd_tile(int bid, int nwg) {
     return xcd * base + (xcd < rem ? xcd : rem) + local;
 }
 
+// The fused kernel's work: `full` whole tiles (tiles 0 .. full-1), then `items` split ranges. The
+// hardware deals workgroup ids round-robin over the 8 XCDs and starts each XCD's in id order, so
+// each XCD's first workgroups take its share of the whole tiles (one contiguous run, as xcd_tile
+// deals them) and its later ones its share of the split ranges (contiguous too): the ranges run once
+// the whole tiles are done, on every CU. Returns the whole tile's index, full + the range's index,
+// or -1 for a workgroup past its XCD's share (work_grid rounds each share up).
+__device__ __forceinline__ int xcd_work(int bid, int full, int items) {
+    const int xcd = bid & 7, l = bid >> 3;
+    const int fb = full >> 3, fr = full & 7, fx = fb + (xcd < fr ? 1 : 0);
+    if (l < fx) return xcd * fb + (xcd < fr ? xcd : fr) + l;
+    const int ib = items >> 3, ir = items & 7, ix = ib + (xcd < ir ? 1 : 0);
+    if (l - fx >= ix) return -1;
+    return full + xcd * ib + (xcd < ir ? xcd : ir) + (l - fx);
+}
+
 // blk[mi]: element offset of the wave's token block mi at step 0 in the tiled operand of a T-row
 // activation (rows past the operand's last block read that block again: their products land in
 // rows that are never stored)

@@ -49,6 +49,10 @@ SHAPES = [
     # twin (64 tiles) and attn_qg's adjoint at 1024 tokens (80 tiles)
     ("ref-attn-kv", 4096, 1024, 5120, 16),
     ("ref-attn-qg-1024", 1024, 12288, 5120, 16),
+    # and two whose 320 tiles fill one round and a quarter of another: the tiles of the partial
+    # round split four ways (attn_qg's adjoint at 4096 tokens, ffn_down's twin), the rest whole
+    ("ref-attn-qg-4096", 4096, 12288, 5120, 16),
+    ("ref-ffn-down", 4096, 5120, 17408, 16),
 ]
 
 
