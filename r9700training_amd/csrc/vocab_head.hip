@@ -7,13 +7,18 @@
 // fmas, and the un-rotation. Here it is the fused dX kernel's product. A class's rows go in ranges
 // of about 4096 (whole trellis runs), a batch of up to kBatch ranges at a time: each range is
 // decoded into the int8-code form in the workspace (the standalone decode's kernel writing tiled),
-// the cotangent's columns for the batch's rows are gathered into bf16 [range][rows][Np] operands,
 // and one batched qlinear_dx_kernel<R97Q_CODES8> launch (a grid slice a range, so a head with few
 // token rows or a narrow n_embd still fills the chip) writes each range's (gathered . W) *
 // scale.col -- the class's scale.col in its epilogue, one factor a 128-column tile -- into its own
 // f32 partial; the partials are then added into d_x in range order (deterministic). Ranges are
 // padded to Np (a multiple of 128) rows with zero codes, zero scales and zero cotangent columns.
-// Once every class is in, the unnormalised 128-wide Hadamard runs over each 128 columns of d_x.
+// The products' operands -- the cotangent's columns of every class's rows, bf16 [range][rows][Np] a
+// class -- are gathered first, for all classes in one launch whose token rows vary slowest, so the
+// workgroups in flight cover a few token rows of every class and each cotangent line is fetched
+// from memory about once (the classes split the vocabulary at random: a class on its own touches
+// almost every line). Token rows go in blocks of at most kRowBlock, each block's operands held at
+// once. Once every class is in, the unnormalised 128-wide Hadamard runs over each 128 columns of
+// d_x.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -29,8 +34,10 @@ namespace {
 constexpr int64_t kRangeRows = 4096;  // rows of a range (whole trellis runs)
 constexpr int kBatch = 8;             // ranges a batched launch
 constexpr int kFillWorkgroups = 512;  // a batch large enough for this many workgroups (256 CUs)
+constexpr int64_t kRowBlock = 4096;   // token rows a pass (every class's gathered operands held for them)
 
 int64_t round_up(int64_t n, int64_t m) { return (n + m - 1) / m * m; }
+int64_t row_block(int64_t rows) { return rows < kRowBlock ? rows : kRowBlock; }
 
 // the rows one range takes: whole runs (the decode's rule for a row range), about kRangeRows
 int64_t range_rows(const R97qVocabClass& c) {
@@ -38,6 +45,11 @@ int64_t range_rows(const R97qVocabClass& c) {
     int64_t r = kRangeRows / run * run;
     if (r < run) r = run;
     return r < c.rows ? r : c.rows;
+}
+
+int64_t ranges_of(const R97qVocabClass& c) {
+    const int64_t R = range_rows(c);
+    return (c.rows + R - 1) / R;
 }
 
 // ranges a batch takes: enough for kFillWorkgroups workgroups, at most kBatch
@@ -57,7 +69,9 @@ VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
         const int64_t s = round_up(range_rows(plan.cls[c]), 128);
         Np = s > Np ? s : Np;
     }
-    const int64_t K = plan.n_embd, nkb = K / 128, Z = batch_of(rows, K);
+    const int64_t K = plan.n_embd, nkb = K / 128, rb = row_block(rows), Z = batch_of(rb, K);
+    int64_t nranges = 0;
+    for (int c = 0; c < plan.classes; ++c) nranges += ranges_of(plan.cls[c]);
     VocabWs w{};
     int64_t off = 0;
     auto take = [&](int64_t bytes) {
@@ -67,9 +81,9 @@ VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
     };
     w.codes = take(Z * Np * K);
     w.scale = take(Z * nkb * Np * 2);
-    w.gather = take(Z * rows * Np * 2);
-    w.part = take(Z * rows * K * 4);
-    w.part_lo = take(Z * rows * K * 4);
+    w.gather = take(nranges * rb * Np * 2);
+    w.part = take(Z * rb * K * 4);
+    w.part_lo = take(Z * rb * K * 4);
     w.cf = take(nkb * 4);
     w.total = off;
     return w;
@@ -86,30 +100,51 @@ __global__ __launch_bounds__(256) void vocab_pad_kernel(int8_t* __restrict__ cod
     if (i < pad * nkb) scale_t[(i / pad) * ns_pad + ns + i % pad] = 0;
 }
 
-// a[z][m][n] = dy[m, ids[z*R + n] - vocab_offset] for class rows inside the batch's rows [0, ns)
-// and an id inside this vocabulary, else 0: grid (Np/256, token rows from m0 in groups of
-// kGatherRows, Z), a column and kGatherRows token rows a thread (the id read once for them;
-// measured: 8 columns a thread with one 16-byte store is 40% slower -- fewer loads in flight)
+// The gathered operands of one block of token rows: class c's range z is a[z][m][n] =
+// dy[m, ids[z*R + n] - vocab_offset] for a class row z*R + n < rows and an id inside this
+// vocabulary, else 0 (the range's padding columns up to Np included).
+struct GatherClass {
+    const int32_t* ids;
+    int64_t rows, R;  // the class's rows; rows a range
+    uint16_t* out;    // [ranges][rb][Np]
+    int y0;           // the class's first range in the launch's grid
+};
+struct GatherAll {
+    GatherClass cls[4];
+    int classes, ny;   // ny: every class's ranges
+    int64_t rb, vocab, vocab_offset, Np, nx, ngroups;  // nx: Np / 256; ngroups: token-row groups
+};
+// A workgroup: 256 columns of one range x a group of kGatherRows token rows; a column and
+// kGatherRows token rows a thread (the id read once for them; measured: 8 columns a thread with one
+// 16-byte store is 40% slower -- fewer loads in flight). The workgroups are dealt so that XCD x
+// takes the token-row groups x, x + 8, .. whole, one after another, each for every class and range:
+// a cotangent line is then fetched into one XCD's L2 while its few token rows are gathered, not
+// into all eight (the hardware deals workgroup ids round-robin over the XCDs, in id order on each).
 constexpr int kGatherRows = 8;
-__global__ __launch_bounds__(256) void vocab_gather_kernel(const uint16_t* __restrict__ dy,
-                                                           const int32_t* __restrict__ ids,
-                                                           uint16_t* __restrict__ a, int64_t rows, int64_t vocab,
-                                                           int64_t vocab_offset, int64_t R, int64_t ns, int64_t Np,
-                                                           int64_t m0) {
-    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t mb = m0 + (int64_t)blockIdx.y * kGatherRows, z = blockIdx.z;
-    if (n >= Np) return;
-    const int64_t r = z * R + n;
+__global__ __launch_bounds__(256) void vocab_gather_kernel(const uint16_t* __restrict__ dy, const GatherAll g) {
+    const int64_t xcd = blockIdx.x & 7, l = blockIdx.x >> 3;
+    const int64_t per = g.nx * g.ny;  // workgroups a token-row group
+    const int64_t grp = (l / per) * 8 + xcd;
+    if (grp >= g.ngroups) return;
+    const int y = (int)((l % per) / g.nx);
+    int c = 0;
+    while (c + 1 < g.classes && y >= g.cls[c + 1].y0) ++c;
+    const GatherClass& k = g.cls[c];
+    const int64_t z = y - k.y0;
+    const int64_t n = (l % per % g.nx) * 256 + threadIdx.x;
+    const int64_t mb = grp * kGatherRows;
+    if (n >= g.Np) return;
+    const int64_t r = z * k.R + n;
     int64_t col = -1;
-    if (n < R && r < ns) {
-        const int64_t id = ids[r];
-        if (id >= vocab_offset && id < vocab_offset + vocab) col = id - vocab_offset;
+    if (n < k.R && r < k.rows) {
+        const int64_t id = k.ids[r];
+        if (id >= g.vocab_offset && id < g.vocab_offset + g.vocab) col = id - g.vocab_offset;
     }
 #pragma unroll
     for (int i = 0; i < kGatherRows; ++i) {
         const int64_t m = mb + i;
-        if (m >= rows) break;
-        a[(z * rows + m) * Np + n] = col >= 0 ? dy[m * vocab + col] : (uint16_t)0;
+        if (m >= g.rb) break;
+        k.out[(z * g.rb + m) * g.Np + n] = col >= 0 ? dy[m * g.vocab + col] : (uint16_t)0;
     }
 }
 
@@ -214,82 +249,109 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
     const hipStream_t s = (hipStream_t)stream;
     const int64_t K = plan->n_embd, nkb = K / 128;
 
-    for (int c = 0; c < plan->classes; ++c) {
-        const R97qVocabClass& cls = plan->cls[c];
-        hipLaunchKernelGGL(vocab_cf_kernel, dim3(blocks(nkb, 64)), dim3(64), 0, s,
-                           static_cast<const uint8_t*>(cls.scale_col), cls.scale_col_dtype, nkb, cf);
-        if (int e = launch_status("vocab_cf_kernel")) return e;
-        const int64_t R = range_rows(cls), Np = round_up(R, 128);
-        const int Zmax = batch_of(rows, K);
-        for (int64_t b0 = 0; b0 < cls.rows; b0 += Zmax * R) {
-            const int64_t nb = Zmax * R < cls.rows - b0 ? Zmax * R : cls.rows - b0;  // the batch's class rows
-            const int Z = (int)((nb + R - 1) / R);
-            for (int z = 0; z < Z; ++z) {
-                const int64_t r0 = b0 + z * R;
-                const int64_t ns = R < cls.rows - r0 ? R : cls.rows - r0;
-                int8_t* zc = codes + z * Np * K;
-                uint16_t* zs = scale_t + z * nkb * Np;
-                R97IqrDecodeDesc d = cls.decode;
-                d.row0 = r0;
-                d.rows = ns;
-                d.codes = d.codes + r0 * d.codes_row_bytes;
-                d.scale = d.scale + r0 * d.scale_row_bytes;
-                d.zero = d.zero ? d.zero + r0 * d.zero_row_bytes : nullptr;
-                d.out_codes = zc;
-                d.out_scale = zs;
-                if (validate(d)) {
-                    set_error("%s: the plan's class %d decode is outside the kernel's rules", who, c);
-                    return R97Q_EINVAL;
+    const int64_t rbmax = row_block(rows);
+    const int Zmax = batch_of(rbmax, K);  // the partials' workspace holds this many ranges
+    for (int64_t m0 = 0; m0 < rows; m0 += rbmax) {
+        const int64_t rb = rows - m0 < rbmax ? rows - m0 : rbmax;
+        // every class's gathered operands for token rows [m0, m0 + rb)
+        int64_t Np = 0;
+        for (int c = 0; c < plan->classes; ++c) {
+            const int64_t np = round_up(range_rows(plan->cls[c]), 128);
+            Np = np > Np ? np : Np;
+        }
+        GatherAll g{};
+        g.classes = plan->classes;
+        g.rb = rb;
+        g.vocab = plan->vocab;
+        g.vocab_offset = plan->vocab_offset;
+        g.Np = Np;
+        int ny = 0;
+        int64_t goff = 0;
+        for (int c = 0; c < plan->classes; ++c) {
+            const R97qVocabClass& cls = plan->cls[c];
+            const int64_t nr = ranges_of(cls);
+            g.cls[c] = GatherClass{static_cast<const int32_t*>(cls.ids), cls.rows, range_rows(cls), gathered + goff, ny};
+            ny += (int)nr;
+            goff += nr * rb * Np;
+        }
+        g.ny = ny;
+        g.nx = blocks(Np, 256);
+        g.ngroups = blocks(rb, kGatherRows);
+        const int64_t nwg = (g.ngroups + 7) / 8 * 8 * g.nx * ny;  // every XCD's share whole
+        if (nwg > INT32_MAX) {
+            set_error("%s: %d ranges of %lld rows are more than a launch's grid takes", who, ny, (long long)kRangeRows);
+            return R97Q_EUNSUPPORTED;
+        }
+        hipLaunchKernelGGL(vocab_gather_kernel, dim3((unsigned)nwg), dim3(256), 0, s, dy + m0 * plan->vocab, g);
+        if (int e = launch_status("vocab_gather_kernel")) return e;
+
+        for (int c = 0; c < plan->classes; ++c) {
+            const R97qVocabClass& cls = plan->cls[c];
+            hipLaunchKernelGGL(vocab_cf_kernel, dim3(blocks(nkb, 64)), dim3(64), 0, s,
+                               static_cast<const uint8_t*>(cls.scale_col), cls.scale_col_dtype, nkb, cf);
+            if (int e = launch_status("vocab_cf_kernel")) return e;
+            const int64_t R = range_rows(cls);
+            for (int64_t b0 = 0; b0 < cls.rows; b0 += Zmax * R) {
+                const int64_t nb = Zmax * R < cls.rows - b0 ? Zmax * R : cls.rows - b0;  // the batch's class rows
+                const int Z = (int)((nb + R - 1) / R);
+                for (int z = 0; z < Z; ++z) {
+                    const int64_t r0 = b0 + z * R;
+                    const int64_t ns = R < cls.rows - r0 ? R : cls.rows - r0;
+                    int8_t* zc = codes + z * Np * K;
+                    uint16_t* zs = scale_t + z * nkb * Np;
+                    R97IqrDecodeDesc d = cls.decode;
+                    d.row0 = r0;
+                    d.rows = ns;
+                    d.codes = d.codes + r0 * d.codes_row_bytes;
+                    d.scale = d.scale + r0 * d.scale_row_bytes;
+                    d.zero = d.zero ? d.zero + r0 * d.zero_row_bytes : nullptr;
+                    d.out_codes = zc;
+                    d.out_scale = zs;
+                    if (validate(d)) {
+                        set_error("%s: the plan's class %d decode is outside the kernel's rules", who, c);
+                        return R97Q_EINVAL;
+                    }
+                    if (Np != ns) {
+                        const int64_t n = Np * K / 4 - (ns / 8) * (K / 4) * 8;
+                        const int64_t m = (Np - ns) * nkb;
+                        hipLaunchKernelGGL(vocab_pad_kernel, dim3(blocks(n > m ? n : m, 256)), dim3(256), 0, s, zc,
+                                           zs, ns, Np, K);
+                        if (int e = launch_status("vocab_pad_kernel")) return e;
+                    }
+                    if (int e = decode_tiled(d, Np, s)) return e;
                 }
-                if (Np != ns) {
-                    const int64_t n = Np * K / 4 - (ns / 8) * (K / 4) * 8;
-                    const int64_t m = (Np - ns) * nkb;
-                    hipLaunchKernelGGL(vocab_pad_kernel, dim3(blocks(n > m ? n : m, 256)), dim3(256), 0, s, zc, zs,
-                                       ns, Np, K);
-                    if (int e = launch_status("vocab_pad_kernel")) return e;
-                }
-                if (int e = decode_tiled(d, Np, s)) return e;
+                DxParams p{};
+                p.dY = g.cls[c].out + (b0 / R) * rb * Np;
+                p.T = rb;
+                p.N = Np;
+                p.K = K;
+                p.stream = reinterpret_cast<const uint32_t*>(codes);
+                p.scale_t = scale_t;
+                p.rank = 0;
+                p.dX = part;
+                p.dx_f32 = 1;
+                p.accumulate = 0;
+                p.a_scale = cf;  // one factor a 128-column tile: every row reads cf[kt]
+                p.a_scale_ld = 0;
+                p.mtiles = (int)((rb + kBM - 1) / kBM);
+                p.ktiles = (int)(K / kBN);
+                p.batch = Z;
+                p.z_dy = rb * Np;
+                p.z_w = Np * K / 4;
+                p.z_scale = nkb * Np;
+                p.z_out = rb * K;
+                // each weight as the exact sum of two bf16 values: one launch runs the product over
+                // the high halves and, in slices of its own, over the low halves into partials of
+                // their own (f32 products of bf16 values are exact); the reduction adds each
+                // range's two
+                p.both = 1;
+                p.dX_lo = part_lo;
+                launch_dx<R97Q_CODES8>(p, s);
+                if (int e = launch_status("qlinear_dx_both_kernel (vocab head)")) return e;
+                hipLaunchKernelGGL(vocab_reduce_kernel, dim3(blocks(rb * K, 256)), dim3(256), 0, s, d_x + m0 * K, part,
+                                   part_lo, rb * K, Z);
+                if (int e = launch_status("vocab_reduce_kernel")) return e;
             }
-            const int64_t span = 65535 * (int64_t)kGatherRows;  // gridDim.y's limit
-            for (int64_t m0 = 0; m0 < rows; m0 += span) {
-                const int64_t mr = rows - m0 < span ? rows - m0 : span;
-                hipLaunchKernelGGL(vocab_gather_kernel,
-                                   dim3(blocks(Np, 256), (unsigned)((mr + kGatherRows - 1) / kGatherRows), (unsigned)Z),
-                                   dim3(256), 0,
-                                   s, dy, static_cast<const int32_t*>(cls.ids) + b0, gathered, rows, plan->vocab,
-                                   plan->vocab_offset, R, nb, Np, m0);
-                if (int e = launch_status("vocab_gather_kernel")) return e;
-            }
-            DxParams p{};
-            p.dY = gathered;
-            p.T = rows;
-            p.N = Np;
-            p.K = K;
-            p.stream = reinterpret_cast<const uint32_t*>(codes);
-            p.scale_t = scale_t;
-            p.rank = 0;
-            p.dX = part;
-            p.dx_f32 = 1;
-            p.accumulate = 0;
-            p.a_scale = cf;  // one factor a 128-column tile: every row reads cf[kt]
-            p.a_scale_ld = 0;
-            p.mtiles = (int)((rows + kBM - 1) / kBM);
-            p.ktiles = (int)(K / kBN);
-            p.batch = Z;
-            p.z_dy = rows * Np;
-            p.z_w = Np * K / 4;
-            p.z_scale = nkb * Np;
-            p.z_out = rows * K;
-            // each weight as the exact sum of two bf16 values: one launch runs the product over the
-            // high halves and, in slices of its own, over the low halves into partials of their own
-            // (f32 products of bf16 values are exact); the reduction adds each range's two
-            p.both = 1;
-            p.dX_lo = part_lo;
-            launch_dx<R97Q_CODES8>(p, s);
-            if (int e = launch_status("qlinear_dx_both_kernel (vocab head)")) return e;
-            hipLaunchKernelGGL(vocab_reduce_kernel, dim3(blocks(rows * K, 256)), dim3(256), 0, s, d_x, part, part_lo,
-                               rows * K, Z);
-            if (int e = launch_status("vocab_reduce_kernel")) return e;
         }
     }
     if (plan->transform == 128) {
