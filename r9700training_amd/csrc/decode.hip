@@ -197,11 +197,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(const R97IqrDeco
 // int8-code form, written as two 16-byte stores; canonical: one 4-byte store a row. The same values as
 // decode_kernel, bit for bit.
 template <int BITS, bool TILED, int ROWS>
-__global__ __launch_bounds__(kDecodeThreads) void decode_mad_kernel(const R97IqrDecodeDesc d, int64_t chunks,
-                                                                    int64_t scale_ld) {
+__device__ __forceinline__ void mad_rows(const R97IqrDecodeDesc& d, int64_t ch, int64_t chunks, int64_t scale_ld) {
     using O = DecodeOut<TILED>;
     constexpr int C = (16 + BITS - 1) / BITS;  // codes above a chunk that seed its state
-    const int64_t ch = blockIdx.y + (int64_t)blockIdx.z * gridDim.y;
     const int64_t q4 = (int64_t)blockIdx.x * kDecodeThreads + threadIdx.x;
     if (ch >= chunks || 4 * q4 >= d.cols) return;
     const int64_t j = 4 * q4;  // the thread's first column
@@ -270,6 +268,24 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mad_kernel(const R97Iqr
         for (int i = 0; i < ROWS; ++i)
             d.out_scale[O::scale(d, r + i, kb, scale_ld)] = f32_to_bf16(block_scale(d, r + i, kb));
     }
+}
+
+template <int BITS, bool TILED, int ROWS>
+__global__ __launch_bounds__(kDecodeThreads) void decode_mad_kernel(const R97IqrDecodeDesc d, int64_t chunks,
+                                                                    int64_t scale_ld) {
+    mad_rows<BITS, TILED, ROWS>(d, blockIdx.y + (int64_t)blockIdx.z * gridDim.y, chunks, scale_ld);
+}
+
+// Several row ranges of the common form in one launch (blockIdx.z: the range), into the int8-code
+// form: each range as decode_mad_kernel decodes it alone, the same bits.
+constexpr int kDecodeBatch = 8;
+struct DecodeBatch {
+    R97IqrDecodeDesc d[kDecodeBatch];
+};
+template <int BITS>
+__global__ __launch_bounds__(kDecodeThreads) void decode_mad_batch_kernel(const DecodeBatch b, int64_t scale_ld) {
+    const R97IqrDecodeDesc& d = b.d[blockIdx.z];
+    mad_rows<BITS, true, 8>(d, blockIdx.y, d.rows / 8, scale_ld);
 }
 
 // ---------------------------------------------------------------- preparation
@@ -410,6 +426,34 @@ void launch_decode(const R97IqrDecodeDesc& d, hipStream_t s, int64_t scale_ld = 
 int decode_tiled(const R97IqrDecodeDesc& d, int64_t scale_ld, hipStream_t s) {
     launch_decode<true>(d, s, scale_ld);
     return launch_status("decode_kernel (int8-code form)");
+}
+
+// n valid descriptions (the same scale_ld), each decoded as decode_tiled decodes it: one launch when
+// all n are the common form with the same code width and columns, else one a description
+int decode_tiled_batch(const R97IqrDecodeDesc* ds, int n, int64_t scale_ld, hipStream_t s) {
+    bool one = n >= 1 && n <= kDecodeBatch;
+    int64_t chunks = 0;
+    for (int i = 0; one && i < n; ++i) {
+        one = mad_fast<true>(ds[i]) && ds[i].bits == ds[0].bits && ds[i].cols == ds[0].cols &&
+              ds[i].rows / 8 <= 65535;
+        chunks = ds[i].rows / 8 > chunks ? ds[i].rows / 8 : chunks;
+    }
+    if (!one || chunks == 0) {
+        for (int i = 0; i < n; ++i)
+            if (int e = decode_tiled(ds[i], scale_ld, s)) return e;
+        return R97Q_OK;
+    }
+    DecodeBatch b{};
+    for (int i = 0; i < n; ++i) b.d[i] = ds[i];
+    const dim3 grid((unsigned)((ds[0].cols / 4 + kDecodeThreads - 1) / kDecodeThreads), (unsigned)chunks, (unsigned)n);
+    const dim3 block(kDecodeThreads);
+    switch (ds[0].bits) {
+        case 3: hipLaunchKernelGGL(decode_mad_batch_kernel<3>, grid, block, 0, s, b, scale_ld); break;
+        case 4: hipLaunchKernelGGL(decode_mad_batch_kernel<4>, grid, block, 0, s, b, scale_ld); break;
+        case 5: hipLaunchKernelGGL(decode_mad_batch_kernel<5>, grid, block, 0, s, b, scale_ld); break;
+        default: hipLaunchKernelGGL(decode_mad_batch_kernel<6>, grid, block, 0, s, b, scale_ld); break;
+    }
+    return launch_status("decode_mad_batch_kernel (int8-code form)");
 }
 
 // Whether `d` is a form the fused kernels serve; the reason goes to the error message.

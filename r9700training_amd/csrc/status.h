@@ -29,5 +29,7 @@ int32_t validate(const R97IqrDecodeDesc& d);
 // Rows [d.row0, d.row0 + d.rows) of a valid description decoded into the int8-code form at
 // d.out_codes (units from row row0) and d.out_scale ([cols/128][scale_ld]) (decode.hip).
 int decode_tiled(const R97IqrDecodeDesc& d, int64_t scale_ld, hipStream_t s);
+// n descriptions at once (one launch when they allow it), each as decode_tiled decodes it
+int decode_tiled_batch(const R97IqrDecodeDesc* ds, int n, int64_t scale_ld, hipStream_t s);
 
 }  // namespace r97q

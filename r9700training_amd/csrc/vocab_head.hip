@@ -294,6 +294,7 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
             for (int64_t b0 = 0; b0 < cls.rows; b0 += Zmax * R) {
                 const int64_t nb = Zmax * R < cls.rows - b0 ? Zmax * R : cls.rows - b0;  // the batch's class rows
                 const int Z = (int)((nb + R - 1) / R);
+                R97IqrDecodeDesc dz[kBatch];
                 for (int z = 0; z < Z; ++z) {
                     const int64_t r0 = b0 + z * R;
                     const int64_t ns = R < cls.rows - r0 ? R : cls.rows - r0;
@@ -318,8 +319,9 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
                                            zs, ns, Np, K);
                         if (int e = launch_status("vocab_pad_kernel")) return e;
                     }
-                    if (int e = decode_tiled(d, Np, s)) return e;
+                    dz[z] = d;
                 }
+                if (int e = decode_tiled_batch(dz, Z, Np, s)) return e;
                 DxParams p{};
                 p.dY = g.cls[c].out + (b0 / R) * rb * Np;
                 p.T = rb;
