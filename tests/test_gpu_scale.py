@@ -141,3 +141,38 @@ def test_full_shape(name, T, N, K, r):
     es, edxs = rel_l2(ysum, ysum_ref), rel_l2(dxsum, dxsum_ref)
     print(f"  column sums rel L2  Y {es:.3e}  dX {edxs:.3e}", flush=True)
     assert es <= TOL_BASE and edxs <= TOL_BASE
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_split_tail_accumulate(dtype):
+    """dX added into an existing dX where the product splits only its partial last round: a 4096 x
+    5120 weight at 4096 tokens has 8 x 40 = 320 dX tiles, so the first 256 run whole and the last 64
+    split four ways over the 64-step reduction; the reduce launch adds the ranges in order and then
+    into dX (f32, or bf16 with its one more rounding)."""
+    T, N, K, r, s = 4096, 4096, 5120, 16, 2.0
+    print(f"case split-tail dX T={T} N={N} K={K} {dtype}", flush=True)
+    from r9700training_amd.qlinear import qlinear_lora_bwd, qlinear_lora_fwd
+
+    seed = 4099
+    rng = np.random.default_rng(seed)
+    sc = (0.75 + 0.5 * rng.random(K // 128)).astype(np.float32)
+    p = S.trellis(rows=N, cols=K, bits=5, state_bits=16, run_rows=256, rb=1, mad=1, scale_dtype=S.F32,
+                  rowf=True, seed=seed + 1, scale_col=sc, packed=True)
+    keep = []
+    w = prepared(p, keep)
+    codes, scale = host_weight(p)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    randn = lambda shape, std=1.0: (std * torch.randn(shape, generator=g, device="cuda")).to(torch.bfloat16)
+    Xd, dYd = randn((T, K)), randn((T, N))
+    Ad, Bd = randn((r, K), 0.01), randn((N, r), 0.01)
+    dX0 = (0.5 * torch.randn((T, K), generator=g, device="cuda")).to(dtype)
+    _, t = qlinear_lora_fwd(w, Xd, Ad, Bd, s, y_dtype=torch.float32)
+    dX, _, _ = qlinear_lora_bwd(w, Xd, dYd, Ad, Bd, t, s, dX=dX0.clone(), accumulate=True)
+    torch.cuda.synchronize()
+    W64 = torch.from_numpy(codes).cuda().double() * torch.from_numpy(
+        S.bf16_bits_to_f32(scale).astype(np.float64)).cuda().repeat_interleave(128, dim=1)
+    dY64 = dYd.double()
+    ref = dX0.double() + dY64 @ W64 + (s * (dY64 @ Bd.double())) @ Ad.double()
+    e = float(torch.linalg.vector_norm(dX.double() - ref) / torch.linalg.vector_norm(ref))
+    print(f"  dX (+)= rel L2 {e:.3e}", flush=True)
+    assert e <= (TOL_BASE if dtype == torch.float32 else 1.3 * TOL_BASE)
