@@ -7,7 +7,8 @@
 // 256-row run of one column, each thread decodes an 8-row chunk of a column and seeds its state
 // from the ceil(L/b) codes above the chunk (wrapping inside the run, which is exactly the
 // tail-biting seam), so a launch has rows/8 x cols independent threads and consecutive threads
-// write consecutive columns.
+// write consecutive columns. The common form (trellis.mad, L = 16, rb = 1, bits 3-6) runs on a
+// kernel with its code width compiled in, alone or several row ranges a launch.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>

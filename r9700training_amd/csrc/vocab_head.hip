@@ -5,9 +5,10 @@
 //
 // The reference runs it as a gather, a per-token-row GEMV over the decoded int8 grid with f32
 // fmas, and the un-rotation. Here it is the fused dX kernel's product. A class's rows go in ranges
-// of about 4096 (whole trellis runs), a batch of up to kBatch ranges at a time: each range is
-// decoded into the int8-code form in the workspace (the standalone decode's kernel writing tiled),
-// and one batched qlinear_dx_kernel<R97Q_CODES8> launch (a grid slice a range, so a head with few
+// of about 4096 (whole trellis runs), a batch of up to kBatch ranges at a time: the batch's ranges
+// are decoded into the int8-code form in the workspace (the standalone decode's kernel writing
+// tiled, one launch for the batch when the form allows), and one batched
+// qlinear_dx_kernel<R97Q_CODES8> launch (a grid slice a range, so a head with few
 // token rows or a narrow n_embd still fills the chip) writes each range's (gathered . W) *
 // scale.col -- the class's scale.col in its epilogue, one factor a 128-column tile -- into its own
 // f32 partial; the partials are then added into d_x in range order (deterministic). Ranges are
