@@ -526,9 +526,10 @@ typedef struct {
 /* Workspace for a call over `rows` token rows (-1 when the plan is outside the rules). */
 int64_t r97q_vocab_head_workspace_bytes(const R97qVocabPlan* plan, int64_t rows);
 /* d_x f32 [rows, n_embd] (added to) from dy bf16 [rows, vocab]. Unlike the reference's entry it
- * does not drain the stream: its scratch is the caller's workspace. The class weights are decoded
- * into the workspace as the call goes (the int8-code form, a range of rows at a time), then each
- * range runs through the fused dX kernel with the class's scale.col in its epilogue. */
+ * does not drain the stream: its scratch is the caller's workspace. Every class's weights are
+ * decoded into the workspace each call (the int8-code form, ranges of about 4096 rows), then every
+ * range runs through one launch of the register-fed dX kernel with its class's scale.col in the
+ * epilogue, and the launch's partial sums are added into d_x in a fixed order. */
 int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int64_t rows, float* d_x,
                               void* workspace, int64_t workspace_bytes, R97IqrStream stream);
 /* dst bf16 <- src f32 (RNE, src/adjoint/device/vocab_head.hip:80-86) */

@@ -44,17 +44,6 @@ struct DxParams {
     const float* a_scale;  // null, or f32 [T, a_scale_ld]: dX[m, k] is multiplied by a_scale[m, k/128]
     int64_t a_scale_ld;
     int mtiles, ktiles;
-    // batch > 1 (the int8-code form only): gridDim.z independent products, slice z at dY + z*z_dy,
-    // stream + z*z_w (uint32 units), scale_t + z*z_scale, dX + z*z_out (elements of dX's dtype)
-    int batch;
-    int64_t z_dy, z_w, z_scale, z_out;
-    // batched int8-code form with a_scale: the tile holds the low half of each weight's split,
-    // bf16(w - bf16(w)) (a second pass completing the exact weight)
-    int lo;
-    // batched int8-code form with a_scale, both halves in one launch: gridDim.z = 2 * batch, slices
-    // z >= batch the low halves of slice z - batch, into dX_lo (+ (z - batch) * z_out)
-    int both;
-    void* dX_lo;
 };
 
 template <int BITS>

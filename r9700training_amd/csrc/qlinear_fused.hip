@@ -205,10 +205,7 @@ __device__ __forceinline__ int xcd_tile(int bid, int nwg) {
 //      of the step's two; lane = 2 columns 2*lane; each lane writes one 16-byte chunk (8 n) a
 //      column, so a write instruction's rows are the even (or odd) ones and its chunks cover all
 //      eight swizzle positions.
-// LO (the int8-code form only): the tile holds the low half of each weight's split, bf16(w -
-// bf16(w)) -- exact, since code * bf16 scale has at most 16 significant bits -- so a second product
-// over it completes the exact product of the weight (the vocabulary head's f32-level parity).
-template <bool FWD, int BITS, int WAVE, bool LO = false>
+template <bool FWD, int BITS, int WAVE>
 struct Loop {
     static constexpr int ROWS = FWD ? 4 : 8;
     static constexpr int COLS = FWD ? 4 : 2;
@@ -284,11 +281,7 @@ struct Loop {
                     // two pieces; dX: column c of the pair, row i: byte 2*i + c
                     const int byte = FWD ? 8 * (c >> 1) + 2 * i + (c & 1) : 2 * i + c;
                     const uint32_t w = comp(wd.c, byte >> 2) ^ 0x80808080u;
-                    const float v = code8_value(w, byte & 3, sc[i], off[i]);
-                    // the high half rounded by the hardware's RNE conversion (the one that packs
-                    // the high tile), so the two halves are exactly the split of v
-                    if constexpr (LO) return v - (float)(__bf16)v;
-                    return v;
+                    return code8_value(w, byte & 3, sc[i], off[i]);
                 } else {
                     return slice_value<BITS, ROWS, COLS, SLICE>(wd, c, i, a24, b, sc[i], off[i]);
                 }
@@ -477,14 +470,14 @@ __device__ __forceinline__ void fwd_wave(const FwdParams& p, const Lds& lds, int
     store(acc, p.Y, p.N, L.m0, L.o0, p.T, lane, p.y_f32, 0);
 }
 
-template <int BITS, int SLICE, bool SCALED, bool LO = false>
+template <int BITS, int SLICE, bool SCALED>
 __device__ __forceinline__ void dx_wave(const DxParams& p, const Lds& lds, int lane, int mt, int kt) {
     f32x16 acc[2][4];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = (f32x16){};
-    Loop<false, BITS, SLICE, LO> L{p.dY, p.N, p.N, p.K, p.stream, p.scale_t, p.a24, p.b, p.run_rows,
+    Loop<false, BITS, SLICE> L{p.dY, p.N, p.N, p.K, p.stream, p.scale_t, p.a24, p.b, p.run_rows,
                                (int64_t)mt * kBM + 64 * SLICE, (int64_t)kt * kBN, p.T, lane};
     L.run(lds, acc);
     if (p.rank > 0) adapter<false>(p.P, p.At, p.rank, L.m0, L.o0, p.T, lane, acc);
@@ -508,7 +501,6 @@ __device__ __forceinline__ void dx_wave(const DxParams& p, const Lds& lds, int l
         default: fn<R97Q_BITS, 7 X>(__VA_ARGS__); break;   \
     }
 #define R97Q_COMMA_SCALED , SCALED
-#define R97Q_COMMA_SCALED_LO , SCALED, LO
 
 __global__ __launch_bounds__(kThreads, 1) void qlinear_fwd_kernel(const FwdParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t w0[kTileBytes], w1[kTileBytes], x0[kActBytes], x1[kActBytes];
@@ -519,53 +511,15 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_fwd_kernel(const FwdParam
     R97Q_WAVE_SWITCH(fwd_wave, , p, lds, lane, mt, nt)
 }
 
-// SCALED: dX in the code basis of an i8a8h activation (p.a_scale set); BATCHED: slice blockIdx.z of
-// a batch of independent products (the slices' pointers p.z_* apart); LO: the low half of the
-// int8-code weight's split (p.lo)
-template <bool SCALED, bool BATCHED = false, bool LO = false>
-__global__ __launch_bounds__(kThreads, 1) void qlinear_dx_kernel(const DxParams pb) {
-    __shared__ __attribute__((aligned(16))) uint8_t w0[kTileBytes], w1[kTileBytes], x0[kActBytes], x1[kActBytes];
-    const Lds lds{{w0, w1}, {x0, x1}};
-    DxParams p = pb;
-    if constexpr (BATCHED) {
-        const int64_t z = blockIdx.z;
-        p.dY += z * pb.z_dy;
-        p.stream += z * pb.z_w;
-        p.scale_t += z * pb.z_scale;
-        p.dX = p.dx_f32 ? static_cast<void*>(static_cast<float*>(pb.dX) + z * pb.z_out)
-                        : static_cast<void*>(static_cast<uint16_t*>(pb.dX) + z * pb.z_out);
-    }
-    const int tile = xcd_tile(blockIdx.x, p.mtiles * p.ktiles);
-    const int mt = tile / p.ktiles, kt = tile % p.ktiles;
-    const int lane = threadIdx.x & 63;
-    R97Q_WAVE_SWITCH(dx_wave, R97Q_COMMA_SCALED_LO, p, lds, lane, mt, kt)
-}
-
-// both halves of the int8-code weight's split in one batched launch: slices z < batch over the
-// high halves into dX, slices z >= batch over the low halves of slice z - batch into dX_lo
+// SCALED: dX in the code basis of an i8a8h activation (p.a_scale set)
 template <bool SCALED>
-__global__ __launch_bounds__(kThreads, 1) void qlinear_dx_both_kernel(const DxParams pb) {
+__global__ __launch_bounds__(kThreads, 1) void qlinear_dx_kernel(const DxParams p) {
     __shared__ __attribute__((aligned(16))) uint8_t w0[kTileBytes], w1[kTileBytes], x0[kActBytes], x1[kActBytes];
     const Lds lds{{w0, w1}, {x0, x1}};
-    DxParams p = pb;
-    const bool low = (int)blockIdx.z >= pb.batch;
-    const int64_t z = low ? (int64_t)blockIdx.z - pb.batch : (int64_t)blockIdx.z;
-    p.dY += z * pb.z_dy;
-    p.stream += z * pb.z_w;
-    p.scale_t += z * pb.z_scale;
-    void* base = low ? pb.dX_lo : pb.dX;
-    p.dX = p.dx_f32 ? static_cast<void*>(static_cast<float*>(base) + z * pb.z_out)
-                    : static_cast<void*>(static_cast<uint16_t*>(base) + z * pb.z_out);
     const int tile = xcd_tile(blockIdx.x, p.mtiles * p.ktiles);
     const int mt = tile / p.ktiles, kt = tile % p.ktiles;
     const int lane = threadIdx.x & 63;
-    if (low) {
-        constexpr bool LO = true;
-        R97Q_WAVE_SWITCH(dx_wave, R97Q_COMMA_SCALED_LO, p, lds, lane, mt, kt)
-    } else {
-        constexpr bool LO = false;
-        R97Q_WAVE_SWITCH(dx_wave, R97Q_COMMA_SCALED_LO, p, lds, lane, mt, kt)
-    }
+    R97Q_WAVE_SWITCH(dx_wave, R97Q_COMMA_SCALED, p, lds, lane, mt, kt)
 }
 
 }  // namespace
@@ -577,28 +531,6 @@ void launch_fwd<R97Q_BITS>(const FwdParams& p, hipStream_t s) {
 
 template <>
 void launch_dx<R97Q_BITS>(const DxParams& p, hipStream_t s) {
-    if constexpr (R97Q_BITS == R97Q_CODES8) {
-        if (p.both) {
-            const dim3 grid((unsigned)(p.mtiles * p.ktiles), 1, (unsigned)(2 * (p.batch > 1 ? p.batch : 1)));
-            if (p.a_scale)
-                hipLaunchKernelGGL(qlinear_dx_both_kernel<true>, grid, dim3(kThreads), 0, s, p);
-            else
-                hipLaunchKernelGGL(qlinear_dx_both_kernel<false>, grid, dim3(kThreads), 0, s, p);
-            return;
-        }
-        if (p.batch > 1 || p.lo) {
-            const dim3 grid((unsigned)(p.mtiles * p.ktiles), 1, (unsigned)(p.batch > 1 ? p.batch : 1));
-            if (p.lo && p.a_scale)
-                hipLaunchKernelGGL((qlinear_dx_kernel<true, true, true>), grid, dim3(kThreads), 0, s, p);
-            else if (p.lo)
-                hipLaunchKernelGGL((qlinear_dx_kernel<false, true, true>), grid, dim3(kThreads), 0, s, p);
-            else if (p.a_scale)
-                hipLaunchKernelGGL((qlinear_dx_kernel<true, true>), grid, dim3(kThreads), 0, s, p);
-            else
-                hipLaunchKernelGGL((qlinear_dx_kernel<false, true>), grid, dim3(kThreads), 0, s, p);
-            return;
-        }
-    }
     const dim3 grid((unsigned)(p.mtiles * p.ktiles));
     if (p.a_scale)
         hipLaunchKernelGGL(qlinear_dx_kernel<true>, grid, dim3(kThreads), 0, s, p);

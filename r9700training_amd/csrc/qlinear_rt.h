@@ -63,6 +63,25 @@ void launch_pd(const Params& p, bool fwd, hipStream_t s);
 // product's partials)
 void launch_split_reduce(const Params& p, bool fwd, hipStream_t s);
 inline int64_t wt_bytes(int64_t N, int64_t K) { return N * K * 2; }
+// The vocabulary head's dX products over the int8-code form (the int8-code build's
+// qlinear_rt_vocab_kernel), grid (tiles, slices): `p` is range 0's dX product (p.act its gathered
+// cotangent columns in the tiled layout, p.stream / p.scale_t its int8-code form; p.out the slices'
+// f32 partials [slices][T, K]); range y's operands are y * z_act, z_w (uint32 units) and z_scale
+// further on. Slice s holds the ranges first[s] .. first[s+1]-1, all of class cls[s]: a workgroup
+// reduces its tile over each of them, over the weights' high halves and then their low halves, into
+// one f32 accumulator, and writes it times cf[cls[s] * cf_ld + its 128-column tile] into partial s.
+constexpr int kVocabSlices = 64;
+struct VocabRtParams {
+    Params p;
+    int64_t z_act, z_w, z_scale;
+    const float* cf;
+    int64_t cf_ld;
+    int slices;
+    int first[kVocabSlices + 1];
+    int cls[kVocabSlices];
+};
+void launch_vocab(const VocabRtParams& v, hipStream_t s);
+
 // the fused kernel's grid for `full` whole tiles and `items` split ranges: 8 x the largest share
 // of an XCD (each XCD's share of either kind rounded up; the workgroups past its share do no
 // product)

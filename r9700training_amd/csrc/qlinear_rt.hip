@@ -53,10 +53,11 @@ namespace r97q {
 namespace rt {
 namespace {
 
-__device__ __forceinline__ uint32_t comp(const uint4& v, int c) {
+// (the trellis forms' word access; the int8-code build does not use them)
+[[maybe_unused]] __device__ __forceinline__ uint32_t comp(const uint4& v, int c) {
     return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
 }
-__device__ __forceinline__ uint32_t comp(const uint2& v, int c) { return c == 0 ? v.x : v.y; }
+[[maybe_unused]] __device__ __forceinline__ uint32_t comp(const uint2& v, int c) { return c == 0 ? v.x : v.y; }
 
 // ---------------------------------------------------------------- one lane's slice of a tile
 // ROWS consecutive rows ROWS*SLICE.. of a 32-row segment. Their trellis states are the 16-bit
@@ -113,7 +114,11 @@ __device__ __forceinline__ void load_scales(const uint16_t* src, uint32_t (&s)[N
 // DX:  decoded tile [128 k][64 n] (n contiguous). Wave w decodes DR = 64 / WAVES rows of the step's
 //      64, rows DR*(w % (WAVES/2)) .. of segment w / (WAVES/2); lane = 2 columns 2*lane; each lane
 //      writes DR/8 16-byte chunks (8 n each) a column.
-template <bool FWD, int WAVES, int WAVE>
+// LO (the int8-code form only): with `lo` set, the tile holds the low half of each weight's split,
+// bf16(w - bf16(w)) -- exact, since code * bf16 scale has at most 16 significant bits -- so a second
+// pass over it completes the exact product of the weight (the vocabulary head's f32-level parity).
+// A run-time choice, so both passes share one copy of the loop (two copies spill registers).
+template <bool FWD, int WAVES, int WAVE, bool LO = false>
 struct Wave {
     using G = Geo<WAVES>;
     static constexpr int kMI = G::kMI;
@@ -135,6 +140,7 @@ struct Wave {
     int lane;
     int nsteps;      // the walk's end: steps s0 .. nsteps-1 (an even count)
     int s0 = 0;      // the walk's first step (split-K: the range's first)
+    bool lo = false; // LO: this pass decodes the weights' low halves
     // forward, trellis forms: the stream offsets of the lane's 32-row segment g and of its halo (the
     // segment below, or the run's top one at the tail-biting seam)
     int64_t fwd_seg = 0, fwd_halo = 0;
@@ -232,7 +238,11 @@ struct Wave {
             // of its unit i>>3
             const int byte = FWD ? 2 * ROWS * (c >> 1) + 2 * i + (c & 1) : 16 * (i >> 3) + 2 * (i & 7) + c;
             const uint32_t w = wd.c[byte >> 2] ^ 0x80808080u;
-            return __builtin_fmaf((float)((w >> (8 * (byte & 3))) & 0xFFu), sc, off);
+            const float v = __builtin_fmaf((float)((w >> (8 * (byte & 3))) & 0xFFu), sc, off);
+            // the high half rounded by the hardware's RNE conversion (the one that packs the high
+            // tile), so the two halves are exactly the split of v
+            if constexpr (LO) return lo ? v - (float)(__bf16)v : v;
+            return v;
         } else {
             using S = Span<BITS, ROWS, SLICE>;
             const int o = BITS * (31 - (ROWS * SLICE + i)) - 32 * S::D0;
@@ -435,6 +445,75 @@ __global__ __launch_bounds__(64 * WAVES, 1) void qlinear_rt_kernel(const Params 
     }
 }
 
+#if R97Q_BITS == R97Q_CODES8
+// ---------------------------------------------------------------- the vocabulary head's products
+// The vocabulary head's dX products over the int8-code form: grid (tiles, slices); a workgroup
+// takes its tile of each range of its slice in turn, each a plain dX product (the token operand the
+// range's gathered cotangent columns, tiled) over the weights' high halves and then over their low
+// halves (w = hi + lo exactly, bf16 each), all into one f32 accumulator; the sum times the tile's
+// scale.col factor is written in f32 into the slice's partial.
+template <int WAVES, int WAVE>
+__device__ __forceinline__ void vocab_wave(const VocabRtParams& v, uint8_t* t0, uint8_t* t1, int sl, int mt, int ot) {
+    using G = Geo<WAVES>;
+    f32x16 acc[G::kMI][kNI];
+#pragma unroll
+    for (int mi = 0; mi < G::kMI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < kNI; ++ni) acc[mi][ni] = (f32x16){};
+    const int lane = threadIdx.x & 63;
+    const int64_t m0 = (int64_t)mt * kBM + G::kWaveM * WAVE, o0 = (int64_t)ot * kBN;
+#pragma clang loop unroll(disable)
+    for (int it = 2 * v.first[sl]; it < 2 * v.first[sl + 1]; ++it) {
+        const int64_t y = it >> 1;
+        Params p = v.p;
+        p.act += y * v.z_act;
+        p.stream += y * v.z_w;
+        p.scale_t += y * v.z_scale;
+        // the lane index made opaque each pass, so the lane's addresses are derived inside the pass
+        // and not held across passes (which spills registers)
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        Wave<false, WAVES, WAVE, true> w{p, p.N, m0, o0, act_tile_blocks(p.T) * kBlock, ln, (int)(p.N / kStep)};
+        w.lo = (it & 1) != 0;
+        w.setup();
+        w.run(p.act, t0, t1, acc);
+        // every wave past its last reads of the LDS tiles before the next pass decodes into them
+        __syncthreads();
+    }
+    const float f = v.cf[v.cls[sl] * v.cf_ld + ot];
+#pragma unroll
+    for (int mi = 0; mi < G::kMI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < kNI; ++ni)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[mi][ni][e] *= f;
+    store<G::kMI>(acc, static_cast<float*>(v.p.out) + (int64_t)sl * v.p.T * v.p.K, v.p.K, m0, o0, v.p.T, lane, 1, 0);
+}
+
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void qlinear_rt_vocab_kernel(const VocabRtParams v) {
+    __shared__ __attribute__((aligned(16))) uint8_t t0[kTileBytes], t1[kTileBytes];
+    const int tile = xcd_tile(blockIdx.x, v.p.mtiles * v.p.otiles);
+    const int mt = tile / v.p.otiles, ot = tile % v.p.otiles;
+    const int sl = blockIdx.y;
+#define R97Q_VOCAB_WAVE(W)                             \
+    case W:                                            \
+        vocab_wave<WAVES, W>(v, t0, t1, sl, mt, ot); \
+        break;
+    switch (threadIdx.x >> 6) {
+        R97Q_VOCAB_WAVE(0)
+        R97Q_VOCAB_WAVE(1)
+        R97Q_VOCAB_WAVE(2)
+        R97Q_VOCAB_WAVE(3)
+        R97Q_VOCAB_WAVE(4)
+        R97Q_VOCAB_WAVE(5)
+        R97Q_VOCAB_WAVE(6)
+        default: R97Q_VOCAB_WAVE(7)
+    }
+#undef R97Q_VOCAB_WAVE
+}
+#endif
+
 // ---------------------------------------------------------------- the weight decoded once a call
 // Every tile a product walks, decoded to bf16 in the LDS tile format (rt_core.h) and stored in
 // walk order: tile (o, s) -- outputs 128o.. (features n, or columns k for dX), reduction values
@@ -525,6 +604,14 @@ void launch_fwd<R97Q_BITS>(const Params& p, hipStream_t s) {
     const int grid = p.ksplit > 1 ? work_grid(p.nfull, p.ksplit * (ntiles - p.nfull)) : ntiles;
     hipLaunchKernelGGL((qlinear_rt_kernel<true, R97Q_RT_WAVES>), dim3((unsigned)grid), dim3(64 * R97Q_RT_WAVES), 0, s, p);
 }
+
+#if R97Q_BITS == R97Q_CODES8
+void launch_vocab(const VocabRtParams& v, hipStream_t s) {
+    static_assert(R97Q_RT_WAVES == 8, "the vocabulary head's kernel takes 8 waves");
+    hipLaunchKernelGGL(qlinear_rt_vocab_kernel<R97Q_RT_WAVES>, dim3((unsigned)(v.p.mtiles * v.p.otiles), (unsigned)v.slices),
+                       dim3(64 * R97Q_RT_WAVES), 0, s, v);
+}
+#endif
 
 template <>
 void launch_dx<R97Q_BITS>(const Params& p, hipStream_t s) {

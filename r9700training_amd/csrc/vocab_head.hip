@@ -4,38 +4,41 @@
 //   d_x[rows, n_embd] += H . sum over classes c of (dy[:, ids_c] . W_c) * scale.col_c
 //
 // The reference runs it as a gather, a per-token-row GEMV over the decoded int8 grid with f32
-// fmas, and the un-rotation. Here it is the fused dX kernel's product. A class's rows go in ranges
-// of about 4096 (whole trellis runs), a batch of up to kBatch ranges at a time: the batch's ranges
-// are decoded into the int8-code form in the workspace (the standalone decode's kernel writing
-// tiled, one launch for the batch when the form allows), and one batched
-// qlinear_dx_kernel<R97Q_CODES8> launch (a grid slice a range, so a head with few
-// token rows or a narrow n_embd still fills the chip) writes each range's (gathered . W) *
-// scale.col -- the class's scale.col in its epilogue, one factor a 128-column tile -- into its own
-// f32 partial; the partials are then added into d_x in range order (deterministic). Ranges are
-// padded to Np (a multiple of 128) rows with zero codes, zero scales and zero cotangent columns.
-// The products' operands -- the cotangent's columns of every class's rows, bf16 [range][rows][Np] a
-// class -- are gathered first, for all classes in one launch whose token rows vary slowest, so the
-// workgroups in flight cover a few token rows of every class and each cotangent line is fetched
-// from memory about once (the classes split the vocabulary at random: a class on its own touches
-// almost every line). Token rows go in blocks of at most kRowBlock, each block's operands held at
-// once. Once every class is in, the unnormalised 128-wide Hadamard runs over each 128 columns of
-// d_x.
+// fmas, and the un-rotation. Here it is the register-fed dX kernel's product. A class's rows go in
+// ranges of about 4096 (whole trellis runs), a batch of up to kBatch ranges at a time: the batch's
+// ranges are decoded into the int8-code form in the workspace (the standalone decode's kernel
+// writing tiled, one launch for the batch when the form allows), and one
+// qlinear_rt_vocab_kernel launch (a grid slice a range, so a head with few token rows or a narrow
+// n_embd still fills the chip) writes each range's (gathered . W) * scale.col -- the weight as the
+// exact sum of two bf16 halves, both reduced into one f32 accumulator; the class's scale.col one
+// factor a 128-column tile -- into its own f32 partial; the partials are then added into d_x in
+// range order (deterministic). Ranges are padded to Np (a multiple of 128) rows with zero codes,
+// zero scales and zero cotangent columns. The products' operands -- the cotangent's columns of
+// every class's rows, each range's [rows, Np] in the fused kernels' tiled layout -- are gathered
+// first, for all classes in one launch whose token rows vary slowest, so the workgroups in flight
+// cover a few token rows of every class and each cotangent line is fetched from memory about once
+// (the classes split the vocabulary at random: a class on its own touches almost every line).
+// Token rows go in blocks of at most kRowBlock, each block's operands held at once. Once every
+// class is in, the unnormalised 128-wide Hadamard runs over each 128 columns of d_x.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
 #include "../../include/r97q.h"
+#include "act_tiles.h"
 #include "iqr_device.h"
-#include "qlinear_fused.h"
+#include "qlinear_rt.h"
 #include "status.h"
 
 namespace r97q {
 namespace {
 
 constexpr int64_t kRangeRows = 4096;  // rows of a range (whole trellis runs)
-constexpr int kBatch = 8;             // ranges a batched launch
-constexpr int kFillWorkgroups = 512;  // a batch large enough for this many workgroups (256 CUs)
+constexpr int kDecodeRanges = 8;      // ranges a decode launch
+constexpr int kFillWorkgroups = 1024;  // slices enough for this many product workgroups (4 x 256 CUs)
 constexpr int64_t kRowBlock = 4096;   // token rows a pass (every class's gathered operands held for them)
+constexpr int kGatherRows = 8;
+constexpr int kGatherLd = 256 + 8;  // LDS row length: a row's 16-byte units start 16 bytes later each row
 
 int64_t round_up(int64_t n, int64_t m) { return (n + m - 1) / m * m; }
 int64_t row_block(int64_t rows) { return rows < kRowBlock ? rows : kRowBlock; }
@@ -53,26 +56,56 @@ int64_t ranges_of(const R97qVocabClass& c) {
     return (c.rows + R - 1) / R;
 }
 
-// ranges a batch takes: enough for kFillWorkgroups workgroups, at most kBatch
-int batch_of(int64_t rows, int64_t K) {
-    const int64_t wgs = (rows + kBM - 1) / kBM * (K / kBN);
-    const int64_t b = (kFillWorkgroups + wgs - 1) / wgs;
-    return (int)(b < 1 ? 1 : b > kBatch ? kBatch : b);
-}
-
-struct VocabWs {
-    int64_t codes, scale, gather, part, part_lo, cf, total;
-};
-
-VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
+// every range's rows padded to this: the product's shared reduction length (a multiple of 128)
+int64_t padded_rows(const R97qVocabPlan& plan) {
     int64_t Np = 0;
     for (int c = 0; c < plan.classes; ++c) {
         const int64_t s = round_up(range_rows(plan.cls[c]), 128);
         Np = s > Np ? s : Np;
     }
-    const int64_t K = plan.n_embd, nkb = K / 128, rb = row_block(rows), Z = batch_of(rb, K);
-    int64_t nranges = 0;
-    for (int c = 0; c < plan.classes; ++c) nranges += ranges_of(plan.cls[c]);
+    return Np;
+}
+
+int64_t ranges_all(const R97qVocabPlan& plan) {
+    int64_t n = 0;
+    for (int c = 0; c < plan.classes; ++c) n += ranges_of(plan.cls[c]);
+    return n;
+}
+
+// The product's slices (the ranges counted class by class): enough for kFillWorkgroups workgroups
+// of `rows` token rows, at most kVocabSlices; a class's ranges split evenly over slices of at most
+// L ranges, L the ranges over the slices wanted. A slice's ranges share a class (its scale.col
+// factor), so a class takes at least one. Returns the slices; slice s holds ranges first[s] ..
+// first[s+1]-1 of class cls[s].
+int vocab_slices(const R97qVocabPlan& plan, int64_t rows, int* first, int* cls) {
+    const int64_t wgs = (rows + rt::kBM - 1) / rt::kBM * (plan.n_embd / rt::kBN);
+    const int64_t nr = ranges_all(plan);
+    int64_t want = (kFillWorkgroups + wgs - 1) / wgs;
+    const int64_t most = rt::kVocabSlices - plan.classes + 1;  // the classes' rounding up adds at most one each
+    want = want < 1 ? 1 : want > most ? most : want;
+    const int64_t L = (nr + want - 1) / want;  // ranges a slice at most
+    int n = 0, y = 0;
+    for (int c = 0; c < plan.classes; ++c) {
+        const int64_t r = ranges_of(plan.cls[c]), k = (r + L - 1) / L;
+        for (int64_t j = 0; j < k; ++j) {
+            first[n] = y + (int)(j * r / k);
+            cls[n++] = c;
+        }
+        y += (int)r;
+    }
+    first[n] = y;
+    return n;
+}
+
+struct VocabWs {
+    int64_t codes, scale, gather, part, cf, total;
+};
+
+VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
+    const int64_t Np = padded_rows(plan), K = plan.n_embd, nkb = K / 128, rb = row_block(rows);
+    const int64_t nranges = ranges_all(plan);
+    int first[rt::kVocabSlices + 1], cls[rt::kVocabSlices];
+    const int64_t S = vocab_slices(plan, rb, first, cls);
     VocabWs w{};
     int64_t off = 0;
     auto take = [&](int64_t bytes) {
@@ -80,12 +113,11 @@ VocabWs vocab_ws(const R97qVocabPlan& plan, int64_t rows) {
         off += round_up(bytes, 256);
         return at;
     };
-    w.codes = take(Z * Np * K);
-    w.scale = take(Z * nkb * Np * 2);
-    w.gather = take(nranges * rb * Np * 2);
-    w.part = take(Z * rb * K * 4);
-    w.part_lo = take(Z * rb * K * 4);
-    w.cf = take(nkb * 4);
+    w.codes = take(nranges * Np * K);
+    w.scale = take(nranges * nkb * Np * 2);
+    w.gather = take(nranges * act_tile_bytes(rb, Np));
+    w.part = take(S * rb * K * 4);
+    w.cf = take(plan.classes * nkb * 4);
     w.total = off;
     return w;
 }
@@ -101,63 +133,86 @@ __global__ __launch_bounds__(256) void vocab_pad_kernel(int8_t* __restrict__ cod
     if (i < pad * nkb) scale_t[(i / pad) * ns_pad + ns + i % pad] = 0;
 }
 
-// The gathered operands of one block of token rows: class c's range z is a[z][m][n] =
-// dy[m, ids[z*R + n] - vocab_offset] for a class row z*R + n < rows and an id inside this
-// vocabulary, else 0 (the range's padding columns up to Np included).
+// The gathered operands of one block of token rows, each range's [rb, Np] in the fused kernels'
+// tiled layout (act_tiles.h): class c's range z holds a[m][n] = dy[m, ids[z*R + n] - vocab_offset]
+// for a class row z*R + n < rows and an id inside this vocabulary, else 0 (the range's padding
+// columns up to Np and its padding rows up to a multiple of 32 included).
 struct GatherClass {
     const int32_t* ids;
     int64_t rows, R;  // the class's rows; rows a range
-    uint16_t* out;    // [ranges][rb][Np]
-    int y0;           // the class's first range in the launch's grid
+    uint16_t* out;    // [ranges][the tiled copy of rb x Np]
+    int y0;           // the class's first range (ranges of every class counted in class order)
 };
 struct GatherAll {
     GatherClass cls[4];
-    int classes, ny;   // ny: every class's ranges
-    int64_t rb, vocab, vocab_offset, Np, nx, ngroups;  // nx: Np / 256; ngroups: token-row groups
+    int classes;
+    uint32_t nx, per;  // column blocks a range (Np / 256); workgroups a token-row group (nx x ranges)
+    int64_t rb, vocab, vocab_offset, Np, ngroups;  // ngroups: token-row groups to 32-row padding
 };
-// A workgroup: 256 columns of one range x a group of kGatherRows token rows; a column and
-// kGatherRows token rows a thread (the id read once for them; measured: 8 columns a thread with one
-// 16-byte store is 40% slower -- fewer loads in flight). The workgroups are dealt so that XCD x
-// takes the token-row groups x, x + 8, .. whole, one after another, each for every class and range:
-// a cotangent line is then fetched into one XCD's L2 while its few token rows are gathered, not
+// A workgroup: 256 columns of one range x a group of kGatherRows (8) token rows, written as the
+// fused kernel's tiled copy (act_tiles.h). The loads go a column a thread, one token row an
+// instruction (a wave's 64 columns of a row: their ids ascend within a class, so a few lines of dy),
+// into LDS; the stores then go 8 columns of one row a lane, one 16-byte unit of the tiled layout, so
+// each of a wave's 8 column groups is 8 rows x 16 contiguous bytes. (Measured: the loads a lane's 8
+// columns x 8 rows at once touch ~64 lines an instruction and are 2x slower; 2-byte stores straight
+// into the tiled layout, 8 pieces of 16 bytes an instruction, 1.3x.) The workgroups are dealt so
+// that XCD x takes the token-row groups x, x + 8, .. whole, one after another, each for every class
+// and range: a cotangent line is then fetched into one L2 while its few token rows are gathered, not
 // into all eight (the hardware deals workgroup ids round-robin over the XCDs, in id order on each).
-constexpr int kGatherRows = 8;
+// Within a group the blocks go class by class, range by range. (Measured slower: the classes' blocks
+// interleaved in proportion, so that a line's readers of every class run close together in time,
+// 1.2x; 512 or 1024 columns a workgroup, more loads in flight, 1.06x and 1.15x.)
 __global__ __launch_bounds__(256) void vocab_gather_kernel(const uint16_t* __restrict__ dy, const GatherAll g) {
-    const int64_t xcd = blockIdx.x & 7, l = blockIdx.x >> 3;
-    const int64_t per = g.nx * g.ny;  // workgroups a token-row group
-    const int64_t grp = (l / per) * 8 + xcd;
-    if (grp >= g.ngroups) return;
-    const int y = (int)((l % per) / g.nx);
+    __shared__ __align__(16) uint16_t tile[kGatherRows * kGatherLd];
+    const uint32_t xcd = blockIdx.x & 7, l = blockIdx.x >> 3;
+    const uint32_t gi = l / g.per, q = l - gi * g.per;  // 32-bit: the 64-bit divisions cost 5% here
+    const int64_t grp = (int64_t)gi * 8 + xcd;
+    if (grp >= g.ngroups) return;  // the whole workgroup: the barrier below is reached by all or none
+    const uint32_t y = q / g.nx, xb = q - y * g.nx;
     int c = 0;
-    while (c + 1 < g.classes && y >= g.cls[c + 1].y0) ++c;
+    while (c + 1 < g.classes && (int)y >= g.cls[c + 1].y0) ++c;
     const GatherClass& k = g.cls[c];
-    const int64_t z = y - k.y0;
-    const int64_t n = (l % per % g.nx) * 256 + threadIdx.x;
+    const int64_t z = (int)y - k.y0;
+    const int64_t nb = (int64_t)xb * 256;  // the workgroup's first column
     const int64_t mb = grp * kGatherRows;
-    if (n >= g.Np) return;
-    const int64_t r = z * k.R + n;
-    int64_t col = -1;
-    if (n < k.R && r < k.rows) {
-        const int64_t id = k.ids[r];
-        if (id >= g.vocab_offset && id < g.vocab_offset + g.vocab) col = id - g.vocab_offset;
-    }
+    const int t = threadIdx.x;
+    {
+        const int64_t n = nb + t, r = z * k.R + n;
+        int64_t col = -1;
+        if (n < k.R && r < k.rows) {
+            const int64_t id = k.ids[r];
+            if (id >= g.vocab_offset && id < g.vocab_offset + g.vocab) col = id - g.vocab_offset;
+        }
 #pragma unroll
-    for (int i = 0; i < kGatherRows; ++i) {
-        const int64_t m = mb + i;
-        if (m >= g.rb) break;
-        k.out[(z * g.rb + m) * g.Np + n] = col >= 0 ? dy[m * g.vocab + col] : (uint16_t)0;
+        for (int i = 0; i < kGatherRows; ++i) {
+            const int64_t m = mb + i;
+            tile[i * kGatherLd + t] = col >= 0 && m < g.rb ? dy[m * g.vocab + col] : (uint16_t)0;
+        }
     }
+    __syncthreads();
+    const int lane = t & 63, wave = t >> 6, i = lane & 7;
+    const int nl = 64 * wave + 8 * (lane >> 3);  // the lane's first column in the workgroup
+    if (nb + nl >= g.Np) return;
+    const uint4 v = *reinterpret_cast<const uint4*>(tile + i * kGatherLd + nl);
+    uint16_t* a = k.out + z * act_tile_blocks(g.rb) * 32 * g.Np;
+    *reinterpret_cast<uint4*>(a + act_tile_index(mb + i, nb + nl, g.rb)) = v;
 }
 
-// d_x[i] += (hi[0][i] + lo[0][i]) + (hi[1][i] + lo[1][i]) + ... (the ranges in order; a range's
-// product over the weights' high halves plus its product over their low halves)
-__global__ __launch_bounds__(256) void vocab_reduce_kernel(float* __restrict__ d_x, const float* __restrict__ hi,
-                                                           const float* __restrict__ lo, int64_t n, int Z) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// d_x[i] += part[0][i] + part[1][i] + ... (the slices in order), four values a thread (n a multiple
+// of 4)
+__global__ __launch_bounds__(256) void vocab_reduce_kernel(float* __restrict__ d_x, const float* __restrict__ part,
+                                                           int64_t n, int S) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= n) return;
-    float v = d_x[i];
-    for (int z = 0; z < Z; ++z) v += hi[z * n + i] + lo[z * n + i];
-    d_x[i] = v;
+    float4 v = *reinterpret_cast<const float4*>(d_x + i);
+    for (int z = 0; z < S; ++z) {
+        const float4 p = *reinterpret_cast<const float4*>(part + z * n + i);
+        v.x += p.x;
+        v.y += p.y;
+        v.z += p.z;
+        v.w += p.w;
+    }
+    *reinterpret_cast<float4*>(d_x + i) = v;
 }
 
 __global__ __launch_bounds__(64) void vocab_cf_kernel(const uint8_t* __restrict__ cf, int32_t dtype, int64_t nkb,
@@ -245,117 +300,118 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
     uint16_t* scale_t = reinterpret_cast<uint16_t*>(wsb + ws.scale);
     uint16_t* gathered = reinterpret_cast<uint16_t*>(wsb + ws.gather);
     float* part = reinterpret_cast<float*>(wsb + ws.part);
-    float* part_lo = reinterpret_cast<float*>(wsb + ws.part_lo);
     float* cf = reinterpret_cast<float*>(wsb + ws.cf);
     const hipStream_t s = (hipStream_t)stream;
     const int64_t K = plan->n_embd, nkb = K / 128;
 
+    const int64_t Np = padded_rows(*plan);
+    const uint32_t nranges = (uint32_t)ranges_all(*plan);
+    const uint32_t nx = blocks(Np, 256), per = nx * nranges;  // a token-row group's gather workgroups
+
+    // every class's scale.col factors, and every range decoded into the int8-code form (range y
+    // at codes + y * Np * K, its scales at scale_t + y * nkb * Np), once a call
+    for (int c = 0, y = 0; c < plan->classes; ++c) {
+        const R97qVocabClass& cls = plan->cls[c];
+        hipLaunchKernelGGL(vocab_cf_kernel, dim3(blocks(nkb, 64)), dim3(64), 0, s,
+                           static_cast<const uint8_t*>(cls.scale_col), cls.scale_col_dtype, nkb, cf + c * nkb);
+        if (int e = launch_status("vocab_cf_kernel")) return e;
+        const int64_t R = range_rows(cls), nr = ranges_of(cls);
+        for (int64_t z0 = 0; z0 < nr; z0 += kDecodeRanges) {
+            const int nz = (int)(nr - z0 < kDecodeRanges ? nr - z0 : kDecodeRanges);
+            R97IqrDecodeDesc dz[kDecodeRanges];
+            for (int i = 0; i < nz; ++i, ++y) {
+                const int64_t r0 = (z0 + i) * R;
+                const int64_t ns = R < cls.rows - r0 ? R : cls.rows - r0;
+                int8_t* zc = codes + (int64_t)y * Np * K;
+                uint16_t* zs = scale_t + (int64_t)y * nkb * Np;
+                R97IqrDecodeDesc d = cls.decode;
+                d.row0 = r0;
+                d.rows = ns;
+                d.codes = d.codes + r0 * d.codes_row_bytes;
+                d.scale = d.scale + r0 * d.scale_row_bytes;
+                d.zero = d.zero ? d.zero + r0 * d.zero_row_bytes : nullptr;
+                d.out_codes = zc;
+                d.out_scale = zs;
+                if (validate(d)) {
+                    set_error("%s: the plan's class %d decode is outside the kernel's rules", who, c);
+                    return R97Q_EINVAL;
+                }
+                if (Np != ns) {
+                    const int64_t n = Np * K / 4 - (ns / 8) * (K / 4) * 8;
+                    const int64_t m = (Np - ns) * nkb;
+                    hipLaunchKernelGGL(vocab_pad_kernel, dim3(blocks(n > m ? n : m, 256)), dim3(256), 0, s, zc, zs,
+                                       ns, Np, K);
+                    if (int e = launch_status("vocab_pad_kernel")) return e;
+                }
+                dz[i] = d;
+            }
+            if (int e = decode_tiled_batch(dz, nz, Np, s)) return e;
+        }
+    }
+
     const int64_t rbmax = row_block(rows);
-    const int Zmax = batch_of(rbmax, K);  // the partials' workspace holds this many ranges
+    rt::VocabRtParams v{};
+    v.slices = vocab_slices(*plan, rbmax, v.first, v.cls);  // the partials' workspace holds these
     for (int64_t m0 = 0; m0 < rows; m0 += rbmax) {
         const int64_t rb = rows - m0 < rbmax ? rows - m0 : rbmax;
         // every class's gathered operands for token rows [m0, m0 + rb)
-        int64_t Np = 0;
-        for (int c = 0; c < plan->classes; ++c) {
-            const int64_t np = round_up(range_rows(plan->cls[c]), 128);
-            Np = np > Np ? np : Np;
-        }
         GatherAll g{};
         g.classes = plan->classes;
+        g.nx = nx;
+        g.per = per;
         g.rb = rb;
         g.vocab = plan->vocab;
         g.vocab_offset = plan->vocab_offset;
         g.Np = Np;
-        int ny = 0;
         int64_t goff = 0;
+        int y0 = 0;
         for (int c = 0; c < plan->classes; ++c) {
             const R97qVocabClass& cls = plan->cls[c];
-            const int64_t nr = ranges_of(cls);
-            g.cls[c] = GatherClass{static_cast<const int32_t*>(cls.ids), cls.rows, range_rows(cls), gathered + goff, ny};
-            ny += (int)nr;
-            goff += nr * rb * Np;
+            g.cls[c] = GatherClass{static_cast<const int32_t*>(cls.ids), cls.rows, range_rows(cls), gathered + goff, y0};
+            goff += ranges_of(cls) * act_tile_blocks(rb) * 32 * Np;
+            y0 += (int)ranges_of(cls);
         }
-        g.ny = ny;
-        g.nx = blocks(Np, 256);
-        g.ngroups = blocks(rb, kGatherRows);
-        const int64_t nwg = (g.ngroups + 7) / 8 * 8 * g.nx * ny;  // every XCD's share whole
+        g.ngroups = act_tile_blocks(rb) * 32 / kGatherRows;
+        const int64_t nwg = (g.ngroups + 7) / 8 * 8 * (int64_t)per;  // every XCD's share whole
         if (nwg > INT32_MAX) {
-            set_error("%s: %d ranges of %lld rows are more than a launch's grid takes", who, ny, (long long)kRangeRows);
+            set_error("%s: %u ranges of %lld rows are more than a launch's grid takes", who, nranges,
+                      (long long)kRangeRows);
             return R97Q_EUNSUPPORTED;
         }
         hipLaunchKernelGGL(vocab_gather_kernel, dim3((unsigned)nwg), dim3(256), 0, s, dy + m0 * plan->vocab, g);
         if (int e = launch_status("vocab_gather_kernel")) return e;
 
-        for (int c = 0; c < plan->classes; ++c) {
-            const R97qVocabClass& cls = plan->cls[c];
-            hipLaunchKernelGGL(vocab_cf_kernel, dim3(blocks(nkb, 64)), dim3(64), 0, s,
-                               static_cast<const uint8_t*>(cls.scale_col), cls.scale_col_dtype, nkb, cf);
-            if (int e = launch_status("vocab_cf_kernel")) return e;
-            const int64_t R = range_rows(cls);
-            for (int64_t b0 = 0; b0 < cls.rows; b0 += Zmax * R) {
-                const int64_t nb = Zmax * R < cls.rows - b0 ? Zmax * R : cls.rows - b0;  // the batch's class rows
-                const int Z = (int)((nb + R - 1) / R);
-                R97IqrDecodeDesc dz[kBatch];
-                for (int z = 0; z < Z; ++z) {
-                    const int64_t r0 = b0 + z * R;
-                    const int64_t ns = R < cls.rows - r0 ? R : cls.rows - r0;
-                    int8_t* zc = codes + z * Np * K;
-                    uint16_t* zs = scale_t + z * nkb * Np;
-                    R97IqrDecodeDesc d = cls.decode;
-                    d.row0 = r0;
-                    d.rows = ns;
-                    d.codes = d.codes + r0 * d.codes_row_bytes;
-                    d.scale = d.scale + r0 * d.scale_row_bytes;
-                    d.zero = d.zero ? d.zero + r0 * d.zero_row_bytes : nullptr;
-                    d.out_codes = zc;
-                    d.out_scale = zs;
-                    if (validate(d)) {
-                        set_error("%s: the plan's class %d decode is outside the kernel's rules", who, c);
-                        return R97Q_EINVAL;
-                    }
-                    if (Np != ns) {
-                        const int64_t n = Np * K / 4 - (ns / 8) * (K / 4) * 8;
-                        const int64_t m = (Np - ns) * nkb;
-                        hipLaunchKernelGGL(vocab_pad_kernel, dim3(blocks(n > m ? n : m, 256)), dim3(256), 0, s, zc,
-                                           zs, ns, Np, K);
-                        if (int e = launch_status("vocab_pad_kernel")) return e;
-                    }
-                    dz[z] = d;
-                }
-                if (int e = decode_tiled_batch(dz, Z, Np, s)) return e;
-                DxParams p{};
-                p.dY = g.cls[c].out + (b0 / R) * rb * Np;
-                p.T = rb;
-                p.N = Np;
-                p.K = K;
-                p.stream = reinterpret_cast<const uint32_t*>(codes);
-                p.scale_t = scale_t;
-                p.rank = 0;
-                p.dX = part;
-                p.dx_f32 = 1;
-                p.accumulate = 0;
-                p.a_scale = cf;  // one factor a 128-column tile: every row reads cf[kt]
-                p.a_scale_ld = 0;
-                p.mtiles = (int)((rb + kBM - 1) / kBM);
-                p.ktiles = (int)(K / kBN);
-                p.batch = Z;
-                p.z_dy = rb * Np;
-                p.z_w = Np * K / 4;
-                p.z_scale = nkb * Np;
-                p.z_out = rb * K;
-                // each weight as the exact sum of two bf16 values: one launch runs the product over
-                // the high halves and, in slices of its own, over the low halves into partials of
-                // their own (f32 products of bf16 values are exact); the reduction adds each
-                // range's two
-                p.both = 1;
-                p.dX_lo = part_lo;
-                launch_dx<R97Q_CODES8>(p, s);
-                if (int e = launch_status("qlinear_dx_both_kernel (vocab head)")) return e;
-                hipLaunchKernelGGL(vocab_reduce_kernel, dim3(blocks(rb * K, 256)), dim3(256), 0, s, d_x + m0 * K, part,
-                                   part_lo, rb * K, Z);
-                if (int e = launch_status("vocab_reduce_kernel")) return e;
-            }
-        }
+        // every range's product on the register-fed kernel (qlinear_rt_vocab_kernel), one launch:
+        // each weight as the exact sum of two bf16 values, a workgroup reducing its tile over the
+        // high halves and then the low halves of each range of its slice into one f32 accumulator
+        // (f32 products of bf16 values are exact), a slice's partial of its own; the partials are
+        // then added into d_x in slice order
+        rt::Params& p = v.p;
+        p.act = gathered;
+        p.T = rb;
+        p.N = Np;
+        p.K = K;
+        p.stream = reinterpret_cast<const uint32_t*>(codes);
+        p.scale_t = scale_t;
+        p.run_rows = 1;
+        p.rank = 0;
+        p.out = part;
+        p.out_f32 = 1;
+        p.accumulate = 0;
+        p.mtiles = (int)((rb + rt::kBM - 1) / rt::kBM);
+        p.otiles = (int)(K / rt::kBN);
+        p.ksplit = 1;
+        p.nfull = p.mtiles * p.otiles;
+        v.z_act = act_tile_blocks(rb) * 32 * Np;
+        v.z_w = Np * K / 4;
+        v.z_scale = nkb * Np;
+        v.cf = cf;
+        v.cf_ld = nkb;
+        rt::launch_vocab(v, s);
+        if (int e = launch_status("qlinear_rt_vocab_kernel")) return e;
+        hipLaunchKernelGGL(vocab_reduce_kernel, dim3(blocks(rb * K / 4, 256)), dim3(256), 0, s, d_x + m0 * K, part,
+                           rb * K, v.slices);
+        if (int e = launch_status("vocab_reduce_kernel")) return e;
     }
     if (plan->transform == 128) {
         hipLaunchKernelGGL(vocab_unrotate_kernel, dim3((unsigned)rows, (unsigned)nkb), dim3(128), 0, s, d_x, K);
