@@ -18,11 +18,14 @@
 // first, for all classes in one launch whose token rows vary slowest, so the workgroups in flight
 // cover a few token rows of every class and each cotangent line is fetched from memory about once
 // (the classes split the vocabulary at random: a class on its own touches almost every line).
-// Token rows go in blocks of at most kRowBlock, each block's operands held at once. Once every
-// class is in, the unnormalised 128-wide Hadamard runs over each 128 columns of d_x.
+// Token rows go in blocks of at most kRowBlock, each block's operands held at once. The decode runs
+// on a side stream of the device beside the first block's gather, joined back into the caller's
+// stream before the first product. Once every class is in, the unnormalised 128-wide Hadamard runs
+// over each 128 columns of d_x.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 #include "../../include/r97q.h"
 #include "act_tiles.h"
@@ -37,7 +40,7 @@ constexpr int64_t kRangeRows = 4096;  // rows of a range (whole trellis runs)
 constexpr int kDecodeRanges = 8;      // ranges a decode launch
 constexpr int kFillWorkgroups = 1024;  // slices enough for this many product workgroups (4 x 256 CUs)
 constexpr int64_t kRowBlock = 4096;   // token rows a pass (every class's gathered operands held for them)
-constexpr int kGatherRows = 8;
+constexpr int kGatherRows = 16;  // token rows a gather workgroup
 constexpr int kGatherLd = 256 + 8;  // LDS row length: a row's 16-byte units start 16 bytes later each row
 
 int64_t round_up(int64_t n, int64_t m) { return (n + m - 1) / m * m; }
@@ -149,19 +152,22 @@ struct GatherAll {
     uint32_t nx, per;  // column blocks a range (Np / 256); workgroups a token-row group (nx x ranges)
     int64_t rb, vocab, vocab_offset, Np, ngroups;  // ngroups: token-row groups to 32-row padding
 };
-// A workgroup: 256 columns of one range x a group of kGatherRows (8) token rows, written as the
+// A workgroup: 256 columns of one range x a group of kGatherRows (16) token rows, written as the
 // fused kernel's tiled copy (act_tiles.h). The loads go a column a thread, one token row an
 // instruction (a wave's 64 columns of a row: their ids ascend within a class, so a few lines of dy),
-// into LDS; the stores then go 8 columns of one row a lane, one 16-byte unit of the tiled layout, so
-// each of a wave's 8 column groups is 8 rows x 16 contiguous bytes. (Measured: the loads a lane's 8
-// columns x 8 rows at once touch ~64 lines an instruction and are 2x slower; 2-byte stores straight
-// into the tiled layout, 8 pieces of 16 bytes an instruction, 1.3x.) The workgroups are dealt so
+// into LDS; the stores then go one 16-byte unit of the tiled layout (8 columns of a row) a thread,
+// rows fastest, so 16 consecutive threads write 256 contiguous bytes. The workgroups are dealt so
 // that XCD x takes the token-row groups x, x + 8, .. whole, one after another, each for every class
 // and range: a cotangent line is then fetched into one L2 while its few token rows are gathered, not
 // into all eight (the hardware deals workgroup ids round-robin over the XCDs, in id order on each).
-// Within a group the blocks go class by class, range by range. (Measured slower: the classes' blocks
-// interleaved in proportion, so that a line's readers of every class run close together in time,
-// 1.2x; 512 or 1024 columns a workgroup, more loads in flight, 1.06x and 1.15x.)
+// Within a group the blocks go class by class, range by range. The workgroups' own costs (the ids,
+// the dependent loads' latency) weigh more than the lines fetched again for each class (a group's
+// rows overflow the L2, the 256 MB cache behind it holds them): measured, 16 rows a group 1.43 ms,
+// 8 rows 1.48 (a third of the bytes fetched fewer), 32 rows 1.45, 4 rows 1.82, 2 rows 2.64. Also
+// slower: a lane's 8 columns x 8 rows loaded at once (~64 lines an instruction, 2x); 2-byte stores
+// straight into the tiled layout (8 pieces of 16 bytes an instruction, 1.3x); the classes' blocks
+// interleaved in proportion so that a line's readers of every class run close together in time
+// (1.2x); 512 or 1024 columns a workgroup (1.06x, 1.15x).
 __global__ __launch_bounds__(256) void vocab_gather_kernel(const uint16_t* __restrict__ dy, const GatherAll g) {
     __shared__ __align__(16) uint16_t tile[kGatherRows * kGatherLd];
     const uint32_t xcd = blockIdx.x & 7, l = blockIdx.x >> 3;
@@ -190,12 +196,17 @@ __global__ __launch_bounds__(256) void vocab_gather_kernel(const uint16_t* __res
         }
     }
     __syncthreads();
-    const int lane = t & 63, wave = t >> 6, i = lane & 7;
-    const int nl = 64 * wave + 8 * (lane >> 3);  // the lane's first column in the workgroup
-    if (nb + nl >= g.Np) return;
-    const uint4 v = *reinterpret_cast<const uint4*>(tile + i * kGatherLd + nl);
+    // the store: the tile's kGatherRows x 32 units of 16 bytes, a unit a thread at a time, row
+    // fastest
     uint16_t* a = k.out + z * act_tile_blocks(g.rb) * 32 * g.Np;
-    *reinterpret_cast<uint4*>(a + act_tile_index(mb + i, nb + nl, g.rb)) = v;
+#pragma unroll
+    for (int u = t; u < kGatherRows * 32; u += 256) {
+        const int i = u % kGatherRows;
+        const int nl = 8 * (u / kGatherRows);  // the unit's first column in the workgroup
+        if (nb + nl < g.Np)
+            *reinterpret_cast<uint4*>(a + act_tile_index(mb + i, nb + nl, g.rb)) =
+                *reinterpret_cast<const uint4*>(tile + i * kGatherLd + nl);
+    }
 }
 
 // d_x[i] += part[0][i] + part[1][i] + ... (the slices in order), four values a thread (n a multiple
@@ -268,6 +279,57 @@ bool plan_ok(const R97qVocabPlan* plan, int64_t rows, const char* who) {
     return true;
 }
 
+// The side stream of a device (and its fork and join events), made on the first call that finds
+// none with that device current and its stream not capturing a graph (a call that cannot make one
+// runs the decode on its own stream). Held until the process ends; used under g_side_mu, so calls
+// from several threads fork and join one at a time.
+struct SideStream {
+    hipStream_t s;
+    hipEvent_t fork, join;
+};
+constexpr int kSideDevices = 64;
+SideStream g_side[kSideDevices];
+bool g_side_ok[kSideDevices] = {};
+std::mutex g_side_mu;
+
+const SideStream* side_stream(hipStream_t caller) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kSideDevices) return nullptr;
+    if (g_side_ok[dev]) return &g_side[dev];
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(caller, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    SideStream& sd = g_side[dev];
+    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;  // the stream is kept (and made again on a later call): a rare failure
+    }
+    g_side_ok[dev] = true;
+    return &sd;
+}
+
+// The caller's stream made to wait for the side stream's work so far, once: by the call when the
+// decode is needed, else when the call returns (an error return included).
+struct SideJoin {
+    const SideStream* side = nullptr;
+    hipStream_t caller{};
+    bool done = true;
+    int wait(const char* who) {
+        if (done) return R97Q_OK;
+        done = true;
+        if (hipEventRecord(side->join, side->s) != hipSuccess || hipStreamWaitEvent(caller, side->join, 0) != hipSuccess) {
+            set_error("%s: the decode stream's join failed", who);
+            return R97Q_ELAUNCH;
+        }
+        return R97Q_OK;
+    }
+    ~SideJoin() { (void)wait("r97q_vocab_head_transpose"); }
+};
+
 }  // namespace
 }  // namespace r97q
 
@@ -308,44 +370,66 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
     const uint32_t nranges = (uint32_t)ranges_all(*plan);
     const uint32_t nx = blocks(Np, 256), per = nx * nranges;  // a token-row group's gather workgroups
 
-    // every class's scale.col factors, and every range decoded into the int8-code form (range y
-    // at codes + y * Np * K, its scales at scale_t + y * nkb * Np), once a call
+    // range z of class c (range y of all): its decode into the int8-code form, at codes + y * Np * K,
+    // its scales at scale_t + y * nkb * Np; every one checked before anything is launched
+    auto range_desc = [&](int c, int64_t z, int64_t y) {
+        const R97qVocabClass& cls = plan->cls[c];
+        const int64_t R = range_rows(cls), r0 = z * R;
+        R97IqrDecodeDesc d = cls.decode;
+        d.row0 = r0;
+        d.rows = R < cls.rows - r0 ? R : cls.rows - r0;
+        d.codes = d.codes + r0 * d.codes_row_bytes;
+        d.scale = d.scale + r0 * d.scale_row_bytes;
+        d.zero = d.zero ? d.zero + r0 * d.zero_row_bytes : nullptr;
+        d.out_codes = codes + y * Np * K;
+        d.out_scale = scale_t + y * nkb * Np;
+        return d;
+    };
+    for (int c = 0, y = 0; c < plan->classes; ++c)
+        for (int64_t z = 0; z < ranges_of(plan->cls[c]); ++z, ++y)
+            if (validate(range_desc(c, z, y))) {
+                set_error("%s: the plan's class %d decode is outside the kernel's rules", who, c);
+                return R97Q_EINVAL;
+            }
+
+    // The decode (every class's scale.col factors and every range, once a call) runs on the
+    // device's side stream, beside the first token-row block's gather on the caller's stream; the
+    // caller's stream waits for it before the first product (and on any early return).
+    std::unique_lock<std::mutex> lock(g_side_mu);
+    const SideStream* side = side_stream(s);
+    const hipStream_t ds = side ? side->s : s;
+    SideJoin join;
+    if (side) {
+        if (hipEventRecord(side->fork, s) != hipSuccess || hipStreamWaitEvent(ds, side->fork, 0) != hipSuccess) {
+            set_error("%s: the decode stream's fork failed", who);
+            return R97Q_ELAUNCH;
+        }
+        join.side = side;
+        join.caller = s;
+        join.done = false;
+    }
     for (int c = 0, y = 0; c < plan->classes; ++c) {
         const R97qVocabClass& cls = plan->cls[c];
-        hipLaunchKernelGGL(vocab_cf_kernel, dim3(blocks(nkb, 64)), dim3(64), 0, s,
+        hipLaunchKernelGGL(vocab_cf_kernel, dim3(blocks(nkb, 64)), dim3(64), 0, ds,
                            static_cast<const uint8_t*>(cls.scale_col), cls.scale_col_dtype, nkb, cf + c * nkb);
         if (int e = launch_status("vocab_cf_kernel")) return e;
-        const int64_t R = range_rows(cls), nr = ranges_of(cls);
+        const int64_t nr = ranges_of(cls);
         for (int64_t z0 = 0; z0 < nr; z0 += kDecodeRanges) {
             const int nz = (int)(nr - z0 < kDecodeRanges ? nr - z0 : kDecodeRanges);
             R97IqrDecodeDesc dz[kDecodeRanges];
             for (int i = 0; i < nz; ++i, ++y) {
-                const int64_t r0 = (z0 + i) * R;
-                const int64_t ns = R < cls.rows - r0 ? R : cls.rows - r0;
-                int8_t* zc = codes + (int64_t)y * Np * K;
-                uint16_t* zs = scale_t + (int64_t)y * nkb * Np;
-                R97IqrDecodeDesc d = cls.decode;
-                d.row0 = r0;
-                d.rows = ns;
-                d.codes = d.codes + r0 * d.codes_row_bytes;
-                d.scale = d.scale + r0 * d.scale_row_bytes;
-                d.zero = d.zero ? d.zero + r0 * d.zero_row_bytes : nullptr;
-                d.out_codes = zc;
-                d.out_scale = zs;
-                if (validate(d)) {
-                    set_error("%s: the plan's class %d decode is outside the kernel's rules", who, c);
-                    return R97Q_EINVAL;
-                }
+                const R97IqrDecodeDesc d = range_desc(c, z0 + i, y);
+                const int64_t ns = d.rows;
                 if (Np != ns) {
                     const int64_t n = Np * K / 4 - (ns / 8) * (K / 4) * 8;
                     const int64_t m = (Np - ns) * nkb;
-                    hipLaunchKernelGGL(vocab_pad_kernel, dim3(blocks(n > m ? n : m, 256)), dim3(256), 0, s, zc, zs,
-                                       ns, Np, K);
+                    hipLaunchKernelGGL(vocab_pad_kernel, dim3(blocks(n > m ? n : m, 256)), dim3(256), 0, ds,
+                                       d.out_codes, d.out_scale, ns, Np, K);
                     if (int e = launch_status("vocab_pad_kernel")) return e;
                 }
                 dz[i] = d;
             }
-            if (int e = decode_tiled_batch(dz, nz, Np, s)) return e;
+            if (int e = decode_tiled_batch(dz, nz, Np, ds)) return e;
         }
     }
 
@@ -380,6 +464,10 @@ int r97q_vocab_head_transpose(const R97qVocabPlan* plan, const uint16_t* dy, int
         }
         hipLaunchKernelGGL(vocab_gather_kernel, dim3((unsigned)nwg), dim3(256), 0, s, dy + m0 * plan->vocab, g);
         if (int e = launch_status("vocab_gather_kernel")) return e;
+        if (m0 == 0) {  // the decode joins the caller's stream before the first product
+            if (int e = join.wait(who)) return e;
+            lock.unlock();
+        }
 
         // every range's product on the register-fed kernel (qlinear_rt_vocab_kernel), one launch:
         // each weight as the exact sum of two bf16 values, a workgroup reducing its tile over the

@@ -131,6 +131,36 @@ def test_vocab_head_one_hot_and_chunking():
     assert rel_l2(got, 2 * want) > 0.3  # teeth: a doubled transform misses
 
 
+def test_vocab_head_in_a_graph():
+    """The head captured in a HIP graph and replayed: a call forks its weights' decode onto the
+    device's side stream (beside the gather on the caller's stream) and joins it back before the
+    products, which a capture records as a branch of the graph. Each replay, with eager work and
+    synchronisation between replays, equals the eager call bit for bit (the arithmetic's order is
+    fixed)."""
+    print("case vocab head in a graph rows=300 K=256", flush=True)
+    rng = np.random.default_rng(12)
+    K, rows = 256, 300
+    head, _, vocab = head_and_oracle(rng, K, [1500, 900], ["trunk-b5", "stored-u4"])
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    dy = torch.randn((rows, vocab), generator=gen, device="cuda").to(torch.bfloat16)
+    ws = torch.empty(head.workspace_bytes(rows), dtype=torch.uint8, device="cuda")
+    d_x = torch.zeros((rows, K), device="cuda")
+    head.transpose(dy, d_x, ws)  # eager first: the side stream is made outside the capture
+    torch.cuda.synchronize()
+    eager = d_x.clone()
+    assert float(eager.abs().sum()) > 0
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        d_x.zero_()  # a fill kernel, not a memset node
+        head.transpose(dy, d_x, ws, stream=torch.cuda.current_stream())
+    for i in range(4):
+        d_x.fill_(float("nan"))  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(d_x, eager), i
+
+
 def test_vocab_head_cast():
     from r9700training_amd.vocab_head import cast
 
