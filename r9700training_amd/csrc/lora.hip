@@ -306,33 +306,48 @@ __global__ __launch_bounds__(512) void lora_down_kernel(DownArgs a) {
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int e = 0; e < 4; ++e) red(wave, 16 * b + 4 * grp + e, 16 * nb + row16) = acc[b][nb][e];
+    // The transposed splits (Pt, Pt2) go out through LDS: [2r][the workgroup's 16 MB tokens] each,
+    // then a row's tokens as 16-byte stores (stored a value at a time, a wave's 2-byte stores land
+    // in as many rows of Pt, ldt apart: at rank 64 that cost the backward launch 12%). They are zero
+    // past T: the gradient kernel reduces over whole 32-row steps.
+    constexpr int NM = 16 * MB;
+    __shared__ __attribute__((aligned(16))) uint16_t tsp[2][2 * RD][NM];
+    const bool tr = a.Pt != nullptr || a.Pt2 != nullptr;  // the same for the whole launch
     __syncthreads();
-    for (int i = threadIdx.x; i < 16 * MB * RD; i += blockDim.x) {
+    for (int i = threadIdx.x; i < NM * RD; i += blockDim.x) {
         const int ml = i / RD, j = i % RD;
         const int64_t m = m0 + ml;
-        if (j >= a.r || m >= a.ldt) continue;
-        float v = red(0, ml, j);
-        for (int w = 1; w < nw; ++w) v += red(w, ml, j);
-        uint16_t hi = 0, lo = 0;
+        if (j >= a.r) continue;
+        uint16_t hi = 0, lo = 0, h2 = 0, l2 = 0;
         if (m < a.T) {
+            float v = red(0, ml, j);
+            for (int w = 1; w < nw; ++w) v += red(w, ml, j);
             if (a.out) a.out[m * a.r + j] = a.out_add ? a.out[m * a.r + j] + a.sa * v : a.sa * v;
             split(a.sb * v, hi, lo);
             if (a.P) {
                 a.P[m * 2 * a.r + j] = hi;
                 a.P[m * 2 * a.r + a.r + j] = lo;
             }
+            if (a.Pt2) split(a.s2 * a.U2[m * a.r + j], h2, l2);
         }
-        // the transposed splits are zero past T: the gradient kernel reduces over whole 32-row steps
-        if (a.Pt) {
-            a.Pt[(int64_t)j * a.ldt + m] = hi;
-            a.Pt[(int64_t)(a.r + j) * a.ldt + m] = lo;
+        if (tr) {
+            tsp[0][j][ml] = hi;
+            tsp[0][a.r + j][ml] = lo;
+            tsp[1][j][ml] = h2;
+            tsp[1][a.r + j][ml] = l2;
         }
-        if (a.Pt2) {
-            uint16_t h2 = 0, l2 = 0;
-            if (m < a.T) split(a.s2 * a.U2[m * a.r + j], h2, l2);
-            a.Pt2[(int64_t)j * a.ldt + m] = h2;
-            a.Pt2[(int64_t)(a.r + j) * a.ldt + m] = l2;
-        }
+    }
+    if (!tr) return;
+    __syncthreads();
+    // a 16-byte piece a thread: 8 tokens of one row (ldt is a multiple of 64, so a piece lies wholly
+    // below it or wholly past it; rows past ldt are the tiled copy's padding only)
+    const int nrow = 2 * a.r;
+    for (int i = threadIdx.x; i < 2 * nrow * (NM / 8); i += blockDim.x) {
+        const int which = i / (nrow * (NM / 8)), v = (i / (NM / 8)) % nrow, q = i % (NM / 8);
+        uint16_t* dst = which ? a.Pt2 : a.Pt;
+        const int64_t m = m0 + 8 * q;
+        if (dst == nullptr || m >= a.ldt) continue;
+        *reinterpret_cast<u32x4*>(dst + (int64_t)v * a.ldt + m) = *reinterpret_cast<const u32x4*>(&tsp[which][v][8 * q]);
     }
 }
 
