@@ -291,23 +291,46 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_mad_batch_kernel(const 
 
 // ---------------------------------------------------------------- preparation
 // One workgroup per (segment g, 256 columns): the segment's 32 packed rows over those columns are
-// staged in LDS (every byte load of the workgroup in flight at once, each row's bytes contiguous),
-// then each thread assembles its column's 32 codes into the `BITS` stream dwords (row 32g+i's
-// code at bit BITS*(31-i)), written coalesced: consecutive columns are consecutive dwords.
+// staged in LDS (each row's bytes contiguous; every load of the workgroup issued before any LDS
+// write, so the loads are in flight together), then each thread assembles its column's 32 codes
+// into the `BITS` stream dwords (row 32g+i's code at bit BITS*(31-i)), written coalesced:
+// consecutive columns are consecutive dwords. Rows whose stride and start are dword-aligned (every
+// packed row of a multiple of 128 columns) are staged a dword a load, others a byte a load.
 constexpr int kPrepCols = 256;
 template <int BITS>
 __global__ __launch_bounds__(kPrepCols) void prepare_stream_kernel(const R97IqrDecodeDesc d,
                                                                    uint32_t* __restrict__ stream) {
     constexpr int kSpan = kPrepCols * BITS / 8 + 1;  // a row's bytes over the block's columns (+ a straddle)
-    __shared__ uint8_t rows[32][kSpan + 3];
+    constexpr int kRow = kSpan + 3;                  // LDS bytes a row: 32 BITS + 4, a whole number of dwords
+    __shared__ __attribute__((aligned(4))) uint8_t rows[32][kRow];
     const int64_t c0 = (int64_t)blockIdx.x * kPrepCols;
     const int64_t g = blockIdx.y;
-    const int64_t byte0 = c0 * BITS / 8;  // c0 is a multiple of 8: the block starts on a byte
+    const int64_t byte0 = c0 * BITS / 8;  // c0 is a multiple of 256: the block starts on a dword
     const int64_t avail = d.codes_row_bytes - byte0;
     const int span = (int)(avail < kSpan ? avail : kSpan);
-    for (int idx = threadIdx.x; idx < 32 * span; idx += kPrepCols) {
-        const int i = idx / span, b = idx - i * span;
-        rows[i][b] = d.codes[(g * 32 + i) * d.codes_row_bytes + byte0 + b];
+    if (d.codes_row_bytes % 4 == 0 && reinterpret_cast<uintptr_t>(d.codes) % 4 == 0) {
+        // a row's dwords: ceil(span / 4), within the row (avail is a multiple of 4; a full block's
+        // last dword reaches 3 bytes into the next block's)
+        const int sd = (span + 3) / 4;
+        constexpr int kLoads = (32 * (kRow / 4) + kPrepCols - 1) / kPrepCols;
+        uint32_t v[kLoads];
+#pragma unroll
+        for (int u = 0; u < kLoads; ++u) {
+            const int idx = (int)threadIdx.x + kPrepCols * u, i = idx / sd, q = idx - i * sd;
+            v[u] = idx < 32 * sd ? *reinterpret_cast<const uint32_t*>(d.codes + (g * 32 + i) * d.codes_row_bytes + byte0 +
+                                                                      4 * q)
+                                 : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kLoads; ++u) {
+            const int idx = (int)threadIdx.x + kPrepCols * u, i = idx / sd, q = idx - i * sd;
+            if (idx < 32 * sd) *reinterpret_cast<uint32_t*>(&rows[i][4 * q]) = v[u];
+        }
+    } else {
+        for (int idx = threadIdx.x; idx < 32 * span; idx += kPrepCols) {
+            const int i = idx / span, b = idx - i * span;
+            rows[i][b] = d.codes[(g * 32 + i) * d.codes_row_bytes + byte0 + b];
+        }
     }
     __syncthreads();
     const int64_t col = c0 + threadIdx.x;
