@@ -131,6 +131,66 @@ def test_vocab_head_one_hot_and_chunking():
     assert rel_l2(got, 2 * want) > 0.3  # teeth: a doubled transform misses
 
 
+def test_vocab_head_full_size():
+    """The benchmark's head at its full size: four b5 trellis.mad classes of 32768, 65536, 98304 and
+    51712 rows (248320 in all, ids ascending within a class, a random partition of the vocabulary),
+    n_embd 2048, fwht128, 4096 token rows -- 61 ranges, 8 product slices. Checked against float64
+    products of the oracle's decoded weights: 8 sampled token rows (the first, tile edges, the last),
+    and every row at once through the column sum (the head is linear in its token rows:
+    sum_m d_x[m] = H . sum_c ((sum_m dy[m, ids_c]) . W_c) * scale.col_c). The rows within TOL (1e-5;
+    measured 1.7e-6), the column sum within 1e-4 (measured 1.0e-5: the 4096 rows' f32 results,
+    each rounded on its own, summed against a sum taken before the product, with much
+    cancellation); a dropped low half misses by ~2e-3."""
+    from r9700training_amd.vocab_head import VocabHead
+
+    print("case vocab head full size: 248320 rows, n_embd 2048, 4096 token rows", flush=True)
+    sizes, K, rows = [32768, 65536, 98304, 51712], 2048, 4096
+    vocab = sum(sizes)
+    rng = np.random.default_rng(248320)
+    perm = rng.permutation(vocab)
+    keep, dev_cls, orc, at = [], [], [], 0
+    for i, n in enumerate(sizes):
+        p = S.trellis(rows=n, cols=K, bits=5, state_bits=16, run_rows=256, rb=1, mad=1, scale_dtype=S.F32,
+                      rowf=True, seed=700 + i, packed=True)
+        p.scale_col = None  # the head multiplies its scale.col after the product
+        ids = np.sort(perm[at:at + n]).astype(np.int32)
+        at += n
+        cf = (0.5 + rng.random(K // 128)).astype(np.float32)
+        d = device_desc(p, keep)
+        ids_d, cf_d = dev(ids), dev(cf)
+        keep += [ids_d, cf_d]
+        dev_cls.append((d, ids_d, cf_d))
+        codes, gscale = O.decode(p.desc())
+        orc.append((codes, S.bf16_bits_to_f32(gscale.astype(np.uint16)).astype(np.float64), ids, cf.astype(np.float64)))
+    head = VocabHead(K, vocab, dev_cls, transform=128)
+    head._keep += keep
+    gen = torch.Generator(device="cuda").manual_seed(248320)
+    dy = torch.randn((rows, vocab), generator=gen, device="cuda").to(torch.bfloat16)
+    d_x = torch.zeros((rows, K), device="cuda")
+    head.transpose(dy, d_x)
+    torch.cuda.synchronize()
+    sample = np.array([0, 1, 511, 512, 2047, 2048, 4094, 4095])
+    ridx = torch.from_numpy(sample).cuda()
+    dys = dy.index_select(0, ridx).double().cpu().numpy()
+    dysum = dy.sum(0, dtype=torch.float64).cpu().numpy()[None]
+    got, gotsum = d_x.index_select(0, ridx).double().cpu().numpy(), d_x.sum(0, dtype=torch.float64).cpu().numpy()[None]
+    del dy, d_x
+    torch.cuda.empty_cache()
+
+    def reference(y):  # float64: sum over classes and 128-column blocks of (y[:, ids] * scale) . codes * cf
+        out = np.zeros((y.shape[0], K))
+        for codes, scale, ids, cf in orc:
+            yc = y[:, ids]
+            for kb in range(K // 128):
+                blk = slice(128 * kb, 128 * kb + 128)
+                out[:, blk] += ((yc * scale[:, kb]) @ codes[:, blk].astype(np.float64)) * cf[kb]
+        return O.fwht128(out)
+
+    e, es = rel_l2(got, reference(dys)), rel_l2(gotsum, reference(dysum))
+    print(f"  rows {sample.tolist()}: rel L2 {e:.3e}; column sums rel L2 {es:.3e}", flush=True)
+    assert e <= TOL and es <= 1e-4
+
+
 def test_vocab_head_in_a_graph():
     """The head captured in a HIP graph and replayed: a call forks its weights' decode onto the
     device's side stream (beside the gather on the caller's stream) and joins it back before the
