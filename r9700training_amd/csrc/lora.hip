@@ -373,7 +373,10 @@ __device__ __forceinline__ float device_load(const float* p) {
 // iterations before it is multiplied (two register sets in flight) and written to one of two LDS
 // slots the iteration before. The token tile is read back transposed with ds_read_b64_tr_b16
 // (the MFMA's B operand), the Pt rows straight (the A operand). Token rows are padded to 576
-// bytes so the transposing reads of four consecutive rows land on distinct banks.
+// bytes so the transposing reads of four consecutive rows land on distinct banks. A Pt row's
+// 16-byte chunks are stored XOR-swizzled by the row (pt_chunk), so the 16 rows that 16 consecutive
+// lanes read at one chunk land on all 64 banks (stored in order, rows 128 or 64 bytes apart put
+// every 2nd or 4th row on the same banks).
 constexpr int kGradCols = 256;
 constexpr int kGradRow = 2 * kGradCols + 64;
 
@@ -389,7 +392,17 @@ struct GradShape {
     static constexpr int NREG = LOADS + NP;
     static constexpr int VTILE = TOK * kGradRow;
     static constexpr int SLOT = VTILE + PTB;
+    static constexpr int CPR = 2 * TOK / 16;            // 16-byte chunks a Pt row (8 or 4)
 };
+
+// the LDS byte of chunk c of Pt row v in a tile: the row's chunks permuted by the row, so rows
+// v and v + 16/CPR.. differ in chunk where they share banks (a row is CPR * 4 banks of 64)
+template <int R>
+__device__ __forceinline__ int pt_chunk(int v, int c) {
+    using S = GradShape<R>;
+    const int f = (v / (16 / S::CPR)) & (S::CPR - 1);
+    return v * (2 * S::TOK) + 16 * (c ^ f);
+}
 
 // one lane's loads of a gradient tile: its token row halves (16 bytes each) and Pt pieces
 struct GradLane {
@@ -431,7 +444,11 @@ __device__ __forceinline__ void grad_store(const GradLane& L, const u32x4 (&r)[G
 #pragma unroll
     for (int u = 0; u < S::NP; ++u) {
         const int piece = L.wave + 8 * u;
-        if (piece < S::PTB / 1024) *reinterpret_cast<u32x4*>(st + S::VTILE + 1024 * piece + 16 * L.lane) = r[S::LOADS + u];
+        // the lane's 16 bytes: chunk (byte % (2 TOK)) / 16 of Pt row byte / (2 TOK)
+        const int byte = 1024 * piece + 16 * L.lane;
+        if (piece < S::PTB / 1024)
+            *reinterpret_cast<u32x4*>(st + S::VTILE + pt_chunk<R>(byte / (2 * S::TOK), (byte % (2 * S::TOK)) / 16)) =
+                r[S::LOADS + u];
     }
 }
 
@@ -444,8 +461,8 @@ __device__ __forceinline__ void grad_multiply(const uint8_t* st, int wave, int i
         bf16x8 pa[S::VB];  // lane (i, grp): Pt row 16vb + i, tokens 32ks + 8grp .. +8
 #pragma unroll
         for (int vb = 0; vb < S::VB; ++vb)
-            pa[vb] = as_bf16x8(*reinterpret_cast<const uint4*>(st + S::VTILE + (16 * vb + i16) * (2 * S::TOK) +
-                                                                2 * (32 * ks + 8 * grp)));
+            pa[vb] = as_bf16x8(
+                *reinterpret_cast<const uint4*>(st + S::VTILE + pt_chunk<R>(16 * vb + i16, 4 * ks + grp)));
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
             const int col = 32 * wave + 16 * cb;
@@ -465,8 +482,10 @@ template <int R>
 __global__ __launch_bounds__(512) void lora_grads_kernel(GradArgs ga) {
     using S = GradShape<R>;
     constexpr int VB = S::VB;
+    // (the `last` flag below lives in the slots' first bytes once every wave is done with them: at
+    // rank 16 the slots are exactly 80 KiB, so two workgroups fit a CU)
     __shared__ __attribute__((aligned(16))) uint8_t lds[2 * S::SLOT];
-    __shared__ int last;
+    int& last = *reinterpret_cast<int*>(lds);
     const GradOne& g = ga.one[blockIdx.z];
     const int64_t C = g.C;
     const int64_t c0 = (int64_t)blockIdx.x * kGradCols;
