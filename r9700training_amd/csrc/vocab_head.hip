@@ -280,9 +280,10 @@ bool plan_ok(const R97qVocabPlan* plan, int64_t rows, const char* who) {
 }
 
 // The side stream of a device (and its fork and join events), made on the first call that finds
-// none with that device current and its stream not capturing a graph (a call that cannot make one
-// runs the decode on its own stream). Held until the process ends; used under g_side_mu, so calls
-// from several threads fork and join one at a time.
+// none with that device current and its stream not capturing a graph. A call that cannot make one,
+// or whose stream belongs to another device than the current one, runs the decode on its own
+// stream. Held until the process ends; used under g_side_mu, so calls from several threads fork
+// and join one at a time.
 struct SideStream {
     hipStream_t s;
     hipEvent_t fork, join;
@@ -295,18 +296,24 @@ std::mutex g_side_mu;
 const SideStream* side_stream(hipStream_t caller) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kSideDevices) return nullptr;
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(caller, &sdev) != hipSuccess || sdev != dev) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
     if (g_side_ok[dev]) return &g_side[dev];
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(caller, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
     SideStream& sd = g_side[dev];
-    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess) {
+    bool ok = hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) == hipSuccess;
+    bool fork = ok && hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) == hipSuccess;
+    ok = fork && hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) == hipSuccess;
+    if (!ok) {  // what was made is given back; a later call tries again
         (void)hipGetLastError();
+        if (fork) (void)hipEventDestroy(sd.fork);
+        if (sd.s) (void)hipStreamDestroy(sd.s);
+        sd = SideStream{};
         return nullptr;
-    }
-    if (hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) {
-        (void)hipGetLastError();
-        return nullptr;  // the stream is kept (and made again on a later call): a rare failure
     }
     g_side_ok[dev] = true;
     return &sd;
