@@ -308,6 +308,102 @@ VOCAB_CLASSES = [32768, 65536, 98304, 51712]  # rows a class (one trellis width 
 VOCAB_EMBD = 2048
 
 
+def rows_cpu_baseline(fn, rows, target_s, nthreads, ops, unit, fixed_s=0.0, what="", reps=3, div=1e12,
+                      kind=None):
+    """A host path timed over token rows: `fn(idx)` runs it over the rows idx (numpy int64), first on a
+    probe to price a row, then on an evenly spaced sample sized for about target_s over `reps` passes
+    (the median taken), extrapolated linearly to all `rows`; `fixed_s` (a once-a-call cost, the
+    weight's decode) added. ops: the whole call's operations (or bytes), for `value` = ops / seconds /
+    div in `unit`. The host path is the reference's own code from oracle/_ref when built
+    ("reference"), else the oracle's restatement ("port"); `kind` overrides."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    os.environ["R97_THREADS"] = str(nthreads)
+    O.set_threads(nthreads)
+    probe = np.arange(min(rows, 2 * nthreads))
+    t0 = time.perf_counter()
+    fn(probe)
+    per_row = (time.perf_counter() - t0) / len(probe)
+    n = int(max(len(probe), min(rows, target_s / reps / max(per_row, 1e-9))))
+    n = max(len(probe), n // len(probe) * len(probe))
+    idx = np.linspace(0, rows - 1, n).astype(np.int64)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn(idx)
+        times.append(time.perf_counter() - t0)
+    t_rows = sorted(times)[len(times) // 2]
+    call_s = fixed_s + t_rows * rows / n
+    return {
+        "value": round(ops / call_s / div, 6), "unit": unit, "s_per_call": round(call_s, 4), "cores": nthreads,
+        "kind": kind or ("reference" if O.ref() is not None else "port"),
+        "sample": f"{n} of {rows} token rows (evenly spaced){what}, f64, {nthreads} threads; the median of "
+                  f"{reps} passes ({', '.join(f'{x:.2f}' for x in times)} s) extrapolated linearly in rows"
+                  + (f", plus the weight's decode once ({fixed_s:.2f} s)" if fixed_s else ""),
+    }
+
+
+def vocab_cpu_baseline(src, dy, K, target_s, nthreads, reps=3):
+    """The host restatement of the reference's vocabulary-head kernels (oracle: orc_vocab_class_product
+    and orc_fwht128, f64, following src/adjoint/device/vocab_head.hip:88-163) over an evenly spaced
+    sample of token rows, split over `nthreads` threads, plus every class's decode (the reference's
+    r97_iqr_decode_host from oracle/_ref when built, else the oracle's), as the reference decodes
+    each call; the rows timed `reps` times (the median) and extrapolated linearly to all rows.
+    src: (packed codes, f32 row scale, scale.col, ids, rows) a class, on the card; dy: bf16 on the
+    card."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    O.set_threads(nthreads)
+    decode_s, classes = 0.0, []
+    for codes_d, scale_d, cf_d, ids_d, n in src:
+        codes, scale, s = ref_decode(codes_d.cpu().numpy(), scale_d.cpu().numpy().view(np.float32),
+                                     np.ones(K // 128, np.float32), n, K, 0x2F1E3D | 1, 0x9E3779B9)
+        decode_s += s
+        classes.append((codes, scale, ids_d.cpu().numpy(), cf_d.cpu().numpy()))
+    rows = dy.shape[0]
+
+    def bits(idx):
+        it = torch.from_numpy(np.asarray(idx, np.int64)).to(dy.device)
+        return dy.index_select(0, it).view(torch.int16).cpu().numpy().view(np.uint16)
+
+    def run(b):  # the sample's rows, a block a thread (the C calls release the GIL)
+        parts = np.array_split(np.arange(b.shape[0]), nthreads)
+        with ThreadPoolExecutor(nthreads) as ex:
+            list(ex.map(lambda p: O.vocab_head_transpose(b[p], classes, transform=128), [p for p in parts if len(p)]))
+
+    probe = bits(np.arange(min(rows, nthreads)))
+    t0 = time.perf_counter()
+    run(probe)
+    per_pass_row = (time.perf_counter() - t0) / probe.shape[0]  # per row, all threads busy
+    n = int(max(nthreads, min(rows, target_s / reps / max(per_pass_row, 1e-9))))
+    n = max(nthreads, n // nthreads * nthreads)
+    sample = bits(np.linspace(0, rows - 1, n).astype(np.int64))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run(sample)
+        times.append(time.perf_counter() - t0)
+    t_rows = sorted(times)[len(times) // 2]
+    call_s = decode_s + t_rows * rows / n
+    vocab = sum(c[0].shape[0] for c in classes)
+    return {
+        "value": round(2.0 * rows * vocab * K / call_s / 1e12, 6), "unit": "TFLOP/s",
+        "s_per_call": round(call_s, 1), "cores": nthreads, "kind": "port",
+        "sample": f"{n} of {rows} token rows (evenly spaced) through the classes' products and the transform "
+                  f"(f64, {nthreads} threads, a block of rows each), the median of {reps} passes "
+                  f"({', '.join(f'{x:.1f}' for x in times)} s) extrapolated linearly in rows, plus the "
+                  f"classes' decode once ({decode_s:.2f} s, {'the reference' if O.ref() is not None else 'the oracle'}"
+                  f"'s host decode)",
+    }
+
+
 def vocab_head_bench(args):
     """The vocabulary head's transposed product (r97q_vocab_head_transpose) on a synthetic head the
     size of the reference container's (four b5 trellis.mad classes, f32 row scale + scale.col, the
@@ -326,7 +422,7 @@ def vocab_head_bench(args):
     g = torch.Generator(device="cuda").manual_seed(args.seed)
     perm = torch.randperm(vocab, device="cuda", generator=g).to(torch.int32)
     rng = np.random.default_rng(args.seed)
-    classes, keep, at = [], [], 0
+    classes, keep, src, at = [], [], [], 0
     for n in VOCAB_CLASSES:
         codes = torch.randint(0, 256, (n, K * 5 // 8), dtype=torch.uint8, device="cuda", generator=g)
         scale = torch.from_numpy((0.0005 + 0.01 * rng.random(n)).astype(np.float32).view(np.uint8)).to(dev)
@@ -338,6 +434,7 @@ def vocab_head_bench(args):
         at += n
         classes.append((d, ids, cf))
         keep += [codes, scale, cf, ids]
+        src.append((codes, scale, cf, ids, n))
     head = VocabHead(K, vocab, classes, transform=128)
     dy = torch.randn((rows, vocab), dtype=torch.bfloat16, device=dev, generator=g)
     d_x = torch.zeros((rows, K), device=dev)
@@ -353,6 +450,7 @@ def vocab_head_bench(args):
     ms = (time.perf_counter() - t0) * 1e3 / steps
     flops = 2.0 * rows * vocab * K
     tf = flops / (ms * 1e-3) / 1e12
+    cpu = vocab_cpu_baseline(src, dy, K, args.cpu_seconds, min(8, host_cores())) if args.cpu_seconds > 0 else None
     print(json.dumps({
         "metric": "vocab head transposed product TFLOP/s (decode + gather + MFMA + transform per call)",
         "value": round(tf, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -362,6 +460,7 @@ def vocab_head_bench(args):
                    "n_embd": K, "rows": rows},
         "roofline": {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        **({"cpu_baseline": cpu} if cpu else {}),
     }), flush=True)
 
 
@@ -421,6 +520,17 @@ def coded_fwd_bench(args):
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ops = 2 * T * N * K
     tops = ops / (ms * 1e-3) / 1e12
+    cpu = None
+    if args.cpu_seconds > 0:
+        import numpy as np
+
+        from oracle import oracle as O
+
+        a_h, as_h = a.cpu().numpy().astype(np.float64), a_scale.cpu().numpy().astype(np.float64)
+        codes_h, scale_h = codes.cpu().numpy(), scale.view(torch.int16).cpu().numpy().view(np.uint16)
+        cpu = rows_cpu_baseline(
+            lambda idx: O.gemm_nt_q_twin(a_h[idx], as_h[idx], codes_h, scale_h, use_ref=O.ref() is not None),
+            T, args.cpu_seconds, min(8, host_cores()), ops, "TOP/s", what=" through the gemm_nt_q twin")
     print(json.dumps({
         "metric": "coded forward (gemm_nt_q twin) TOP/s at C2's square layer",
         "value": round(tops, 3), "unit": "TOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -431,6 +541,7 @@ def coded_fwd_bench(args):
                                "group 128, Y f32", "T": T, "N": N, "K": K},
         "roofline": {"bound": "mfma", "kernel": "qlinear_q_kernel", "achieved": round(tops, 3),
                      "peak": PEAK_INT8_TOPS, "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": None},
+        **({"cpu_baseline": cpu} if cpu else {}),
     }), flush=True)
 
 
@@ -510,6 +621,22 @@ def ref_shapes_bench(args):
             res[tag] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4),
                         "tiles_512x128": tiles}
         res["reference_r9700_adjoint_kernel_ms"] = ref_ms
+        if args.cpu_seconds > 0:
+            from oracle import oracle as O
+
+            wc, ws_, dec_s = ref_decode(codes.cpu().numpy(), scale.cpu().numpy().view(np.float32), cf.cpu().numpy(),
+                                        N, K, 0x2F1E3D | 1, 0x9E3779B9)
+            use_ref = O.ref() is not None
+            x_h, dy_h = X.float().cpu().numpy().astype(np.float64), dY.float().cpu().numpy().astype(np.float64)
+
+            def host(idx):
+                O.gemm_nt_twin(x_h[idx], wc, ws_, use_ref=use_ref)
+                O.gemm_nt_adjoint(dy_h[idx], wc, ws_, use_ref=use_ref)
+
+            res["cpu_baseline"] = rows_cpu_baseline(host, M, args.cpu_seconds / len(REF_SHAPES), min(8, host_cores()),
+                                                    4 * M * N * K, "TFLOP/s", fixed_s=dec_s,
+                                                    what=" through the gemm_nt twin and adjoint", reps=1)
+            del x_h, dy_h, wc, ws_
         out.append(res)
         print(json.dumps(res), file=sys.stderr, flush=True)
         del w, codes, scale, cf, X, dY, Y, dX, wsf, wsb
@@ -523,6 +650,14 @@ def ref_shapes_bench(args):
         "config": {"workload": "ref_shapes: docs/kernels/linear.md:261-268, M x N x K, no adapter, outputs f32",
                    "decode": args.decode},
         "shapes": out,
+        **({"cpu_baseline": {
+            "value": round(sum(4 * r["M"] * r["N"] * r["K"] for r in out) /
+                           sum(r["cpu_baseline"]["s_per_call"] for r in out) / 1e12, 6),
+            "unit": "TFLOP/s", "cores": out[0]["cpu_baseline"]["cores"], "kind": out[0]["cpu_baseline"]["kind"],
+            "sample": "each shape's twin and adjoint on the host over a sample of its token rows, one pass a "
+                      "shape, extrapolated in rows, plus its weight's decode (the shapes' own lines hold each); "
+                      "the shapes' operations over their summed host seconds"}}
+           if out and "cpu_baseline" in out[0] else {}),
     }), flush=True)
 
 
@@ -588,6 +723,22 @@ def fused_quant_bench(args):
             gbs = fused_quant_bytes(part, rows, n, group, bwd) / (ms * 1e-3) / 1e9
             res[tag] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
                         "bytes": fused_quant_bytes(part, rows, n, group, bwd)}
+        if args.cpu_seconds > 0:
+            import numpy as np
+
+            from oracle import oracle as O
+
+            f64 = lambda t: None if t is None else t.float().cpu().numpy().astype(np.float64)
+            x0_h, x1_h, gc_h, go_h = f64(x0), f64(x1), f64(gc), f64(go)
+
+            def host(idx):  # the oracle's producer and adjoint (single-threaded C) over the rows idx
+                x1_r = x1_h if part == "rmsnorm" else None if x1_h is None else x1_h[idx]
+                _, _, sc = O.fused_quant(part, x0_h[idx], x1_r, group, **kw)
+                O.fused_quant_adjoint(part, x0_h[idx], x1_r, group, sc, gc_h[idx], go_h[idx], **kw)
+
+            res["cpu_baseline"] = rows_cpu_baseline(
+                host, rows, args.cpu_seconds / len(FUSED_SHAPES), 1, res["forward"]["bytes"] + res["adjoint"]["bytes"],
+                "GB/s", what=" through the producer and its adjoint", reps=1, div=1e9, kind="port")
         out.append(res)
         print(json.dumps(res), file=sys.stderr, flush=True)
         del x0, x1, codes, scale, y, gc, go, dx0, dx1
@@ -604,6 +755,13 @@ def fused_quant_bench(args):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
         "ops": out,
+        **({"cpu_baseline": {
+            "value": round(total_bytes / sum(r["cpu_baseline"]["s_per_call"] for r in out) / 1e9, 3),
+            "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "each op's producer and adjoint through the oracle's restatement (single-threaded C) over "
+                      "a sample of its rows, one pass an op, extrapolated in rows (the ops' own lines hold each); "
+                      "the ops' bytes over their summed host seconds"}}
+           if out and "cpu_baseline" in out[0] else {}),
     }), flush=True)
 
 
