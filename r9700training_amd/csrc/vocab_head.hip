@@ -5,15 +5,16 @@
 //
 // The reference runs it as a gather, a per-token-row GEMV over the decoded int8 grid with f32
 // fmas, and the un-rotation. Here it is the register-fed dX kernel's product. A class's rows go in
-// ranges of about 4096 (whole trellis runs), a batch of up to kBatch ranges at a time: the batch's
-// ranges are decoded into the int8-code form in the workspace (the standalone decode's kernel
-// writing tiled, one launch for the batch when the form allows), and one
-// qlinear_rt_vocab_kernel launch (a grid slice a range, so a head with few token rows or a narrow
-// n_embd still fills the chip) writes each range's (gathered . W) * scale.col -- the weight as the
-// exact sum of two bf16 halves, both reduced into one f32 accumulator; the class's scale.col one
-// factor a 128-column tile -- into its own f32 partial; the partials are then added into d_x in
-// range order (deterministic). Ranges are padded to Np (a multiple of 128) rows with zero codes,
-// zero scales and zero cotangent columns. The products' operands -- the cotangent's columns of
+// ranges of about 4096 (whole trellis runs); every range is decoded once a call into the int8-code
+// form in the workspace (the standalone decode's kernel writing tiled, up to kDecodeRanges ranges
+// of a class a launch when the form allows). One qlinear_rt_vocab_kernel launch then runs every
+// range: the ranges go in slices of a few of one class (enough slices to fill the chip, so a head
+// with few token rows or a narrow n_embd still does), a workgroup summing its tile's
+// (gathered . W) over each range of its slice -- the weight as the exact sum of two bf16 halves,
+// both reduced into one f32 accumulator -- times the class's scale.col (one factor a 128-column
+// tile) into the slice's f32 partial; the partials are then added into d_x in slice order
+// (deterministic). Ranges are padded to Np (a multiple of 128) rows with zero codes, zero scales and
+// zero cotangent columns. The products' operands -- the cotangent's columns of
 // every class's rows, each range's [rows, Np] in the fused kernels' tiled layout -- are gathered
 // first, for all classes in one launch whose token rows vary slowest, so the workgroups in flight
 // cover a few token rows of every class and each cotangent line is fetched from memory about once
