@@ -247,8 +247,9 @@ def test_every_decode_form_derives_its_description(name, kw):
     assert ok and (f is None) == (p.scale_col is None)
 
 
-# radiance's plane dtypes by name -> this build's codes: the mapping INTEGRATION.md gives for the
-# copy of a RadEncoding into an R97Encoding (radiance's own numeric values are not in this tree)
+# radiance's plane dtypes by name -> this build's codes: the mapping a caller applies when it copies
+# a RadEncoding into an R97Encoding (each packed width to its bit count, the rest one to one;
+# radiance's own numeric values are not in this tree)
 RAD_TO_R97 = dict({f"RAD_U{b}": R.R97_DT_U[b] for b in range(1, 13)},
                   RAD_I8=R.R97_DT_I8, RAD_U32=R.R97_DT_U32, RAD_F32=R.R97_DT_F32, RAD_BF16=R.R97_DT_BF16,
                   RAD_F16=R.R97_DT_F16, RAD_F8E4M3=R.R97_DT_F8E4M3)
