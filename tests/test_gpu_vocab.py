@@ -83,7 +83,8 @@ def test_vocab_head_matches_oracle(rows, K, sizes, forms, offset, transform):
 
 
 def test_vocab_head_ranges_and_padding():
-    """A class past one decode range (16384 rows) and a short last range padded to 128 rows."""
+    """A class of several 4096-row decode ranges (20077 rows: four whole, one short) whose short last
+    range is padded to a multiple of 128 rows; the ranges split over several product slices."""
     print("case vocab head ranges", flush=True)
     rng = np.random.default_rng(4)
     rows, K = 64, 128
@@ -96,6 +97,26 @@ def test_vocab_head_ranges_and_padding():
     e = rel_l2(d_x.cpu().numpy(), want)
     print(f"  rel L2 {e:.3e}", flush=True)
     assert e <= TOL
+
+
+def test_vocab_head_two_row_blocks():
+    """Token rows past one block (4096 + 4 = 4100 rows): the weights are decoded once, beside the first
+    block's gather, and the second block's gather and product reuse them; d_x is added into."""
+    print("case vocab head rows=4100 (two token-row blocks)", flush=True)
+    rng = np.random.default_rng(4100)
+    rows, K = 4100, 256
+    head, orc_cls, vocab = head_and_oracle(rng, K, [1000, 700], ["trunk-b5", "stored-u4"], transform=128)
+    dy = S.f32_to_bf16_bits(rng.standard_normal((rows, vocab)).astype(np.float32))
+    d0 = rng.standard_normal((rows, K)).astype(np.float32)
+    d_x = torch.tensor(d0, device="cuda")
+    head.transpose(torch.from_numpy(dy.view(np.int16)).cuda().view(torch.bfloat16), d_x)
+    torch.cuda.synchronize()
+    want = O.vocab_head_transpose(dy, orc_cls, transform=128, d_x=d0)
+    base = O.fwht128(d0)
+    got = d_x.cpu().numpy()
+    e, e2 = rel_l2(got - base, want - base), rel_l2(got[4096:] - base[4096:], want[4096:] - base[4096:])
+    print(f"  rel L2 {e:.3e}, the second block's 4 rows {e2:.3e}", flush=True)
+    assert e <= TOL and e2 <= TOL
 
 
 def test_vocab_head_one_hot_and_chunking():
