@@ -242,6 +242,29 @@ def test_vocab_head_in_a_graph():
         assert torch.equal(d_x, eager), i
 
 
+def test_vocab_head_on_a_caller_stream():
+    """The head on a stream of the caller's own (not the default one): the decode forks from that
+    stream and joins back into it, so work the caller enqueues after the call on the same stream
+    sees the whole result; bit-equal to the call on the default stream."""
+    print("case vocab head on a caller stream rows=300 K=256", flush=True)
+    rng = np.random.default_rng(13)
+    K, rows = 256, 300
+    head, _, vocab = head_and_oracle(rng, K, [1500, 900], ["trunk-b5", "stored-u4"])
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    dy = torch.randn((rows, vocab), generator=gen, device="cuda").to(torch.bfloat16)
+    want = torch.zeros((rows, K), device="cuda")
+    head.transpose(dy, want)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    got = torch.zeros((rows, K), device="cuda")
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        head.transpose(dy, got, stream=side)
+        copy = got.clone()  # enqueued after the call on the same stream
+    torch.cuda.synchronize()
+    assert torch.equal(copy, want) and torch.equal(got, want)
+
+
 def test_vocab_head_cast():
     from r9700training_amd.vocab_head import cast
 
